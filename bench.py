@@ -1,0 +1,207 @@
+"""Benchmark: batch-64 paged decode step (append + paged decode attention) on
+one MI355X — BASELINE.json config 3.
+
+A step appends one bf16 K/V row per sequence into its page (pkv_append) and
+runs paged decode attention over every sequence's context
+(pkv_attn_decode: key-range kernel + merge). Contexts are U[512, 8192] per
+sequence (fresh seeded mix per run), pages scattered over a 65,536-page pool
+(2 GiB of K + 2 GiB of V), Hq 16 / Hkv 4 / head_dim 256, page 16. Step i
+appends at position ctx + i and attends ctx + i + 1 keys; the pages for every
+step are reserved up front as the reference's admission does.
+
+Prints one JSON line. `value` is the achieved HBM bandwidth of the whole step
+in GB/s (algorithmic bytes / measured step time); us_per_step and the
+fraction of the 8 TB/s peak ride along. `roofline` is for the dominant kernel
+(the key-range decode kernel), timed with HIP events on the launch stream.
+`cpu_baseline` times the oracle (a scalar C restatement) on the host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "pocket-engine_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--seed", type=int, default=None, help="length-mix seed (default: fresh per run)")
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--pages", type=int, default=65536)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--wg-per-cu", type=int, default=None)
+    ap.add_argument("--min-range", type=int, default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the paged KV path shards by "
+              "sequence with no exchange, so N-GPU throughput is N x the one-GPU figure. Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import pkv
+    from pkv import synth
+
+    if args.wg_per_cu or args.min_range:
+        pkv.attn_decode_config(args.wg_per_cu or 2, args.min_range or 32)
+    seed = args.seed if args.seed is not None else int(time.time()) % 100000
+    dev = torch.device("cuda:0")
+    Hq, Hkv, D, BS = 16, 4, 256, 16
+    B, pages = args.batch, args.pages
+    S = args.warmup + args.steps
+    lens = synth.c3_lengths(seed, batch=B)
+    meta = synth.decode_meta(lens, pages, steps=S, seed=seed)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    kc = torch.empty(pages * BS, Hkv, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty_like(kc)
+    for t in (kc, vc):  # N(0,1) * 0.5, in slices to bound temporaries
+        for i in range(0, t.shape[0], 1 << 18):
+            t[i:i + (1 << 18)] = torch.randn(t[i:i + (1 << 18)].shape, device=dev, generator=gen) * 0.5
+    q = (torch.randn(B, Hq, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    qstride = synth.qkv_stride(Hq, Hkv)
+    qkv = (torch.randn(B, qstride, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev)
+    steps = [meta.step(i) for i in range(S)]
+    pos_d = torch.from_numpy(np.stack([s["pos"] for s in steps])).to(dev)
+    slot_d = torch.from_numpy(np.stack([s["slot_map"] for s in steps])).to(dev)
+    ts = torch.from_numpy(steps[0]["tok_seq"]).to(dev)
+    cu = torch.from_numpy(steps[0]["cu"]).to(dev)
+    bt = torch.from_numpy(meta.block_table).to(dev)
+    ws = torch.empty(pkv.attn_decode_workspace(B, Hq), dtype=torch.uint8, device=dev)
+    k_rows = qkv.data_ptr() + 2 * (2 * Hq * D)
+    v_rows = k_rows + 2 * (Hkv * D)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step(i, ev=None):
+        pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=sp)
+        if ev:
+            ev[0].record(stream)
+        pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu, 0,
+                        None, 1, B, pages, ws, stream=sp, phase="split")
+        if ev:
+            ev[1].record(stream)
+        pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu, 0,
+                        None, 1, B, pages, ws, stream=sp, phase="merge")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    # Timed region: K steps; events bracket the key-range kernel of each step.
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for k in range(args.steps):
+        step(args.warmup + k, evs[k])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    split_ms = [a.elapsed_time(b) for a, b in evs]
+    ms_step = total_ms / args.steps
+
+    keys = [meta.keys(args.warmup + k) for k in range(args.steps)]
+    step_bytes = [synth.algorithmic_bytes_decode(kk, B, Hq, Hkv) + synth.algorithmic_bytes_append(B, Hkv)
+                  for kk in keys]
+    gbs = sum(step_bytes) / (total_ms * 1e-3) / 1e9
+    # Dominant kernel: bytes it must read = every key's K and V rows (all kv
+    # heads) + q; its partials are overhead, not algorithmic.
+    split_bytes = [kk * Hkv * D * 2 * 2 + B * Hq * D * 2 for kk in keys]
+    split_avg_us = 1e3 * sum(split_ms) / len(split_ms)
+    split_gbs = sum(split_bytes) / (sum(split_ms) * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(kc, vc, q, qkv, meta, steps[args.warmup], Hq, Hkv, qstride, dev)
+
+    line = {
+        "metric": "paged decode step us + achieved HBM GB/s (% of peak) at batch 64, 1 MI355X",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "us_per_step": round(ms_step * 1e3, 2),
+        "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 K/V/q, U[512,8192] contexts)",
+        "config": {"workload": "c3: batch-64 paged decode step (append 1 token/seq + paged decode attention)",
+                   "batch": B, "ctx": "U[512,8192]", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
+                   "pool_pages": pages, "seed": seed, "mean_keys_per_step": round(float(np.mean(keys)), 1),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "decode_split_kernel", "achieved": round(split_gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(split_gbs / PEAK_HBM_GBS, 4),
+                     "avg_us": round(split_avg_us, 2), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(kc, vc, q, qkv, meta, st, Hq, Hkv, qstride, dev):
+    """The oracle (scalar C, 1 thread) on the first timed step's workload —
+    append + decode of all 64 sequences — timed on the host."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    BS, D = 16, 256
+    B = meta.B
+    sel = list(range(B))
+    bt = meta.block_table
+    need = [(int(st["pos"][s]) + BS) // BS for s in sel]
+    sub = np.concatenate([bt[s, :n] for s, n in zip(sel, need)])
+    idx = torch.from_numpy(sub).to(dev).long()
+    kc_h = kc.view(-1, BS, Hkv, D)[idx].cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1, Hkv, D)
+    vc_h = vc.view(-1, BS, Hkv, D)[idx].cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1, Hkv, D)
+    remap = {int(p): i for i, p in enumerate(sub)}
+    bts = np.zeros((len(sel), meta.max_blocks), np.int32)
+    for i, (s, n) in enumerate(zip(sel, need)):
+        bts[i, :n] = [remap[int(p)] for p in bt[s, :n]]
+    q_h = q[sel].cpu().view(torch.int16).numpy().view(np.uint16)
+    qkv_h = qkv[sel].cpu().view(torch.int16).numpy().view(np.uint16)
+    pos = st["pos"][sel]
+    k_new = np.ascontiguousarray(qkv_h[:, 2 * Hq * D:2 * Hq * D + Hkv * D])
+    v_new = np.ascontiguousarray(qkv_h[:, 2 * Hq * D + Hkv * D:2 * Hq * D + 2 * Hkv * D])
+    slots = (bts[np.arange(len(sel)), pos // BS] * BS + pos % BS).astype(np.int32)
+    t = time.perf_counter()
+    oracle.append(k_new, v_new, slots, kc_h, vc_h)
+    oracle.attn_decode(q_h, kc_h, vc_h, qkv_h, qstride, Hq, Hkv, pos, np.arange(len(sel), dtype=np.int32), bts,
+                       meta.max_blocks, BS, 1 / 16)
+    dt = time.perf_counter() - t
+    sample_keys = int((pos + 1).sum())
+    full_keys = int((st["pos"] + 1).sum())
+    us_step = dt * 1e6 * full_keys / sample_keys
+    return {"value": round(us_step, 1), "unit": "us/step", "cores": 1, "kind": "port",
+            "sample": f"oracle append + decode of one full step: all {len(sel)} sequences, {sample_keys} keys, "
+                      f"{dt:.2f} s once (scale factor {full_keys / sample_keys:.3f})",
+            "cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    main()

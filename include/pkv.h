@@ -1,0 +1,156 @@
+/*
+ * pkv — MI355X (gfx950) paged KV cache: the C-ABI boundary of libpkv.so.
+ *
+ * Every entry point returns an int status: 0 on success, a HIP error code
+ * (hipError_t, passed through) when a HIP call fails, PKV_ERR_INVALID for
+ * arguments that fail validation, PKV_ERR_UNSUPPORTED (801, the reference's
+ * CUDA_ERROR_NOT_SUPPORTED convention, reference src/hip.rs:17-18, 61-66) for
+ * shapes the kernels do not implement. Nothing aborts. pkv_strerror() names
+ * a status.
+ *
+ * Device entry points are asynchronous on the caller's stream (`stream` is a
+ * hipStream_t; NULL = the null stream), never allocate and never synchronize,
+ * so they can be captured into HIP graphs (the reference's forward pass makes
+ * the same promise, model.rs:1739-1741). Device pointers are plain device
+ * addresses; the caller owns every buffer (reference gpu.rs:46-58).
+ *
+ * Cache layout (reference model.rs:1166-1197): one K and one V pool per
+ * attention layer of [pages * block_size][Hkv][head_dim] elements; the slot
+ * of key position p of a sequence is block_table[p / block_size] *
+ * block_size + p % block_size (reference sched.rs:1113-1114).
+ *
+ * Host allocator entry points (pkv_pool_*, pkv_kv_*) are single-threaded like
+ * the reference's Scheduler, which owns them on the engine thread.
+ */
+#ifndef PKV_H
+#define PKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PKV_OK 0
+#define PKV_ERR_INVALID 1      /* same value as hipErrorInvalidValue */
+#define PKV_ERR_UNSUPPORTED 801
+#define PKV_ERR_NO_BLOCKS 802  /* the pool cannot satisfy a request */
+
+const char* pkv_strerror(int status);
+/* ABI version: bumps when a signature changes. */
+int pkv_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Device: data movement (byte-exact)
+ * ------------------------------------------------------------------------- */
+
+/* KV append: for each token t < T with slot = slot_map[t] in [0, num_slots),
+ * copies the Hkv * head_bytes bytes at k_rows + t * row_stride to the K pool
+ * slot row and likewise V. Slots < 0 are padding and skipped.
+ * Replaces the cache stores of the reference's attn_prep kernel
+ * (src/kernels/qwen35.cu:1076-1128, launched at src/model.rs:2340-2365); the
+ * rows are the already normed/rotated K and the V of the qkv projection row,
+ * so for the reference's qkv layout k_rows = qkv + Hq * 512 elements,
+ * v_rows = k_rows + Hkv * 256 elements, row_stride = qstride * 2 bytes. */
+int pkv_append(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map, int T, int Hkv,
+               int head_bytes, void* kcache, void* vcache, int64_t num_slots, void* stream);
+
+/* Gather: k_out[j] = K pool slot row of key j, j < L, through one block-table
+ * row (bt_row, device); likewise V. Rows are Hkv * head_bytes bytes.
+ * The reference reads its cache this way inside every attention kernel
+ * (qwen35.cu:1203-1205, amd/attn_decode.cuh:56-74); it is a separate entry
+ * point here for checks and for exporting a sequence's KV. */
+int pkv_gather(const void* kcache, const void* vcache, const int32_t* bt_row, int L, int block_size, int Hkv,
+               int head_bytes, int64_t num_blocks, void* k_out, void* v_out, void* stream);
+
+/* Page copy (copy-on-write): for i < n, page dst[i] := page src[i] in both
+ * pools; page_bytes = block_size * Hkv * head_bytes (a multiple of 16).
+ * src/dst are device arrays. Destinations must be distinct and not sources.
+ * No reference counterpart: the reference never writes into a shared page
+ * (prefix entries cover whole 64-token units, sched.rs:322, 1044-1067); this
+ * is the device half of pkv_kv_prepare_append's copy-on-write. */
+int pkv_page_copy(void* kcache, void* vcache, const int32_t* src, const int32_t* dst, int n, int64_t page_bytes,
+                  int64_t num_blocks, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Device: paged decode attention (bf16, head_dim 256, block_size 16, G = 4)
+ * ------------------------------------------------------------------------- */
+
+/* Workspace bytes pkv_attn_decode needs for T tokens and Hq query heads on
+ * the current device. */
+int pkv_attn_decode_workspace(int T, int Hq, size_t* bytes);
+
+/* Paged decode attention with the reference's semantics and arguments
+ * (attn_paged_g<G> + attn_merge, src/kernels/qwen35.cu:1313-1334 and
+ * 2245-2279, launched at src/model.rs:2366-2437; AMD body
+ * src/kernels/amd/attn_decode.cuh:12-183): for each token t < T that is a
+ * decode token (prompt rows are skipped when skip_prompts, as the reference
+ * leaves them to flash attention), each query head h, attention of
+ * q[t][h] * scale over keys 0..pos[t] of sequence tok_seq[t] through
+ * block_table[tok_seq[t] * max_blocks ..], then
+ * out[t][h] = bf16(bf16(A / S) * sigmoid(gate)), gate = qkv[t * qstride +
+ * h * 512 + 256 ..]. Same pointer meanings as the reference; kscale/vscale/
+ * fq/fs/fmode/frows (E4M3 cache, FP8 outputs) are not part of this path.
+ * The key-range split is the library's own (the reference's part/min_chunk
+ * pair is replaced by `workspace`, of pkv_attn_decode_workspace bytes).
+ * num_blocks bounds page ids (ids outside the pool are clamped, never read
+ * out of bounds). Returns PKV_ERR_UNSUPPORTED unless Hq = 4 Hkv and
+ * block_size = 16. */
+int pkv_attn_decode(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
+                    int Hkv, const int32_t* pos, const int32_t* tok_seq, const int32_t* block_table, int max_blocks,
+                    int block_size, void* out, float scale, const int32_t* cu, int skip_prompts,
+                    const int32_t* outs, int spec, int T, int64_t num_blocks, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* The two launches of pkv_attn_decode, for callers that time or schedule
+ * them apart (the reference likewise launches attn_paged_g<G> and then
+ * attn_merge, src/model.rs:2371-2437): _split runs the key-range kernel,
+ * _merge combines its partials and gates. Same arguments; _merge must follow
+ * _split on the same stream with the same workspace and metadata. */
+int pkv_attn_decode_split(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
+                          int Hkv, const int32_t* pos, const int32_t* tok_seq, const int32_t* block_table,
+                          int max_blocks, int block_size, void* out, float scale, const int32_t* cu,
+                          int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
+                          void* workspace, size_t workspace_bytes, void* stream);
+int pkv_attn_decode_merge(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
+                          int Hkv, const int32_t* pos, const int32_t* tok_seq, const int32_t* block_table,
+                          int max_blocks, int block_size, void* out, float scale, const int32_t* cu,
+                          int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Tuning: key-range workgroups per CU (default 2) and fewest keys per range
+ * (default 32). Process-wide; takes effect for later calls (workspace sizes
+ * follow). */
+int pkv_attn_decode_config(int wg_per_cu, int min_range);
+
+/* ---------------------------------------------------------------------------
+ * Host: block allocator (reference Scheduler.free_blocks / block_refs,
+ * src/sched.rs:461-465, 515, 801-817)
+ * ------------------------------------------------------------------------- */
+
+typedef struct pkv_pool pkv_pool;
+
+/* A pool of n_blocks pages, free list [n-1, ..., 1, 0] like sched.rs:515. */
+pkv_pool* pkv_pool_create(int64_t n_blocks);
+void pkv_pool_destroy(pkv_pool* pool);
+/* take_blocks (sched.rs:801-807): the last n free ids in free-list order,
+ * each with one reference. PKV_ERR_NO_BLOCKS if fewer are free. */
+int pkv_pool_take(pkv_pool* pool, int n, uint32_t* ids);
+/* unref_blocks (sched.rs:809-817): one reference less each; a page reaching
+ * zero returns to the end of the free list. Underflow is PKV_ERR_INVALID. */
+int pkv_pool_unref(pkv_pool* pool, const uint32_t* ids, int n);
+/* One reference more each (prefix sharing, sched.rs:758-760, 1054-1056).
+ * Refcounts are u16 like the reference's. */
+int pkv_pool_ref(pkv_pool* pool, const uint32_t* ids, int n);
+int64_t pkv_pool_free_count(const pkv_pool* pool);
+int64_t pkv_pool_total(const pkv_pool* pool);
+int pkv_pool_refs(const pkv_pool* pool, uint32_t id);
+/* Copies the free list (bottom to top) into out (capacity cap); returns its
+ * length or a negative status. */
+int64_t pkv_pool_free_list(const pkv_pool* pool, uint32_t* out, int64_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PKV_H */

@@ -1,0 +1,168 @@
+"""CPU oracle for the paged KV cache hot path — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this package, as the checker (or the timed CPU baseline). The product
+(libpkv.so, pocket-engine_amd/pkv) never imports it.
+
+numpy wrappers over liboracle.so (pkv_oracle.c, a scalar C restatement of
+the reference's semantics; see the header of that file for the reference
+lines each function follows and how each is pinned) plus the allocator
+restatement in alloc.py.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+
+def build():
+    r = subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("oracle build failed:\n" + r.stdout + r.stderr)
+    return LIB_PATH
+
+
+if not os.path.exists(LIB_PATH):
+    build()
+_lib = ctypes.CDLL(LIB_PATH)
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_long
+_F = ctypes.c_float
+_lib.orc_f2b.restype = ctypes.c_uint16
+_lib.orc_f2b.argtypes = [_F]
+_lib.orc_b2f.restype = _F
+_lib.orc_b2f.argtypes = [ctypes.c_uint16]
+_lib.orc_append.argtypes = [_P, _P, _L, _P, _I, _I, _I, _P, _P]
+_lib.orc_gather.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P, _P]
+_lib.orc_page_copy.argtypes = [_P, _P, _P, _P, _I, _L]
+_lib.orc_attn_decode.restype = _I
+_lib.orc_attn_decode.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _F, _P, _I, _P, _I, _I, _P]
+_lib.orc_attn_single.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P, _I, _I, _F, _P]
+_lib.orc_split_parts.restype = _I
+_lib.orc_split_parts.argtypes = [_I, _I, _I]
+_lib.orc_attn_partial.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P, _I, _I, _I, _F, _P, _P, _P]
+_lib.orc_merge.argtypes = [_P, _P, _P, _I, _P]
+_lib.orc_attn_prefill.restype = _I
+_lib.orc_attn_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I]
+_lib.orc_mtp_slots.argtypes = [_P, _P, _P, _I, _I, _P, _I, _P, _P, _I]
+
+
+def _p(a):
+    """Pointer to a C-contiguous numpy array. The caller keeps the array
+    referenced until the C call returns (never pass a temporary)."""
+    if a is None:
+        return None
+    assert isinstance(a, np.ndarray) and a.flags.c_contiguous, "oracle takes C-contiguous numpy arrays"
+    return a.ctypes.data
+
+
+def _i32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.int32)
+
+
+def f2b(x):
+    """f32 -> bf16 bits, round to nearest even (numpy, vectorised)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x007FFFFF) != 0)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def b2f(b):
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def append(k_src, v_src, slot_map, kcache, vcache):
+    """k_src/v_src: [T][row] arrays (any dtype); kcache/vcache: [slots][row]; in place."""
+    T = k_src.shape[0]
+    row_bytes = k_src[0].nbytes
+    slot_map = _i32(slot_map)
+    _lib.orc_append(_p(k_src), _p(v_src), row_bytes, _p(slot_map), T, 1, row_bytes, _p(kcache), _p(vcache))
+
+
+def gather(kcache, vcache, bt_row, L, block_size):
+    """Returns dense (k, v) of shape [L] + kcache.shape[1:]."""
+    ko = np.empty((L,) + kcache.shape[1:], kcache.dtype)
+    vo = np.empty((L,) + vcache.shape[1:], vcache.dtype)
+    row_bytes = kcache[0].nbytes
+    bt_row = _i32(bt_row)
+    _lib.orc_gather(_p(kcache), _p(vcache), _p(bt_row), L, block_size, 1, row_bytes, _p(ko), _p(vo))
+    return ko, vo
+
+
+def page_copy(kcache, vcache, src, dst, page_bytes):
+    src, dst = _i32(src), _i32(dst)
+    _lib.orc_page_copy(_p(kcache), _p(vcache), _p(src), _p(dst), len(src), page_bytes)
+
+
+def attn_decode(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, scale,
+                cu=None, skip_prompts=0, outs=None, spec=1, out=None):
+    """bf16 (uint16) arrays in; returns (out uint16 [T][Hq][256], o_raw f32)."""
+    T = len(pos)
+    if out is None:
+        out = np.zeros((T, Hq, 256), np.uint16)
+    raw = np.zeros((T, Hq, 256), np.float32)
+    cu, outs, pos, tok_seq, block_table = _i32(cu), _i32(outs), _i32(pos), _i32(tok_seq), _i32(block_table)
+    _lib.orc_attn_decode(_p(q), _p(kcache), _p(vcache), _p(qkv), qstride, Hq, Hkv, _p(pos),
+                         _p(tok_seq), _p(block_table), max_blocks, block_size, _p(out), scale,
+                         _p(cu), skip_prompts, _p(outs), spec, T, _p(raw))
+    return out, raw
+
+
+def attn_single(q, kcache, vcache, D, Hq, Hkv, bt_row, L, block_size, scale):
+    """One query (q: [Hq][D], f32 or bf16-as-uint16) -> f32 [Hq][D], ungated."""
+    dtype = 1 if q.dtype == np.float32 else 0
+    o = np.zeros((Hq, D), np.float32)
+    bt_row = _i32(bt_row)
+    _lib.orc_attn_single(_p(q), _p(kcache), _p(vcache), dtype, D, Hq, Hkv, _p(bt_row), L, block_size, scale, _p(o))
+    return o
+
+
+def split_parts(L, Z, min_chunk):
+    return _lib.orc_split_parts(L, Z, min_chunk)
+
+
+def attn_partial(q, kcache, vcache, Hq, Hkv, t, h, bt_row, block_size, j0, j1, scale):
+    M = np.zeros(1, np.float64)
+    S = np.zeros(1, np.float64)
+    A = np.zeros(256, np.float64)
+    bt_row = _i32(bt_row)
+    _lib.orc_attn_partial(_p(q), _p(kcache), _p(vcache), Hq, Hkv, t, h, _p(bt_row), block_size, j0, j1, scale,
+                          _p(M), _p(S), _p(A))
+    return M[0], S[0], A
+
+
+def merge(Ms, Ss, As):
+    Ms = np.ascontiguousarray(Ms, np.float64)
+    Ss = np.ascontiguousarray(Ss, np.float64)
+    As = np.ascontiguousarray(As, np.float64)
+    o = np.zeros(256, np.float64)
+    _lib.orc_merge(_p(Ms), _p(Ss), _p(As), len(Ms), _p(o))
+    return o
+
+
+def attn_prefill(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks, block_size, scale,
+                 outs=None, spec=1, out=None):
+    T = len(pos)
+    if out is None:
+        out = np.zeros((T, Hq, 256), np.uint16)
+    pos, cu, block_table, outs = _i32(pos), _i32(cu), _i32(block_table), _i32(outs)
+    _lib.orc_attn_prefill(_p(q), _p(kcache), _p(vcache), _p(qkv), qstride, Hq, Hkv, _p(pos), _p(cu), seqs,
+                          _p(block_table), max_blocks, block_size, _p(out), scale, _p(outs), spec)
+    return out
+
+
+def mtp_slots(rows, pos, block_table, max_blocks, block_size, limits, k):
+    S = len(rows)
+    dpos = np.zeros(S, np.int32)
+    dslot = np.zeros(S, np.int32)
+    rows, pos, block_table, limits = _i32(rows), _i32(pos), _i32(block_table), _i32(limits)
+    _lib.orc_mtp_slots(_p(rows), _p(pos), _p(block_table), max_blocks, block_size, _p(limits), k, _p(dpos),
+                       _p(dslot), S)
+    return dpos, dslot

@@ -1,0 +1,291 @@
+/*
+ * CPU oracle for the paged KV cache hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg may load this library, and only as the checker
+ * or the timed CPU baseline. The product path (libpkv.so) never calls it.
+ *
+ * A scalar restatement, written from the reference's semantics, of:
+ *   - the KV append scatter        (reference src/kernels/qwen35.cu:1086-1100, 1120-1127)
+ *   - the gather through the block table (qwen35.cu:1204, amd/attn_decode.cuh:56-74)
+ *   - paged decode attention + gate (qwen35.cu:1146-1309, amd/attn_decode.cuh:12-183)
+ *   - split-K partials and merge    (qwen35.cu:1137-1141, 1264-1288, 2242-2279)
+ *   - chunked-prefill causal attention (qwen35.cu:1364-1585, amd/attention.cuh:12-136)
+ *   - page copy (copy-on-write; build-defined: the reference has no CoW)
+ *
+ * Pinning (what each function is checked against, in tests/test_oracle.py):
+ *   append/gather/page_copy: closed forms, gather(append(x)) == x under
+ *       random permutation block tables, brute-force on tiny pools.
+ *   attention: torch fp64 scaled_dot_product_attention golden fixtures
+ *       (tests/golden/), closed forms (one key -> v; equal keys -> mean of v;
+ *       a dominant key -> its v), split+merge == unsplit.
+ *   Parity unpinned beyond the stated tolerance: the reference GPU kernels'
+ *   exact bf16 rounding of P inside the prefill tiles (amd/attention.cuh:115)
+ *   and expf vs exp2f last bits.
+ *
+ * Arithmetic: softmax and weighted sums in double; the epilogue follows the
+ * reference exactly in f32: o = bf16_round(A / S); y = o / (1 + expf(-gate));
+ * out = bf16_rne(y)  (qwen35.cu:1290-1293, 2270-2273).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+#include <stdlib.h>
+
+#define HEAD_DIM 256
+
+/* ---- bf16 helpers (reference b2f/f2b/rbf, qwen35.cu:26-28; RNE like
+ * __float2bfloat16_rn) ---- */
+float orc_b2f(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+uint16_t orc_f2b(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) /* NaN: keep sign, quiet */
+        return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+static float rbf(float x) { return orc_b2f(orc_f2b(x)); }
+
+/* Speculative rows: outs[s * spec] >= 0 (qwen35.cu:94-100). */
+static int is_spec(const int* outs, int spec, int s) { return outs && outs[(size_t)s * spec] >= 0; }
+
+/* ---- slot of key position p through a block-table row (sched.rs:1113-1114,
+ * qwen35.cu:1204) ---- */
+long orc_slot(const int* bt_row, int p, int block_size) {
+    return (long)bt_row[p / block_size] * block_size + p % block_size;
+}
+
+/* ---- KV append: cache[(slot * Hkv + h) * row] = src[t][h]; slot < 0 skips
+ * (qwen35.cu:1090-1100 for V, 1120-1127 for K after norm/rope, which callers
+ * of this path have already applied). Byte-exact copy. `row_stride` is in
+ * bytes between consecutive tokens' rows; head rows are contiguous. ---- */
+void orc_append(const uint8_t* k_src, const uint8_t* v_src, long row_stride, const int* slot_map, int T,
+                int Hkv, int head_bytes, uint8_t* kcache, uint8_t* vcache) {
+    for (int t = 0; t < T; t++) {
+        const int slot = slot_map[t];
+        if (slot < 0) continue;
+        for (int h = 0; h < Hkv; h++) {
+            const size_t at = ((size_t)slot * Hkv + h) * head_bytes;
+            memcpy(kcache + at, k_src + (size_t)t * row_stride + (size_t)h * head_bytes, head_bytes);
+            memcpy(vcache + at, v_src + (size_t)t * row_stride + (size_t)h * head_bytes, head_bytes);
+        }
+    }
+}
+
+/* ---- gather: dense[j][h] = cache[slot(j)][h] for j < L (implicit in every
+ * reference attention read: qwen35.cu:1203-1205). ---- */
+void orc_gather(const uint8_t* kcache, const uint8_t* vcache, const int* bt_row, int L, int block_size, int Hkv,
+                int head_bytes, uint8_t* k_out, uint8_t* v_out) {
+    const size_t rb = (size_t)Hkv * head_bytes;
+    for (int j = 0; j < L; j++) {
+        const size_t slot = (size_t)orc_slot(bt_row, j, block_size);
+        memcpy(k_out + j * rb, kcache + slot * rb, rb);
+        memcpy(v_out + j * rb, vcache + slot * rb, rb);
+    }
+}
+
+/* ---- page copy (copy-on-write): page dst := page src for K and V, all
+ * block_size slots and all kv heads, byte-exact. ---- */
+void orc_page_copy(uint8_t* kcache, uint8_t* vcache, const int* src, const int* dst, int n, long page_bytes) {
+    for (int i = 0; i < n; i++) {
+        memmove(kcache + (size_t)dst[i] * page_bytes, kcache + (size_t)src[i] * page_bytes, page_bytes);
+        memmove(vcache + (size_t)dst[i] * page_bytes, vcache + (size_t)src[i] * page_bytes, page_bytes);
+    }
+}
+
+/* One (token, q head) over keys [j0, j1): natural-log softmax partial
+ * (M = max score, S = sum e^(s-M), A[d] = sum e^(s-M) v[d]) in double.
+ * Scores are (q . k) * scale (qwen35.cu:1188-1190 scales q by `scale`).
+ * dtype 0: bf16 cache and q; 1: f32. */
+static void partial(const void* q, const void* kc, const void* vc, int dtype, int D, int Hq, int Hkv, int t, int h,
+                    const int* bt, int block_size, int j0, int j1, float scale, double* M, double* S, double* A) {
+    const int G = Hq / Hkv, kvh = h / G;
+    double qd[HEAD_DIM];
+    for (int d = 0; d < D; d++)
+        qd[d] = dtype ? ((const float*)q)[((size_t)t * Hq + h) * D + d]
+                      : orc_b2f(((const uint16_t*)q)[((size_t)t * Hq + h) * D + d]);
+    double m = -INFINITY;
+    double* s = (double*)malloc(sizeof(double) * (size_t)(j1 > j0 ? j1 - j0 : 1));
+    for (int j = j0; j < j1; j++) {
+        const size_t at = ((size_t)orc_slot(bt, j, block_size) * Hkv + kvh) * D;
+        double dot = 0.0;
+        for (int d = 0; d < D; d++)
+            dot += qd[d] * (dtype ? ((const float*)kc)[at + d] : orc_b2f(((const uint16_t*)kc)[at + d]));
+        s[j - j0] = dot * (double)scale;
+        if (s[j - j0] > m) m = s[j - j0];
+    }
+    double sum = 0.0;
+    for (int d = 0; d < D; d++) A[d] = 0.0;
+    for (int j = j0; j < j1; j++) {
+        const double p = exp(s[j - j0] - m);
+        sum += p;
+        const size_t at = ((size_t)orc_slot(bt, j, block_size) * Hkv + kvh) * D;
+        for (int d = 0; d < D; d++)
+            A[d] += p * (dtype ? ((const float*)vc)[at + d] : orc_b2f(((const uint16_t*)vc)[at + d]));
+    }
+    free(s);
+    *M = m;
+    *S = sum;
+}
+
+/* Gated epilogue (qwen35.cu:1290-1293): y = rbf(o) * sigmoid(gate), in f32. */
+static uint16_t gated(double o, float gate) {
+    const float ov = rbf((float)o);
+    const float y = ov / (1.f + expf(-gate));
+    return orc_f2b(y);
+}
+
+/* ---- paged decode attention, bf16 cache (attn_paged_g<G> semantics,
+ * qwen35.cu:1146-1309): for every decode token t (prompt rows skipped when
+ * skip_prompts, qwen35.cu:1171-1172), every q head h: attention over keys
+ * 0 .. pos[t] of its sequence's pages, gated output bf16 into out[t][h][256].
+ * Rows that are skipped are left untouched. Returns the number of rows
+ * written. Optional o_raw (may be NULL) receives the ungated f32 A/S. ---- */
+int orc_attn_decode(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, const uint16_t* qkv,
+                    int qstride, int Hq, int Hkv, const int* pos, const int* tok_seq, const int* block_table,
+                    int max_blocks, int block_size, uint16_t* out, float scale, const int* cu, int skip_prompts,
+                    const int* outs, int spec, int T, float* o_raw) {
+    int rows = 0;
+    double A[HEAD_DIM];
+    for (int t = 0; t < T; t++) {
+        const int sq = tok_seq[t];
+        if (skip_prompts && cu[sq + 1] - cu[sq] > 1 && !is_spec(outs, spec, sq)) continue;
+        const int L = pos[t] + 1;
+        const int* bt = block_table + (size_t)sq * max_blocks;
+        for (int h = 0; h < Hq; h++) {
+            double M, S;
+            partial(q, kcache, vcache, 0, HEAD_DIM, Hq, Hkv, t, h, bt, block_size, 0, L, scale, &M, &S, A);
+            for (int d = 0; d < HEAD_DIM; d++) {
+                const double o = A[d] / S;
+                const float gate = orc_b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d]);
+                out[((size_t)t * Hq + h) * HEAD_DIM + d] = gated(o, gate);
+                if (o_raw) o_raw[((size_t)t * Hq + h) * HEAD_DIM + d] = (float)o;
+            }
+        }
+        rows++;
+    }
+    return rows;
+}
+
+/* ---- generic single-query attention (f32 or bf16 cache, any head dim) for
+ * the CPU plumbing config: o[h][d] = softmax(q . k * scale) v over keys
+ * 0..L-1 of one sequence, ungated, f32 output. ---- */
+void orc_attn_single(const void* q, const void* kcache, const void* vcache, int dtype, int D, int Hq, int Hkv,
+                     const int* bt_row, int L, int block_size, float scale, float* o) {
+    double A[1024];
+    for (int h = 0; h < Hq; h++) {
+        double M, S;
+        partial(q, kcache, vcache, dtype, D, Hq, Hkv, 0, h, bt_row, block_size, 0, L, scale, &M, &S, A);
+        for (int d = 0; d < D; d++) o[(size_t)h * D + d] = (float)(A[d] / S);
+    }
+}
+
+/* ---- split-K semantics (flash decoding): the reference splits a token's L
+ * keys into parts = max(1, min(Z, ceil(L / min_chunk))) ranges of
+ * chunk = ceil(L / parts) keys (qwen35.cu:1137-1141, 1176-1181); each range
+ * yields (M, S, A[256]) and attn_merge combines them in range order
+ * (qwen35.cu:2255-2273). Partials here are natural-log domain doubles. ---- */
+int orc_split_parts(int L, int Z, int min_chunk) {
+    int p = (L + min_chunk - 1) / min_chunk;
+    if (p > Z) p = Z;
+    return p < 1 ? 1 : p;
+}
+
+void orc_attn_partial(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, int Hq, int Hkv, int t,
+                      int h, const int* bt_row, int block_size, int j0, int j1, float scale, double* M, double* S,
+                      double* A) {
+    partial(q, kcache, vcache, 0, HEAD_DIM, Hq, Hkv, t, h, bt_row, block_size, j0, j1, scale, M, S, A);
+}
+
+/* Merge n partials: M* = max M, S* = sum S e^(M-M*), A* likewise; ranges
+ * with M = -inf contribute 0 (qwen35.cu:2258-2266). Writes A* / S* to o. */
+void orc_merge(const double* M, const double* S, const double* A, int n, double* o) {
+    double Mx = -INFINITY;
+    for (int z = 0; z < n; z++)
+        if (M[z] > Mx) Mx = M[z];
+    double St = 0.0;
+    for (int d = 0; d < HEAD_DIM; d++) o[d] = 0.0;
+    for (int z = 0; z < n; z++) {
+        const double f = M[z] == -INFINITY ? 0.0 : exp(M[z] - Mx);
+        St += S[z] * f;
+        for (int d = 0; d < HEAD_DIM; d++) o[d] += A[(size_t)z * HEAD_DIM + d] * f;
+    }
+    for (int d = 0; d < HEAD_DIM; d++) o[d] /= St;
+}
+
+/* ---- chunked-prefill attention over paged context (attn_mfma_g<G>_t<NT> /
+ * attn_flash_group semantics, amd/attention.cuh:12-136, qwen35.cu:1364-1585):
+ * for every prompt sequence s (more than one token and not verifying drafts,
+ * amd/attention.cuh:22-24), every token t of it at position pos[t], every q
+ * head: causal attention over keys 0..pos[t] (a key kp is visible iff
+ * kp <= qp and kp < L, attention.cuh:81-89; with positions contiguous within
+ * the chunk that is kp <= pos[t]). The query is rounded to bf16 after scaling
+ * by scale * log2(e) as the reference does (amd/attention.cuh:37-44); scores
+ * are exp2-domain. The bf16 rounding of P before P.V (attention.cuh:115) is
+ * NOT restated: P is kept in double. Gated epilogue as decode. Returns the
+ * number of token rows written. ---- */
+int orc_attn_prefill(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, const uint16_t* qkv,
+                     int qstride, int Hq, int Hkv, const int* pos, const int* cu, int seqs, const int* block_table,
+                     int max_blocks, int block_size, uint16_t* out, float scale, const int* outs, int spec) {
+    const double LOG2E = 1.4426950408889634;
+    const int G = Hq / Hkv;
+    int rows = 0;
+    double A[HEAD_DIM], qd[HEAD_DIM];
+    for (int s = 0; s < seqs; s++) {
+        const int n = cu[s + 1] - cu[s];
+        if (n <= 1 || is_spec(outs, spec, s)) continue;
+        const int* bt = block_table + (size_t)s * max_blocks;
+        for (int t = cu[s]; t < cu[s + 1]; t++) {
+            const int L = pos[t] + 1;
+            double* sc = (double*)malloc(sizeof(double) * (size_t)L);
+            for (int h = 0; h < Hq; h++) {
+                const int kvh = h / G;
+                for (int d = 0; d < HEAD_DIM; d++)
+                    qd[d] = rbf(orc_b2f(q[((size_t)t * Hq + h) * HEAD_DIM + d]) * (scale * (float)LOG2E));
+                double m = -INFINITY;
+                for (int j = 0; j < L; j++) {
+                    const size_t at = ((size_t)orc_slot(bt, j, block_size) * Hkv + kvh) * HEAD_DIM;
+                    double dot = 0.0;
+                    for (int d = 0; d < HEAD_DIM; d++) dot += qd[d] * orc_b2f(kcache[at + d]);
+                    sc[j] = dot;
+                    if (dot > m) m = dot;
+                }
+                double S = 0.0;
+                for (int d = 0; d < HEAD_DIM; d++) A[d] = 0.0;
+                for (int j = 0; j < L; j++) {
+                    const double p = exp2(sc[j] - m);
+                    S += p;
+                    const size_t at = ((size_t)orc_slot(bt, j, block_size) * Hkv + kvh) * HEAD_DIM;
+                    for (int d = 0; d < HEAD_DIM; d++) A[d] += p * orc_b2f(vcache[at + d]);
+                }
+                for (int d = 0; d < HEAD_DIM; d++) {
+                    const float gate = orc_b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d]);
+                    out[((size_t)t * Hq + h) * HEAD_DIM + d] = gated(A[d] / S, gate);
+                }
+            }
+            free(sc);
+            rows++;
+        }
+    }
+    return rows;
+}
+
+/* ---- draft-token (speculative verify) metadata (mtp_next, qwen35.cu:2633-2650):
+ * dslot = p <= limits[s] ? bt[p / bs] * bs + p % bs : -1. ---- */
+void orc_mtp_slots(const int* rows, const int* pos, const int* block_table, int max_blocks, int block_size,
+                   const int* limits, int k, int* dpos, int* dslot, int S) {
+    for (int s = 0; s < S; s++) {
+        const int p = pos[rows[s]] + k;
+        dpos[s] = p;
+        dslot[s] = p <= limits[s] ? block_table[(size_t)s * max_blocks + p / block_size] * block_size + p % block_size
+                                  : -1;
+    }
+}

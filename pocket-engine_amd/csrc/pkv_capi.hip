@@ -1,0 +1,210 @@
+// C-ABI entry points of libpkv.so (declared in include/pkv.h). Every entry
+// point validates its shapes on the host before launching: a kernel only
+// ever sees arguments its indexing was written for.
+#include "pkv_copy.hip"
+#include "pkv_decode.hip"
+#include "../../include/pkv.h"
+
+#include <mutex>
+
+namespace {
+
+int status_of(hipError_t e) { return e == hipSuccess ? PKV_OK : (int)e; }
+
+int launch_status() { return status_of(hipGetLastError()); }
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int vec_mode(const void* a, const void* b, const void* c, const void* d, int64_t stride, int row_bytes) {
+    if (row_bytes % 16 == 0 && stride % 16 == 0 && aligned(a, 16) && aligned(b, 16) && aligned(c, 16) &&
+        aligned(d, 16))
+        return 2;
+    if (row_bytes % 4 == 0 && stride % 4 == 0 && aligned(a, 4) && aligned(b, 4) && aligned(c, 4) && aligned(d, 4))
+        return 1;
+    return 0;
+}
+
+// Compute units of the current device, cached per device.
+int device_cus() {
+    static std::mutex mu;
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::lock_guard<std::mutex> g(mu);
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+int g_wg_per_cu = 2;
+int g_min_range = 32;
+
+int decode_n_wg() { return device_cus() * g_wg_per_cu; }
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+struct DecodeLayout {
+    size_t offs, ms, acc, total;
+};
+
+DecodeLayout decode_layout(int T, int Hq, int n_wg) {
+    DecodeLayout d;
+    const size_t rows = (size_t)(T + n_wg) * Hq;
+    d.offs = 0;
+    d.ms = round_up((size_t)(T + 2) * 4, 256);
+    d.acc = d.ms + round_up(rows * 2 * 4, 256);
+    d.total = d.acc + rows * pkv::HEAD_DIM * 4;
+    return d;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pkv_strerror(int status) {
+    switch (status) {
+        case PKV_OK: return "ok";
+        case PKV_ERR_INVALID: return "invalid argument";
+        case PKV_ERR_UNSUPPORTED: return "unsupported shape";
+        case PKV_ERR_NO_BLOCKS: return "not enough free KV blocks";
+        default: return hipGetErrorString((hipError_t)status);
+    }
+}
+
+int pkv_version(void) { return 1; }
+
+int pkv_append(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map, int T, int Hkv,
+               int head_bytes, void* kcache, void* vcache, int64_t num_slots, void* stream) {
+    if (T < 0 || Hkv <= 0 || head_bytes <= 0 || num_slots <= 0) return PKV_ERR_INVALID;
+    if (T == 0) return PKV_OK;
+    if (!k_rows || !v_rows || !slot_map || !kcache || !vcache) return PKV_ERR_INVALID;
+    const int64_t row_bytes = (int64_t)Hkv * head_bytes;
+    if (row_bytes > (1 << 24) || row_stride < row_bytes || T > (1 << 30)) return PKV_ERR_INVALID;
+    const int vec = vec_mode(k_rows, v_rows, kcache, vcache, row_stride, (int)row_bytes);
+    hipLaunchKernelGGL(pkv::append_kernel, dim3(T, 2), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)k_rows,
+                       (const uint8_t*)v_rows, (long)row_stride, slot_map, (int)row_bytes, (uint8_t*)kcache,
+                       (uint8_t*)vcache, (long)num_slots, vec);
+    return launch_status();
+}
+
+int pkv_gather(const void* kcache, const void* vcache, const int32_t* bt_row, int L, int block_size, int Hkv,
+               int head_bytes, int64_t num_blocks, void* k_out, void* v_out, void* stream) {
+    if (L < 0 || block_size <= 0 || Hkv <= 0 || head_bytes <= 0 || num_blocks <= 0) return PKV_ERR_INVALID;
+    if (L == 0) return PKV_OK;
+    if (!kcache || !vcache || !bt_row || !k_out || !v_out) return PKV_ERR_INVALID;
+    const int64_t row_bytes = (int64_t)Hkv * head_bytes;
+    if (row_bytes > (1 << 24)) return PKV_ERR_INVALID;
+    const int vec = vec_mode(kcache, vcache, k_out, v_out, row_bytes, (int)row_bytes);
+    hipLaunchKernelGGL(pkv::gather_kernel, dim3((L + 3) / 4, 2), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)kcache, (const uint8_t*)vcache, bt_row, L, block_size, (int)row_bytes,
+                       (long)num_blocks, (uint8_t*)k_out, (uint8_t*)v_out, vec);
+    return launch_status();
+}
+
+int pkv_page_copy(void* kcache, void* vcache, const int32_t* src, const int32_t* dst, int n, int64_t page_bytes,
+                  int64_t num_blocks, void* stream) {
+    if (n < 0 || page_bytes <= 0 || page_bytes % 16 != 0 || num_blocks <= 0) return PKV_ERR_INVALID;
+    if (n == 0) return PKV_OK;
+    if (!kcache || !vcache || !src || !dst || !aligned(kcache, 16) || !aligned(vcache, 16)) return PKV_ERR_INVALID;
+    const int slices = (int)std::min<int64_t>(16, std::max<int64_t>(1, page_bytes / 4096));
+    hipLaunchKernelGGL(pkv::page_copy_kernel, dim3(n, 2, slices), dim3(256), 0, (hipStream_t)stream,
+                       (uint8_t*)kcache, (uint8_t*)vcache, src, dst, (long)page_bytes, (long)num_blocks, slices);
+    return launch_status();
+}
+
+int pkv_attn_decode_config(int wg_per_cu, int min_range) {
+    if (wg_per_cu < 1 || wg_per_cu > 64 || min_range < 1 || min_range > (1 << 20)) return PKV_ERR_INVALID;
+    g_wg_per_cu = wg_per_cu;
+    g_min_range = min_range;
+    return PKV_OK;
+}
+
+int pkv_attn_decode_workspace(int T, int Hq, size_t* bytes) {
+    if (T < 0 || Hq <= 0 || !bytes) return PKV_ERR_INVALID;
+    *bytes = decode_layout(T, Hq, decode_n_wg()).total;
+    return PKV_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// phase bit 1: key-range kernel; bit 2: merge kernel.
+int attn_decode_phases(int phases, const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride,
+                       int Hq, int Hkv, const int32_t* pos, const int32_t* tok_seq, const int32_t* block_table,
+                       int max_blocks, int block_size, void* out, float scale, const int32_t* cu, int skip_prompts,
+                       const int32_t* outs, int spec, int T, int64_t num_blocks, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+    if (T < 0 || Hq <= 0 || Hkv <= 0 || max_blocks <= 0 || num_blocks <= 0 || spec < 1) return PKV_ERR_INVALID;
+    if (Hq != 4 * Hkv || block_size != 16) return PKV_ERR_UNSUPPORTED;
+    if (T == 0) return PKV_OK;
+    if (!q || !kcache || !vcache || !qkv || !pos || !tok_seq || !block_table || !out || !workspace)
+        return PKV_ERR_INVALID;
+    if (skip_prompts && !cu) return PKV_ERR_INVALID;
+    if (qstride < 2 * Hq * pkv::HEAD_DIM || qstride % 8 != 0) return PKV_ERR_INVALID;
+    if (!aligned(q, 16) || !aligned(kcache, 16) || !aligned(vcache, 16) || !aligned(qkv, 16) || !aligned(out, 16) ||
+        !aligned(workspace, 256))
+        return PKV_ERR_INVALID;
+    const int n_wg = decode_n_wg();
+    const DecodeLayout lay = decode_layout(T, Hq, n_wg);
+    if (workspace_bytes < lay.total) return PKV_ERR_INVALID;
+    pkv::DecodeParams p;
+    p.q = (const uint16_t*)q;
+    p.kc = (const uint16_t*)kcache;
+    p.vc = (const uint16_t*)vcache;
+    p.qkv = (const uint16_t*)qkv;
+    p.qstride = qstride;
+    p.Hq = Hq;
+    p.Hkv = Hkv;
+    p.pos = pos;
+    p.tok_seq = tok_seq;
+    p.block_table = block_table;
+    p.max_blocks = max_blocks;
+    p.out = (uint16_t*)out;
+    p.scale = scale;
+    p.cu = cu;
+    p.skip_prompts = skip_prompts;
+    p.outs = outs;
+    p.spec = spec;
+    p.T = T;
+    p.num_blocks = (long)num_blocks;
+    char* ws = (char*)workspace;
+    p.offs = (int*)(ws + lay.offs);
+    p.part_ms = (float*)(ws + lay.ms);
+    p.part_acc = (float*)(ws + lay.acc);
+    p.n_wg = n_wg;
+    p.min_range = g_min_range;
+    const int groups = (Hkv + 3) / 4, threads = 64 * std::min(Hkv, 4);
+    if (phases & 1) {
+        hipLaunchKernelGGL(pkv::decode_split_kernel<4>, dim3(n_wg, groups), dim3(threads), 0, (hipStream_t)stream, p);
+        const int st = launch_status();
+        if (st != PKV_OK) return st;
+    }
+    if (phases & 2) {
+        hipLaunchKernelGGL(pkv::decode_merge_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, p);
+        return launch_status();
+    }
+    return PKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+#define PKV_DECODE_ARGS                                                                                            \
+    const void *q, const void *kcache, const void *vcache, const void *qkv, int qstride, int Hq, int Hkv,          \
+        const int32_t *pos, const int32_t *tok_seq, const int32_t *block_table, int max_blocks, int block_size,    \
+        void *out, float scale, const int32_t *cu, int skip_prompts, const int32_t *outs, int spec, int T,         \
+        int64_t num_blocks, void *workspace, size_t workspace_bytes, void *stream
+#define PKV_DECODE_PASS                                                                                           \
+    q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, out, scale, cu,  \
+        skip_prompts, outs, spec, T, num_blocks, workspace, workspace_bytes, stream
+
+int pkv_attn_decode(PKV_DECODE_ARGS) { return attn_decode_phases(3, PKV_DECODE_PASS); }
+int pkv_attn_decode_split(PKV_DECODE_ARGS) { return attn_decode_phases(1, PKV_DECODE_PASS); }
+int pkv_attn_decode_merge(PKV_DECODE_ARGS) { return attn_decode_phases(2, PKV_DECODE_PASS); }
+
+}  // extern "C"

@@ -1,0 +1,79 @@
+// Shared device helpers for the paged KV cache kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pkv {
+
+constexpr int HEAD_DIM = 256;  // attention head width (reference model.rs:14)
+constexpr float LOG2E = 1.4426950408889634f;
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+__device__ __forceinline__ float b2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// f32 -> bf16, round to nearest even; NaN stays NaN (quiet, sign kept).
+__device__ __forceinline__ uint32_t f2b_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+__device__ __forceinline__ float rbf(float x) { return __uint_as_float(f2b_bits(x) << 16); }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return f2b_bits(lo) | (f2b_bits(hi) << 16); }
+
+// Two bf16 products summed into c in f32 (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+__device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float c) {
+    c = dot2(a.x, b.x, c);
+    c = dot2(a.y, b.y, c);
+    c = dot2(a.z, b.z, c);
+    return dot2(a.w, b.w, c);
+}
+
+// DPP lane moves inside 16-lane rows.
+enum : int {
+    DPP_ROW_MIRROR = 0x140,       // lane i <- lane 15 - i
+    DPP_ROW_HALF_MIRROR = 0x141,  // lane i <- lane i ^ 7 (within 8)
+    DPP_ROW_ROR4 = 0x124,         // lane i <- lane (i + 4) % 16
+    DPP_ROW_ROR8 = 0x128,         // lane i <- lane (i + 8) % 16 == i ^ 8
+    DPP_QUAD_XOR1 = 0xB1,         // quad_perm [1,0,3,2]
+    DPP_QUAD_XOR2 = 0x4E,         // quad_perm [2,3,0,1]
+};
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Speculative rows verify drafts: outs[s * spec] >= 0 (reference qwen35.cu:94-100).
+__device__ __forceinline__ bool is_spec(const int* outs, int spec, int s) {
+    return outs && outs[(size_t)s * spec] >= 0;
+}
+
+// Keys a token attends to in decode attention: pos + 1, or 0 for tokens of
+// prompt sequences when prompts are left to the prefill kernel
+// (reference qwen35.cu:1171-1172).
+__device__ __forceinline__ int decode_len(int t, const int* pos, const int* tok_seq, const int* cu,
+                                          int skip_prompts, const int* outs, int spec) {
+    if (skip_prompts) {
+        const int sq = tok_seq[t];
+        if (cu[sq + 1] - cu[sq] > 1 && !is_spec(outs, spec, sq)) return 0;
+    }
+    return pos[t] + 1;
+}
+
+}  // namespace pkv

@@ -1,0 +1,87 @@
+// Byte-exact data movement of the paged KV cache: append (scatter by slot),
+// gather (through a block table) and page copy (copy-on-write).
+//
+// Cache layout (reference model.rs:1166-1197): K and V pools of
+// [pages * block_size][Hkv][head_dim]; one slot row (all kv heads) is
+// `row_bytes` = Hkv * head_bytes contiguous bytes, so a page is
+// block_size * row_bytes contiguous bytes. Every kernel copies whole slot
+// rows with 16-byte vector accesses when rows and pointers allow it.
+#include "pkv_common.h"
+
+namespace pkv {
+
+template <typename V>
+__device__ __forceinline__ void copy_row(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, int n,
+                                         int tid, int nthr) {
+    V* d = reinterpret_cast<V*>(dst);
+    const V* s = reinterpret_cast<const V*>(src);
+    for (int i = tid; i < n; i += nthr) d[i] = s[i];
+}
+
+// KV append (reference attn_prep's cache stores, qwen35.cu:1090-1100 and
+// 1120-1127, without the norm and rotary which the caller has applied):
+// for token t with slot = slot_map[t] >= 0, cache[slot] := row t. One block
+// per (token, K|V); `vec` selects 16-byte (2), 4-byte (1) or byte (0) moves.
+// Slots outside [0, num_slots) are skipped like padding rows (slot < 0).
+__global__ void __launch_bounds__(256) append_kernel(const uint8_t* __restrict__ ksrc,
+                                                     const uint8_t* __restrict__ vsrc, long stride,
+                                                     const int* __restrict__ slot_map, int row_bytes,
+                                                     uint8_t* __restrict__ kc, uint8_t* __restrict__ vc,
+                                                     long num_slots, int vec) {
+    const int t = blockIdx.x;
+    const long slot = slot_map[t];
+    if (slot < 0 || slot >= num_slots) return;
+    const bool is_v = blockIdx.y != 0;
+    const uint8_t* src = (is_v ? vsrc : ksrc) + (size_t)t * stride;
+    uint8_t* dst = (is_v ? vc : kc) + (size_t)slot * row_bytes;
+    if (vec == 2)
+        copy_row<uint4>(dst, src, row_bytes >> 4, threadIdx.x, blockDim.x);
+    else if (vec == 1)
+        copy_row<uint32_t>(dst, src, row_bytes >> 2, threadIdx.x, blockDim.x);
+    else
+        copy_row<uint8_t>(dst, src, row_bytes, threadIdx.x, blockDim.x);
+}
+
+// Gather one sequence's first L slot rows into dense [L][row] buffers:
+// dense[j] = cache[bt[j / bs] * bs + j % bs]. Four rows per block of 256.
+// Page ids outside [0, num_blocks) are clamped into the pool (garbage in,
+// garbage out, never an out-of-bounds access).
+__global__ void __launch_bounds__(256) gather_kernel(const uint8_t* __restrict__ kc, const uint8_t* __restrict__ vc,
+                                                     const int* __restrict__ bt, int L, int bs, int row_bytes,
+                                                     long num_blocks, uint8_t* __restrict__ ko,
+                                                     uint8_t* __restrict__ vo, int vec) {
+    const int sub = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int j = blockIdx.x * 4 + sub;
+    if (j >= L) return;
+    long page = bt[j / bs];
+    page = page < 0 ? 0 : page >= num_blocks ? num_blocks - 1 : page;
+    const size_t slot = (size_t)page * bs + j % bs;
+    const bool is_v = blockIdx.y != 0;
+    const uint8_t* src = (is_v ? vc : kc) + slot * row_bytes;
+    uint8_t* dst = (is_v ? vo : ko) + (size_t)j * row_bytes;
+    if (vec == 2)
+        copy_row<uint4>(dst, src, row_bytes >> 4, lane, 64);
+    else if (vec == 1)
+        copy_row<uint32_t>(dst, src, row_bytes >> 2, lane, 64);
+    else
+        copy_row<uint8_t>(dst, src, row_bytes, lane, 64);
+}
+
+// Page copy for copy-on-write: page dst[i] := page src[i] in the K and V
+// pools. One block per (pair, K|V, slice of the page); 16-byte moves.
+// Pairs whose ids fall outside the pool are skipped.
+__global__ void __launch_bounds__(256) page_copy_kernel(uint8_t* __restrict__ kc, uint8_t* __restrict__ vc,
+                                                        const int* __restrict__ src, const int* __restrict__ dst,
+                                                        long page_bytes, long num_blocks, int slices) {
+    const int i = blockIdx.x;
+    const long s = src[i], d = dst[i];
+    if (s < 0 || d < 0 || s >= num_blocks || d >= num_blocks) return;
+    uint8_t* pool = blockIdx.y ? vc : kc;
+    const long n = page_bytes >> 4, per = (n + slices - 1) / slices;
+    const long b = blockIdx.z * per, e = min(n, b + per);
+    const uint4* sp = reinterpret_cast<const uint4*>(pool + s * page_bytes);
+    uint4* dp = reinterpret_cast<uint4*>(pool + d * page_bytes);
+    for (long k = b + threadIdx.x; k < e; k += blockDim.x) dp[k] = sp[k];
+}
+
+}  // namespace pkv

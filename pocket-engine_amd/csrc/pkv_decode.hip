@@ -1,0 +1,364 @@
+// Paged decode attention for gfx950 (bf16 cache, head_dim 256, GQA group 4,
+// 16-slot pages). Same results as the reference's attn_paged_g4 +
+// attn_merge (qwen35.cu:1146-1334, 2242-2279; AMD body
+// amd/attn_decode.cuh:12-183), computed a different way:
+//
+// Work split ("flattened key space"). The keys of every decode token are
+// laid end to end: token t owns [offs[t], offs[t] + L_t), L_t = pos[t] + 1.
+// The W keys are cut into n_active equal ranges of R keys (R >= min_range),
+// one per workgroup, whatever the length mix: every workgroup streams the
+// same number of bytes, so a batch of 512..8192-token contexts balances
+// without a work queue. A range crossing token boundaries handles each token
+// piece in turn. A token whose keys all fall in one range is finished in
+// place (gated output); otherwise each piece leaves a partial (max, sum,
+// weighted values) at index t + b (b = range index; t + b strictly grows
+// along the walk, so it is unique and below T + n_wg) and decode_merge
+// combines them in key order.
+//
+// Inside a workgroup wave w takes kv head w, so one page read serves the G
+// query heads of the group and the workgroup as a whole reads whole slot rows
+// (all kv heads, 2 KiB) of each page. Per page (16 keys) a wave:
+//   K: lane (row r = lane / 16, sub s = lane % 16) loads 16-byte chunks s and
+//      s + 16 of keys 4p + r, p = 0..3: 8 loads, each row of 16 lanes reading
+//      256 contiguous bytes. q.k partials (4 keys x 4 heads per lane) use
+//      v_dot2c_f32_bf16 on bf16 pairs, then a reduce-scatter over the 16
+//      lanes of a row (DPP xor 8 / xor 7 / xor 2 / xor 1) leaves lane s with
+//      the full score of (key 4 (s / 4) + r, head s % 4).
+//   softmax: running max per head over its 16 lanes (DPP rotates + two
+//      cross-row shuffles), probabilities in f32, exp2 domain.
+//   V: lane (half h = lane / 32, chunk c = lane % 32) loads keys 8h .. 8h + 7,
+//      dims 8c .. 8c + 7 (16 bytes each: a full 512-byte row per half-wave);
+//      probabilities reach it through 272 bytes of LDS; 256 FMAs per lane.
+// The next page's K is requested right after q.k and its V right after P.V,
+// so one page (16 KiB) is always in flight per wave. No MFMA is used.
+#include "pkv_common.h"
+
+namespace pkv {
+
+struct DecodeParams {
+    const uint16_t* q;        // [T][Hq][256]
+    const uint16_t* kc;       // [pages * 16][Hkv][256]
+    const uint16_t* vc;
+    const uint16_t* qkv;      // gate of head h at row t: qkv[t * qstride + h * 512 + 256 ..]
+    int qstride, Hq, Hkv;
+    const int* pos;
+    const int* tok_seq;
+    const int* block_table;   // [seqs][max_blocks]
+    int max_blocks;
+    uint16_t* out;            // [T][Hq][256]
+    float scale;
+    const int* cu;
+    int skip_prompts;
+    const int* outs;
+    int spec;
+    int T;
+    long num_blocks;
+    int* offs;                // [T + 2]: key offsets, then W and R
+    float* part_ms;           // [(T + n_wg) * Hq][2]: max (log2 units), sum
+    float* part_acc;          // [(T + n_wg) * Hq][256]
+    int n_wg, min_range;
+};
+
+constexpr int PAGE = 16;
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// Exclusive prefix sum over the block; returns the block total in `total`.
+__device__ __forceinline__ int block_scan(int v, int* sh, int& total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) sh[w] = x;
+    __syncthreads();
+    int before = 0;
+    total = 0;
+    for (int k = 0; k < nw; k++) {
+        const int s = sh[k];
+        if (k < w) before += s;
+        total += s;
+    }
+    __syncthreads();
+    return before + x - v;
+}
+
+template <int G>
+struct WaveLds {
+    float p[PAGE * G];  // probabilities [key][head]
+    float c[G];         // rescale factor per head
+    float ml[2 * G];    // final (max, sum) per head
+};
+
+// One wave: token t, kv head kvh, keys [j0, j1) of its sequence.
+template <int G>
+__device__ __forceinline__ void decode_piece(const DecodeParams& p, WaveLds<G>& lds, int t, int kvh, int j0, int j1,
+                                             int L, int idx) {
+    static_assert(G == 4, "lane mapping assumes 4 keys x 4 heads per lane");
+    const int lane = threadIdx.x & 63, sig = lane & 15, rho = lane >> 4;
+    const int hv = lane >> 5, ch = lane & 31;
+    const int Hkv = p.Hkv;
+    const int* bt = p.block_table + (size_t)p.tok_seq[t] * p.max_blocks;
+    const float sl2 = p.scale * LOG2E;
+
+    uint4 qr[G][2];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const uint16_t* qrow = p.q + ((size_t)t * p.Hq + kvh * G + g) * HEAD_DIM;
+        qr[g][0] = *reinterpret_cast<const uint4*>(qrow + 8 * sig);
+        qr[g][1] = *reinterpret_cast<const uint4*>(qrow + 128 + 8 * sig);
+    }
+    const size_t row_elems = (size_t)Hkv * HEAD_DIM;
+    auto page_base = [&](int pi) -> size_t {
+        long pg = bt[pi];
+        pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
+        return (size_t)pg * PAGE * row_elems + (size_t)kvh * HEAD_DIM;
+    };
+    uint4 kb[4][2], vb[8];
+    auto load_k = [&](size_t base) {
+        const uint16_t* kp = p.kc + base + 8 * sig;
+#pragma unroll
+        for (int pp = 0; pp < 4; pp++) {
+            const uint16_t* r = kp + (size_t)(4 * pp + rho) * row_elems;
+            kb[pp][0] = *reinterpret_cast<const uint4*>(r);
+            kb[pp][1] = *reinterpret_cast<const uint4*>(r + 128);
+        }
+    };
+    auto load_v = [&](size_t base) {
+        const uint16_t* vp = p.vc + base + 8 * ch + (size_t)(8 * hv) * row_elems;
+#pragma unroll
+        for (int k = 0; k < 8; k++) vb[k] = *reinterpret_cast<const uint4*>(vp + (size_t)k * row_elems);
+    };
+
+    float m = -INFINITY, l = 0.f;
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
+
+    const int pg0 = j0 / PAGE, pg1 = (j1 - 1) / PAGE;
+    size_t base = page_base(pg0);
+    load_k(base);
+    load_v(base);
+    for (int pi = pg0; pi <= pg1; pi++) {
+        const size_t next = pi < pg1 ? page_base(pi + 1) : base;
+        // q . k partials: v[pp * 4 + g] over this lane's 16 dims.
+        float v[16];
+#pragma unroll
+        for (int pp = 0; pp < 4; pp++)
+#pragma unroll
+            for (int g = 0; g < G; g++) v[pp * 4 + g] = dot8(qr[g][1], kb[pp][1], dot8(qr[g][0], kb[pp][0], 0.f));
+        if (pi < pg1) load_k(next);
+        // Reduce-scatter across the row's 16 lanes: after the step on lane
+        // bit b the lane keeps the half of its values selected by that bit.
+        {
+            const bool b3 = sig & 8;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float keep = b3 ? v[k + 8] : v[k], send = b3 ? v[k] : v[k + 8];
+                v[k] = keep + dpp<DPP_ROW_ROR8>(send);
+            }
+            const bool b2 = sig & 4;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float keep = b2 ? v[k + 4] : v[k], send = b2 ? v[k] : v[k + 4];
+                v[k] = keep + dpp<DPP_ROW_HALF_MIRROR>(send);
+            }
+            const bool b1 = sig & 2;
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const float keep = b1 ? v[k + 2] : v[k], send = b1 ? v[k] : v[k + 2];
+                v[k] = keep + dpp<DPP_QUAD_XOR2>(send);
+            }
+            const bool b0 = sig & 1;
+            const float keep = b0 ? v[1] : v[0], send = b0 ? v[0] : v[1];
+            v[0] = keep + dpp<DPP_QUAD_XOR1>(send);
+        }
+        // Lane (sig, rho) now holds key 4 (sig / 4) + rho, head sig % 4.
+        const int key = 4 * (sig >> 2) + rho, kpos = pi * PAGE + key;
+        const float sc = (kpos >= j0 && kpos < j1) ? v[0] * sl2 : -INFINITY;
+        float mx = fmaxf(sc, dpp<DPP_ROW_ROR4>(sc));
+        mx = fmaxf(mx, dpp<DPP_ROW_ROR8>(mx));
+        mx = fmaxf(mx, shfl_xor(mx, 16));
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float corr = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first page (m = -inf)
+        const float pr = __builtin_amdgcn_exp2f(sc - mn);
+        l = l * corr + pr;
+        m = mn;
+        lds.p[key * G + (sig & 3)] = pr;
+        if (lane < G) lds.c[lane] = corr;
+        wave_sync();
+        const float4 cr = *reinterpret_cast<const float4*>(lds.c);
+        const float cg[4] = {cr.x, cr.y, cr.z, cr.w};
+        if (__any(cr.x != 1.f || cr.y != 1.f || cr.z != 1.f || cr.w != 1.f)) {
+#pragma unroll
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[g][e] *= cg[g];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 pk = *reinterpret_cast<const float4*>(&lds.p[(8 * hv + k) * G]);
+            const float pg[4] = {pk.x, pk.y, pk.z, pk.w};
+            const uint32_t w[4] = {vb[k].x, vb[k].y, vb[k].z, vb[k].w};
+#pragma unroll
+            for (int e2 = 0; e2 < 4; e2++) {
+                const float x0 = bf_lo(w[e2]), x1 = bf_hi(w[e2]);
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    acc[g][2 * e2] = fmaf(pg[g], x0, acc[g][2 * e2]);
+                    acc[g][2 * e2 + 1] = fmaf(pg[g], x1, acc[g][2 * e2 + 1]);
+                }
+            }
+        }
+        wave_sync();  // lds.p / lds.c are rewritten for the next page
+        if (pi < pg1) load_v(next);
+        base = next;
+    }
+    // Totals: the sum over the head's 16 lanes, the two halves' values.
+    l += dpp<DPP_ROW_ROR4>(l);
+    l += dpp<DPP_ROW_ROR8>(l);
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[g][e] += shfl_xor(acc[g][e], 32);
+    if (lane < G) {
+        lds.ml[2 * lane] = m;
+        lds.ml[2 * lane + 1] = l;
+    }
+    wave_sync();
+    if (hv != 0) return;
+    const bool direct = j0 == 0 && j1 == L;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int h = kvh * G + g;
+        if (direct) {
+            const float inv = 1.f / lds.ml[2 * g + 1];
+            const uint4 graw = *reinterpret_cast<const uint4*>(p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM +
+                                                               HEAD_DIM + 8 * ch);
+            const uint32_t gw[4] = {graw.x, graw.y, graw.z, graw.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e2 = 0; e2 < 4; e2++) {
+                const float y0 = rbf(acc[g][2 * e2] * inv) / (1.f + __expf(-bf_lo(gw[e2])));
+                const float y1 = rbf(acc[g][2 * e2 + 1] * inv) / (1.f + __expf(-bf_hi(gw[e2])));
+                o[e2] = pack2(y0, y1);
+            }
+            *reinterpret_cast<uint4*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + 8 * ch) =
+                make_uint4(o[0], o[1], o[2], o[3]);
+        } else {
+            float* pa = p.part_acc + ((size_t)idx * p.Hq + h) * HEAD_DIM + 8 * ch;
+            *reinterpret_cast<float4*>(pa) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+            *reinterpret_cast<float4*>(pa + 4) = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+            if (ch == 0)
+                *reinterpret_cast<float2*>(p.part_ms + ((size_t)idx * p.Hq + h) * 2) =
+                    make_float2(lds.ml[2 * g], lds.ml[2 * g + 1]);
+        }
+    }
+}
+
+// One workgroup per key range and group of up to 4 kv heads (blockIdx.y),
+// a wave per kv head (see the file comment).
+template <int G>
+__global__ void __launch_bounds__(256, 2) decode_split_kernel(DecodeParams p) {
+    __shared__ int sh_scan[16];
+    __shared__ int sh_t0[2];
+    __shared__ WaveLds<G> sh_w[4];
+    const int T = p.T, nthr = blockDim.x, tid = threadIdx.x, b = blockIdx.x;
+    // Pass 1: total keys W.
+    int W = 0;
+    for (int base = 0; base < T; base += nthr) {
+        const int t = base + tid;
+        const int L = t < T ? decode_len(t, p.pos, p.tok_seq, p.cu, p.skip_prompts, p.outs, p.spec) : 0;
+        int tot;
+        block_scan(L, sh_scan, tot);
+        W += tot;
+    }
+    const int R = max(p.min_range, (W + p.n_wg - 1) / p.n_wg);
+    const int start = b * R, end = min(W, start + R);
+    if (b == 0 && tid == 0) {
+        p.offs[T] = W;
+        p.offs[T + 1] = R;
+    }
+    if (start >= W && b != 0) return;
+    // Pass 2: exclusive offsets (written by block 0 for decode_merge); find
+    // the token holding key `start`.
+    int run = 0;
+    for (int base = 0; base < T; base += nthr) {
+        const int t = base + tid;
+        const int L = t < T ? decode_len(t, p.pos, p.tok_seq, p.cu, p.skip_prompts, p.outs, p.spec) : 0;
+        int tot;
+        const int off = run + block_scan(L, sh_scan, tot);
+        if (t < T) {
+            if (b == 0) p.offs[t] = off;
+            if (L > 0 && off <= start && start < off + L) {
+                sh_t0[0] = t;
+                sh_t0[1] = off;
+            }
+        }
+        run += tot;
+        if (b != 0 && run > start) break;  // uniform: every thread has the same run
+    }
+    if (start >= W) return;
+    __syncthreads();
+    // Kv heads 4 y .. 4 y + 3, one per wave.
+    const int wave = tid >> 6, kvh = blockIdx.y * 4 + wave;
+    if (kvh >= p.Hkv) return;
+    int t = sh_t0[0], off = sh_t0[1];
+    while (off < end && t < T) {
+        const int L = decode_len(t, p.pos, p.tok_seq, p.cu, p.skip_prompts, p.outs, p.spec);
+        if (L > 0) {
+            const int j0 = max(start, off) - off, j1 = min(end, off + L) - off;
+            decode_piece<G>(p, sh_w[wave], t, kvh, j0, j1, L, t + b);
+            off += L;
+        }
+        t++;
+    }
+}
+
+// Combines the partials of tokens split over several ranges, in key order,
+// then gates like the reference (rbf(A / S) * sigmoid(gate), qwen35.cu:2255-2273).
+// One block per token; a wave per query head at a time, 4 dims per lane.
+__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
+    const int t = blockIdx.x, T = p.T;
+    const int o0 = p.offs[t], o1 = p.offs[t + 1];  // offs[T] = W
+    if (o1 <= o0) return;
+    const int R = p.offs[T + 1];
+    const int b0 = o0 / R, b1 = (o1 - 1) / R;
+    if (b0 == b1) return;  // finished in place by its range
+    const int lane = threadIdx.x & 63, d = 4 * lane;
+    for (int h = threadIdx.x >> 6; h < p.Hq; h += blockDim.x >> 6) {
+        float M = -INFINITY;
+        for (int b = b0; b <= b1; b++) M = fmaxf(M, p.part_ms[((size_t)(t + b) * p.Hq + h) * 2]);
+        float S = 0.f, A[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int b = b0; b <= b1; b++) {
+            const size_t at = (size_t)(t + b) * p.Hq + h;
+            const float2 ms = *reinterpret_cast<const float2*>(p.part_ms + at * 2);
+            const float f = ms.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms.x - M);
+            S += ms.y * f;
+            const float4 a = *reinterpret_cast<const float4*>(p.part_acc + at * HEAD_DIM + d);
+            A[0] += a.x * f;
+            A[1] += a.y * f;
+            A[2] += a.z * f;
+            A[3] += a.w * f;
+        }
+        const float inv = 1.f / S;
+        const uint2 graw =
+            *reinterpret_cast<const uint2*>(p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d);
+        const float y0 = rbf(A[0] * inv) / (1.f + __expf(-bf_lo(graw.x)));
+        const float y1 = rbf(A[1] * inv) / (1.f + __expf(-bf_hi(graw.x)));
+        const float y2 = rbf(A[2] * inv) / (1.f + __expf(-bf_lo(graw.y)));
+        const float y3 = rbf(A[3] * inv) / (1.f + __expf(-bf_hi(graw.y)));
+        *reinterpret_cast<uint2*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + d) = make_uint2(pack2(y0, y1), pack2(y2, y3));
+    }
+}
+
+template __global__ void decode_split_kernel<4>(DecodeParams);
+
+}  // namespace pkv

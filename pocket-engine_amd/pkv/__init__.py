@@ -1,0 +1,181 @@
+"""pkv: MI355X paged KV cache — Python host mirror over libpkv.so (ctypes).
+
+Device arguments are torch tensors on the GPU (their data_ptr is passed) or
+raw integer device addresses; `stream` defaults to torch's current stream.
+Every call raises PkvError on a non-zero status. There is no fallback: if
+libpkv.so is missing or fails to load, importing this module raises.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libpkv.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"libpkv.so not built at {LIB_PATH}: run __graft_entry__.build()")
+_lib = ctypes.CDLL(LIB_PATH)
+
+OK = 0
+ERR_INVALID = 1
+ERR_UNSUPPORTED = 801
+ERR_NO_BLOCKS = 802
+
+_c_int, _c_i64, _c_p, _c_f, _c_sz = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
+
+_SIGS = {
+    "pkv_strerror": (ctypes.c_char_p, [_c_int]),
+    "pkv_version": (_c_int, []),
+    "pkv_append": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_i64, _c_p]),
+    "pkv_gather": (_c_int, [_c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_p, _c_p, _c_p]),
+    "pkv_page_copy": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_i64, _c_i64, _c_p]),
+    "pkv_attn_decode_workspace": (_c_int, [_c_int, _c_int, ctypes.POINTER(_c_sz)]),
+    "pkv_attn_decode": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_p, _c_int, _c_int,
+                                 _c_p, _c_f, _c_p, _c_int, _c_p, _c_int, _c_int, _c_i64, _c_p, _c_sz, _c_p]),
+    "pkv_attn_decode_config": (_c_int, [_c_int, _c_int]),
+    "pkv_pool_create": (_c_p, [_c_i64]),
+    "pkv_pool_destroy": (None, [_c_p]),
+    "pkv_pool_take": (_c_int, [_c_p, _c_int, ctypes.POINTER(ctypes.c_uint32)]),
+    "pkv_pool_unref": (_c_int, [_c_p, ctypes.POINTER(ctypes.c_uint32), _c_int]),
+    "pkv_pool_ref": (_c_int, [_c_p, ctypes.POINTER(ctypes.c_uint32), _c_int]),
+    "pkv_pool_free_count": (_c_i64, [_c_p]),
+    "pkv_pool_total": (_c_i64, [_c_p]),
+    "pkv_pool_refs": (_c_int, [_c_p, ctypes.c_uint32]),
+    "pkv_pool_free_list": (_c_i64, [_c_p, ctypes.POINTER(ctypes.c_uint32), _c_i64]),
+}
+_SIGS["pkv_attn_decode_split"] = _SIGS["pkv_attn_decode"]
+_SIGS["pkv_attn_decode_merge"] = _SIGS["pkv_attn_decode"]
+for _name, (_res, _args) in _SIGS.items():
+    _f = getattr(_lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+
+class PkvError(RuntimeError):
+    def __init__(self, status, what):
+        self.status = status
+        super().__init__(f"{what}: {strerror(status)} ({status})")
+
+
+def strerror(status):
+    return _lib.pkv_strerror(status).decode()
+
+
+def version():
+    return _lib.pkv_version()
+
+
+def _check(status, what):
+    if status != OK:
+        raise PkvError(status, what)
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def _stream(stream):
+    if stream is not None:
+        return stream if isinstance(stream, int) else stream.cuda_stream
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def append(k_rows, v_rows, row_stride, slot_map, T, Hkv, head_bytes, kcache, vcache, num_slots, stream=None):
+    """KV append; row_stride in bytes (see include/pkv.h)."""
+    _check(_lib.pkv_append(_ptr(k_rows), _ptr(v_rows), row_stride, _ptr(slot_map), T, Hkv, head_bytes,
+                           _ptr(kcache), _ptr(vcache), num_slots, _stream(stream)), "pkv_append")
+
+
+def gather(kcache, vcache, bt_row, L, block_size, Hkv, head_bytes, num_blocks, k_out, v_out, stream=None):
+    _check(_lib.pkv_gather(_ptr(kcache), _ptr(vcache), _ptr(bt_row), L, block_size, Hkv, head_bytes, num_blocks,
+                           _ptr(k_out), _ptr(v_out), _stream(stream)), "pkv_gather")
+
+
+def page_copy(kcache, vcache, src, dst, n, page_bytes, num_blocks, stream=None):
+    _check(_lib.pkv_page_copy(_ptr(kcache), _ptr(vcache), _ptr(src), _ptr(dst), n, page_bytes, num_blocks,
+                              _stream(stream)), "pkv_page_copy")
+
+
+def attn_decode_workspace(T, Hq):
+    n = _c_sz(0)
+    _check(_lib.pkv_attn_decode_workspace(T, Hq, ctypes.byref(n)), "pkv_attn_decode_workspace")
+    return n.value
+
+
+def attn_decode_config(wg_per_cu=2, min_range=32):
+    _check(_lib.pkv_attn_decode_config(wg_per_cu, min_range), "pkv_attn_decode_config")
+
+
+def attn_decode(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, out,
+                scale, cu, skip_prompts, outs, spec, T, num_blocks, workspace, workspace_bytes=None, stream=None,
+                phase="both"):
+    """Paged decode attention (reference attn_paged_g4 + attn_merge semantics).
+    phase: "both", "split" (key-range kernel only) or "merge"."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace.numel() * workspace.element_size()
+    fn = {"both": _lib.pkv_attn_decode, "split": _lib.pkv_attn_decode_split, "merge": _lib.pkv_attn_decode_merge}[phase]
+    _check(fn(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(qkv), qstride, Hq, Hkv, _ptr(pos),
+                                _ptr(tok_seq), _ptr(block_table), max_blocks, block_size, _ptr(out), scale,
+                                _ptr(cu), int(skip_prompts), _ptr(outs), spec, T, num_blocks, _ptr(workspace),
+                                workspace_bytes, _stream(stream)), "pkv_attn_decode")
+
+
+class Pool:
+    """Block allocator (reference Scheduler.free_blocks/block_refs,
+    src/sched.rs:461-465, 515, 801-817)."""
+
+    def __init__(self, n_blocks):
+        self._h = _lib.pkv_pool_create(n_blocks)
+        if not self._h:
+            raise PkvError(ERR_INVALID, "pkv_pool_create")
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.pkv_pool_destroy(h)
+            self._h = None
+
+    @staticmethod
+    def _ids(ids):
+        ids = list(ids)
+        return (ctypes.c_uint32 * max(1, len(ids)))(*ids), len(ids)
+
+    def take(self, n):
+        buf = (ctypes.c_uint32 * max(1, n))()
+        _check(_lib.pkv_pool_take(self._h, n, buf), "pkv_pool_take")
+        return list(buf[:n])
+
+    def unref(self, ids):
+        buf, n = self._ids(ids)
+        _check(_lib.pkv_pool_unref(self._h, buf, n), "pkv_pool_unref")
+
+    def ref(self, ids):
+        buf, n = self._ids(ids)
+        _check(_lib.pkv_pool_ref(self._h, buf, n), "pkv_pool_ref")
+
+    def free_count(self):
+        return _lib.pkv_pool_free_count(self._h)
+
+    def total(self):
+        return _lib.pkv_pool_total(self._h)
+
+    def refs(self, i):
+        r = _lib.pkv_pool_refs(self._h, i)
+        if r < 0:
+            raise PkvError(-r, "pkv_pool_refs")
+        return r
+
+    def free_list(self):
+        n = self.free_count()
+        buf = (ctypes.c_uint32 * max(1, n))()
+        _lib.pkv_pool_free_list(self._h, buf, n)
+        return list(buf[:n])
+
+
+def exported_symbols():
+    """Names of every entry point declared in include/pkv.h that this library exports."""
+    return [n for n in _SIGS if hasattr(_lib, n)]

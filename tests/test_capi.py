@@ -1,0 +1,60 @@
+"""The C-ABI library loads, exports every entry point include/pkv.h declares,
+and rejects bad arguments before launching anything. CPU only: no call here
+reaches a kernel."""
+import os
+import re
+
+import pkv
+
+HDR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "pkv.h")
+
+
+def declared():
+    text = open(HDR).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = declared()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(pkv._lib, n), n
+    assert set(names) <= set(pkv.exported_symbols())
+
+
+def test_status_strings():
+    assert pkv.strerror(0) == "ok"
+    assert pkv.strerror(pkv.ERR_UNSUPPORTED) == "unsupported shape"
+    assert pkv.version() >= 1
+
+
+def test_invalid_and_unsupported_arguments_return_before_launch():
+    L = pkv._lib
+    # decode: G != 4 is unsupported, block size must be 16
+    assert L.pkv_attn_decode(1, 1, 1, 1, 8192, 12, 2, 1, 1, 1, 4, 16, 1, 0.1, 1, 0, None, 1, 3, 10, 1, 1 << 30,
+                             None) == pkv.ERR_UNSUPPORTED
+    assert L.pkv_attn_decode(1, 1, 1, 1, 8192, 16, 4, 1, 1, 1, 4, 32, 1, 0.1, 1, 0, None, 1, 3, 10, 1, 1 << 30,
+                             None) == pkv.ERR_UNSUPPORTED
+    # null pointers, short workspace, misaligned pointers
+    assert L.pkv_attn_decode(None, 16, 16, 16, 10240, 16, 4, 16, 16, 16, 4, 16, 16, 0.1, 16, 0, None, 1, 3, 10, 256,
+                             1 << 30, None) == pkv.ERR_INVALID
+    assert L.pkv_attn_decode(16, 16, 16, 16, 10240, 16, 4, 16, 16, 16, 4, 16, 16, 0.1, 16, 0, None, 1, 3, 10, 256,
+                             16, None) == pkv.ERR_INVALID
+    assert L.pkv_attn_decode(18, 16, 16, 16, 10240, 16, 4, 16, 16, 16, 4, 16, 16, 0.1, 16, 0, None, 1, 3, 10, 256,
+                             1 << 30, None) == pkv.ERR_INVALID
+    # zero tokens is a no-op
+    assert L.pkv_attn_decode(None, None, None, None, 10240, 16, 4, None, None, None, 4, 16, None, 0.1, None, 0, None,
+                             1, 0, 10, None, 0, None) == pkv.OK
+    assert L.pkv_append(1, 1, 16, 1, -1, 4, 512, 1, 1, 10, None) == pkv.ERR_INVALID
+    assert L.pkv_append(1, 1, 100, 1, 4, 4, 512, 1, 1, 10, None) == pkv.ERR_INVALID  # stride < row
+    assert L.pkv_append(None, None, 0, None, 0, 4, 512, None, None, 10, None) == pkv.OK
+    assert L.pkv_page_copy(16, 16, 16, 16, 1, 100, 10, None) == pkv.ERR_INVALID  # page bytes % 16
+    assert L.pkv_gather(16, 16, 16, -1, 16, 4, 512, 10, 16, 16, None) == pkv.ERR_INVALID
+    assert L.pkv_attn_decode_config(0, 32) == pkv.ERR_INVALID
+
+
+def test_workspace_grows_with_tokens():
+    a, b = pkv.attn_decode_workspace(1, 16), pkv.attn_decode_workspace(64, 16)
+    assert b > a > 0
+    assert (b - a) >= 63 * 16 * 256 * 4

@@ -1,0 +1,217 @@
+"""Pins the CPU oracle (oracle/pkv_oracle.c) before it is trusted as the
+checker: against the torch-fp64 golden fixtures (tests/golden/), closed forms
+and brute force. A plausible mistake in the oracle (a dropped scale, a wrong
+kv-head index, a transposed operand, a wrong causal bound) fails one of these.
+CPU only."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _util import BS, D, bf16_bits, decode_case, hash_bf16
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "attn_small.npz")
+
+
+def test_f2b_matches_torch_rne():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10,
+                        np.array([0.0, -0.0, 1.0, 1.00390625, 1.01171875, 3.0e38, -3.0e38, 1e-40, np.inf, -np.inf],
+                                 np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.f2b(x), want)
+    # the C helper agrees with the numpy one
+    for v in x[:200]:
+        assert oracle._lib.orc_f2b(float(v)) == oracle.f2b(np.array([v]))[0]
+
+
+def test_hash_inputs_match_reference_formula_small_cases():
+    # bench-attn inputs (main.rs:739-748) computed by hand for i = 0, 1, seed 1:
+    # h = (i ^ 0x9e3779b9) * 2654435761 mod 2^64; x = (h % 2001) / 1000 - 1
+    for i in (0, 1, 7):
+        h = ((i ^ 0x9E3779B9) * 2654435761) % (1 << 64)
+        x = np.float32((h % 2001)) / np.float32(1000.0) - np.float32(1.0)
+        assert hash_bf16(8, 1)[i] == bf16_bits(np.array([x]))[0]
+
+
+@pytest.mark.parametrize("row", [(2, 64, np.float32), (4, 256, np.uint16)])
+def test_append_gather_roundtrip_and_closed_form(row):
+    Hkv, Dh, dt = row
+    rng = np.random.default_rng(1)
+    pages = 64
+    lens = rng.integers(1, 201, size=4)
+    perm = rng.permutation(pages)
+    bt = np.zeros((4, 13), np.int32)
+    at = 0
+    for s, L in enumerate(lens):
+        n = (L + BS - 1) // BS
+        bt[s, :n] = perm[at:at + n]
+        at += n
+    kc = np.zeros((pages * BS, Hkv, Dh), dt)
+    vc = np.zeros((pages * BS, Hkv, Dh), dt)
+    dense = []
+    for s, L in enumerate(lens):
+        k = rng.standard_normal((L, Hkv, Dh)).astype(np.float32)
+        v = rng.standard_normal((L, Hkv, Dh)).astype(np.float32)
+        if dt == np.uint16:
+            k, v = bf16_bits(k), bf16_bits(v)
+        slot = (bt[s, np.arange(L) // BS] * BS + np.arange(L) % BS).astype(np.int32)
+        oracle.append(k, v, slot, kc, vc)
+        # closed form: the rows sit exactly at their slots
+        assert np.array_equal(kc[slot], k) and np.array_equal(vc[slot], v)
+        dense.append((k, v))
+    for s, L in enumerate(lens):
+        ko, vo = oracle.gather(kc, vc, bt[s], int(L), BS)
+        assert np.array_equal(ko, dense[s][0]) and np.array_equal(vo, dense[s][1])
+
+
+def test_append_skips_padding_slots():
+    kc = np.zeros((32, 1, 4), np.float32)
+    vc = np.zeros_like(kc)
+    k = np.ones((3, 1, 4), np.float32)
+    oracle.append(k, k * 2, np.array([5, -1, 7], np.int32), kc, vc)
+    assert kc[5].sum() == 4 and kc[7].sum() == 4 and kc.sum() == 8 and vc.sum() == 16
+
+
+def test_page_copy_closed_form():
+    rng = np.random.default_rng(2)
+    kc = rng.standard_normal((8 * BS, 2, 8)).astype(np.float32)
+    vc = rng.standard_normal((8 * BS, 2, 8)).astype(np.float32)
+    k0, v0 = kc.copy(), vc.copy()
+    page_bytes = BS * 2 * 8 * 4
+    oracle.page_copy(kc, vc, [1, 3], [6, 0], page_bytes)
+    ref_k, ref_v = k0.copy(), v0.copy()
+    ref_k[6 * BS:7 * BS] = k0[BS:2 * BS]
+    ref_k[0:BS] = k0[3 * BS:4 * BS]
+    ref_v[6 * BS:7 * BS] = v0[BS:2 * BS]
+    ref_v[0:BS] = v0[3 * BS:4 * BS]
+    assert np.array_equal(kc, ref_k) and np.array_equal(vc, ref_v)
+
+
+@pytest.mark.parametrize("name", ["a", "b", "c"])
+def test_decode_oracle_matches_torch_sdpa_golden(name):
+    g = np.load(GOLD)
+    c = {k[2:]: g[k] for k in g.files if k.startswith(name + "_")}
+    Hq, Hkv = int(c["Hq"]), int(c["Hkv"])
+    B = len(c["pos"])
+    qstride = (2 * Hq + 2 * Hkv) * D
+    gate = np.zeros((B, qstride), np.uint16)  # gate 0 -> sigmoid 1/2
+    out, raw = oracle.attn_decode(c["q"], c["kc"], c["vc"], gate, qstride, Hq, Hkv, c["pos"],
+                                  np.arange(B, dtype=np.int32), c["bt"], c["bt"].shape[1], BS, 1.0 / 16.0)
+    np.testing.assert_allclose(raw, c["expect"], rtol=1e-5, atol=1e-6)
+    # gated epilogue: bf16(bf16(o) * 0.5) == bf16(o) * 0.5 exactly (a power of two)
+    want = bf16_bits(oracle.b2f(bf16_bits(raw)) * 0.5)
+    assert np.array_equal(out, want)
+
+
+def test_decode_gate_and_closed_forms():
+    Hq, Hkv = 4, 1
+    c = decode_case([1, 20, 20], Hq, Hkv, seed=3)
+    # sequence 1: every key equal -> output = mean of v
+    bt1 = c["bt"][1]
+    slots = bt1[np.arange(20) // BS] * BS + np.arange(20) % BS
+    c["kc"][slots] = c["kc"][slots[0]]
+    # sequence 2: one key hugely aligned with q -> output = its v
+    bt2 = c["bt"][2]
+    slots2 = bt2[np.arange(20) // BS] * BS + np.arange(20) % BS
+    qf = oracle.b2f(c["q"][2, 0])
+    c["kc"][slots2[7], 0] = bf16_bits(qf * 64)
+    c["kc"][slots2[np.arange(20) != 7], 0] = 0
+    out, raw = oracle.attn_decode(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["tok_seq"],
+                                  c["bt"], c["max_blocks"], BS, 1.0 / 16.0)
+    v = oracle.b2f(c["vc"])
+    # one key: o = v of that key for every head
+    np.testing.assert_allclose(raw[0], np.broadcast_to(v[c["bt"][0][0] * BS, 0], (Hq, D)), rtol=1e-6)
+    np.testing.assert_allclose(raw[1], np.broadcast_to(v[slots, 0].astype(np.float64).mean(0), (Hq, D)),
+                               rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(raw[2, 0], v[slots2[7], 0], rtol=1e-5, atol=1e-6)
+    # gate: y = bf16(bf16(o) / (1 + exp(-gate)))
+    gate = oracle.b2f(c["qkv"][:, :Hq * 2 * D].reshape(3, Hq, 2, D)[:, :, 1, :])
+    want = bf16_bits(oracle.b2f(bf16_bits(raw)) / (np.float32(1) + np.exp(-gate, dtype=np.float32)))
+    assert np.array_equal(out, want)
+
+
+def test_decode_wrong_head_mapping_would_fail():
+    """GQA: q head h reads kv head h // G. Pools whose kv heads differ give
+    different outputs per group, and equal outputs within a group only when q
+    is equal."""
+    Hq, Hkv = 8, 2
+    c = decode_case([30], Hq, Hkv, seed=4)
+    c["q"][0, :] = c["q"][0, 0]
+    _, raw = oracle.attn_decode(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["tok_seq"],
+                                c["bt"], c["max_blocks"], BS, 0.0625)
+    assert np.array_equal(raw[0, 0], raw[0, 3]) and not np.allclose(raw[0, 0], raw[0, 4])
+
+
+def test_skip_prompts_and_spec_rows():
+    Hq, Hkv = 4, 1
+    c = decode_case([10, 12, 9], Hq, Hkv, seed=5)
+    # sequence 0: 1 decode token; sequence 1: a 2-token prompt chunk; sequence 2: verifying (outs >= 0)
+    pos = np.array([9, 10, 11, 7, 8], np.int32)
+    tok_seq = np.array([0, 1, 1, 2, 2], np.int32)
+    cu = np.array([0, 1, 3, 5], np.int32)
+    outs = np.array([-1, -1, 4], np.int32)
+    q = np.concatenate([c["q"], c["q"][:2]])
+    qkv = np.concatenate([c["qkv"], c["qkv"][:2]])
+    sentinel = np.full((5, Hq, D), 0x7777, np.uint16)
+    out, _ = oracle.attn_decode(q, c["kc"], c["vc"], qkv, c["qstride"], Hq, Hkv, pos, tok_seq, c["bt"],
+                                c["max_blocks"], BS, 0.0625, cu=cu, skip_prompts=1, outs=outs, spec=1,
+                                out=sentinel.copy())
+    assert (out[1:3] == 0x7777).all(), "prompt rows are left to prefill"
+    assert not (out[0] == 0x7777).any() and not (out[3:] == 0x7777).any()
+
+
+def test_split_merge_equals_unsplit():
+    Hq, Hkv = 4, 1
+    c = decode_case([300], Hq, Hkv, seed=6)
+    L = 300
+    M, S, A = oracle.attn_partial(c["q"], c["kc"], c["vc"], Hq, Hkv, 0, 2, c["bt"][0], BS, 0, L, 0.0625)
+    for cuts in ([0, 100, 300], [0, 1, 64, 65, 299, 300], [0, 150, 300]):
+        parts = [oracle.attn_partial(c["q"], c["kc"], c["vc"], Hq, Hkv, 0, 2, c["bt"][0], BS, a, b, 0.0625)
+                 for a, b in zip(cuts[:-1], cuts[1:])]
+        o = oracle.merge([p[0] for p in parts], [p[1] for p in parts], [p[2] for p in parts])
+        np.testing.assert_allclose(o, A / S, rtol=1e-12, atol=1e-14)
+
+
+def test_split_parts_examples():
+    # model.rs:44-46 / qwen35.cu:1139-1141 at 256 CUs, ROCm min_chunk 64
+    assert oracle.split_parts(4097, 64, 64) == 64
+    assert oracle.split_parts(100, 4, 64) == 2
+    assert oracle.split_parts(1, 4, 64) == 1
+    assert oracle.split_parts(8193, 4, 64) == 4
+
+
+def test_prefill_oracle_matches_causal_sdpa():
+    """Prefill rows: causal over keys 0..pos[t]; q rounded to bf16 after
+    scaling by scale*log2(e), exp2 softmax == SDPA(q', K, V, scale=ln 2)."""
+    Hq, Hkv, n, ctx = 8, 2, 21, 13
+    rng = np.random.default_rng(7)
+    L = ctx + n
+    c = decode_case([L], Hq, Hkv, seed=7)
+    q = bf16_bits(rng.standard_normal((n, Hq, D)) * 0.5)
+    qkv = np.zeros((n, c["qstride"]), np.uint16)
+    pos = np.arange(ctx, ctx + n, dtype=np.int32)
+    cu = np.array([0, n], np.int32)
+    out = oracle.attn_prefill(q, c["kc"], c["vc"], qkv, c["qstride"], Hq, Hkv, pos, cu, 1, c["bt"], c["max_blocks"],
+                              BS, 0.0625)
+    slots = c["bt"][0][np.arange(L) // BS] * BS + np.arange(L) % BS
+    K = torch.from_numpy(oracle.b2f(c["kc"][slots]).astype(np.float64)).permute(1, 0, 2).repeat_interleave(4, 0)
+    V = torch.from_numpy(oracle.b2f(c["vc"][slots]).astype(np.float64)).permute(1, 0, 2).repeat_interleave(4, 0)
+    qs = oracle.b2f(bf16_bits(oracle.b2f(q) * np.float32(0.0625 * 1.4426950408889634)))
+    Q = torch.from_numpy(qs.astype(np.float64)).permute(1, 0, 2)  # [Hq][n][D]
+    mask = torch.from_numpy(np.arange(L)[None, :] <= pos[:, None])
+    o = torch.nn.functional.scaled_dot_product_attention(Q, K, V, attn_mask=mask, scale=float(np.log(2.0)))
+    want = bf16_bits(oracle.b2f(bf16_bits(o.permute(1, 0, 2).numpy().astype(np.float32))) * 0.5)
+    got = oracle.b2f(out)
+    assert np.abs(got - oracle.b2f(want)).max() <= 2 ** -9  # one bf16 rounding apart at most
+    # the causal bound matters: the first row differs from attending all keys
+    assert not np.allclose(o[:, 0], o[:, -1])
+
+
+def test_mtp_slots_closed_form():
+    bt = np.array([[5, 9, 2], [7, 1, 0]], np.int32)
+    dpos, dslot = oracle.mtp_slots([0, 1], [15, 3], bt, 3, BS, [47, 4], 2)
+    assert list(dpos) == [17, 5]
+    assert list(dslot) == [9 * 16 + 1, -1]
