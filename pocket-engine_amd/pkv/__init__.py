@@ -13,6 +13,14 @@ LIB_PATH = os.path.join(_HERE, "libpkv.so")
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(f"libpkv.so not built at {LIB_PATH}: run __graft_entry__.build()")
+# One HIP runtime per process. torch ships its own libamdhip64 (same SONAME,
+# libamdhip64.so.7); loading torch first makes libpkv's dependency resolve to
+# that already-loaded runtime, so device pointers and streams from torch are
+# valid in libpkv. Without torch the system ROCm runtime is used.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
 _lib = ctypes.CDLL(LIB_PATH)
 
 OK = 0
