@@ -53,7 +53,7 @@ def main():
     from pkv import synth
 
     if args.wg_per_cu or args.min_range:
-        pkv.attn_decode_config(args.wg_per_cu or 2, args.min_range or 32)
+        pkv.attn_decode_config(args.wg_per_cu or 1, args.min_range or 32)
     seed = args.seed if args.seed is not None else int(time.time()) % 100000
     dev = torch.device("cuda:0")
     Hq, Hkv, D, BS = 16, 4, 256, 16

@@ -119,7 +119,7 @@ int pkv_attn_decode_merge(const void* q, const void* kcache, const void* vcache,
                           int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
                           void* workspace, size_t workspace_bytes, void* stream);
 
-/* Tuning: key-range workgroups per CU (default 2) and fewest keys per range
+/* Tuning: key-range workgroups per CU (default 1) and fewest keys per range
  * (default 32). Process-wide; takes effect for later calls (workspace sizes
  * follow). */
 int pkv_attn_decode_config(int wg_per_cu, int min_range);

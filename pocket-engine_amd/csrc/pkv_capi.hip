@@ -39,7 +39,7 @@ int device_cus() {
     return cus[dev];
 }
 
-int g_wg_per_cu = 2;
+int g_wg_per_cu = 1;
 int g_min_range = 32;
 
 int decode_n_wg() { return device_cus() * g_wg_per_cu; }
@@ -179,12 +179,13 @@ int attn_decode_phases(int phases, const void* q, const void* kcache, const void
     p.min_range = g_min_range;
     const int groups = (Hkv + 3) / 4, threads = 64 * std::min(Hkv, 4);
     if (phases & 1) {
-        hipLaunchKernelGGL(pkv::decode_split_kernel<4>, dim3(n_wg, groups), dim3(threads), 0, (hipStream_t)stream, p);
+        hipLaunchKernelGGL(pkv::decode_split_kernel<4>, dim3(n_wg, groups), dim3(threads), 0, (hipStream_t)stream, p, pos,
+                           tok_seq, block_table, cu, outs);
         const int st = launch_status();
         if (st != PKV_OK) return st;
     }
     if (phases & 2) {
-        hipLaunchKernelGGL(pkv::decode_merge_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, p);
+        hipLaunchKernelGGL(pkv::decode_merge_kernel, dim3(T, (Hq + 3) / 4), dim3(256), 0, (hipStream_t)stream, p);
         return launch_status();
     }
     return PKV_OK;

@@ -33,6 +33,8 @@
 // so one page (16 KiB) is always in flight per wave. No MFMA is used.
 #include "pkv_common.h"
 
+#include <type_traits>
+
 namespace pkv {
 
 struct DecodeParams {
@@ -93,14 +95,20 @@ struct WaveLds {
 };
 
 // One wave: token t, kv head kvh, keys [j0, j1) of its sequence.
+// Read-only step metadata, passed as separate __restrict__ kernel arguments
+// so the compiler may read it through the scalar cache (uniform s_load):
+// no store of the kernel can alias it.
+
 template <int G>
-__device__ __forceinline__ void decode_piece(const DecodeParams& p, WaveLds<G>& lds, int t, int kvh, int j0, int j1,
-                                             int L, int idx) {
+__device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* __restrict__ tok_seq,
+                                             const int* __restrict__ block_table, WaveLds<G>& lds, int t, int kvh,
+                                             int j0, int j1, int L, int idx) {
     static_assert(G == 4, "lane mapping assumes 4 keys x 4 heads per lane");
     const int lane = threadIdx.x & 63, sig = lane & 15, rho = lane >> 4;
     const int hv = lane >> 5, ch = lane & 31;
     const int Hkv = p.Hkv;
-    const int* bt = p.block_table + (size_t)p.tok_seq[t] * p.max_blocks;
+    const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
+    const int* __restrict__ bt = block_table + (size_t)seq * p.max_blocks;
     const float sl2 = p.scale * LOG2E;
 
     uint4 qr[G][2];
@@ -122,14 +130,14 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, WaveLds<G>& 
 #pragma unroll
         for (int pp = 0; pp < 4; pp++) {
             const uint16_t* r = kp + (size_t)(4 * pp + rho) * row_elems;
-            kb[pp][0] = *reinterpret_cast<const uint4*>(r);
-            kb[pp][1] = *reinterpret_cast<const uint4*>(r + 128);
+            kb[pp][0] = load_nt(r);
+            kb[pp][1] = load_nt(r + 128);
         }
     };
     auto load_v = [&](size_t base) {
         const uint16_t* vp = p.vc + base + 8 * ch + (size_t)(8 * hv) * row_elems;
 #pragma unroll
-        for (int k = 0; k < 8; k++) vb[k] = *reinterpret_cast<const uint4*>(vp + (size_t)k * row_elems);
+        for (int k = 0; k < 8; k++) vb[k] = load_nt(vp + (size_t)k * row_elems);
     };
 
     float m = -INFINITY, l = 0.f;
@@ -140,18 +148,19 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, WaveLds<G>& 
         for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
 
     const int pg0 = j0 / PAGE, pg1 = (j1 - 1) / PAGE;
-    size_t base = page_base(pg0);
-    load_k(base);
-    load_v(base);
-    for (int pi = pg0; pi <= pg1; pi++) {
-        const size_t next = pi < pg1 ? page_base(pi + 1) : base;
+    // One page: q.k, softmax, P.V. With PREFETCH the next page's K is
+    // requested right after q.k and its V right after P.V; the last page is
+    // peeled off so the loop body always prefetches and the compiler keeps
+    // the loads in flight across iterations (partial vmcnt waits).
+    auto page = [&](int pi, size_t next, auto prefetch) {
+        constexpr bool PREFETCH = decltype(prefetch)::value;
         // q . k partials: v[pp * 4 + g] over this lane's 16 dims.
         float v[16];
 #pragma unroll
         for (int pp = 0; pp < 4; pp++)
 #pragma unroll
             for (int g = 0; g < G; g++) v[pp * 4 + g] = dot8(qr[g][1], kb[pp][1], dot8(qr[g][0], kb[pp][0], 0.f));
-        if (pi < pg1) load_k(next);
+        if constexpr (PREFETCH) load_k(next);
         // Reduce-scatter across the row's 16 lanes: after the step on lane
         // bit b the lane keeps the half of its values selected by that bit.
         {
@@ -216,9 +225,15 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, WaveLds<G>& 
             }
         }
         wave_sync();  // lds.p / lds.c are rewritten for the next page
-        if (pi < pg1) load_v(next);
-        base = next;
+        if constexpr (PREFETCH) load_v(next);
+    };
+    {
+        const size_t base = page_base(pg0);
+        load_k(base);
+        load_v(base);
     }
+    for (int pi = pg0; pi < pg1; pi++) page(pi, page_base(pi + 1), std::true_type{});
+    page(pg1, 0, std::false_type{});
     // Totals: the sum over the head's 16 lanes, the two halves' values.
     l += dpp<DPP_ROW_ROR4>(l);
     l += dpp<DPP_ROW_ROR8>(l);
@@ -266,7 +281,10 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, WaveLds<G>& 
 // One workgroup per key range and group of up to 4 kv heads (blockIdx.y),
 // a wave per kv head (see the file comment).
 template <int G>
-__global__ void __launch_bounds__(256, 2) decode_split_kernel(DecodeParams p) {
+__global__ void __launch_bounds__(256, 2)
+    decode_split_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
+                        const int* __restrict__ block_table, const int* __restrict__ cu,
+                        const int* __restrict__ outs) {
     __shared__ int sh_scan[16];
     __shared__ int sh_t0[2];
     __shared__ WaveLds<G> sh_w[4];
@@ -275,11 +293,12 @@ __global__ void __launch_bounds__(256, 2) decode_split_kernel(DecodeParams p) {
     int W = 0;
     for (int base = 0; base < T; base += nthr) {
         const int t = base + tid;
-        const int L = t < T ? decode_len(t, p.pos, p.tok_seq, p.cu, p.skip_prompts, p.outs, p.spec) : 0;
+        const int L = t < T ? decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec) : 0;
         int tot;
         block_scan(L, sh_scan, tot);
         W += tot;
     }
+    W = __builtin_amdgcn_readfirstlane(W);  // block-uniform: keep it in scalar registers
     const int R = max(p.min_range, (W + p.n_wg - 1) / p.n_wg);
     const int start = b * R, end = min(W, start + R);
     if (b == 0 && tid == 0) {
@@ -292,7 +311,7 @@ __global__ void __launch_bounds__(256, 2) decode_split_kernel(DecodeParams p) {
     int run = 0;
     for (int base = 0; base < T; base += nthr) {
         const int t = base + tid;
-        const int L = t < T ? decode_len(t, p.pos, p.tok_seq, p.cu, p.skip_prompts, p.outs, p.spec) : 0;
+        const int L = t < T ? decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec) : 0;
         int tot;
         const int off = run + block_scan(L, sh_scan, tot);
         if (t < T) {
@@ -308,14 +327,14 @@ __global__ void __launch_bounds__(256, 2) decode_split_kernel(DecodeParams p) {
     if (start >= W) return;
     __syncthreads();
     // Kv heads 4 y .. 4 y + 3, one per wave.
-    const int wave = tid >> 6, kvh = blockIdx.y * 4 + wave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = blockIdx.y * 4 + wave;
     if (kvh >= p.Hkv) return;
-    int t = sh_t0[0], off = sh_t0[1];
+    int t = __builtin_amdgcn_readfirstlane(sh_t0[0]), off = __builtin_amdgcn_readfirstlane(sh_t0[1]);
     while (off < end && t < T) {
-        const int L = decode_len(t, p.pos, p.tok_seq, p.cu, p.skip_prompts, p.outs, p.spec);
+        const int L = decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec);
         if (L > 0) {
             const int j0 = max(start, off) - off, j1 = min(end, off + L) - off;
-            decode_piece<G>(p, sh_w[wave], t, kvh, j0, j1, L, t + b);
+            decode_piece<G>(p, tok_seq, block_table, sh_w[wave], t, kvh, j0, j1, L, t + b);
             off += L;
         }
         t++;
@@ -324,7 +343,9 @@ __global__ void __launch_bounds__(256, 2) decode_split_kernel(DecodeParams p) {
 
 // Combines the partials of tokens split over several ranges, in key order,
 // then gates like the reference (rbf(A / S) * sigmoid(gate), qwen35.cu:2255-2273).
-// One block per token; a wave per query head at a time, 4 dims per lane.
+// One block per (token, 4 query heads), a wave per head, 4 dims per lane:
+// the maximum over the partials is taken 64 partials at a time across the
+// lanes, then the weighted sums stream the partials 4 at a time.
 __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
     const int t = blockIdx.x, T = p.T;
     const int o0 = p.offs[t], o1 = p.offs[t + 1];  // offs[T] = W
@@ -332,33 +353,57 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
     const int R = p.offs[T + 1];
     const int b0 = o0 / R, b1 = (o1 - 1) / R;
     if (b0 == b1) return;  // finished in place by its range
-    const int lane = threadIdx.x & 63, d = 4 * lane;
-    for (int h = threadIdx.x >> 6; h < p.Hq; h += blockDim.x >> 6) {
-        float M = -INFINITY;
-        for (int b = b0; b <= b1; b++) M = fmaxf(M, p.part_ms[((size_t)(t + b) * p.Hq + h) * 2]);
-        float S = 0.f, A[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int b = b0; b <= b1; b++) {
-            const size_t at = (size_t)(t + b) * p.Hq + h;
-            const float2 ms = *reinterpret_cast<const float2*>(p.part_ms + at * 2);
-            const float f = ms.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms.x - M);
-            S += ms.y * f;
-            const float4 a = *reinterpret_cast<const float4*>(p.part_acc + at * HEAD_DIM + d);
-            A[0] += a.x * f;
-            A[1] += a.y * f;
-            A[2] += a.z * f;
-            A[3] += a.w * f;
+    const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (h >= p.Hq) return;
+    const int lane = threadIdx.x & 63, d = 4 * lane, n = b1 - b0 + 1;
+    const float* ms = p.part_ms + ((size_t)(t + b0) * p.Hq + h) * 2;
+    const float* acc = p.part_acc + ((size_t)(t + b0) * p.Hq + h) * HEAD_DIM + d;
+    const size_t step = (size_t)p.Hq;  // partial b + 1 is Hq rows further
+    float M = -INFINITY;
+    for (int i = lane; i < n; i += 64) M = fmaxf(M, ms[i * step * 2]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    float S = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+        float2 m4[4];
+        float4 a4[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            m4[u] = *reinterpret_cast<const float2*>(ms + (i + u) * step * 2);
+            a4[u] = *reinterpret_cast<const float4*>(acc + (i + u) * step * HEAD_DIM);
         }
-        const float inv = 1.f / S;
-        const uint2 graw =
-            *reinterpret_cast<const uint2*>(p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d);
-        const float y0 = rbf(A[0] * inv) / (1.f + __expf(-bf_lo(graw.x)));
-        const float y1 = rbf(A[1] * inv) / (1.f + __expf(-bf_hi(graw.x)));
-        const float y2 = rbf(A[2] * inv) / (1.f + __expf(-bf_lo(graw.y)));
-        const float y3 = rbf(A[3] * inv) / (1.f + __expf(-bf_hi(graw.y)));
-        *reinterpret_cast<uint2*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + d) = make_uint2(pack2(y0, y1), pack2(y2, y3));
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float f = m4[u].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m4[u].x - M);
+            S += m4[u].y * f;
+            A0 += a4[u].x * f;
+            A1 += a4[u].y * f;
+            A2 += a4[u].z * f;
+            A3 += a4[u].w * f;
+        }
     }
+    for (; i < n; i++) {
+        const float2 m = *reinterpret_cast<const float2*>(ms + i * step * 2);
+        const float4 a = *reinterpret_cast<const float4*>(acc + i * step * HEAD_DIM);
+        const float f = m.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m.x - M);
+        S += m.y * f;
+        A0 += a.x * f;
+        A1 += a.y * f;
+        A2 += a.z * f;
+        A3 += a.w * f;
+    }
+    const float inv = 1.f / S;
+    const uint2 graw =
+        *reinterpret_cast<const uint2*>(p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d);
+    const float y0 = rbf(A0 * inv) / (1.f + __expf(-bf_lo(graw.x)));
+    const float y1 = rbf(A1 * inv) / (1.f + __expf(-bf_hi(graw.x)));
+    const float y2 = rbf(A2 * inv) / (1.f + __expf(-bf_lo(graw.y)));
+    const float y3 = rbf(A3 * inv) / (1.f + __expf(-bf_hi(graw.y)));
+    *reinterpret_cast<uint2*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + d) = make_uint2(pack2(y0, y1), pack2(y2, y3));
 }
 
-template __global__ void decode_split_kernel<4>(DecodeParams);
+template __global__ void decode_split_kernel<4>(DecodeParams, const int*, const int*, const int*, const int*,
+                                                const int*);
 
 }  // namespace pkv

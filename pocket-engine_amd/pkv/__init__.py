@@ -114,7 +114,7 @@ def attn_decode_workspace(T, Hq):
     return n.value
 
 
-def attn_decode_config(wg_per_cu=2, min_range=32):
+def attn_decode_config(wg_per_cu=1, min_range=32):
     _check(_lib.pkv_attn_decode_config(wg_per_cu, min_range), "pkv_attn_decode_config")
 
 

@@ -49,9 +49,9 @@ def run_oracle(c, **kw):
 
 @pytest.fixture(autouse=True)
 def default_config():
-    pkv.attn_decode_config(2, 32)
+    pkv.attn_decode_config(1, 32)
     yield
-    pkv.attn_decode_config(2, 32)
+    pkv.attn_decode_config(1, 32)
 
 
 @pytest.mark.parametrize("lens,Hkv,seed", [
