@@ -39,6 +39,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--wg-per-cu", type=int, default=None)
     ap.add_argument("--min-range", type=int, default=None)
+    ap.add_argument("--graph", action="store_true", help="replay each step from a captured HIP graph")
+    ap.add_argument("--unfused", action="store_true",
+                    help="append, key ranges and merge as three launches instead of the fused step")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the paged KV path shards by "
@@ -84,21 +87,41 @@ def main():
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
 
+
+    def step_on(i, strm):
+        s_ = strm.cuda_stream
+        if args.unfused:
+            pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=s_)
+            pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu,
+                            0, None, 1, B, pages, ws, stream=s_)
+        else:
+            pkv.attn_decode_step(k_rows, v_rows, qstride * 2, slot_d[i], q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts,
+                                 bt, meta.max_blocks, BS, out, 1 / 16, cu, 0, None, 1, B, pages, ws, stream=s_)
+
     def step(i, ev=None):
-        pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=sp)
-        if ev:
-            ev[0].record(stream)
-        pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu, 0,
-                        None, 1, B, pages, ws, stream=sp, phase="split")
-        if ev:
-            ev[1].record(stream)
-        pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu, 0,
-                        None, 1, B, pages, ws, stream=sp, phase="merge")
+        if args.unfused:
+            pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=sp)
+            if ev:
+                ev[0].record(stream)
+            pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu,
+                            0, None, 1, B, pages, ws, stream=sp, phase="split")
+            if ev:
+                ev[1].record(stream)
+            pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu,
+                            0, None, 1, B, pages, ws, stream=sp, phase="merge")
+        else:
+            if ev:
+                ev[0].record(stream)
+            pkv.attn_decode_step(k_rows, v_rows, qstride * 2, slot_d[i], q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts,
+                                 bt, meta.max_blocks, BS, out, 1 / 16, cu, 0, None, 1, B, pages, ws, stream=sp)
+            if ev:
+                ev[1].record(stream)
 
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    # Timed region: K steps; events bracket the key-range kernel of each step.
+    # Timed region: K steps; events bracket the dominant kernel of each step
+    # (the fused step kernel, or the key-range kernel with --unfused).
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -108,18 +131,46 @@ def main():
     t1.record(stream)
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
-    split_ms = [a.elapsed_time(b) for a, b in evs]
+    kern_ms = [a.elapsed_time(b) for a, b in evs]
     ms_step = total_ms / args.steps
+
+    graph_us = None
+    if args.graph:
+        # The same K steps captured into one HIP graph and replayed: the
+        # device time without per-launch dispatch gaps (the reference engine
+        # replays a captured graph per step, src/engine.rs:704-720).
+        g = torch.cuda.CUDAGraph()
+        cs = torch.cuda.Stream()
+        cs.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cs):
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=cs):
+                for k in range(args.steps):
+                    step_on(args.warmup + k, cs)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g0.record(stream)
+        g.replay()
+        g1.record(stream)
+        torch.cuda.synchronize()
+        graph_us = 1e3 * g0.elapsed_time(g1) / args.steps
 
     keys = [meta.keys(args.warmup + k) for k in range(args.steps)]
     step_bytes = [synth.algorithmic_bytes_decode(kk, B, Hq, Hkv) + synth.algorithmic_bytes_append(B, Hkv)
                   for kk in keys]
     gbs = sum(step_bytes) / (total_ms * 1e-3) / 1e9
-    # Dominant kernel: bytes it must read = every key's K and V rows (all kv
-    # heads) + q; its partials are overhead, not algorithmic.
-    split_bytes = [kk * Hkv * D * 2 * 2 + B * Hq * D * 2 for kk in keys]
-    split_avg_us = 1e3 * sum(split_ms) / len(split_ms)
-    split_gbs = sum(split_bytes) / (sum(split_ms) * 1e-3) / 1e9
+    if args.unfused:
+        # key-range kernel: every key's K and V rows (all kv heads) + q; its
+        # partials are overhead, not algorithmic.
+        kern_bytes = [kk * Hkv * D * 2 * 2 + B * Hq * D * 2 for kk in keys]
+        kname = "decode_range_kernel<4,false>"
+    else:
+        kern_bytes = step_bytes  # the fused kernel does the whole step
+        kname = "decode_range_kernel<4,true> (fused append + attention + merge)"
+    kern_avg_us = 1e3 * sum(kern_ms) / len(kern_ms)
+    kern_gbs = sum(kern_bytes) / (sum(kern_ms) * 1e-3) / 1e9
 
     cpu = None
     if not args.no_cpu:
@@ -135,18 +186,20 @@ def main():
         "ms_per_step": round(ms_step, 5),
         "us_per_step": round(ms_step * 1e3, 2),
         "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "us_per_step_graph": None if graph_us is None else round(graph_us, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1)*0.5 K/V/q, U[512,8192] contexts)",
         "config": {"workload": "c3: batch-64 paged decode step (append 1 token/seq + paged decode attention)",
+                   "path": "unfused (append, key ranges, merge)" if args.unfused else "fused step (one launch)",
                    "batch": B, "ctx": "U[512,8192]", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
                    "pool_pages": pages, "seed": seed, "mean_keys_per_step": round(float(np.mean(keys)), 1),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "decode_split_kernel", "achieved": round(split_gbs, 1),
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(split_gbs / PEAK_HBM_GBS, 4),
-                     "avg_us": round(split_avg_us, 2), "traffic": None},
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(kern_gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
+                     "avg_us": round(kern_avg_us, 2), "traffic": None},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

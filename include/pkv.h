@@ -119,10 +119,30 @@ int pkv_attn_decode_merge(const void* q, const void* kcache, const void* vcache,
                           int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Fused decode step: KV append + paged decode attention in two launches
+ * (the key-range kernel appends the step's rows itself, then the merge).
+ * Same result as pkv_append(k_rows, v_rows, row_stride, slot_map, T, Hkv,
+ * 512, kcache, vcache, num_blocks * 16) followed by pkv_attn_decode(...) —
+ * the reference's attn_prep cache stores followed by attn_paged_g<G> +
+ * attn_merge (src/model.rs:2340-2437) — provided the step's metadata is the
+ * scheduler's (src/sched.rs:1105-1115): each sequence's tokens of the step
+ * are consecutive rows cu[s] .. cu[s+1]-1 at consecutive positions and
+ * slot_map[t] is the slot of pos[t]. Keys at positions the step itself feeds
+ * are read from k_rows/v_rows; the step's rows are written to the pools.
+ * `cu` is required. row_stride is in bytes (a multiple of 16). No
+ * reference counterpart as one call: it saves the append launch. */
+int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map,
+                         const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
+                         int Hkv, const int32_t* pos, const int32_t* tok_seq, const int32_t* block_table,
+                         int max_blocks, int block_size, void* out, float scale, const int32_t* cu,
+                         int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
 /* Tuning: key-range workgroups per CU (default 1) and fewest keys per range
  * (default 32). Process-wide; takes effect for later calls (workspace sizes
  * follow). */
 int pkv_attn_decode_config(int wg_per_cu, int min_range);
+
 
 /* ---------------------------------------------------------------------------
  * Host: block allocator (reference Scheduler.free_blocks / block_refs,

@@ -46,6 +46,7 @@ int decode_n_wg() { return device_cus() * g_wg_per_cu; }
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Workspace: [offs: T + 2 ints][part_ms][part_acc].
 struct DecodeLayout {
     size_t offs, ms, acc, total;
 };
@@ -122,6 +123,7 @@ int pkv_attn_decode_config(int wg_per_cu, int min_range) {
     return PKV_OK;
 }
 
+
 int pkv_attn_decode_workspace(int T, int Hq, size_t* bytes) {
     if (T < 0 || Hq <= 0 || !bytes) return PKV_ERR_INVALID;
     *bytes = decode_layout(T, Hq, decode_n_wg()).total;
@@ -132,14 +134,23 @@ int pkv_attn_decode_workspace(int T, int Hq, size_t* bytes) {
 
 namespace {
 
-// phase bit 1: key-range kernel; bit 2: merge kernel.
-int attn_decode_phases(int phases, const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride,
-                       int Hq, int Hkv, const int32_t* pos, const int32_t* tok_seq, const int32_t* block_table,
-                       int max_blocks, int block_size, void* out, float scale, const int32_t* cu, int skip_prompts,
-                       const int32_t* outs, int spec, int T, int64_t num_blocks, void* workspace,
-                       size_t workspace_bytes, void* stream) {
+struct AppendArgs {
+    const void* k_rows;
+    const void* v_rows;
+    int64_t row_stride;  // bytes
+    const int32_t* slot_map;
+};
+
+// phase bit 1: key-range kernel; bit 2: merge kernel; bit 4: the key-range
+// kernel with the step's append fused in (needs `app`).
+int attn_decode_phases(int phases, const AppendArgs* app, const void* q, const void* kcache, const void* vcache,
+                       const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos, const int32_t* tok_seq,
+                       const int32_t* block_table, int max_blocks, int block_size, void* out, float scale,
+                       const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
+                       void* workspace, size_t workspace_bytes, void* stream) {
     if (T < 0 || Hq <= 0 || Hkv <= 0 || max_blocks <= 0 || num_blocks <= 0 || spec < 1) return PKV_ERR_INVALID;
-    if (Hq != 4 * Hkv || block_size != 16) return PKV_ERR_UNSUPPORTED;
+    if (Hq != 4 * Hkv || block_size != 16 || (Hkv > 4 && Hkv % 4 != 0)) return PKV_ERR_UNSUPPORTED;
+    if (num_blocks > (int64_t)INT32_MAX / 16) return PKV_ERR_INVALID;
     if (T == 0) return PKV_OK;
     if (!q || !kcache || !vcache || !qkv || !pos || !tok_seq || !block_table || !out || !workspace)
         return PKV_ERR_INVALID;
@@ -148,26 +159,28 @@ int attn_decode_phases(int phases, const void* q, const void* kcache, const void
     if (!aligned(q, 16) || !aligned(kcache, 16) || !aligned(vcache, 16) || !aligned(qkv, 16) || !aligned(out, 16) ||
         !aligned(workspace, 256))
         return PKV_ERR_INVALID;
+    const int groups = (Hkv + 3) / 4, threads = 64 * std::min(Hkv, 4);
+    if (phases & 4) {
+        if (!app || !app->k_rows || !app->v_rows || !app->slot_map || !cu) return PKV_ERR_INVALID;
+        if (!aligned(app->k_rows, 16) || !aligned(app->v_rows, 16) || app->row_stride % 16 != 0 ||
+            app->row_stride < (int64_t)Hkv * pkv::HEAD_DIM * 2)
+            return PKV_ERR_INVALID;
+    }
     const int n_wg = decode_n_wg();
     const DecodeLayout lay = decode_layout(T, Hq, n_wg);
     if (workspace_bytes < lay.total) return PKV_ERR_INVALID;
     pkv::DecodeParams p;
     p.q = (const uint16_t*)q;
-    p.kc = (const uint16_t*)kcache;
-    p.vc = (const uint16_t*)vcache;
+    p.kc = (uint16_t*)kcache;
+    p.vc = (uint16_t*)vcache;
     p.qkv = (const uint16_t*)qkv;
     p.qstride = qstride;
     p.Hq = Hq;
     p.Hkv = Hkv;
-    p.pos = pos;
-    p.tok_seq = tok_seq;
-    p.block_table = block_table;
     p.max_blocks = max_blocks;
     p.out = (uint16_t*)out;
     p.scale = scale;
-    p.cu = cu;
     p.skip_prompts = skip_prompts;
-    p.outs = outs;
     p.spec = spec;
     p.T = T;
     p.num_blocks = (long)num_blocks;
@@ -177,10 +190,18 @@ int attn_decode_phases(int phases, const void* q, const void* kcache, const void
     p.part_acc = (float*)(ws + lay.acc);
     p.n_wg = n_wg;
     p.min_range = g_min_range;
-    const int groups = (Hkv + 3) / 4, threads = 64 * std::min(Hkv, 4);
-    if (phases & 1) {
-        hipLaunchKernelGGL(pkv::decode_split_kernel<4>, dim3(n_wg, groups), dim3(threads), 0, (hipStream_t)stream, p, pos,
-                           tok_seq, block_table, cu, outs);
+    p.k_rows = app ? (const uint16_t*)app->k_rows : nullptr;
+    p.v_rows = app ? (const uint16_t*)app->v_rows : nullptr;
+    p.row_stride = app ? (long)(app->row_stride / 2) : 0;
+    const int32_t* slot_map = app ? app->slot_map : nullptr;
+    if (phases & 4) {
+        hipLaunchKernelGGL((pkv::decode_range_kernel<4, true>), dim3(n_wg, groups), dim3(threads), 0,
+                           (hipStream_t)stream, p, pos, tok_seq, block_table, cu, outs, slot_map);
+        const int st = launch_status();
+        if (st != PKV_OK) return st;
+    } else if (phases & 1) {
+        hipLaunchKernelGGL((pkv::decode_range_kernel<4, false>), dim3(n_wg, groups), dim3(threads), 0,
+                           (hipStream_t)stream, p, pos, tok_seq, block_table, cu, outs, slot_map);
         const int st = launch_status();
         if (st != PKV_OK) return st;
     }
@@ -204,8 +225,14 @@ extern "C" {
     q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, out, scale, cu,  \
         skip_prompts, outs, spec, T, num_blocks, workspace, workspace_bytes, stream
 
-int pkv_attn_decode(PKV_DECODE_ARGS) { return attn_decode_phases(3, PKV_DECODE_PASS); }
-int pkv_attn_decode_split(PKV_DECODE_ARGS) { return attn_decode_phases(1, PKV_DECODE_PASS); }
-int pkv_attn_decode_merge(PKV_DECODE_ARGS) { return attn_decode_phases(2, PKV_DECODE_PASS); }
+int pkv_attn_decode(PKV_DECODE_ARGS) { return attn_decode_phases(3, nullptr, PKV_DECODE_PASS); }
+int pkv_attn_decode_split(PKV_DECODE_ARGS) { return attn_decode_phases(1, nullptr, PKV_DECODE_PASS); }
+int pkv_attn_decode_merge(PKV_DECODE_ARGS) { return attn_decode_phases(2, nullptr, PKV_DECODE_PASS); }
+
+int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map,
+                         PKV_DECODE_ARGS) {
+    const AppendArgs app{k_rows, v_rows, row_stride, slot_map};
+    return attn_decode_phases(4 | 2, &app, PKV_DECODE_PASS);
+}
 
 }  // extern "C"

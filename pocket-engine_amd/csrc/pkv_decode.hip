@@ -5,15 +5,15 @@
 //
 // Work split ("flattened key space"). The keys of every decode token are
 // laid end to end: token t owns [offs[t], offs[t] + L_t), L_t = pos[t] + 1.
-// The W keys are cut into n_active equal ranges of R keys (R >= min_range),
-// one per workgroup, whatever the length mix: every workgroup streams the
-// same number of bytes, so a batch of 512..8192-token contexts balances
-// without a work queue. A range crossing token boundaries handles each token
-// piece in turn. A token whose keys all fall in one range is finished in
-// place (gated output); otherwise each piece leaves a partial (max, sum,
-// weighted values) at index t + b (b = range index; t + b strictly grows
-// along the walk, so it is unique and below T + n_wg) and decode_merge
-// combines them in key order.
+// The W keys are cut into equal ranges of R keys (R >= min_range), one per
+// workgroup, whatever the length mix: every workgroup streams the same
+// number of bytes, so a batch of 512..8192-token contexts balances without a
+// work queue. A range crossing token boundaries handles each token piece in
+// turn. A token whose keys all fall in one range is finished in place (gated
+// output); otherwise each piece leaves a partial (max, sum, weighted values)
+// at index t + b (b = range index; t + b strictly grows along the walk, so it
+// is unique and below T + n_wg), combined in key order by decode_merge_kernel
+// (the same for the fused step).
 //
 // Inside a workgroup wave w takes kv head w, so one page read serves the G
 // query heads of the group and the workgroup as a whole reads whole slot rows
@@ -29,29 +29,35 @@
 //   V: lane (half h = lane / 32, chunk c = lane % 32) loads keys 8h .. 8h + 7,
 //      dims 8c .. 8c + 7 (16 bytes each: a full 512-byte row per half-wave);
 //      probabilities reach it through 272 bytes of LDS; 256 FMAs per lane.
-// The next page's K is requested right after q.k and its V right after P.V,
-// so one page (16 KiB) is always in flight per wave. No MFMA is used.
+// K/V loads are nontemporal (read once). The next page's K is requested
+// right after q.k and its V right after P.V, so one page (16 KiB) is always
+// in flight per wave; page ids come through the scalar cache. No MFMA.
+//
+// Fused append (decode_range_kernel<G, true>): the same kernel also appends
+// the step's new K/V rows to their slots and reads every key of the step's
+// own tokens (positions >= the first position the sequence feeds this step)
+// from those source rows instead of the cache, so no range waits for another
+// range's write. (Merging inside the kernel as well would need agent-scope
+// release/acquire fences per token piece, an L2 writeback and invalidate on
+// this multi-XCD part; measured at +45 us per batch-64 step, so the merge
+// stays a second launch.)
 #include "pkv_common.h"
 
+#include <climits>
 #include <type_traits>
 
 namespace pkv {
 
 struct DecodeParams {
     const uint16_t* q;        // [T][Hq][256]
-    const uint16_t* kc;       // [pages * 16][Hkv][256]
-    const uint16_t* vc;
+    uint16_t* kc;             // [pages * 16][Hkv][256]
+    uint16_t* vc;
     const uint16_t* qkv;      // gate of head h at row t: qkv[t * qstride + h * 512 + 256 ..]
     int qstride, Hq, Hkv;
-    const int* pos;
-    const int* tok_seq;
-    const int* block_table;   // [seqs][max_blocks]
     int max_blocks;
     uint16_t* out;            // [T][Hq][256]
     float scale;
-    const int* cu;
     int skip_prompts;
-    const int* outs;
     int spec;
     int T;
     long num_blocks;
@@ -59,6 +65,10 @@ struct DecodeParams {
     float* part_ms;           // [(T + n_wg) * Hq][2]: max (log2 units), sum
     float* part_acc;          // [(T + n_wg) * Hq][256]
     int n_wg, min_range;
+    // fused step: the step's new rows (k_rows + t * row_stride, Hkv * 256 each)
+    const uint16_t* k_rows;
+    const uint16_t* v_rows;
+    long row_stride;          // elements
 };
 
 constexpr int PAGE = 16;
@@ -94,21 +104,83 @@ struct WaveLds {
     float ml[2 * G];    // final (max, sum) per head
 };
 
-// One wave: token t, kv head kvh, keys [j0, j1) of its sequence.
-// Read-only step metadata, passed as separate __restrict__ kernel arguments
-// so the compiler may read it through the scalar cache (uniform s_load):
-// no store of the kernel can alias it.
+// Gated output of 4 dims: y = bf16(rbf(a * inv) * sigmoid(gate)) (reference
+// qwen35.cu:1290-1293).
+__device__ __forceinline__ uint2 gate4(float a0, float a1, float a2, float a3, float inv, uint2 graw) {
+    const float y0 = rbf(a0 * inv) / (1.f + __expf(-bf_lo(graw.x)));
+    const float y1 = rbf(a1 * inv) / (1.f + __expf(-bf_hi(graw.x)));
+    const float y2 = rbf(a2 * inv) / (1.f + __expf(-bf_lo(graw.y)));
+    const float y3 = rbf(a3 * inv) / (1.f + __expf(-bf_hi(graw.y)));
+    return make_uint2(pack2(y0, y1), pack2(y2, y3));
+}
 
-template <int G>
-__device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* __restrict__ tok_seq,
-                                             const int* __restrict__ block_table, WaveLds<G>& lds, int t, int kvh,
-                                             int j0, int j1, int L, int idx) {
+// Combines the n partials of token t (indices t + b0 .. t + b0 + n - 1) for
+// query heads [h0, h1), a wave per head at a time and 4 dims per lane: the
+// maximum over the partials is taken 64 at a time across the lanes, then the
+// weighted sums stream the partials 4 at a time (reference attn_merge,
+// qwen35.cu:2255-2273, in exp2 units).
+__device__ __forceinline__ void merge_token(const DecodeParams& p, int t, int b0, int n, int h0, int h1) {
+    const int lane = threadIdx.x & 63, d = 4 * lane;
+    for (int h = h0 + (threadIdx.x >> 6); h < h1; h += blockDim.x >> 6) {
+        const float* ms = p.part_ms + ((size_t)(t + b0) * p.Hq + h) * 2;
+        const float* acc = p.part_acc + ((size_t)(t + b0) * p.Hq + h) * HEAD_DIM + d;
+        const size_t step = (size_t)p.Hq;  // partial i + 1 is Hq rows further
+        float M = -INFINITY;
+        for (int i = lane; i < n; i += 64) M = fmaxf(M, ms[i * step * 2]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        float S = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
+        int i = 0;
+        for (; i + 4 <= n; i += 4) {
+            float2 m4[4];
+            float4 a4[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                m4[u] = *reinterpret_cast<const float2*>(ms + (i + u) * step * 2);
+                a4[u] = *reinterpret_cast<const float4*>(acc + (i + u) * step * HEAD_DIM);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float f = m4[u].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m4[u].x - M);
+                S += m4[u].y * f;
+                A0 += a4[u].x * f;
+                A1 += a4[u].y * f;
+                A2 += a4[u].z * f;
+                A3 += a4[u].w * f;
+            }
+        }
+        for (; i < n; i++) {
+            const float2 m = *reinterpret_cast<const float2*>(ms + i * step * 2);
+            const float4 a = *reinterpret_cast<const float4*>(acc + i * step * HEAD_DIM);
+            const float f = m.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m.x - M);
+            S += m.y * f;
+            A0 += a.x * f;
+            A1 += a.y * f;
+            A2 += a.z * f;
+            A3 += a.w * f;
+        }
+        const uint2 graw =
+            *reinterpret_cast<const uint2*>(p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d);
+        *reinterpret_cast<uint2*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + d) = gate4(A0, A1, A2, A3, 1.f / S, graw);
+    }
+}
+
+// One wave: token t, kv head kvh, keys [j0, j1) of its sequence. With FRESH,
+// keys at positions [P0, L) come from the step's source rows (row
+// row0 + position - P0) instead of the cache. The metadata pointers arrive as
+// __restrict__ kernel arguments so the compiler reads them with scalar loads
+// (no store of the kernel aliases them).
+// FUSED: pages holding keys the step itself feeds (from the page of
+// position P0 on) choose every K/V address per lane between the cache and
+// the source rows (no branch, so the loads stay pipelined); earlier pages of
+// the piece take the plain path.
+template <int G, bool FUSED>
+__device__ __forceinline__ void piece_body(const DecodeParams& p, const int* __restrict__ bt, WaveLds<G>& lds,
+                                           int t, int kvh, int j0, int j1, int L, int idx, int P0, int row0) {
     static_assert(G == 4, "lane mapping assumes 4 keys x 4 heads per lane");
     const int lane = threadIdx.x & 63, sig = lane & 15, rho = lane >> 4;
     const int hv = lane >> 5, ch = lane & 31;
     const int Hkv = p.Hkv;
-    const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
-    const int* __restrict__ bt = block_table + (size_t)seq * p.max_blocks;
     const float sl2 = p.scale * LOG2E;
 
     uint4 qr[G][2];
@@ -124,21 +196,36 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* _
         pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
         return (size_t)pg * PAGE * row_elems + (size_t)kvh * HEAD_DIM;
     };
+    // Address of key `key` of page pi (cache slot row, or the source row of
+    // a key this step feeds), plus `off` elements.
+    auto src = [&](const uint16_t* pool, const uint16_t* rows, int pi, size_t base, int key, int off) {
+        const int kp = pi * PAGE + key;
+        const uint16_t* c = pool + base + (size_t)key * row_elems + off;
+        const uint16_t* f = rows + (ptrdiff_t)(row0 + kp - P0) * p.row_stride + (size_t)kvh * HEAD_DIM + off;
+        return (kp >= P0 && kp < L) ? f : c;
+    };
     uint4 kb[4][2], vb[8];
-    auto load_k = [&](size_t base) {
-        const uint16_t* kp = p.kc + base + 8 * sig;
+    // MODE 1: plain cache addresses; MODE 2: per-lane cache / source rows.
+    auto load_k = [&](int pi, size_t base, auto mode) {
+        constexpr bool FRESH = decltype(mode)::value == 2;
 #pragma unroll
         for (int pp = 0; pp < 4; pp++) {
-            const uint16_t* r = kp + (size_t)(4 * pp + rho) * row_elems;
+            const uint16_t* r = FRESH ? src(p.kc, p.k_rows, pi, base, 4 * pp + rho, 8 * sig)
+                                      : p.kc + base + 8 * sig + (size_t)(4 * pp + rho) * row_elems;
             kb[pp][0] = load_nt(r);
             kb[pp][1] = load_nt(r + 128);
         }
     };
-    auto load_v = [&](size_t base) {
-        const uint16_t* vp = p.vc + base + 8 * ch + (size_t)(8 * hv) * row_elems;
+    auto load_v = [&](int pi, size_t base, auto mode) {
+        constexpr bool FRESH = decltype(mode)::value == 2;
 #pragma unroll
-        for (int k = 0; k < 8; k++) vb[k] = load_nt(vp + (size_t)k * row_elems);
+        for (int k = 0; k < 8; k++)
+            vb[k] = load_nt(FRESH ? src(p.vc, p.v_rows, pi, base, 8 * hv + k, 8 * ch)
+                                  : p.vc + base + 8 * ch + (size_t)(8 * hv + k) * row_elems);
     };
+    using NONE = std::integral_constant<int, 0>;
+    using PLAIN = std::integral_constant<int, 1>;
+    using FRESHM = std::integral_constant<int, 2>;
 
     float m = -INFINITY, l = 0.f;
     float acc[G][8];
@@ -152,15 +239,15 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* _
     // requested right after q.k and its V right after P.V; the last page is
     // peeled off so the loop body always prefetches and the compiler keeps
     // the loads in flight across iterations (partial vmcnt waits).
-    auto page = [&](int pi, size_t next, auto prefetch) {
-        constexpr bool PREFETCH = decltype(prefetch)::value;
+    auto page = [&](int pi, int next_pi, size_t next, auto prefetch) {
+        constexpr bool PREFETCH = decltype(prefetch)::value != 0;
         // q . k partials: v[pp * 4 + g] over this lane's 16 dims.
         float v[16];
 #pragma unroll
         for (int pp = 0; pp < 4; pp++)
 #pragma unroll
             for (int g = 0; g < G; g++) v[pp * 4 + g] = dot8(qr[g][1], kb[pp][1], dot8(qr[g][0], kb[pp][0], 0.f));
-        if constexpr (PREFETCH) load_k(next);
+        if constexpr (PREFETCH) load_k(next_pi, next, prefetch);
         // Reduce-scatter across the row's 16 lanes: after the step on lane
         // bit b the lane keeps the half of its values selected by that bit.
         {
@@ -225,15 +312,29 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* _
             }
         }
         wave_sync();  // lds.p / lds.c are rewritten for the next page
-        if constexpr (PREFETCH) load_v(next);
+        if constexpr (PREFETCH) load_v(next_pi, next, prefetch);
     };
-    {
+    // First page holding keys of the step (none: pg1 + 1).
+    const int pf = FUSED ? max(pg0, min(pg1 + 1, P0 / PAGE)) : pg1 + 1;
+    if (pf > pg1) {
         const size_t base = page_base(pg0);
-        load_k(base);
-        load_v(base);
+        load_k(pg0, base, PLAIN{});
+        load_v(pg0, base, PLAIN{});
+        for (int pi = pg0; pi < pg1; pi++) page(pi, pi + 1, page_base(pi + 1), PLAIN{});
+    } else if constexpr (FUSED) {
+        const size_t base = page_base(pg0);
+        if (pf == pg0) {
+            load_k(pg0, base, FRESHM{});
+            load_v(pg0, base, FRESHM{});
+        } else {
+            load_k(pg0, base, PLAIN{});
+            load_v(pg0, base, PLAIN{});
+            for (int pi = pg0; pi < pf - 1; pi++) page(pi, pi + 1, page_base(pi + 1), PLAIN{});
+            page(pf - 1, pf, page_base(pf), FRESHM{});
+        }
+        for (int pi = pf; pi < pg1; pi++) page(pi, pi + 1, page_base(pi + 1), FRESHM{});
     }
-    for (int pi = pg0; pi < pg1; pi++) page(pi, page_base(pi + 1), std::true_type{});
-    page(pg1, 0, std::false_type{});
+    page(pg1, pg1, 0, NONE{});
     // Totals: the sum over the head's 16 lanes, the two halves' values.
     l += dpp<DPP_ROW_ROR4>(l);
     l += dpp<DPP_ROW_ROR8>(l);
@@ -257,16 +358,10 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* _
             const float inv = 1.f / lds.ml[2 * g + 1];
             const uint4 graw = *reinterpret_cast<const uint4*>(p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM +
                                                                HEAD_DIM + 8 * ch);
-            const uint32_t gw[4] = {graw.x, graw.y, graw.z, graw.w};
-            uint32_t o[4];
-#pragma unroll
-            for (int e2 = 0; e2 < 4; e2++) {
-                const float y0 = rbf(acc[g][2 * e2] * inv) / (1.f + __expf(-bf_lo(gw[e2])));
-                const float y1 = rbf(acc[g][2 * e2 + 1] * inv) / (1.f + __expf(-bf_hi(gw[e2])));
-                o[e2] = pack2(y0, y1);
-            }
+            const uint2 lo = gate4(acc[g][0], acc[g][1], acc[g][2], acc[g][3], inv, make_uint2(graw.x, graw.y));
+            const uint2 hi = gate4(acc[g][4], acc[g][5], acc[g][6], acc[g][7], inv, make_uint2(graw.z, graw.w));
             *reinterpret_cast<uint4*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + 8 * ch) =
-                make_uint4(o[0], o[1], o[2], o[3]);
+                make_uint4(lo.x, lo.y, hi.x, hi.y);
         } else {
             float* pa = p.part_acc + ((size_t)idx * p.Hq + h) * HEAD_DIM + 8 * ch;
             *reinterpret_cast<float4*>(pa) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
@@ -278,17 +373,52 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* _
     }
 }
 
-// One workgroup per key range and group of up to 4 kv heads (blockIdx.y),
-// a wave per kv head (see the file comment).
-template <int G>
-__global__ void __launch_bounds__(256, 2)
-    decode_split_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
+template <int G, bool FUSED>
+__device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* __restrict__ tok_seq,
+                                             const int* __restrict__ block_table, const int* __restrict__ pos,
+                                             const int* __restrict__ cu, WaveLds<G>& lds, int t, int kvh, int j0,
+                                             int j1, int L, int idx) {
+    const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
+    const int* __restrict__ bt = block_table + (size_t)seq * p.max_blocks;
+    if constexpr (FUSED) {
+        const int row0 = __builtin_amdgcn_readfirstlane(cu[seq]);
+        const int P0 = __builtin_amdgcn_readfirstlane(pos[row0]);
+        piece_body<G, true>(p, bt, lds, t, kvh, j0, j1, L, idx, P0, row0);
+    } else {
+        piece_body<G, false>(p, bt, lds, t, kvh, j0, j1, L, idx, INT_MAX, 0);
+    }
+}
+
+// Key-range kernel (FUSED = false) or fused step kernel (FUSED = true): one
+// workgroup per key range and group of up to 4 kv heads (blockIdx.y), a wave
+// per kv head. Block: 64 * min(Hkv, 4) threads (the host rejects Hkv > 4 that
+// is not a multiple of 4).
+template <int G, bool FUSED>
+__global__ void __launch_bounds__(256, 1)
+    decode_range_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                         const int* __restrict__ block_table, const int* __restrict__ cu,
-                        const int* __restrict__ outs) {
+                        const int* __restrict__ outs, const int* __restrict__ slot_map) {
     __shared__ int sh_scan[16];
     __shared__ int sh_t0[2];
     __shared__ WaveLds<G> sh_w[4];
     const int T = p.T, nthr = blockDim.x, tid = threadIdx.x, b = blockIdx.x;
+    const int nkv = nthr >> 6, kv0 = blockIdx.y * 4;
+    if constexpr (FUSED) {
+        // Append the step's rows of this block's kv heads: tokens b, b + n_wg, ..
+        // (no range reads these slots from the cache in this launch).
+        const int per_row = nkv * HEAD_DIM / 8;  // uint4 per K (or V) row slice
+        for (int t = b; t < T; t += p.n_wg) {
+            const long slot = slot_map[t];
+            if (slot < 0 || slot >= p.num_blocks * PAGE) continue;
+            for (int i = tid; i < 2 * per_row; i += nthr) {
+                const bool is_v = i >= per_row;
+                const int j = is_v ? i - per_row : i;
+                const uint16_t* s = (is_v ? p.v_rows : p.k_rows) + (size_t)t * p.row_stride + (size_t)kv0 * HEAD_DIM;
+                uint16_t* d = (is_v ? p.vc : p.kc) + ((size_t)slot * p.Hkv + kv0) * HEAD_DIM;
+                reinterpret_cast<uint4*>(d)[j] = reinterpret_cast<const uint4*>(s)[j];
+            }
+        }
+    }
     // Pass 1: total keys W.
     int W = 0;
     for (int base = 0; base < T; base += nthr) {
@@ -301,13 +431,13 @@ __global__ void __launch_bounds__(256, 2)
     W = __builtin_amdgcn_readfirstlane(W);  // block-uniform: keep it in scalar registers
     const int R = max(p.min_range, (W + p.n_wg - 1) / p.n_wg);
     const int start = b * R, end = min(W, start + R);
-    if (b == 0 && tid == 0) {
+    if (b == 0 && blockIdx.y == 0 && tid == 0) {
         p.offs[T] = W;
         p.offs[T + 1] = R;
     }
     if (start >= W && b != 0) return;
-    // Pass 2: exclusive offsets (written by block 0 for decode_merge); find
-    // the token holding key `start`.
+    // Pass 2: exclusive offsets (written by block 0 for decode_merge_kernel);
+    // find the token holding key `start`.
     int run = 0;
     for (int base = 0; base < T; base += nthr) {
         const int t = base + tid;
@@ -315,7 +445,7 @@ __global__ void __launch_bounds__(256, 2)
         int tot;
         const int off = run + block_scan(L, sh_scan, tot);
         if (t < T) {
-            if (b == 0) p.offs[t] = off;
+            if (b == 0 && blockIdx.y == 0) p.offs[t] = off;
             if (L > 0 && off <= start && start < off + L) {
                 sh_t0[0] = t;
                 sh_t0[1] = off;
@@ -326,26 +456,21 @@ __global__ void __launch_bounds__(256, 2)
     }
     if (start >= W) return;
     __syncthreads();
-    // Kv heads 4 y .. 4 y + 3, one per wave.
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = blockIdx.y * 4 + wave;
-    if (kvh >= p.Hkv) return;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = kv0 + wave;
     int t = __builtin_amdgcn_readfirstlane(sh_t0[0]), off = __builtin_amdgcn_readfirstlane(sh_t0[1]);
     while (off < end && t < T) {
         const int L = decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec);
         if (L > 0) {
             const int j0 = max(start, off) - off, j1 = min(end, off + L) - off;
-            decode_piece<G>(p, tok_seq, block_table, sh_w[wave], t, kvh, j0, j1, L, t + b);
+            decode_piece<G, FUSED>(p, tok_seq, block_table, pos, cu, sh_w[wave], t, kvh, j0, j1, L, t + b);
             off += L;
         }
         t++;
     }
 }
 
-// Combines the partials of tokens split over several ranges, in key order,
-// then gates like the reference (rbf(A / S) * sigmoid(gate), qwen35.cu:2255-2273).
-// One block per (token, 4 query heads), a wave per head, 4 dims per lane:
-// the maximum over the partials is taken 64 partials at a time across the
-// lanes, then the weighted sums stream the partials 4 at a time.
+// Combines the partials of tokens split over several ranges (after
+// decode_range_kernel<G, false>). One block per (token, 4 query heads).
 __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
     const int t = blockIdx.x, T = p.T;
     const int o0 = p.offs[t], o1 = p.offs[t + 1];  // offs[T] = W
@@ -353,57 +478,13 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
     const int R = p.offs[T + 1];
     const int b0 = o0 / R, b1 = (o1 - 1) / R;
     if (b0 == b1) return;  // finished in place by its range
-    const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (h >= p.Hq) return;
-    const int lane = threadIdx.x & 63, d = 4 * lane, n = b1 - b0 + 1;
-    const float* ms = p.part_ms + ((size_t)(t + b0) * p.Hq + h) * 2;
-    const float* acc = p.part_acc + ((size_t)(t + b0) * p.Hq + h) * HEAD_DIM + d;
-    const size_t step = (size_t)p.Hq;  // partial b + 1 is Hq rows further
-    float M = -INFINITY;
-    for (int i = lane; i < n; i += 64) M = fmaxf(M, ms[i * step * 2]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    float S = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
-    int i = 0;
-    for (; i + 4 <= n; i += 4) {
-        float2 m4[4];
-        float4 a4[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            m4[u] = *reinterpret_cast<const float2*>(ms + (i + u) * step * 2);
-            a4[u] = *reinterpret_cast<const float4*>(acc + (i + u) * step * HEAD_DIM);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const float f = m4[u].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m4[u].x - M);
-            S += m4[u].y * f;
-            A0 += a4[u].x * f;
-            A1 += a4[u].y * f;
-            A2 += a4[u].z * f;
-            A3 += a4[u].w * f;
-        }
-    }
-    for (; i < n; i++) {
-        const float2 m = *reinterpret_cast<const float2*>(ms + i * step * 2);
-        const float4 a = *reinterpret_cast<const float4*>(acc + i * step * HEAD_DIM);
-        const float f = m.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m.x - M);
-        S += m.y * f;
-        A0 += a.x * f;
-        A1 += a.y * f;
-        A2 += a.z * f;
-        A3 += a.w * f;
-    }
-    const float inv = 1.f / S;
-    const uint2 graw =
-        *reinterpret_cast<const uint2*>(p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d);
-    const float y0 = rbf(A0 * inv) / (1.f + __expf(-bf_lo(graw.x)));
-    const float y1 = rbf(A1 * inv) / (1.f + __expf(-bf_hi(graw.x)));
-    const float y2 = rbf(A2 * inv) / (1.f + __expf(-bf_lo(graw.y)));
-    const float y3 = rbf(A3 * inv) / (1.f + __expf(-bf_hi(graw.y)));
-    *reinterpret_cast<uint2*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + d) = make_uint2(pack2(y0, y1), pack2(y2, y3));
+    const int h0 = blockIdx.y * 4;
+    merge_token(p, t, b0, b1 - b0 + 1, h0, min(p.Hq, h0 + 4));
 }
 
-template __global__ void decode_split_kernel<4>(DecodeParams, const int*, const int*, const int*, const int*,
-                                                const int*);
+template __global__ void decode_range_kernel<4, false>(DecodeParams, const int*, const int*, const int*, const int*,
+                                                       const int*, const int*);
+template __global__ void decode_range_kernel<4, true>(DecodeParams, const int*, const int*, const int*, const int*,
+                                                      const int*, const int*);
 
 }  // namespace pkv

@@ -40,6 +40,9 @@ _SIGS = {
     "pkv_attn_decode": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_p, _c_int, _c_int,
                                  _c_p, _c_f, _c_p, _c_int, _c_p, _c_int, _c_int, _c_i64, _c_p, _c_sz, _c_p]),
     "pkv_attn_decode_config": (_c_int, [_c_int, _c_int]),
+    "pkv_attn_decode_step": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p,
+                                      _c_p, _c_p, _c_int, _c_int, _c_p, _c_f, _c_p, _c_int, _c_p, _c_int, _c_int,
+                                      _c_i64, _c_p, _c_sz, _c_p]),
     "pkv_pool_create": (_c_p, [_c_i64]),
     "pkv_pool_destroy": (None, [_c_p]),
     "pkv_pool_take": (_c_int, [_c_p, _c_int, ctypes.POINTER(ctypes.c_uint32)]),
@@ -116,6 +119,19 @@ def attn_decode_workspace(T, Hq):
 
 def attn_decode_config(wg_per_cu=1, min_range=32):
     _check(_lib.pkv_attn_decode_config(wg_per_cu, min_range), "pkv_attn_decode_config")
+
+
+def attn_decode_step(k_rows, v_rows, row_stride, slot_map, q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq,
+                     block_table, max_blocks, block_size, out, scale, cu, skip_prompts, outs, spec, T, num_blocks,
+                     workspace, workspace_bytes=None, stream=None):
+    """Fused KV append + paged decode attention (see include/pkv.h)."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace.numel() * workspace.element_size()
+    _check(_lib.pkv_attn_decode_step(_ptr(k_rows), _ptr(v_rows), row_stride, _ptr(slot_map), _ptr(q), _ptr(kcache),
+                                     _ptr(vcache), _ptr(qkv), qstride, Hq, Hkv, _ptr(pos), _ptr(tok_seq),
+                                     _ptr(block_table), max_blocks, block_size, _ptr(out), scale, _ptr(cu),
+                                     int(skip_prompts), _ptr(outs), spec, T, num_blocks, _ptr(workspace),
+                                     workspace_bytes, _stream(stream)), "pkv_attn_decode_step")
 
 
 def attn_decode(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, out,

@@ -1,0 +1,177 @@
+"""GPU parity: the fused decode step (the key-range kernel appends the step's
+rows itself, then the merge: pkv_attn_decode_step) against the unfused
+launches and the oracle, eager and replayed from a HIP graph.
+
+The fused kernel computes the same partials in the same order as
+pkv_append + pkv_attn_decode, so its outputs must be bit-identical to theirs;
+the caches it writes must equal the oracle's append bit for bit; outputs are
+within the north-star tolerance of the oracle (max-abs 2e-3, rel 1e-2)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import pkv
+from _util import BS, D, bf16_bits, close, decode_case
+
+pytestmark = pytest.mark.gpu
+SCALE = 1.0 / 16.0
+
+
+def i16(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+
+
+def i32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+
+
+@pytest.fixture(autouse=True)
+def default_config():
+    pkv.attn_decode_config(1, 32)
+    yield
+    pkv.attn_decode_config(1, 32)
+
+
+def step_case(lens, Hkv, seed, per_seq=1):
+    """A step in which every sequence feeds `per_seq` new tokens (decode,
+    or verification of per_seq - 1 drafts) at consecutive positions ending at
+    len - 1; their K/V rows come from qkv rows like the reference's layout."""
+    Hq = 4 * Hkv
+    c = decode_case(lens, Hq, Hkv, seed)
+    rng = np.random.default_rng(seed + 100)
+    B = len(lens)
+    pos = np.concatenate([np.arange(L - per_seq, L) for L in lens]).astype(np.int32)
+    tok_seq = np.repeat(np.arange(B), per_seq).astype(np.int32)
+    T = len(pos)
+    slot = (c["bt"][tok_seq, pos // BS] * BS + pos % BS).astype(np.int32)
+    qkv = bf16_bits(rng.standard_normal((T, c["qstride"])) * 0.5)
+    q = bf16_bits(rng.standard_normal((T, Hq, D)) * 0.5)
+    cu = (np.arange(B + 1) * per_seq).astype(np.int32)
+    outs = np.full(B, 0 if per_seq > 1 else -1, np.int32)
+    return dict(c, q=q, qkv=qkv, pos=pos, tok_seq=tok_seq, cu=cu, slot=slot, T=T, outs=outs, Hq=Hq, Hkv=Hkv)
+
+
+def run(c, dev, fused, repeat=1):
+    Hq, Hkv, T = c["Hq"], c["Hkv"], c["T"]
+    kc, vc = i16(c["kc"], dev), i16(c["vc"], dev)
+    q, qkv = i16(c["q"], dev), i16(c["qkv"], dev)
+    pos, ts, bt, cu, slot = (i32(c[k], dev) for k in ("pos", "tok_seq", "bt", "cu", "slot"))
+    outs = i32(c["outs"], dev)
+    out = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev)
+    ws = torch.empty(pkv.attn_decode_workspace(T, Hq), dtype=torch.uint8, device=dev)
+    k_rows = qkv.data_ptr() + 2 * (2 * Hq * D)
+    v_rows = k_rows + 2 * Hkv * D
+    stride = c["qstride"] * 2
+    for _ in range(repeat):
+        if fused:
+            pkv.attn_decode_step(k_rows, v_rows, stride, slot, q, kc, vc, qkv, c["qstride"], Hq, Hkv, pos, ts, bt,
+                                 c["max_blocks"], BS, out, SCALE, cu, 0, outs, 1, T, c["pages"], ws)
+        else:
+            pkv.append(k_rows, v_rows, stride, slot, T, Hkv, D * 2, kc, vc, c["pages"] * BS)
+            pkv.attn_decode(q, kc, vc, qkv, c["qstride"], Hq, Hkv, pos, ts, bt, c["max_blocks"], BS, out, SCALE, cu,
+                            0, outs, 1, T, c["pages"], ws)
+    torch.cuda.synchronize()
+    return (out.cpu().numpy().view(np.uint16), kc.cpu().numpy().view(np.uint16), vc.cpu().numpy().view(np.uint16))
+
+
+def oracle_step(c):
+    kc, vc = c["kc"].copy(), c["vc"].copy()
+    Hq, Hkv = c["Hq"], c["Hkv"]
+    k_rows = np.ascontiguousarray(c["qkv"][:, 2 * Hq * D:2 * Hq * D + Hkv * D])
+    v_rows = np.ascontiguousarray(c["qkv"][:, 2 * Hq * D + Hkv * D:2 * Hq * D + 2 * Hkv * D])
+    oracle.append(k_rows, v_rows, c["slot"], kc, vc)
+    out, _ = oracle.attn_decode(c["q"], kc, vc, c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["tok_seq"], c["bt"],
+                                c["max_blocks"], BS, SCALE, cu=c["cu"], skip_prompts=0, outs=c["outs"], spec=1)
+    return out, kc, vc
+
+
+@pytest.mark.parametrize("lens,Hkv,per_seq,seed", [
+    ([1, 2, 17, 33, 700, 4097], 4, 1, 0),      # decode rows, first key fresh for len 1
+    ([3000, 5000, 100, 8193], 4, 1, 1),
+    ([900, 1200, 64], 4, 4, 2),                # verify rows: 4 fresh tokens per sequence
+    ([50] * 30, 4, 2, 3),                      # many short sequences, 2 fresh each
+    ([2000, 3000], 8, 1, 4),                   # two kv-head groups
+])
+def test_fused_step_matches_unfused_and_oracle(dev, lens, Hkv, per_seq, seed):
+    print(f"case step lens={lens[:6]} Hkv={Hkv} per_seq={per_seq}", flush=True)
+    c = step_case(lens, Hkv, seed, per_seq)
+    f_out, f_kc, f_vc = run(c, dev, fused=True)
+    u_out, u_kc, u_vc = run(c, dev, fused=False)
+    o_out, o_kc, o_vc = oracle_step(c)
+    assert np.array_equal(f_kc, o_kc) and np.array_equal(f_vc, o_vc), "fused append differs from the oracle"
+    assert np.array_equal(u_kc, o_kc) and np.array_equal(u_vc, o_vc)
+    assert np.array_equal(f_out, u_out), "fused and unfused outputs differ"
+    ok, err = close(f_out, o_out)
+    assert ok, err
+
+
+def test_fused_step_repeated_calls_are_idempotent(dev):
+    """Ten calls in a row on the same workspace (re-appending the same rows)
+    give identical outputs; a finer range split stays within tolerance."""
+    print("case step repeat", flush=True)
+    c = step_case([5000, 3000, 1000, 40], 4, 5)
+    once, _, _ = run(c, dev, fused=True, repeat=1)
+    many, _, _ = run(c, dev, fused=True, repeat=10)
+    assert np.array_equal(once, many)
+    pkv.attn_decode_config(1, 16)  # more ranges per token
+    finer, _, _ = run(c, dev, fused=True, repeat=3)
+    ok, err = close(finer, once)
+    assert ok, err
+
+
+def test_fused_step_many_one_key_sequences(dev):
+    """16,400 one-key sequences (every key is the step's own): fused equals
+    unfused, and the output is the closed form of a single key."""
+    print("case step many tokens", flush=True)
+    B = 16400
+    c = step_case([1] * B, 1, 6)
+    f_out, f_kc, _ = run(c, dev, fused=True)
+    u_out, u_kc, _ = run(c, dev, fused=False)
+    assert np.array_equal(f_out, u_out) and np.array_equal(f_kc, u_kc)
+    # one key: the output is bf16(rbf(v) * sigmoid(gate))
+    v = oracle.b2f(c["qkv"][:, 2 * 4 * D + D:2 * 4 * D + 2 * D])  # V rows, Hkv = 1
+    gate = oracle.b2f(c["qkv"][:, :4 * 2 * D].reshape(B, 4, 2, D)[:, :, 1, :])
+    want = bf16_bits(v[:, None, :] / (np.float32(1) + np.exp(-gate, dtype=np.float32)))
+    ok, err = close(f_out, want)
+    assert ok, err
+
+
+def test_step_graph_replay_matches_eager(dev):
+    """The step captured into a HIP graph (torch.cuda.CUDAGraph) and replayed
+    5 times, with eager launches and synchronizations in between, reproduces
+    the eager outputs and caches bit for bit each time."""
+    print("case step graph replay", flush=True)
+    c = step_case([4000, 900, 6000, 33], 4, 7)
+    Hq, Hkv, T = c["Hq"], c["Hkv"], c["T"]
+    eager_out, eager_kc, _ = run(c, dev, fused=True)
+    kc, vc = i16(c["kc"], dev), i16(c["vc"], dev)
+    q, qkv = i16(c["q"], dev), i16(c["qkv"], dev)
+    pos, ts, bt, cu, slot = (i32(c[k], dev) for k in ("pos", "tok_seq", "bt", "cu", "slot"))
+    out = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev)
+    ws = torch.empty(pkv.attn_decode_workspace(T, Hq), dtype=torch.uint8, device=dev)
+    k_rows = qkv.data_ptr() + 2 * (2 * Hq * D)
+    v_rows = k_rows + 2 * Hkv * D
+
+    def launch():
+        pkv.attn_decode_step(k_rows, v_rows, c["qstride"] * 2, slot, q, kc, vc, qkv, c["qstride"], Hq, Hkv, pos, ts,
+                             bt, c["max_blocks"], BS, out, SCALE, cu, 0, None, 1, T, c["pages"], ws)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        launch()  # warm up outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch()
+    for r in range(5):
+        out.fill_(0)
+        launch() if r % 2 else None  # eager work between replays
+        torch.cuda.synchronize()
+        out.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), eager_out), f"replay {r}"
+        assert np.array_equal(kc.cpu().numpy().view(np.uint16), eager_kc)
