@@ -28,6 +28,37 @@ sys.path.insert(0, ROOT)
 PEAK_HBM_GBS = 8000.0
 
 
+class HipEvents:
+    """Raw hipEvent_t pairs from the process's HIP runtime (the one torch
+    loaded), for kernels that record events themselves."""
+
+    def __init__(self, n):
+        import ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")  # resolves to the already-loaded runtime
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.pairs = []
+        for _ in range(n):
+            a, b = ctypes.c_void_p(), ctypes.c_void_p()
+            assert self.hip.hipEventCreate(ctypes.byref(a)) == 0 and self.hip.hipEventCreate(ctypes.byref(b)) == 0
+            self.pairs.append((a.value, b.value))
+
+    def elapsed_ms(self):
+        import ctypes
+        out = []
+        for a, b in self.pairs:
+            ms = ctypes.c_float()
+            assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+            out.append(ms.value)
+        return out
+
+    def __del__(self):
+        for a, b in getattr(self, "pairs", []):
+            self.hip.hipEventDestroy(a)
+            self.hip.hipEventDestroy(b)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -40,6 +71,8 @@ def main():
     ap.add_argument("--wg-per-cu", type=int, default=None)
     ap.add_argument("--min-range", type=int, default=None)
     ap.add_argument("--graph", action="store_true", help="replay each step from a captured HIP graph")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 2 GiB device copy (x3), to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--unfused", action="store_true",
                     help="append, key ranges and merge as three launches instead of the fused step")
     args = ap.parse_args()
@@ -51,6 +84,15 @@ def main():
 
     import numpy as np
     import torch
+
+    if args.calibrate_copy:
+        src = torch.ones(1 << 30, dtype=torch.int16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)  # reads 2 GiB, writes 2 GiB
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": 2 << 30, "copies": 3}))
+        return
 
     import pkv
     from pkv import synth
@@ -99,30 +141,19 @@ def main():
                                  bt, meta.max_blocks, BS, out, 1 / 16, cu, 0, None, 1, B, pages, ws, stream=s_)
 
     def step(i, ev=None):
-        if args.unfused:
-            pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=sp)
-            if ev:
-                ev[0].record(stream)
-            pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu,
-                            0, None, 1, B, pages, ws, stream=sp, phase="split")
-            if ev:
-                ev[1].record(stream)
-            pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu,
-                            0, None, 1, B, pages, ws, stream=sp, phase="merge")
-        else:
-            if ev:
-                ev[0].record(stream)
-            pkv.attn_decode_step(k_rows, v_rows, qstride * 2, slot_d[i], q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts,
-                                 bt, meta.max_blocks, BS, out, 1 / 16, cu, 0, None, 1, B, pages, ws, stream=sp)
-            if ev:
-                ev[1].record(stream)
+        # ev: the key-range kernel records these HIP events at its own start
+        # and end (hipExtLaunchKernelGGL), so no dispatch gap is counted.
+        if ev:
+            pkv.time_next_range_kernel(ev[0], ev[1])
+        step_on(i, stream)
 
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
     # Timed region: K steps; events bracket the dominant kernel of each step
     # (the fused step kernel, or the key-range kernel with --unfused).
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    kev = HipEvents(args.steps)
+    evs = kev.pairs
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0.record(stream)
@@ -131,7 +162,7 @@ def main():
     t1.record(stream)
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
-    kern_ms = [a.elapsed_time(b) for a, b in evs]
+    kern_ms = kev.elapsed_ms()
     ms_step = total_ms / args.steps
 
     graph_us = None

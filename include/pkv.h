@@ -138,6 +138,14 @@ int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_str
                          int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* Measurement: the next key-range kernel this thread launches (the dominant
+ * kernel of pkv_attn_decode / _split / _step) records start_event when it
+ * starts executing and stop_event when it ends (hipExtLaunchKernelGGL), so
+ * hipEventElapsedTime gives its own duration without dispatch gaps, like the
+ * reference's Gpu::time_us event timing (src/gpu.rs:1461-1510). Events are
+ * hipEvent_t created with timing enabled; NULL clears. */
+int pkv_time_next_range_kernel(void* start_event, void* stop_event);
+
 /* Tuning: key-range workgroups per CU (default 1) and fewest keys per range
  * (default 32). Process-wide; takes effect for later calls (workspace sizes
  * follow). */

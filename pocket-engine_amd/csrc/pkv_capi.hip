@@ -5,6 +5,8 @@
 #include "pkv_decode.hip"
 #include "../../include/pkv.h"
 
+#include <hip/hip_ext.h>
+
 #include <mutex>
 
 namespace {
@@ -41,6 +43,9 @@ int device_cus() {
 
 int g_wg_per_cu = 1;
 int g_min_range = 32;
+// Events the next key-range launch of this thread records at its start and
+// end (hipExtLaunchKernelGGL), then forgets.
+thread_local hipEvent_t t_ev_start = nullptr, t_ev_stop = nullptr;
 
 int decode_n_wg() { return device_cus() * g_wg_per_cu; }
 
@@ -114,6 +119,12 @@ int pkv_page_copy(void* kcache, void* vcache, const int32_t* src, const int32_t*
     hipLaunchKernelGGL(pkv::page_copy_kernel, dim3(n, 2, slices), dim3(256), 0, (hipStream_t)stream,
                        (uint8_t*)kcache, (uint8_t*)vcache, src, dst, (long)page_bytes, (long)num_blocks, slices);
     return launch_status();
+}
+
+int pkv_time_next_range_kernel(void* start_event, void* stop_event) {
+    t_ev_start = (hipEvent_t)start_event;
+    t_ev_stop = (hipEvent_t)stop_event;
+    return PKV_OK;
 }
 
 int pkv_attn_decode_config(int wg_per_cu, int min_range) {
@@ -194,14 +205,15 @@ int attn_decode_phases(int phases, const AppendArgs* app, const void* q, const v
     p.v_rows = app ? (const uint16_t*)app->v_rows : nullptr;
     p.row_stride = app ? (long)(app->row_stride / 2) : 0;
     const int32_t* slot_map = app ? app->slot_map : nullptr;
-    if (phases & 4) {
-        hipLaunchKernelGGL((pkv::decode_range_kernel<4, true>), dim3(n_wg, groups), dim3(threads), 0,
-                           (hipStream_t)stream, p, pos, tok_seq, block_table, cu, outs, slot_map);
-        const int st = launch_status();
-        if (st != PKV_OK) return st;
-    } else if (phases & 1) {
-        hipLaunchKernelGGL((pkv::decode_range_kernel<4, false>), dim3(n_wg, groups), dim3(threads), 0,
-                           (hipStream_t)stream, p, pos, tok_seq, block_table, cu, outs, slot_map);
+    if (phases & 5) {
+        hipEvent_t e0 = t_ev_start, e1 = t_ev_stop;
+        t_ev_start = t_ev_stop = nullptr;
+        if (phases & 4)
+            hipExtLaunchKernelGGL((pkv::decode_range_kernel<4, true>), dim3(n_wg, groups), dim3(threads), 0,
+                                  (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs, slot_map);
+        else
+            hipExtLaunchKernelGGL((pkv::decode_range_kernel<4, false>), dim3(n_wg, groups), dim3(threads), 0,
+                                  (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs, slot_map);
         const int st = launch_status();
         if (st != PKV_OK) return st;
     }
