@@ -153,6 +153,27 @@ int pkv_attn_decode_config(int wg_per_cu, int min_range);
 
 
 /* ---------------------------------------------------------------------------
+ * Device: chunked-prefill attention over paged context (MFMA bf16)
+ * ------------------------------------------------------------------------- */
+
+/* Causal attention for prompt rows with the reference's semantics and
+ * arguments (attn_mfma_g<G>_t<NT> / attn_flash_group: ATTN_FLASH_ARGS at
+ * src/kernels/qwen35.cu:1351-1356, amd/attention.cuh:12-136, launched at
+ * src/model.rs:2438-2493): for every sequence s < seqs with more than one
+ * token in cu[s] .. cu[s+1]-1 that is not verifying drafts (outs), each of
+ * its tokens t attends over keys 0 .. pos[t] of its pages (positions within
+ * a sequence's chunk are consecutive), q scaled by scale * log2(e) and
+ * rounded to bf16, exp2 softmax, P rounded to bf16 for P.V, output
+ * bf16(bf16(O / l) * sigmoid(gate)). Other rows are left untouched. The
+ * chunk's own K/V must already be in the cache (pkv_append first). T is the
+ * number of token rows. bf16, head_dim 256, G = Hq / Hkv = 4; any block
+ * size. kscale/vscale (E4M3 cache) are not part of this path. */
+int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
+                     int Hkv, const int32_t* pos, const int32_t* cu, int seqs, const int32_t* block_table,
+                     int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec, int T,
+                     int64_t num_blocks, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Host: block allocator (reference Scheduler.free_blocks / block_refs,
  * src/sched.rs:461-465, 515, 801-817)
  * ------------------------------------------------------------------------- */

@@ -3,6 +3,7 @@
 // ever sees arguments its indexing was written for.
 #include "pkv_copy.hip"
 #include "pkv_decode.hip"
+#include "pkv_prefill.hip"
 #include "../../include/pkv.h"
 
 #include <hip/hip_ext.h>
@@ -118,6 +119,52 @@ int pkv_page_copy(void* kcache, void* vcache, const int32_t* src, const int32_t*
     const int slices = (int)std::min<int64_t>(16, std::max<int64_t>(1, page_bytes / 4096));
     hipLaunchKernelGGL(pkv::page_copy_kernel, dim3(n, 2, slices), dim3(256), 0, (hipStream_t)stream,
                        (uint8_t*)kcache, (uint8_t*)vcache, src, dst, (long)page_bytes, (long)num_blocks, slices);
+    return launch_status();
+}
+
+int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
+                     int Hkv, const int32_t* pos, const int32_t* cu, int seqs, const int32_t* block_table,
+                     int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec, int T,
+                     int64_t num_blocks, void* stream) {
+    if (T < 0 || seqs < 0 || Hq <= 0 || Hkv <= 0 || max_blocks <= 0 || block_size <= 0 || num_blocks <= 0 ||
+        spec < 1)
+        return PKV_ERR_INVALID;
+    if (Hq != 4 * Hkv) return PKV_ERR_UNSUPPORTED;
+    if (T == 0 || seqs == 0) return PKV_OK;
+    if (!q || !kcache || !vcache || !qkv || !pos || !cu || !block_table || !out) return PKV_ERR_INVALID;
+    if (qstride < 2 * Hq * pkv::HEAD_DIM || qstride % 8 != 0) return PKV_ERR_INVALID;
+    if (!aligned(q, 16) || !aligned(kcache, 16) || !aligned(vcache, 16) || !aligned(qkv, 16) || !aligned(out, 16))
+        return PKV_ERR_INVALID;
+    static bool attr_set = false;  // per process: the kernel's LDS above the 64 KiB default
+    const size_t smem = pkv::prefill_smem_bytes();
+    if (!attr_set) {
+        const int st = status_of(
+            hipFuncSetAttribute((const void*)pkv::prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        if (st != PKV_OK) return st;
+        attr_set = true;
+    }
+    pkv::PrefillParams p;
+    p.q = (const uint16_t*)q;
+    p.kc = (const uint16_t*)kcache;
+    p.vc = (const uint16_t*)vcache;
+    p.qkv = (const uint16_t*)qkv;
+    p.qstride = qstride;
+    p.Hq = Hq;
+    p.Hkv = Hkv;
+    p.pos = pos;
+    p.cu = cu;
+    p.seqs = seqs;
+    p.block_table = block_table;
+    p.max_blocks = max_blocks;
+    p.block_size = block_size;
+    p.out = (uint16_t*)out;
+    p.scale = scale;
+    p.outs = outs;
+    p.spec = spec;
+    p.num_blocks = (long)num_blocks;
+    // Upper bound on query tiles: each prompt sequence rounds up once.
+    const int tiles = (T + pkv::PF_BQ - 1) / pkv::PF_BQ + seqs;
+    hipLaunchKernelGGL(pkv::prefill_kernel, dim3(tiles, Hkv), dim3(pkv::PF_THREADS), smem, (hipStream_t)stream, p);
     return launch_status();
 }
 

@@ -41,6 +41,8 @@ _SIGS = {
                                  _c_p, _c_f, _c_p, _c_int, _c_p, _c_int, _c_int, _c_i64, _c_p, _c_sz, _c_p]),
     "pkv_attn_decode_config": (_c_int, [_c_int, _c_int]),
     "pkv_time_next_range_kernel": (_c_int, [_c_p, _c_p]),
+    "pkv_attn_prefill": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_int, _c_p, _c_int,
+                                  _c_int, _c_p, _c_f, _c_p, _c_int, _c_int, _c_i64, _c_p]),
     "pkv_attn_decode_step": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p,
                                       _c_p, _c_p, _c_int, _c_int, _c_p, _c_f, _c_p, _c_int, _c_p, _c_int, _c_int,
                                       _c_i64, _c_p, _c_sz, _c_p]),
@@ -154,6 +156,14 @@ def attn_decode(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_ta
                                 _ptr(tok_seq), _ptr(block_table), max_blocks, block_size, _ptr(out), scale,
                                 _ptr(cu), int(skip_prompts), _ptr(outs), spec, T, num_blocks, _ptr(workspace),
                                 workspace_bytes, _stream(stream)), "pkv_attn_decode")
+
+
+def attn_prefill(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks, block_size, out,
+                 scale, outs, spec, T, num_blocks, stream=None):
+    """Causal chunked-prefill attention over paged context (MFMA bf16)."""
+    _check(_lib.pkv_attn_prefill(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(qkv), qstride, Hq, Hkv, _ptr(pos),
+                                 _ptr(cu), seqs, _ptr(block_table), max_blocks, block_size, _ptr(out), scale,
+                                 _ptr(outs), spec, T, num_blocks, _stream(stream)), "pkv_attn_prefill")
 
 
 class Pool:
