@@ -26,6 +26,7 @@ sys.path.insert(0, os.path.join(ROOT, "pocket-engine_amd"))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 
 class HipEvents:
@@ -65,6 +66,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--seed", type=int, default=None, help="length-mix seed (default: fresh per run)")
+    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4"],
+                    help="c3 (default, the metric): batch-64 decode step; c2: single-sequence decode at 4096 "
+                         "context; c4: chunked prefill of 8 x 2048 tokens over a shared 16,384-token prefix")
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--pages", type=int, default=65536)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -97,6 +101,9 @@ def main():
     import pkv
     from pkv import synth
 
+    if args.config == "c4":
+        return bench_prefill(args)
+
     if args.wg_per_cu or args.min_range:
         pkv.attn_decode_config(args.wg_per_cu or 1, args.min_range or 32)
     seed = args.seed if args.seed is not None else int(time.time()) % 100000
@@ -104,7 +111,11 @@ def main():
     Hq, Hkv, D, BS = 16, 4, 256, 16
     B, pages = args.batch, args.pages
     S = args.warmup + args.steps
-    lens = synth.c3_lengths(seed, batch=B)
+    if args.config == "c2":
+        B, pages = 1, 4096 + (S + 15) // 16 + 1
+        lens = np.array([4096])
+    else:
+        lens = synth.c3_lengths(seed, batch=B)
     meta = synth.decode_meta(lens, pages, steps=S, seed=seed)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
@@ -204,7 +215,7 @@ def main():
     kern_gbs = sum(kern_bytes) / (sum(kern_ms) * 1e-3) / 1e9
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and args.config == "c3":
         cpu = cpu_baseline(kc, vc, q, qkv, meta, steps[args.warmup], Hq, Hkv, qstride, dev)
 
     line = {
@@ -223,7 +234,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1)*0.5 K/V/q, U[512,8192] contexts)",
-        "config": {"workload": "c3: batch-64 paged decode step (append 1 token/seq + paged decode attention)",
+        "config": {"workload": ("c3: batch-64 paged decode step (append 1 token/seq + paged decode attention)"
+                                if args.config == "c3" else
+                                "c2: single-sequence paged decode step at 4096 context (append + attention)"),
                    "path": "unfused (append, key ranges, merge)" if args.unfused else "fused step (one launch)",
                    "batch": B, "ctx": "U[512,8192]", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
                    "pool_pages": pages, "seed": seed, "mean_keys_per_step": round(float(np.mean(keys)), 1),
@@ -232,6 +245,92 @@ def main():
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
                      "avg_us": round(kern_avg_us, 2), "traffic": None},
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_prefill(args):
+    """Config 4: 8 sequences share a refcounted 16,384-token cached prefix
+    (the same 1,024 pages in every block table); each appends a 2,048-token
+    chunk (pkv_append) and runs causal paged attention of the chunk over
+    prefix + chunk (pkv_attn_prefill). FLOPs = 4 * 256 * Hq * sum over query
+    rows of keys attended (QK^T and PV, the reference bench-attn formula,
+    src/main.rs:950-952)."""
+    import numpy as np
+    import torch
+
+    import pkv
+
+    seed = args.seed if args.seed is not None else int(time.time()) % 100000
+    dev = torch.device("cuda:0")
+    Hq, Hkv, D, BS, B, P, N = 16, 4, 256, 16, 8, 16384, 2048
+    pp, cp = P // BS, N // BS
+    pages = pp + B * cp + 8
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    kc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    vc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(pages).astype(np.int32)
+    bt = np.zeros((B, pp + cp), np.int32)
+    for s in range(B):
+        bt[s, :pp] = perm[:pp]
+        bt[s, pp:] = perm[pp + s * cp:pp + (s + 1) * cp]
+    T = B * N
+    pos = np.tile(np.arange(P, P + N, dtype=np.int32), B)
+    slot = (bt[np.repeat(np.arange(B), N), pos // BS] * BS + pos % BS).astype(np.int32)
+    cu = (np.arange(B + 1) * N).astype(np.int32)
+    q = (torch.randn(T, Hq, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    qstride = (2 * Hq + 2 * Hkv) * D
+    qkv = (torch.randn(T, qstride, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    out = torch.empty(T, Hq, D, dtype=torch.bfloat16, device=dev)
+    bt_d, pos_d, cu_d, slot_d = (torch.from_numpy(a).to(dev) for a in (bt, pos, cu, slot))
+    k_rows = qkv.data_ptr() + 2 * (2 * Hq * D)
+    v_rows = k_rows + 2 * Hkv * D
+    stream = torch.cuda.current_stream()
+    evs = HipEvents(args.steps)
+
+    def step(ev=None):
+        pkv.append(k_rows, v_rows, qstride * 2, slot_d, T, Hkv, D * 2, kc, vc, pages * BS)
+        if ev:
+            pkv.time_next_prefill_kernel(ev[0], ev[1])
+        pkv.attn_prefill(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d, cu_d, B, bt_d, pp + cp, BS, out, 1 / 16, None, 1,
+                         T, pages)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for k in range(args.steps):
+        step(evs.pairs[k])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / args.steps
+    kern_ms = evs.elapsed_ms()
+    flops = 4.0 * D * Hq * float((pos.astype(np.int64) + 1).sum())
+    kern_us = 1e3 * sum(kern_ms) / len(kern_ms)
+    tflops = flops / (kern_us * 1e-6) / 1e12
+    line = {
+        "metric": "chunked-prefill attention TFLOP/s over paged context (config 4), 1 MI355X",
+        "value": round(tflops, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5)",
+        "config": {"workload": "c4: 8 seqs x 2048-token chunk over a shared 16,384-token prefix (append + prefill)",
+                   "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS, "flop_per_step": flops,
+                   "seed": seed, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "prefill_kernel", "achieved": round(tflops, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "avg_us": round(kern_us, 1), "traffic": None},
+        "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
 

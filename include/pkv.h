@@ -145,6 +145,8 @@ int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_str
  * reference's Gpu::time_us event timing (src/gpu.rs:1461-1510). Events are
  * hipEvent_t created with timing enabled; NULL clears. */
 int pkv_time_next_range_kernel(void* start_event, void* stop_event);
+/* The same for the next pkv_attn_prefill kernel of this thread. */
+int pkv_time_next_prefill_kernel(void* start_event, void* stop_event);
 
 /* Tuning: key-range workgroups per CU (default 1) and fewest keys per range
  * (default 32). Process-wide; takes effect for later calls (workspace sizes
@@ -166,8 +168,8 @@ int pkv_attn_decode_config(int wg_per_cu, int min_range);
  * rounded to bf16, exp2 softmax, P rounded to bf16 for P.V, output
  * bf16(bf16(O / l) * sigmoid(gate)). Other rows are left untouched. The
  * chunk's own K/V must already be in the cache (pkv_append first). T is the
- * number of token rows. bf16, head_dim 256, G = Hq / Hkv = 4; any block
- * size. kscale/vscale (E4M3 cache) are not part of this path. */
+ * number of token rows. bf16, head_dim 256, G = Hq / Hkv = 4, block size a
+ * power of two. kscale/vscale (E4M3 cache) are not part of this path. */
 int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
                      int Hkv, const int32_t* pos, const int32_t* cu, int seqs, const int32_t* block_table,
                      int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec, int T,

@@ -47,6 +47,7 @@ int g_min_range = 32;
 // Events the next key-range launch of this thread records at its start and
 // end (hipExtLaunchKernelGGL), then forgets.
 thread_local hipEvent_t t_ev_start = nullptr, t_ev_stop = nullptr;
+thread_local hipEvent_t t_pf_start = nullptr, t_pf_stop = nullptr;  // same for the prefill kernel
 
 int decode_n_wg() { return device_cus() * g_wg_per_cu; }
 
@@ -129,7 +130,7 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
     if (T < 0 || seqs < 0 || Hq <= 0 || Hkv <= 0 || max_blocks <= 0 || block_size <= 0 || num_blocks <= 0 ||
         spec < 1)
         return PKV_ERR_INVALID;
-    if (Hq != 4 * Hkv) return PKV_ERR_UNSUPPORTED;
+    if (Hq != 4 * Hkv || (block_size & (block_size - 1)) != 0) return PKV_ERR_UNSUPPORTED;
     if (T == 0 || seqs == 0) return PKV_OK;
     if (!q || !kcache || !vcache || !qkv || !pos || !cu || !block_table || !out) return PKV_ERR_INVALID;
     if (qstride < 2 * Hq * pkv::HEAD_DIM || qstride % 8 != 0) return PKV_ERR_INVALID;
@@ -157,6 +158,7 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
     p.block_table = block_table;
     p.max_blocks = max_blocks;
     p.block_size = block_size;
+    p.bs_log2 = __builtin_ctz((unsigned)block_size);
     p.out = (uint16_t*)out;
     p.scale = scale;
     p.outs = outs;
@@ -164,13 +166,22 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
     p.num_blocks = (long)num_blocks;
     // Upper bound on query tiles: each prompt sequence rounds up once.
     const int tiles = (T + pkv::PF_BQ - 1) / pkv::PF_BQ + seqs;
-    hipLaunchKernelGGL(pkv::prefill_kernel, dim3(tiles, Hkv), dim3(pkv::PF_THREADS), smem, (hipStream_t)stream, p);
+    hipEvent_t e0 = t_pf_start, e1 = t_pf_stop;
+    t_pf_start = t_pf_stop = nullptr;
+    hipExtLaunchKernelGGL(pkv::prefill_kernel, dim3(tiles, Hkv), dim3(pkv::PF_THREADS), smem, (hipStream_t)stream, e0,
+                          e1, 0, p);
     return launch_status();
 }
 
 int pkv_time_next_range_kernel(void* start_event, void* stop_event) {
     t_ev_start = (hipEvent_t)start_event;
     t_ev_stop = (hipEvent_t)stop_event;
+    return PKV_OK;
+}
+
+int pkv_time_next_prefill_kernel(void* start_event, void* stop_event) {
+    t_pf_start = (hipEvent_t)start_event;
+    t_pf_stop = (hipEvent_t)stop_event;
     return PKV_OK;
 }
 

@@ -8,18 +8,22 @@
 // bf16(rbf(O / l) * sigmoid(gate)).
 //
 // Tiling (this build's own). A workgroup takes 64 consecutive query
-// positions of one sequence and one kv head: 8 waves, wave w = (query head
-// w % 4 of the group, query block w / 4 of 32 positions). Keys stream in
-// tiles of 32 (two pages) staged in LDS once for all 8 waves (GQA sharing):
-// K row-major [key][d] and V transposed [d][key]. Per tile a wave computes
+// positions of one sequence and one kv head: 4 waves, wave w = query head w
+// of the group, each over both 32-query blocks. Keys stream in tiles of 32
+// (two pages) staged in LDS once for the 4 waves (GQA sharing): K row-major
+// [key][d] and V transposed [d][key]. Per tile and query block a wave computes
 //   S^T[32 keys][32 queries] = K Q^T     16 x v_mfma_f32_32x32x16_bf16
 //   O^T[256 d][32 queries] += V^T P^T    16 x v_mfma_f32_32x32x16_bf16
+// and every K / V^T fragment read from LDS feeds both blocks' MFMAs, which
+// halves LDS read traffic per MFMA (one fragment per MFMA would need the
+// whole 128 B/clk of LDS bandwidth at the MFMA peak).
 // Computing S transposed leaves each lane with one query's 16 scores (keys
 // 8 (r / 4) + 4 (lane / 32) + r % 4), so the online softmax is in-lane plus
 // one cross-half shuffle, and the probabilities are already the B operand of
 // the second product once the matching V^T rows are read (keys
-// 16 kk + 4 (lane / 32) + {0..3, 8..11}). q stays in registers (64 VGPRs);
-// O^T takes 128 accumulators. The next tile's K/V are loaded into registers
+// 16 kk + 4 (lane / 32) + {0..3, 8..11}). q stays in registers (128 VGPRs
+// for the two blocks); O^T takes 256 accumulators (one wave per SIMD, so the
+// whole 512-register file). The next tile's K/V are loaded into registers
 // while the current one is multiplied (double-buffered LDS).
 #include "pkv_common.h"
 
@@ -35,7 +39,7 @@ struct PrefillParams {
     const int* cu;
     int seqs;
     const int* block_table;
-    int max_blocks, block_size;
+    int max_blocks, block_size, bs_log2;
     uint16_t* out;
     float scale;
     const int* outs;
@@ -52,19 +56,28 @@ constexpr int PF_KSTR = HEAD_DIM + 8;  // K tile row stride (elements)
 constexpr int PF_VSTR = PF_BK + 4;
 constexpr int PF_K_ELEMS = PF_BK * PF_KSTR;
 constexpr int PF_V_ELEMS = HEAD_DIM * PF_VSTR;
-constexpr int PF_THREADS = 512;
+// 32-query blocks per wave: 2 halves LDS reads per MFMA but needs 128 q +
+// 256 accumulator registers per wave (spills at one wave per SIMD); 1 runs
+// 8 waves, two per SIMD.
+#ifndef PKV_PF_NQB
+#define PKV_PF_NQB 1
+#endif
+constexpr int PF_NQB = PKV_PF_NQB;
+constexpr int PF_WAVES = 4 * (PF_BQ / 32) / PF_NQB;
+constexpr int PF_THREADS = 64 * PF_WAVES;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
 __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {
+    static_assert(PF_BK * HEAD_DIM / 8 % PF_THREADS == 0, "whole 16-byte chunks per thread");
     extern __shared__ __align__(16) uint16_t pf_smem[];
     // Buffer b: K tile at pf_smem + b * STAGE, V^T tile right after it.
     constexpr int STAGE = PF_K_ELEMS + PF_V_ELEMS;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, lh = lane >> 5;
     const int kvh = blockIdx.y;
-    const int G = 4, h = kvh * G + (wave & 3), qb = wave >> 2;
+    const int G = 4, h = kvh * G + (wave & 3), qb0 = (wave >> 2) * PF_NQB;  // first query block
     // Find this block's query tile among the prompt sequences.
     int s = -1, tile = blockIdx.x;
     for (int i = 0; i < p.seqs; i++) {
@@ -84,62 +97,83 @@ __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p)
     const int* bt = p.block_table + (size_t)s * p.max_blocks;
     const size_t row = (size_t)p.Hkv * HEAD_DIM;
 
-    // This wave's 32 queries (block qb): q^T operand, scaled into log2 units.
-    const int myq = qb * 32 + lq;  // query index within the tile
-    bf16x8 qf[16];
-    {
+    // This wave's queries: blocks qb0 + qb of 32 (query (qb0 + qb) * 32 + lq
+    // of the tile), q^T operands scaled into log2 units.
+    bf16x8 qf[PF_NQB][16];
+    const float f = p.scale * LOG2E;
+#pragma unroll
+    for (int qb = 0; qb < PF_NQB; qb++) {
+        const int myq = (qb0 + qb) * 32 + lq;
         const bool ok = myq < nb;
         const uint16_t* qrow = p.q + ((size_t)(tb + (ok ? myq : 0)) * p.Hq + h) * HEAD_DIM;
-        const float f = p.scale * LOG2E;
 #pragma unroll
         for (int kk = 0; kk < 16; kk++) {
             uint4 raw = ok ? *reinterpret_cast<const uint4*>(qrow + 16 * kk + 8 * lh) : make_uint4(0, 0, 0, 0);
             raw = make_uint4(pack2(bf_lo(raw.x) * f, bf_hi(raw.x) * f), pack2(bf_lo(raw.y) * f, bf_hi(raw.y) * f),
                              pack2(bf_lo(raw.z) * f, bf_hi(raw.z) * f), pack2(bf_lo(raw.w) * f, bf_hi(raw.w) * f));
-            qf[kk] = as_bf16x8(raw);
+            // (outside the key loop: exact software rounding, NaN-preserving)
+            qf[qb][kk] = as_bf16x8(raw);
         }
     }
-    f32x16 o[8];
+    f32x16 o[PF_NQB][8];
 #pragma unroll
-    for (int db = 0; db < 8; db++)
+    for (int qb = 0; qb < PF_NQB; qb++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) o[db][r] = 0.f;
-    float m = -INFINITY, l = 0.f;
-    const int last = qp0 + min(nb, qb * 32 + 32) - 1;  // this wave's last query position
+        for (int db = 0; db < 8; db++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[qb][db][r] = 0.f;
+    float m[PF_NQB], l[PF_NQB];
+#pragma unroll
+    for (int qb = 0; qb < PF_NQB; qb++) {
+        m[qb] = -INFINITY;
+        l[qb] = 0.f;
+    }
+    const int last = qp0 + min(nb, (qb0 + PF_NQB) * 32) - 1;  // this wave's last query position
 
     // Tile loads: 32 keys x 256 dims of K and of V = 2 x 1024 chunks of 16 B,
-    // 2 + 2 per thread. K: thread e takes key e / 32, chunk e % 32 (whole rows
-    // per 32 lanes). V: thread takes keys 2 (tid % 16) and + 1 of chunk
-    // tid / 16, so it can store (key, key + 1) pairs of each dim as one word
-    // of the transposed tile. Keys at or past L load zeros.
-    uint4 kr[2], vr[2];
+    // NCH + NCH per thread. K: chunk e = tid + PF_THREADS u is key e / 32,
+    // dims 8 (e % 32) (whole rows per 32 lanes). V: the thread takes keys
+    // 2 (tid % 16) and + 1 of chunks tid / 16 + (PF_THREADS / 16) i, so it can
+    // store (key, key + 1) pairs of each dim as one word of the transposed
+    // tile. Keys at or past L load zeros.
+    constexpr int NCH = PF_BK * HEAD_DIM / 8 / PF_THREADS;
+    uint4 kr[NCH], vr[NCH];
+    // Block size is a power of two (checked on the host): shifts, no division.
+    const int bs_log2 = p.bs_log2, bs_mask = (1 << bs_log2) - 1;
     auto slot_at = [&](int kp, int c) -> size_t {
-        long pg = bt[kp / p.block_size];
+        long pg = bt[kp >> bs_log2];
         pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
-        return ((size_t)pg * p.block_size + kp % p.block_size) * row + (size_t)kvh * HEAD_DIM + c;
+        return (((size_t)pg << bs_log2) + (kp & bs_mask)) * row + (size_t)kvh * HEAD_DIM + c;
     };
     auto load_tile = [&](int k0) {
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
+        for (int u = 0; u < NCH; u++) {
             const int e = tid + u * PF_THREADS, kp = k0 + (e >> 5);
             kr[u] = kp < L ? *reinterpret_cast<const uint4*>(p.kc + slot_at(kp, (e & 31) * 8)) : make_uint4(0, 0, 0, 0);
-            const int vp = k0 + 2 * (tid & 15) + u;
-            vr[u] = vp < L ? *reinterpret_cast<const uint4*>(p.vc + slot_at(vp, (tid >> 4) * 8)) : make_uint4(0, 0, 0, 0);
+            const int vp = k0 + 2 * (tid & 15) + (u & 1), vc = ((tid >> 4) + (PF_THREADS / 16) * (u >> 1)) * 8;
+            vr[u] = vp < L ? *reinterpret_cast<const uint4*>(p.vc + slot_at(vp, vc)) : make_uint4(0, 0, 0, 0);
         }
     };
     auto store_tile = [&](int buf) {
+        uint16_t* sk = pf_smem + buf * STAGE;
+        uint16_t* sv = sk + PF_K_ELEMS;
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
+        for (int u = 0; u < NCH; u++) {
             const int e = tid + u * PF_THREADS;
-            *reinterpret_cast<uint4*>(pf_smem + buf * STAGE + (e >> 5) * PF_KSTR + (e & 31) * 8) = kr[u];
+            *reinterpret_cast<uint4*>(sk + (e >> 5) * PF_KSTR + (e & 31) * 8) = kr[u];
         }
-        const int j = 2 * (tid & 15), c = (tid >> 4) * 8;
-        const uint32_t a[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w}, b[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+        const int j = 2 * (tid & 15);
 #pragma unroll
-        for (int d = 0; d < 4; d++) {
-            // dims c + 2d (low halves) and c + 2d + 1 (high halves) of keys j, j + 1
-            *reinterpret_cast<uint32_t*>(pf_smem + buf * STAGE + PF_K_ELEMS + (c + 2 * d) * PF_VSTR + j) = (a[d] & 0xffffu) | (b[d] << 16);
-            *reinterpret_cast<uint32_t*>(pf_smem + buf * STAGE + PF_K_ELEMS + (c + 2 * d + 1) * PF_VSTR + j) = (a[d] >> 16) | (b[d] & 0xffff0000u);
+        for (int half = 0; half < NCH / 2; half++) {
+            const int c = ((tid >> 4) + (PF_THREADS / 16) * half) * 8;
+            const uint4 va = vr[2 * half], vb = vr[2 * half + 1];
+            const uint32_t a[4] = {va.x, va.y, va.z, va.w}, b[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                // dims c + 2d (low halves) and c + 2d + 1 (high halves) of keys j, j + 1
+                *reinterpret_cast<uint32_t*>(sv + (c + 2 * d) * PF_VSTR + j) = (a[d] & 0xffffu) | (b[d] << 16);
+                *reinterpret_cast<uint32_t*>(sv + (c + 2 * d + 1) * PF_VSTR + j) = (a[d] >> 16) | (b[d] & 0xffff0000u);
+            }
         }
     };
 
@@ -153,59 +187,78 @@ __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p)
         if (k0 <= last) {
             const uint16_t* K = pf_smem + buf * STAGE;
             const uint16_t* Vt = K + PF_K_ELEMS;
-            // S^T = K Q^T: lane (lh, lq) ends with query lq's scores of keys
+            // S^T = K Q^T for both query blocks; each K fragment feeds two
+            // MFMAs. Lane (lh, lq) ends with query (qb, lq)'s scores of keys
             // k0 + 8 (r / 4) + 4 lh + r % 4.
-            f32x16 st;
+            f32x16 st[PF_NQB];
 #pragma unroll
-            for (int r = 0; r < 16; r++) st[r] = 0.f;
+            for (int qb = 0; qb < PF_NQB; qb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) st[qb][r] = 0.f;
 #pragma unroll
             for (int kk = 0; kk < 16; kk++) {
-                const uint4 a = *reinterpret_cast<const uint4*>(K + lq * PF_KSTR + 16 * kk + 8 * lh);
-                st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[kk], st, 0, 0, 0);
+                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(K + lq * PF_KSTR + 16 * kk + 8 * lh));
+#pragma unroll
+                for (int qb = 0; qb < PF_NQB; qb++)
+                    st[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb][kk], st[qb], 0, 0, 0);
             }
-            const int qp = qp0 + myq;
-            if (k0 + PF_BK - 1 > qp0 + qb * 32 || k0 + PF_BK > L) {
+            uint4 pb[PF_NQB][2];
+#pragma unroll
+            for (int qb = 0; qb < PF_NQB; qb++) {
+                const int qp = qp0 + (qb0 + qb) * 32 + lq;
+                if (k0 + PF_BK - 1 > qp0 + (qb0 + qb) * 32 || k0 + PF_BK > L) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int kp = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        if (kp > qp || kp >= L) st[qb][r] = -INFINITY;
+                    }
+                }
+                float mx = m[qb];
+#pragma unroll
+                for (int r = 0; r < 16; r++) mx = fmaxf(mx, st[qb][r]);
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                // A query with no key yet keeps -inf; it subtracts 0 so exp2 gives 0.
+                const float bse = mx == -INFINITY ? 0.f : mx;
+                const float corr = __builtin_amdgcn_exp2f(m[qb] - bse);
+                float sum = 0.f;
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int kp = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    if (kp > qp || kp >= L) st[r] = -INFINITY;
+                    st[qb][r] = __builtin_amdgcn_exp2f(st[qb][r] - bse);
+                    sum += st[qb][r];
                 }
+                sum += __shfl_xor(sum, 32, 64);
+                l[qb] = l[qb] * corr + sum;
+                m[qb] = mx;
+                // Rescale only when some query's max moved (rare after the
+                // first tiles).
+                if (__any(corr != 1.f)) {
+#pragma unroll
+                    for (int db = 0; db < 8; db++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) o[qb][db][r] *= corr;
+                }
+                // P^T (bf16) as the B operand: step kk, element e <-> key
+                // 16 kk + 8 (e / 4) + 4 lh + e % 4, i.e. register 8 kk + e.
+#pragma unroll
+                for (int kk = 0; kk < 2; kk++)
+                    pb[qb][kk] = make_uint4(pack2_hw(st[qb][8 * kk + 0], st[qb][8 * kk + 1]),
+                                            pack2_hw(st[qb][8 * kk + 2], st[qb][8 * kk + 3]),
+                                            pack2_hw(st[qb][8 * kk + 4], st[qb][8 * kk + 5]),
+                                            pack2_hw(st[qb][8 * kk + 6], st[qb][8 * kk + 7]));
             }
-            float mx = m;
+            // O^T += V^T P^T: each V^T fragment feeds both query blocks.
 #pragma unroll
-            for (int r = 0; r < 16; r++) mx = fmaxf(mx, st[r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            // A query with no key yet keeps -inf; it subtracts 0 so exp2 gives 0.
-            const float bse = mx == -INFINITY ? 0.f : mx;
-            const float corr = __builtin_amdgcn_exp2f(m - bse);
-            float sum = 0.f;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                st[r] = __builtin_amdgcn_exp2f(st[r] - bse);
-                sum += st[r];
-            }
-            sum += __shfl_xor(sum, 32, 64);
-            l = l * corr + sum;
-            m = mx;
-#pragma unroll
-            for (int db = 0; db < 8; db++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) o[db][r] *= corr;
-            // P^T (bf16) as the B operand: step kk, element e <-> key
-            // 16 kk + 8 (e / 4) + 4 lh + e % 4, i.e. register 8 kk + e.
-#pragma unroll
-            for (int kk = 0; kk < 2; kk++) {
-                const uint4 pb = make_uint4(pack2(st[8 * kk + 0], st[8 * kk + 1]), pack2(st[8 * kk + 2], st[8 * kk + 3]),
-                                            pack2(st[8 * kk + 4], st[8 * kk + 5]), pack2(st[8 * kk + 6], st[8 * kk + 7]));
+            for (int kk = 0; kk < 2; kk++)
 #pragma unroll
                 for (int db = 0; db < 8; db++) {
                     const uint16_t* vrow = Vt + (32 * db + lq) * PF_VSTR + 16 * kk + 4 * lh;
                     const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
                     const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)),
-                                                                   as_bf16x8(pb), o[db], 0, 0, 0);
+                    const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                    for (int qb = 0; qb < PF_NQB; qb++)
+                        o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pb[qb][kk]), o[qb][db], 0, 0, 0);
                 }
-            }
         }
         if (it + 1 < ntiles) {
             __syncthreads();  // everyone is done with the buffer two tiles back
@@ -213,23 +266,28 @@ __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p)
             __syncthreads();
         }
     }
-    if (myq >= nb) return;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const size_t t = (size_t)tb + myq;
-    const uint16_t* gate = p.qkv + t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM;
-    uint16_t* orow = p.out + (t * p.Hq + h) * HEAD_DIM;
 #pragma unroll
-    for (int db = 0; db < 8; db++)
+    for (int qb = 0; qb < PF_NQB; qb++) {
+        const int myq = (qb0 + qb) * 32 + lq;
+        if (myq >= nb) continue;
+        const float inv = l[qb] > 0.f ? 1.f / l[qb] : 0.f;
+        const size_t t = (size_t)tb + myq;
+        const uint16_t* gate = p.qkv + t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM;
+        uint16_t* orow = p.out + (t * p.Hq + h) * HEAD_DIM;
 #pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) {
-            const int d = 32 * db + 8 * g4 + 4 * lh;
-            const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
-            *reinterpret_cast<uint2*>(orow + d) =
-                make_uint2(pack2(rbf(o[db][4 * g4] * inv) / (1.f + __expf(-bf_lo(graw.x))),
-                                 rbf(o[db][4 * g4 + 1] * inv) / (1.f + __expf(-bf_hi(graw.x)))),
-                           pack2(rbf(o[db][4 * g4 + 2] * inv) / (1.f + __expf(-bf_lo(graw.y))),
-                                 rbf(o[db][4 * g4 + 3] * inv) / (1.f + __expf(-bf_hi(graw.y)))));
-        }
+        for (int db = 0; db < 8; db++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const int d = 32 * db + 8 * g4 + 4 * lh;
+                const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
+                const f32x16& oo = o[qb][db];
+                *reinterpret_cast<uint2*>(orow + d) =
+                    make_uint2(pack2(rbf(oo[4 * g4] * inv) / (1.f + __expf(-bf_lo(graw.x))),
+                                     rbf(oo[4 * g4 + 1] * inv) / (1.f + __expf(-bf_hi(graw.x)))),
+                               pack2(rbf(oo[4 * g4 + 2] * inv) / (1.f + __expf(-bf_lo(graw.y))),
+                                     rbf(oo[4 * g4 + 3] * inv) / (1.f + __expf(-bf_hi(graw.y)))));
+            }
+    }
 }
 
 constexpr size_t prefill_smem_bytes() { return (size_t)2 * (PF_K_ELEMS + PF_V_ELEMS) * 2; }

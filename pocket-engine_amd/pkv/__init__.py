@@ -41,6 +41,7 @@ _SIGS = {
                                  _c_p, _c_f, _c_p, _c_int, _c_p, _c_int, _c_int, _c_i64, _c_p, _c_sz, _c_p]),
     "pkv_attn_decode_config": (_c_int, [_c_int, _c_int]),
     "pkv_time_next_range_kernel": (_c_int, [_c_p, _c_p]),
+    "pkv_time_next_prefill_kernel": (_c_int, [_c_p, _c_p]),
     "pkv_attn_prefill": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_int, _c_p, _c_int,
                                   _c_int, _c_p, _c_f, _c_p, _c_int, _c_int, _c_i64, _c_p]),
     "pkv_attn_decode_step": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p,
@@ -125,6 +126,11 @@ def time_next_range_kernel(start_event, stop_event):
     (or raw hipEvent_t ints) at its start and end."""
     h = lambda e: e if (e is None or isinstance(e, int)) else e.cuda_event
     _check(_lib.pkv_time_next_range_kernel(h(start_event), h(stop_event)), "pkv_time_next_range_kernel")
+
+
+def time_next_prefill_kernel(start_event, stop_event):
+    h = lambda e: e if (e is None or isinstance(e, int)) else e.cuda_event
+    _check(_lib.pkv_time_next_prefill_kernel(h(start_event), h(stop_event)), "pkv_time_next_prefill_kernel")
 
 
 def attn_decode_config(wg_per_cu=1, min_range=32):
