@@ -201,6 +201,85 @@ int pkv_pool_refs(const pkv_pool* pool, uint32_t id);
  * length or a negative status. */
 int64_t pkv_pool_free_list(const pkv_pool* pool, uint32_t* out, int64_t cap);
 
+/* ---------------------------------------------------------------------------
+ * Host: KV manager — sequences' block tables over a pool, the prefix cache,
+ * step metadata, copy-on-write and truncation (the KV bookkeeping of the
+ * reference Scheduler, src/sched.rs). Sequence ids are small ints.
+ * ------------------------------------------------------------------------- */
+
+typedef struct pkv_kv pkv_kv;
+
+/* A manager over n_blocks pages of block_size slots; max_entries bounds the
+ * prefix cache (0 = unbounded; the reference bounds it by its snapshot
+ * slots, sched.rs:530-560). */
+pkv_kv* pkv_kv_create(int64_t n_blocks, int block_size, int64_t max_entries);
+void pkv_kv_destroy(pkv_kv* kv);
+/* The manager's block allocator (for pkv_pool_free_count / _refs). */
+pkv_pool* pkv_kv_pool(pkv_kv* kv);
+
+/* Admission (Scheduler::admit's KV part, sched.rs:669-799): reserves
+ * ceil((prompt_len + max_new) / block_size) blocks; with use_cache, the
+ * longest cached whole-64-token-unit prefix of prompt[..prompt_len-1] is
+ * shared (its blocks gain a reference, *cached = its length, the sequence's
+ * length starts there) and least recently used entries are evicted while
+ * blocks are short. PKV_ERR_NO_BLOCKS leaves the request waiting (entries
+ * already evicted stay evicted, as in the reference). */
+int pkv_kv_admit(pkv_kv* kv, uint32_t adapter, const uint32_t* prompt, int64_t prompt_len, int64_t max_new,
+                 int use_cache, int* seq_id, int64_t* cached);
+/* Longest cached whole-unit prefix leaving one token (sched.rs:832-842). */
+int pkv_kv_lookup(pkv_kv* kv, uint32_t adapter, const uint32_t* prompt, int64_t prompt_len, int64_t* hit_len);
+/* Makes tokens[..len] (len a multiple of 64) of sequence seq_id a cache
+ * entry holding a reference on its len / block_size blocks (add_entry,
+ * sched.rs:1044-1067); evicts the oldest entry first when the cache is full. */
+int pkv_kv_cache_add(pkv_kv* kv, int seq_id, uint32_t adapter, const uint32_t* tokens, int64_t len);
+/* Evicts the least recently used entry (sched.rs:820-828); returns 1 if one was. */
+int pkv_kv_evict_one(pkv_kv* kv);
+int64_t pkv_kv_cache_entries(const pkv_kv* kv);
+/* Drops a sequence and its block references (release, sched.rs:844-854). */
+int pkv_kv_release(pkv_kv* kv, int seq_id);
+
+/* An empty sequence (no blocks) for on-demand growth or sharing. */
+int pkv_kv_new_seq(pkv_kv* kv, int* seq_id);
+/* Ensures blocks for n_tokens positions (take_blocks order, LIFO). */
+int pkv_kv_reserve(pkv_kv* kv, int seq_id, int64_t n_tokens);
+/* Empty sequence dst shares src's first n_tokens (ceil(n / block_size)
+ * pages, a partial last page included): each page gains a reference. */
+int pkv_kv_share(pkv_kv* kv, int dst_id, int src_id, int64_t n_tokens);
+/* Before writing positions [pos, pos + n): grows the table as needed and
+ * copies on write every page in range that another sequence or entry also
+ * references — a fresh page replaces it in this table, its old reference is
+ * dropped, and (cow_src[i], cow_dst[i]) lists the device page copies to run
+ * with pkv_page_copy before the write (*n_copies of them, at most cap). No
+ * reference counterpart: the reference never writes into a shared page. */
+int pkv_kv_prepare_write(pkv_kv* kv, int seq_id, int64_t pos, int n, int32_t* cow_src, int32_t* cow_dst, int cap,
+                         int* n_copies);
+/* Sets the number of positions whose K/V are written ("fed"). */
+int pkv_kv_set_len(pkv_kv* kv, int seq_id, int64_t len);
+/* Speculative rollback: the sequence keeps new_len (<= its length)
+ * positions. free_pages = 0 keeps every reserved page, as the reference does
+ * after rejected drafts (sched.rs:1297-1327); 1 also returns pages wholly
+ * past ceil(new_len / block_size) to the pool (on-demand mode). The kept
+ * positions' bytes are untouched either way. */
+int pkv_kv_truncate(pkv_kv* kv, int seq_id, int64_t new_len, int free_pages);
+int64_t pkv_kv_len(pkv_kv* kv, int seq_id);
+/* Copies the sequence's block table into out (capacity cap); returns its length. */
+int64_t pkv_kv_blocks(pkv_kv* kv, int seq_id, uint32_t* out, int64_t cap);
+
+/* Step metadata (Scheduler::fill's KV arrays, sched.rs:1105-1187): rows
+ * si < nrows feed ntok[si] tokens of sequence seq_ids[si] at positions
+ * len .. len + ntok - 1. Writes pos, slot_map (bt[p / bs] * bs + p % bs),
+ * tok_seq, cu[nrows + 1], limits (blocks * bs - 1) and block_table
+ * [nrows][max_blocks] (unused entries 0), host arrays. */
+int pkv_kv_fill(pkv_kv* kv, const int* seq_ids, const int* ntok, int nrows, int max_tokens, int max_blocks,
+                int32_t* pos, int32_t* slot_map, int32_t* tok_seq, int32_t* cu, int32_t* limits,
+                int32_t* block_table);
+/* Padding rows [from, to) of n tokens each for a graph bucket (Scheduler::pad,
+ * sched.rs:1219-1261): pos = k, slot_map = -1 (no KV write), tok_seq = row,
+ * cu advancing by n, limits = -1, block_table rows 0. Arrays hold max_rows
+ * rows (cu: max_rows + 1) and max_tokens tokens; to * n must fit. */
+int pkv_kv_pad(int from, int to, int n, int max_rows, int max_tokens, int max_blocks, int32_t* pos,
+               int32_t* slot_map, int32_t* tok_seq, int32_t* cu, int32_t* limits, int32_t* block_table);
+
 #ifdef __cplusplus
 }
 #endif

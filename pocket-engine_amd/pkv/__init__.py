@@ -56,6 +56,29 @@ _SIGS = {
     "pkv_pool_total": (_c_i64, [_c_p]),
     "pkv_pool_refs": (_c_int, [_c_p, ctypes.c_uint32]),
     "pkv_pool_free_list": (_c_i64, [_c_p, ctypes.POINTER(ctypes.c_uint32), _c_i64]),
+    "pkv_kv_create": (_c_p, [_c_i64, _c_int, _c_i64]),
+    "pkv_kv_destroy": (None, [_c_p]),
+    "pkv_kv_pool": (_c_p, [_c_p]),
+    "pkv_kv_admit": (_c_int, [_c_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32), _c_i64, _c_i64, _c_int,
+                              ctypes.POINTER(_c_int), ctypes.POINTER(_c_i64)]),
+    "pkv_kv_lookup": (_c_int, [_c_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32), _c_i64,
+                               ctypes.POINTER(_c_i64)]),
+    "pkv_kv_cache_add": (_c_int, [_c_p, _c_int, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32), _c_i64]),
+    "pkv_kv_evict_one": (_c_int, [_c_p]),
+    "pkv_kv_cache_entries": (_c_i64, [_c_p]),
+    "pkv_kv_release": (_c_int, [_c_p, _c_int]),
+    "pkv_kv_new_seq": (_c_int, [_c_p, ctypes.POINTER(_c_int)]),
+    "pkv_kv_reserve": (_c_int, [_c_p, _c_int, _c_i64]),
+    "pkv_kv_share": (_c_int, [_c_p, _c_int, _c_int, _c_i64]),
+    "pkv_kv_prepare_write": (_c_int, [_c_p, _c_int, _c_i64, _c_int, ctypes.POINTER(ctypes.c_int32),
+                                      ctypes.POINTER(ctypes.c_int32), _c_int, ctypes.POINTER(_c_int)]),
+    "pkv_kv_set_len": (_c_int, [_c_p, _c_int, _c_i64]),
+    "pkv_kv_truncate": (_c_int, [_c_p, _c_int, _c_i64, _c_int]),
+    "pkv_kv_len": (_c_i64, [_c_p, _c_int]),
+    "pkv_kv_blocks": (_c_i64, [_c_p, _c_int, ctypes.POINTER(ctypes.c_uint32), _c_i64]),
+    "pkv_kv_fill": (_c_int, [_c_p, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), _c_int, _c_int, _c_int] +
+                    [ctypes.POINTER(ctypes.c_int32)] * 6),
+    "pkv_kv_pad": (_c_int, [_c_int] * 6 + [ctypes.POINTER(ctypes.c_int32)] * 6),
 }
 _SIGS["pkv_attn_decode_split"] = _SIGS["pkv_attn_decode"]
 _SIGS["pkv_attn_decode_merge"] = _SIGS["pkv_attn_decode"]
@@ -177,6 +200,7 @@ class Pool:
     src/sched.rs:461-465, 515, 801-817)."""
 
     def __init__(self, n_blocks):
+        self._lib = _lib  # keeps the library alive until this handle is destroyed
         self._h = _lib.pkv_pool_create(n_blocks)
         if not self._h:
             raise PkvError(ERR_INVALID, "pkv_pool_create")
@@ -184,7 +208,7 @@ class Pool:
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:
-            _lib.pkv_pool_destroy(h)
+            self._lib.pkv_pool_destroy(h)
             self._h = None
 
     @staticmethod
@@ -222,6 +246,129 @@ class Pool:
         buf = (ctypes.c_uint32 * max(1, n))()
         _lib.pkv_pool_free_list(self._h, buf, n)
         return list(buf[:n])
+
+
+def _u32(tokens):
+    tokens = list(tokens)
+    return (ctypes.c_uint32 * max(1, len(tokens)))(*tokens), len(tokens)
+
+
+class Kv:
+    """KV manager: block tables, prefix cache, step metadata, copy-on-write
+    and truncation (include/pkv.h pkv_kv_*; the reference Scheduler's KV
+    bookkeeping, src/sched.rs)."""
+
+    def __init__(self, n_blocks, block_size=16, max_entries=0):
+        self._lib = _lib
+        self._h = _lib.pkv_kv_create(n_blocks, block_size, max_entries)
+        if not self._h:
+            raise PkvError(ERR_INVALID, "pkv_kv_create")
+        self.block_size = block_size
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self._lib.pkv_kv_destroy(h)
+            self._h = None
+
+    def free_count(self):
+        return _lib.pkv_pool_free_count(_lib.pkv_kv_pool(self._h))
+
+    def refs(self, page):
+        return _lib.pkv_pool_refs(_lib.pkv_kv_pool(self._h), page)
+
+    def admit(self, prompt, max_new, use_cache=True, adapter=0):
+        """Returns (seq_id, cached_tokens); raises PkvError(ERR_NO_BLOCKS) when the request must wait."""
+        buf, n = _u32(prompt)
+        sid, cached = _c_int(0), _c_i64(0)
+        _check(_lib.pkv_kv_admit(self._h, adapter, buf, n, max_new, int(use_cache), ctypes.byref(sid),
+                                 ctypes.byref(cached)), "pkv_kv_admit")
+        return sid.value, cached.value
+
+    def lookup(self, prompt, adapter=0):
+        buf, n = _u32(prompt)
+        hit = _c_i64(0)
+        _check(_lib.pkv_kv_lookup(self._h, adapter, buf, n, ctypes.byref(hit)), "pkv_kv_lookup")
+        return hit.value
+
+    def cache_add(self, seq, tokens, adapter=0):
+        buf, n = _u32(tokens)
+        _check(_lib.pkv_kv_cache_add(self._h, seq, adapter, buf, n), "pkv_kv_cache_add")
+
+    def evict_one(self):
+        return bool(_lib.pkv_kv_evict_one(self._h))
+
+    def entries(self):
+        return _lib.pkv_kv_cache_entries(self._h)
+
+    def release(self, seq):
+        _check(_lib.pkv_kv_release(self._h, seq), "pkv_kv_release")
+
+    def new_seq(self):
+        sid = _c_int(0)
+        _check(_lib.pkv_kv_new_seq(self._h, ctypes.byref(sid)), "pkv_kv_new_seq")
+        return sid.value
+
+    def reserve(self, seq, n_tokens):
+        _check(_lib.pkv_kv_reserve(self._h, seq, n_tokens), "pkv_kv_reserve")
+
+    def share(self, dst, src, n_tokens):
+        _check(_lib.pkv_kv_share(self._h, dst, src, n_tokens), "pkv_kv_share")
+
+    def prepare_write(self, seq, pos, n, cap=64):
+        """Returns the (src, dst) page copies copy-on-write needs before writing [pos, pos + n)."""
+        src, dst, k = (ctypes.c_int32 * cap)(), (ctypes.c_int32 * cap)(), _c_int(0)
+        _check(_lib.pkv_kv_prepare_write(self._h, seq, pos, n, src, dst, cap, ctypes.byref(k)), "pkv_kv_prepare_write")
+        return list(src[:k.value]), list(dst[:k.value])
+
+    def set_len(self, seq, n):
+        _check(_lib.pkv_kv_set_len(self._h, seq, n), "pkv_kv_set_len")
+
+    def truncate(self, seq, new_len, free_pages=False):
+        _check(_lib.pkv_kv_truncate(self._h, seq, new_len, int(free_pages)), "pkv_kv_truncate")
+
+    def len(self, seq):
+        n = _lib.pkv_kv_len(self._h, seq)
+        if n < 0:
+            raise PkvError(-n, "pkv_kv_len")
+        return n
+
+    def blocks(self, seq):
+        n = _lib.pkv_kv_blocks(self._h, seq, None, 0)
+        if n < 0:
+            raise PkvError(-n, "pkv_kv_blocks")
+        buf = (ctypes.c_uint32 * max(1, n))()
+        _lib.pkv_kv_blocks(self._h, seq, buf, n)
+        return list(buf[:n])
+
+    def fill(self, rows, max_tokens, max_blocks, max_rows=None):
+        """rows: [(seq, ntok)]. Returns a dict of numpy int32 arrays (pos, slot_map, tok_seq, cu, limits,
+        block_table) sized for max_rows rows (default len(rows)), the reference's Meta arrays for the step."""
+        import numpy as np
+        nrows = len(rows)
+        max_rows = max(nrows, max_rows or 0)
+        ids = (_c_int * max(1, nrows))(*[r[0] for r in rows])
+        nt = (_c_int * max(1, nrows))(*[r[1] for r in rows])
+        out = {k: np.zeros(n, np.int32) for k, n in (("pos", max_tokens), ("slot_map", max_tokens),
+                                                       ("tok_seq", max_tokens), ("cu", max_rows + 1),
+                                                       ("limits", max(1, max_rows)),
+                                                       ("block_table", max(1, max_rows) * max_blocks))}
+        P = ctypes.POINTER(ctypes.c_int32)
+        args = [out[k].ctypes.data_as(P) for k in ("pos", "slot_map", "tok_seq", "cu", "limits", "block_table")]
+        _check(_lib.pkv_kv_fill(self._h, ids, nt, nrows, max_tokens, max_blocks, *args), "pkv_kv_fill")
+        out["block_table"] = out["block_table"].reshape(-1, max_blocks)
+        return out
+
+
+def pad_rows(meta, frm, to, n):
+    """Writes padding rows [frm, to) of n tokens into a fill() dict in place."""
+    import ctypes as C
+    P = C.POINTER(C.c_int32)
+    max_rows, max_tokens = len(meta["cu"]) - 1, len(meta["pos"])
+    max_blocks = meta["block_table"].shape[1]
+    bt = meta["block_table"]
+    args = [meta[k].ctypes.data_as(P) for k in ("pos", "slot_map", "tok_seq", "cu", "limits")] + [bt.ctypes.data_as(P)]
+    _check(_lib.pkv_kv_pad(frm, to, n, max_rows, max_tokens, max_blocks, *args), "pkv_kv_pad")
 
 
 def exported_symbols():
