@@ -66,9 +66,10 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--seed", type=int, default=None, help="length-mix seed (default: fresh per run)")
-    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4"],
+    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5"],
                     help="c3 (default, the metric): batch-64 decode step; c2: single-sequence decode at 4096 "
-                         "context; c4: chunked prefill of 8 x 2048 tokens over a shared 16,384-token prefix")
+                         "context; c4: chunked prefill of 8 x 2048 tokens over a shared 16,384-token prefix; "
+                         "c5: speculative verify of 4 drafts x 16 sequences at 32k..128k context")
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--pages", type=int, default=65536)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -77,6 +78,8 @@ def main():
     ap.add_argument("--graph", action="store_true", help="replay each step from a captured HIP graph")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 2 GiB device copy (x3), to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--verify-kernel", action="store_true",
+                    help="c2/c3 unfused through the verify kernels (pkv_attn_verify) instead of decode")
     ap.add_argument("--unfused", action="store_true",
                     help="append, key ranges and merge as three launches instead of the fused step")
     args = ap.parse_args()
@@ -103,6 +106,8 @@ def main():
 
     if args.config == "c4":
         return bench_prefill(args)
+    if args.config == "c5":
+        return bench_verify(args)
 
     if args.wg_per_cu or args.min_range:
         pkv.attn_decode_config(args.wg_per_cu or 1, args.min_range or 32)
@@ -134,7 +139,10 @@ def main():
     ts = torch.from_numpy(steps[0]["tok_seq"]).to(dev)
     cu = torch.from_numpy(steps[0]["cu"]).to(dev)
     bt = torch.from_numpy(meta.block_table).to(dev)
-    ws = torch.empty(pkv.attn_decode_workspace(B, Hq), dtype=torch.uint8, device=dev)
+    ws = torch.empty(max(pkv.attn_decode_workspace(B, Hq), pkv.attn_verify_workspace(B, Hq)), dtype=torch.uint8,
+                     device=dev)
+    if args.verify_kernel:
+        args.unfused = True
     k_rows = qkv.data_ptr() + 2 * (2 * Hq * D)
     v_rows = k_rows + 2 * (Hkv * D)
     stream = torch.cuda.current_stream()
@@ -145,7 +153,8 @@ def main():
         s_ = strm.cuda_stream
         if args.unfused:
             pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=s_)
-            pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu,
+            fn = pkv.attn_verify if args.verify_kernel else pkv.attn_decode
+            fn(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu,
                             0, None, 1, B, pages, ws, stream=s_)
         else:
             pkv.attn_decode_step(k_rows, v_rows, qstride * 2, slot_d[i], q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts,
@@ -207,7 +216,7 @@ def main():
         # key-range kernel: every key's K and V rows (all kv heads) + q; its
         # partials are overhead, not algorithmic.
         kern_bytes = [kk * Hkv * D * 2 * 2 + B * Hq * D * 2 for kk in keys]
-        kname = "decode_range_kernel<4,false>"
+        kname = "verify_range_kernel" if args.verify_kernel else "decode_range_kernel<4,false>"
     else:
         kern_bytes = step_bytes  # the fused kernel does the whole step
         kname = "decode_range_kernel<4,true> (fused append + attention + merge)"
@@ -330,6 +339,123 @@ def bench_prefill(args):
         "roofline": {"bound": "mfma", "kernel": "prefill_kernel", "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "avg_us": round(kern_us, 1), "traffic": None},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_verify(args):
+    """Config 5: 16 sequences with U[32768, 131072] cached tokens; a step
+    appends 4 draft rows per sequence (pkv_append) and verifies them
+    (pkv_attn_verify: each row attends causally, every page read once for
+    the sequence's 4 rows), then the host rewinds each sequence to its
+    accepted length (seeded a in 0..4: length += a + 1; pages stay reserved
+    as the reference's finish does, src/sched.rs:1297-1327). Unique bytes
+    per step = sum over sequences of (len + 4) keys x 4 KiB + append + q,
+    gate, out. The same steps through per-token decode attention (each row
+    re-reads its sequence's pages, as the reference) ride along."""
+    import numpy as np
+    import torch
+
+    import pkv
+    from pkv import synth
+
+    seed = args.seed if args.seed is not None else int(time.time()) % 100000
+    dev = torch.device("cuda:0")
+    Hq, Hkv, D, BS, B, n = 16, 4, 256, 16, 16, 4
+    S = args.warmup + args.steps
+    rng = np.random.default_rng(seed)
+    L0 = rng.integers(32768, 131072 + 1, size=B).astype(np.int64)
+    acc = rng.integers(0, n + 1, size=(S, B))  # accepted drafts per step
+    lens = L0 + np.concatenate([np.zeros((1, B), np.int64), np.cumsum(acc + 1, axis=0)[:-1]])  # [S][B]
+    need = (lens[-1] + n + BS - 1) // BS
+    pages = int(need.sum()) + 16
+    mb = int(need.max())
+    perm = rng.permutation(pages).astype(np.int32)
+    bt = np.zeros((B, mb), np.int32)
+    at = 0
+    for s_ in range(B):
+        bt[s_, :need[s_]] = perm[at:at + need[s_]]
+        at += need[s_]
+    pos = (lens[:, :, None] + np.arange(n)[None, None, :]).reshape(S, B * n).astype(np.int32)
+    seqs = np.repeat(np.arange(B), n)
+    slot = (bt[seqs[None, :], pos // BS] * BS + pos % BS).astype(np.int32)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    kc = torch.empty(pages * BS, Hkv, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty_like(kc)
+    for t in (kc, vc):
+        for i in range(0, t.shape[0], 1 << 18):
+            t[i:i + (1 << 18)] = torch.randn(t[i:i + (1 << 18)].shape, device=dev, generator=gen) * 0.5
+    T = B * n
+    q = (torch.randn(T, Hq, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    qstride = synth.qkv_stride(Hq, Hkv)
+    qkv = (torch.randn(T, qstride, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    out = torch.empty(T, Hq, D, dtype=torch.bfloat16, device=dev)
+    pos_d, slot_d = torch.from_numpy(pos).to(dev), torch.from_numpy(slot).to(dev)
+    ts = torch.from_numpy(seqs.astype(np.int32)).to(dev)
+    cu = torch.from_numpy((np.arange(B + 1) * n).astype(np.int32)).to(dev)
+    outs = torch.zeros(B, dtype=torch.int32, device=dev)  # every sequence verifies (spec rows)
+    bt_d = torch.from_numpy(bt).to(dev)
+    ws = torch.empty(max(pkv.attn_verify_workspace(T, Hq), pkv.attn_decode_workspace(T, Hq)), dtype=torch.uint8,
+                     device=dev)
+    k_rows = qkv.data_ptr() + 2 * (2 * Hq * D)
+    v_rows = k_rows + 2 * Hkv * D
+    stream = torch.cuda.current_stream()
+
+    def step(i, ev=None, fn=pkv.attn_verify):
+        pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], T, Hkv, D * 2, kc, vc, pages * BS)
+        if ev:
+            pkv.time_next_range_kernel(ev[0], ev[1])
+        fn(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt_d, mb, BS, out, 1 / 16, cu, 1, outs, 1, T, pages, ws)
+
+    def timed(fn, k0, K):
+        evs = HipEvents(K)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for k in range(K):
+            step(k0 + k, evs.pairs[k], fn)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1), evs.elapsed_ms()
+
+    for i in range(args.warmup):
+        step(i)
+    total_ms, kern_ms = timed(pkv.attn_verify, args.warmup, args.steps)
+    ms_step = total_ms / args.steps
+    keys = [int((lens[args.warmup + k] + n).sum()) for k in range(args.steps)]  # unique keys per step
+    step_bytes = [kk * Hkv * D * 2 * 2 + 3 * T * Hq * D * 2 + synth.algorithmic_bytes_append(T, Hkv) for kk in keys]
+    gbs = sum(step_bytes) / (total_ms * 1e-3) / 1e9
+    kern_bytes = [kk * Hkv * D * 2 * 2 + T * Hq * D * 2 for kk in keys]
+    kern_gbs = sum(kern_bytes) / (sum(kern_ms) * 1e-3) / 1e9
+    kern_avg_us = 1e3 * sum(kern_ms) / len(kern_ms)
+    # per-token decode attention on the same steps (each row re-reads its pages)
+    Kd = min(args.steps, 20)
+    dec_ms, _ = timed(pkv.attn_decode, args.warmup, Kd)
+    line = {
+        "metric": "speculative verify step us + achieved HBM GB/s over unique KV bytes (config 5), 1 MI355X",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "us_per_step": round(ms_step * 1e3, 2),
+        "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "us_per_step_per_token_decode": round(1e3 * dec_ms / Kd, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 K/V/q, U[32768,131072] contexts, seeded accepted counts)",
+        "config": {"workload": "c5: 16 seqs x 4 draft rows, append + verify attention + rewind",
+                   "batch": B, "drafts": n, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
+                   "pool_pages": pages, "seed": seed, "mean_unique_keys_per_step": round(float(np.mean(keys)), 1),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "verify_range_kernel", "achieved": round(kern_gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
+                     "avg_us": round(kern_avg_us, 2), "traffic": None},
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)

@@ -138,8 +138,25 @@ int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_str
                          int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* Draft-verify attention: the same results as pkv_attn_decode (every
+ * decode row t attends keys 0..pos[t] of its sequence, gated output), for
+ * batches whose sequences feed several rows at once — the reference's
+ * speculative rows (is_spec, src/kernels/qwen35.cu:94-100), which its
+ * attn_paged_g<G> serves one token per block, each re-reading the
+ * sequence's pages (launched at src/model.rs:2366-2437). Here up to 4
+ * consecutive rows of a sequence share one pass over its pages. `cu` is
+ * required and each sequence's rows must be consecutive (cu[s] ..
+ * cu[s+1]-1, as Scheduler::fill writes them, src/sched.rs:1105-1115).
+ * Workspace: pkv_attn_verify_workspace bytes. Shapes as pkv_attn_decode. */
+int pkv_attn_verify_workspace(int T, int Hq, size_t* bytes);
+int pkv_attn_verify(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
+                    int Hkv, const int32_t* pos, const int32_t* tok_seq, const int32_t* block_table, int max_blocks,
+                    int block_size, void* out, float scale, const int32_t* cu, int skip_prompts,
+                    const int32_t* outs, int spec, int T, int64_t num_blocks, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 /* Measurement: the next key-range kernel this thread launches (the dominant
- * kernel of pkv_attn_decode / _split / _step) records start_event when it
+ * kernel of pkv_attn_decode / _split / _step / pkv_attn_verify) records start_event when it
  * starts executing and stop_event when it ends (hipExtLaunchKernelGGL), so
  * hipEventElapsedTime gives its own duration without dispatch gaps, like the
  * reference's Gpu::time_us event timing (src/gpu.rs:1461-1510). Events are

@@ -4,6 +4,7 @@
 #include "pkv_copy.hip"
 #include "pkv_decode.hip"
 #include "pkv_prefill.hip"
+#include "pkv_verify.hip"
 #include "../../include/pkv.h"
 
 #include <hip/hip_ext.h>
@@ -58,9 +59,11 @@ struct DecodeLayout {
     size_t offs, ms, acc, total;
 };
 
-DecodeLayout decode_layout(int T, int Hq, int n_wg) {
+// Partial rows: (T + n_wg) indices x Hq heads, times 4 query rows per index
+// for the verify kernel.
+DecodeLayout decode_layout(int T, int Hq, int n_wg, bool verify = false) {
     DecodeLayout d;
-    const size_t rows = (size_t)(T + n_wg) * Hq;
+    const size_t rows = (size_t)(T + n_wg) * Hq * (verify ? pkv::VF_ROWS : 1);
     d.offs = 0;
     d.ms = round_up((size_t)(T + 2) * 4, 256);
     d.acc = d.ms + round_up(rows * 2 * 4, 256);
@@ -199,6 +202,12 @@ int pkv_attn_decode_workspace(int T, int Hq, size_t* bytes) {
     return PKV_OK;
 }
 
+int pkv_attn_verify_workspace(int T, int Hq, size_t* bytes) {
+    if (T < 0 || Hq <= 0 || !bytes) return PKV_ERR_INVALID;
+    *bytes = decode_layout(T, Hq, decode_n_wg(), true).total;
+    return PKV_OK;
+}
+
 }  // extern "C"
 
 namespace {
@@ -211,7 +220,9 @@ struct AppendArgs {
 };
 
 // phase bit 1: key-range kernel; bit 2: merge kernel; bit 4: the key-range
-// kernel with the step's append fused in (needs `app`).
+// kernel with the step's append fused in (needs `app`); bit 8: the verify
+// kernels (rows grouped by sequence, 4 per page pass) instead of per-token
+// decode (with bits 1 and 2).
 int attn_decode_phases(int phases, const AppendArgs* app, const void* q, const void* kcache, const void* vcache,
                        const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos, const int32_t* tok_seq,
                        const int32_t* block_table, int max_blocks, int block_size, void* out, float scale,
@@ -223,7 +234,9 @@ int attn_decode_phases(int phases, const AppendArgs* app, const void* q, const v
     if (T == 0) return PKV_OK;
     if (!q || !kcache || !vcache || !qkv || !pos || !tok_seq || !block_table || !out || !workspace)
         return PKV_ERR_INVALID;
-    if (skip_prompts && !cu) return PKV_ERR_INVALID;
+    if ((skip_prompts || (phases & 8)) && !cu) return PKV_ERR_INVALID;
+    const bool verify = phases & 8;
+    if (verify && (phases & 4)) return PKV_ERR_INVALID;
     if (qstride < 2 * Hq * pkv::HEAD_DIM || qstride % 8 != 0) return PKV_ERR_INVALID;
     if (!aligned(q, 16) || !aligned(kcache, 16) || !aligned(vcache, 16) || !aligned(qkv, 16) || !aligned(out, 16) ||
         !aligned(workspace, 256))
@@ -236,7 +249,7 @@ int attn_decode_phases(int phases, const AppendArgs* app, const void* q, const v
             return PKV_ERR_INVALID;
     }
     const int n_wg = decode_n_wg();
-    const DecodeLayout lay = decode_layout(T, Hq, n_wg);
+    const DecodeLayout lay = decode_layout(T, Hq, n_wg, verify);
     if (workspace_bytes < lay.total) return PKV_ERR_INVALID;
     pkv::DecodeParams p;
     p.q = (const uint16_t*)q;
@@ -266,7 +279,10 @@ int attn_decode_phases(int phases, const AppendArgs* app, const void* q, const v
     if (phases & 5) {
         hipEvent_t e0 = t_ev_start, e1 = t_ev_stop;
         t_ev_start = t_ev_stop = nullptr;
-        if (phases & 4)
+        if (verify)
+            hipExtLaunchKernelGGL(pkv::verify_range_kernel, dim3(n_wg, groups), dim3(threads), 0, (hipStream_t)stream,
+                                  e0, e1, 0, p, pos, tok_seq, block_table, cu, outs);
+        else if (phases & 4)
             hipExtLaunchKernelGGL((pkv::decode_range_kernel<4, true>), dim3(n_wg, groups), dim3(threads), 0,
                                   (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs, slot_map);
         else
@@ -275,8 +291,13 @@ int attn_decode_phases(int phases, const AppendArgs* app, const void* q, const v
         const int st = launch_status();
         if (st != PKV_OK) return st;
     }
+    if ((phases & 2) && verify) {
+        hipLaunchKernelGGL(pkv::verify_merge_kernel, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p, pos,
+                           tok_seq, cu, outs);
+        return launch_status();
+    }
     if (phases & 2) {
-        hipLaunchKernelGGL(pkv::decode_merge_kernel, dim3(T, (Hq + 3) / 4), dim3(256), 0, (hipStream_t)stream, p);
+        hipLaunchKernelGGL(pkv::decode_merge_kernel, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p);
         return launch_status();
     }
     return PKV_OK;
@@ -298,6 +319,8 @@ extern "C" {
 int pkv_attn_decode(PKV_DECODE_ARGS) { return attn_decode_phases(3, nullptr, PKV_DECODE_PASS); }
 int pkv_attn_decode_split(PKV_DECODE_ARGS) { return attn_decode_phases(1, nullptr, PKV_DECODE_PASS); }
 int pkv_attn_decode_merge(PKV_DECODE_ARGS) { return attn_decode_phases(2, nullptr, PKV_DECODE_PASS); }
+
+int pkv_attn_verify(PKV_DECODE_ARGS) { return attn_decode_phases(8 | 3, nullptr, PKV_DECODE_PASS); }
 
 int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map,
                          PKV_DECODE_ARGS) {

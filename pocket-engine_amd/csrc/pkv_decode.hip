@@ -114,54 +114,82 @@ __device__ __forceinline__ uint2 gate4(float a0, float a1, float a2, float a3, f
     return make_uint2(pack2(y0, y1), pack2(y2, y3));
 }
 
-// Combines the n partials of token t (indices t + b0 .. t + b0 + n - 1) for
-// query heads [h0, h1), a wave per head at a time and 4 dims per lane: the
-// maximum over the partials is taken 64 at a time across the lanes, then the
-// weighted sums stream the partials 4 at a time (reference attn_merge,
-// qwen35.cu:2255-2273, in exp2 units).
-__device__ __forceinline__ void merge_token(const DecodeParams& p, int t, int b0, int n, int h0, int h1) {
-    const int lane = threadIdx.x & 63, d = 4 * lane;
-    for (int h = h0 + (threadIdx.x >> 6); h < h1; h += blockDim.x >> 6) {
-        const float* ms = p.part_ms + ((size_t)(t + b0) * p.Hq + h) * 2;
-        const float* acc = p.part_acc + ((size_t)(t + b0) * p.Hq + h) * HEAD_DIM + d;
-        const size_t step = (size_t)p.Hq;  // partial i + 1 is Hq rows further
-        float M = -INFINITY;
-        for (int i = lane; i < n; i += 64) M = fmaxf(M, ms[i * step * 2]);
+// Combines n partials of token t for query head h into its gated output:
+// partial i is row (base + i * stride) * Hq + h of part_ms / part_acc (max in
+// log2 units, sum, weighted values; reference attn_merge,
+// qwen35.cu:2255-2273, in exp2 units). One block of 256 threads: wave w
+// folds partials w, w + 4, .. into a running (max, sum, values) with 16
+// partials in flight per lane (4 dims per lane), then the 4 waves' results
+// are combined through LDS. Every thread reaches the block-wide syncs.
+__device__ __forceinline__ void merge_head(const DecodeParams& p, int t, int base, int stride, int n, int h) {
+    constexpr int U = 16;
+    __shared__ __align__(16) float sh_a[4][HEAD_DIM + 4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, d = 4 * lane;
+    const size_t step = (size_t)stride * p.Hq;  // rows from one partial to the next
+    const float* ms = p.part_ms + ((size_t)base * p.Hq + h) * 2;
+    const float* acc = p.part_acc + ((size_t)base * p.Hq + h) * HEAD_DIM + d;
+    float M = -INFINITY, S = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
+    for (int i0 = w; i0 < n; i0 += 4 * U) {
+        float2 mu[U];
+        float4 au[U];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-        float S = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
-        int i = 0;
-        for (; i + 4 <= n; i += 4) {
-            float2 m4[4];
-            float4 a4[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                m4[u] = *reinterpret_cast<const float2*>(ms + (i + u) * step * 2);
-                a4[u] = *reinterpret_cast<const float4*>(acc + (i + u) * step * HEAD_DIM);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const float f = m4[u].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m4[u].x - M);
-                S += m4[u].y * f;
-                A0 += a4[u].x * f;
-                A1 += a4[u].y * f;
-                A2 += a4[u].z * f;
-                A3 += a4[u].w * f;
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + 4 * u;
+            if (i < n) {
+                mu[u] = *reinterpret_cast<const float2*>(ms + i * step * 2);
+                au[u] = *reinterpret_cast<const float4*>(acc + i * step * HEAD_DIM);
+            } else {
+                mu[u] = make_float2(-INFINITY, 0.f);
+                au[u] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
-        for (; i < n; i++) {
-            const float2 m = *reinterpret_cast<const float2*>(ms + i * step * 2);
-            const float4 a = *reinterpret_cast<const float4*>(acc + i * step * HEAD_DIM);
-            const float f = m.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m.x - M);
-            S += m.y * f;
-            A0 += a.x * f;
-            A1 += a.y * f;
-            A2 += a.z * f;
-            A3 += a.w * f;
+        float Mn = M;
+#pragma unroll
+        for (int u = 0; u < U; u++) Mn = fmaxf(Mn, mu[u].x);
+        if (Mn == -INFINITY) continue;  // nothing attended yet
+        const float c = __builtin_amdgcn_exp2f(M - Mn);  // 0 while M = -inf
+        S *= c;
+        A0 *= c;
+        A1 *= c;
+        A2 *= c;
+        A3 *= c;
+        M = Mn;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float f = __builtin_amdgcn_exp2f(mu[u].x - M);  // 0 for an empty partial (-inf)
+            S += mu[u].y * f;
+            A0 += au[u].x * f;
+            A1 += au[u].y * f;
+            A2 += au[u].z * f;
+            A3 += au[u].w * f;
+        }
+    }
+    *reinterpret_cast<float4*>(&sh_a[w][d]) = make_float4(A0, A1, A2, A3);
+    if (lane == 0) {
+        sh_a[w][HEAD_DIM] = M;
+        sh_a[w][HEAD_DIM + 1] = S;
+    }
+    __syncthreads();
+    if (w == 0) {
+        float Mt = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < 4; k++) Mt = fmaxf(Mt, sh_a[k][HEAD_DIM]);
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float mk = sh_a[k][HEAD_DIM];
+            const float f = mk == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mk - Mt);
+            const float4 b = *reinterpret_cast<const float4*>(&sh_a[k][d]);
+            a.x += b.x * f;
+            a.y += b.y * f;
+            a.z += b.z * f;
+            a.w += b.w * f;
+            s += sh_a[k][HEAD_DIM + 1] * f;
         }
         const uint2 graw =
             *reinterpret_cast<const uint2*>(p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d);
-        *reinterpret_cast<uint2*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + d) = gate4(A0, A1, A2, A3, 1.f / S, graw);
+        *reinterpret_cast<uint2*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + d) = gate4(a.x, a.y, a.z, a.w, 1.f / s, graw);
     }
 }
 
@@ -470,7 +498,7 @@ __global__ void __launch_bounds__(256, 1)
 }
 
 // Combines the partials of tokens split over several ranges (after
-// decode_range_kernel<G, false>). One block per (token, 4 query heads).
+// decode_range_kernel). One 256-thread block per (token, query head).
 __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
     const int t = blockIdx.x, T = p.T;
     const int o0 = p.offs[t], o1 = p.offs[t + 1];  // offs[T] = W
@@ -478,8 +506,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
     const int R = p.offs[T + 1];
     const int b0 = o0 / R, b1 = (o1 - 1) / R;
     if (b0 == b1) return;  // finished in place by its range
-    const int h0 = blockIdx.y * 4;
-    merge_token(p, t, b0, b1 - b0 + 1, h0, min(p.Hq, h0 + 4));
+    merge_head(p, t, t + b0, 1, b1 - b0 + 1, blockIdx.y);
 }
 
 template __global__ void decode_range_kernel<4, false>(DecodeParams, const int*, const int*, const int*, const int*,

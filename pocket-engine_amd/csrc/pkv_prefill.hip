@@ -66,10 +66,6 @@ constexpr int PF_NQB = PKV_PF_NQB;
 constexpr int PF_WAVES = 4 * (PF_BQ / 32) / PF_NQB;
 constexpr int PF_THREADS = 64 * PF_WAVES;
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
-
 __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {
     static_assert(PF_BK * HEAD_DIM / 8 % PF_THREADS == 0, "whole 16-byte chunks per thread");
     extern __shared__ __align__(16) uint16_t pf_smem[];

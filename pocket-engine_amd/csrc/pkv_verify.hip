@@ -1,0 +1,262 @@
+// Draft-verify attention for gfx950: the decode rows of a sequence that
+// feeds several tokens in one step (the target pass of speculative decoding,
+// reference is_spec rows, qwen35.cu:94-100, attended by attn_paged_g4 one
+// token at a time, qwen35.cu:1146-1334) read each KV page once for all of
+// them. Same results per row as paged decode attention: row t attends keys
+// [0, pos[t] + 1) (causal among the drafts), online softmax in f32, gated
+// bf16 output, split partials merged in key order.
+//
+// Segments. Up to 4 consecutive rows of one sequence form a segment (rows
+// cu[s] + 4i ..); a segment's keys are [0, max over its rows of L_t). The
+// key space is the segments' keys laid end to end, cut into equal ranges as
+// for decode (one workgroup per range and group of 4 kv heads, a wave per kv
+// head); partials go to index (head token + range index) * 4 + row.
+//
+// Per page (16 keys) a wave computes the 16 x 16 score block of 16 keys
+// against 16 query columns (4 rows x the 4 query heads of its kv head) on
+// MFMA:
+//   S^T[16 keys][16 cols] = K Q^T      8 x v_mfma_f32_16x16x32_bf16
+//     A = K straight from HBM: lane (key l % 16, group l / 16) loads 16
+//     bytes at dims 32c + 8 (l / 16) for c = 0..7 (each instruction reads 64
+//     contiguous bytes of 16 key rows; two consecutive ones a full 128-byte
+//     line). B = Q^T with the same dims, held in registers for the piece.
+//   O^T[256 dims][16 cols] += V^T P^T  16 x v_mfma_f32_16x16x16_bf16
+//     B = P^T is the S^T accumulator itself, rounded to bf16 (lane l holds
+//     keys 4 (l / 16) + i of column l % 16 in both layouts). A = V^T comes
+//     from the page's V staged row-major in LDS (one fully coalesced 512-byte
+//     row per half-wave load) through ds_read_b64_tr_b16, which transposes
+//     4 x 4 blocks of 16-bit values on the way out of LDS.
+// Column softmax: per lane over its 4 keys, then across the 4 lane groups
+// (two cross-lane shuffles). The MFMA work per page is ~0.3 us of one SIMD's
+// time against the ~2.3 us the page's 16 KiB take at the HBM share of a
+// SIMD, so the kernel stays bandwidth-bound with the compute hidden.
+#include "pkv_common.h"
+
+namespace pkv {
+
+constexpr int VF_ROWS = 4;                // query rows per segment
+constexpr int VF_VSTR = HEAD_DIM + 16;    // u16 per staged V row (544 B: conflict-free transposed reads)
+constexpr int VF_LDS = PAGE * VF_VSTR;    // u16 per wave
+
+// Keys of the segment headed by token t; 0 when t does not head a segment
+// (it is not at offset 4i of its sequence) or none of its rows attends.
+__device__ __forceinline__ int seg_len(int t, int T, const int* __restrict__ pos, const int* __restrict__ tok_seq,
+                                       const int* __restrict__ cu, int skip, const int* __restrict__ outs, int spec,
+                                       int& nrows) {
+    const int s = tok_seq[t];
+    nrows = 0;
+    if ((t - cu[s]) & (VF_ROWS - 1)) return 0;
+    nrows = min(VF_ROWS, min(cu[s + 1], T) - t);
+    int L = 0;
+    for (int r = 0; r < nrows; r++) L = max(L, decode_len(t + r, pos, tok_seq, cu, skip, outs, spec));
+    return L;
+}
+
+// One wave: segment headed by token t (rows t + r, r < 4, attending Lr[r]
+// keys; Lr = 0 for absent rows), kv head kvh, keys [j0, j1).
+__device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* __restrict__ bt, uint16_t* vl, int t,
+                                             int kvh, int j0, int j1, int Ls, int L0, int L1, int L2, int L3,
+                                             int idx) {
+    const int lane = threadIdx.x & 63, c16 = lane & 15, gq = lane >> 4;
+    const int r_me = c16 >> 2, g_me = c16 & 3;
+    const int myL = r_me == 0 ? L0 : r_me == 1 ? L1 : r_me == 2 ? L2 : L3;
+    const float sl2 = p.scale * LOG2E;
+    const size_t row_elems = (size_t)p.Hkv * HEAD_DIM;
+
+    bf16x8 qf[8];
+    if (myL > 0) {
+        const uint16_t* qrow = p.q + ((size_t)(t + r_me) * p.Hq + kvh * 4 + g_me) * HEAD_DIM + 8 * gq;
+#pragma unroll
+        for (int c = 0; c < 8; c++) qf[c] = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + 32 * c));
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; c++) qf[c] = as_bf16x8(make_uint4(0, 0, 0, 0));
+    }
+    auto page_base = [&](int pi) -> size_t {
+        long pg = bt[pi];
+        pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
+        return (size_t)pg * PAGE * row_elems + (size_t)kvh * HEAD_DIM;
+    };
+    uint4 kb[8], vb[8];
+    auto load_k = [&](size_t base) {
+        const uint16_t* r = p.kc + base + (size_t)c16 * row_elems + 8 * gq;
+#pragma unroll
+        for (int c = 0; c < 8; c++) kb[c] = load_nt(r + 32 * c);
+    };
+    auto load_v = [&](size_t base) {
+        const uint16_t* r = p.vc + base + (size_t)(lane >> 5) * row_elems + 8 * (lane & 31);
+#pragma unroll
+        for (int k = 0; k < 8; k++) vb[k] = load_nt(r + (size_t)(2 * k) * row_elems);
+    };
+
+    f32x4 acc[16];
+#pragma unroll
+    for (int db = 0; db < 16; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+
+    // transposed-read address of this lane: key row 4 gq + c16 / 4, dims 4 (c16 % 4) + 16 db
+    const uint16_t* tr = vl + (4 * gq + (c16 >> 2)) * VF_VSTR + 4 * (c16 & 3);
+    uint16_t* st = vl + (lane >> 5) * VF_VSTR + 8 * (lane & 31);
+
+    auto page = [&](int pi, size_t next, bool prefetch) {
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 8; c++) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kb[c]), qf[c], s, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 8; k++) *reinterpret_cast<uint4*>(st + 2 * k * VF_VSTR) = vb[k];
+        if (prefetch) {
+            load_k(next);
+            load_v(next);
+        }
+        const int k0 = pi * PAGE + 4 * gq;
+        float sc[4], mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int kp = k0 + i;
+            sc[i] = (kp >= j0 && kp < j1 && kp < myL) ? s[i] * sl2 : -INFINITY;
+            mx = fmaxf(mx, sc[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m, mx);
+        const float mref = mn == -INFINITY ? 0.f : mn;  // a column with no key yet keeps zeros
+        const float corr = __builtin_amdgcn_exp2f(m - mref);
+        const uint32_t p01 = pack2_hw(__builtin_amdgcn_exp2f(sc[0] - mref), __builtin_amdgcn_exp2f(sc[1] - mref));
+        const uint32_t p23 = pack2_hw(__builtin_amdgcn_exp2f(sc[2] - mref), __builtin_amdgcn_exp2f(sc[3] - mref));
+        // the denominator sums the same bf16 weights P.V uses
+        l = l * corr + ((bf_lo(p01) + bf_hi(p01)) + (bf_lo(p23) + bf_hi(p23)));
+        m = mn;
+        if (__any(corr != 1.f)) {
+#pragma unroll
+            for (int db = 0; db < 16; db++) acc[db] *= corr;
+        }
+        const s16x4 pb = __builtin_bit_cast(s16x4, make_uint2(p01, p23));
+        wave_sync();  // V staged
+#pragma unroll
+        for (int db = 0; db < 16; db++) {
+            const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)(tr + 16 * db));
+            acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb, acc[db], 0, 0, 0);
+        }
+        wave_sync();  // reads done before the next page is staged
+    };
+    const int pg0 = j0 / PAGE, pg1 = (j1 - 1) / PAGE;
+    {
+        const size_t b0 = page_base(pg0);
+        load_k(b0);
+        load_v(b0);
+    }
+    for (int pi = pg0; pi < pg1; pi++) page(pi, page_base(pi + 1), true);
+    page(pg1, 0, false);
+
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (myL == 0) return;
+    const int h = kvh * 4 + g_me, tr_row = t + r_me;
+    if (j0 == 0 && j1 == Ls) {
+        const float inv = 1.f / l;
+        const uint16_t* gate = p.qkv + (size_t)tr_row * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + 4 * gq;
+        uint16_t* o = p.out + ((size_t)tr_row * p.Hq + h) * HEAD_DIM + 4 * gq;
+#pragma unroll
+        for (int db = 0; db < 16; db++) {
+            const uint2 graw = *reinterpret_cast<const uint2*>(gate + 16 * db);
+            *reinterpret_cast<uint2*>(o + 16 * db) = gate4(acc[db][0], acc[db][1], acc[db][2], acc[db][3], inv, graw);
+        }
+    } else {
+        const size_t row = ((size_t)idx * VF_ROWS + r_me) * p.Hq + h;
+        float* pa = p.part_acc + row * HEAD_DIM + 4 * gq;
+#pragma unroll
+        for (int db = 0; db < 16; db++)
+            *reinterpret_cast<float4*>(pa + 16 * db) = make_float4(acc[db][0], acc[db][1], acc[db][2], acc[db][3]);
+        if (gq == 0) *reinterpret_cast<float2*>(p.part_ms + row * 2) = make_float2(m, l);
+    }
+}
+
+// Key-range kernel over segments; grid (n_wg, ceil(Hkv / 4)), 64 * min(Hkv, 4)
+// threads. Same range split as decode_range_kernel with segment lengths in
+// place of token lengths; block 0 writes offs[t] (segment offsets by head
+// token, equal neighbours for other tokens), offs[T] = W, offs[T + 1] = R.
+__global__ void __launch_bounds__(256, 1)
+    verify_range_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
+                        const int* __restrict__ block_table, const int* __restrict__ cu,
+                        const int* __restrict__ outs) {
+    __shared__ int sh_scan[16];
+    __shared__ int sh_t0[2];
+    __shared__ __align__(16) uint16_t sh_v[4][VF_LDS];
+    const int T = p.T, nthr = blockDim.x, tid = threadIdx.x, b = blockIdx.x;
+    int W = 0, nr;
+    for (int base = 0; base < T; base += nthr) {
+        const int t = base + tid;
+        const int L = t < T ? seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr) : 0;
+        int tot;
+        block_scan(L, sh_scan, tot);
+        W += tot;
+    }
+    W = __builtin_amdgcn_readfirstlane(W);
+    const int R = max(p.min_range, (W + p.n_wg - 1) / p.n_wg);
+    const int start = b * R, end = min(W, start + R);
+    if (b == 0 && blockIdx.y == 0 && tid == 0) {
+        p.offs[T] = W;
+        p.offs[T + 1] = R;
+    }
+    if (start >= W && b != 0) return;
+    int run = 0;
+    for (int base = 0; base < T; base += nthr) {
+        const int t = base + tid;
+        const int L = t < T ? seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr) : 0;
+        int tot;
+        const int off = run + block_scan(L, sh_scan, tot);
+        if (t < T) {
+            if (b == 0 && blockIdx.y == 0) p.offs[t] = off;
+            if (L > 0 && off <= start && start < off + L) {
+                sh_t0[0] = t;
+                sh_t0[1] = off;
+            }
+        }
+        run += tot;
+        if (b != 0 && run > start) break;
+    }
+    if (start >= W) return;
+    __syncthreads();
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = blockIdx.y * 4 + wave;
+    int t = __builtin_amdgcn_readfirstlane(sh_t0[0]), off = __builtin_amdgcn_readfirstlane(sh_t0[1]);
+    while (off < end && t < T) {
+        const int Ls = __builtin_amdgcn_readfirstlane(seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr));
+        if (Ls > 0) {
+            nr = __builtin_amdgcn_readfirstlane(nr);
+            int Lr[VF_ROWS];
+#pragma unroll
+            for (int r = 0; r < VF_ROWS; r++)
+                Lr[r] = r < nr ? __builtin_amdgcn_readfirstlane(
+                                     decode_len(t + r, pos, tok_seq, cu, p.skip_prompts, outs, p.spec))
+                               : 0;
+            const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
+            const int j0 = max(start, off) - off, j1 = min(end, off + Ls) - off;
+            verify_piece(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Ls, Lr[0], Lr[1],
+                         Lr[2], Lr[3], t + b);
+            off += Ls;
+        }
+        t++;
+    }
+}
+
+// Merges the split segments: one block per (row, query head); row t's
+// segment is headed by the row at offset 4 * floor((t - cu[s]) / 4) of its
+// sequence.
+__global__ void __launch_bounds__(256)
+    verify_merge_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
+                        const int* __restrict__ cu, const int* __restrict__ outs) {
+    const int t = blockIdx.x, T = p.T;
+    if (decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec) <= 0) return;
+    const int c0 = cu[tok_seq[t]];
+    const int r = (t - c0) & (VF_ROWS - 1), th = t - r;
+    if (th < 0) return;
+    const int o0 = p.offs[th], o1 = p.offs[th + 1];
+    if (o1 <= o0) return;
+    const int R = p.offs[T + 1];
+    const int b0 = o0 / R, b1 = (o1 - 1) / R;
+    if (b0 == b1) return;
+    merge_head(p, t, (th + b0) * VF_ROWS + r, VF_ROWS, b1 - b0 + 1, blockIdx.y);
+}
+
+}  // namespace pkv

@@ -81,6 +81,8 @@ _SIGS = {
     "pkv_kv_pad": (_c_int, [_c_int] * 6 + [ctypes.POINTER(ctypes.c_int32)] * 6),
 }
 _SIGS["pkv_attn_decode_split"] = _SIGS["pkv_attn_decode"]
+_SIGS["pkv_attn_verify"] = _SIGS["pkv_attn_decode"]
+_SIGS["pkv_attn_verify_workspace"] = _SIGS["pkv_attn_decode_workspace"]
 _SIGS["pkv_attn_decode_merge"] = _SIGS["pkv_attn_decode"]
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(_lib, _name)
@@ -144,6 +146,12 @@ def attn_decode_workspace(T, Hq):
     return n.value
 
 
+def attn_verify_workspace(T, Hq):
+    n = _c_sz(0)
+    _check(_lib.pkv_attn_verify_workspace(T, Hq, ctypes.byref(n)), "pkv_attn_verify_workspace")
+    return n.value
+
+
 def time_next_range_kernel(start_event, stop_event):
     """Have the next key-range kernel record these torch.cuda.Event objects
     (or raw hipEvent_t ints) at its start and end."""
@@ -185,6 +193,18 @@ def attn_decode(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_ta
                                 _ptr(tok_seq), _ptr(block_table), max_blocks, block_size, _ptr(out), scale,
                                 _ptr(cu), int(skip_prompts), _ptr(outs), spec, T, num_blocks, _ptr(workspace),
                                 workspace_bytes, _stream(stream)), "pkv_attn_decode")
+
+
+def attn_verify(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, out,
+                scale, cu, skip_prompts, outs, spec, T, num_blocks, workspace, workspace_bytes=None, stream=None):
+    """Draft-verify attention: decode semantics per row, up to 4 rows of a
+    sequence per pass over its pages (workspace: attn_verify_workspace)."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace.numel() * workspace.element_size()
+    _check(_lib.pkv_attn_verify(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(qkv), qstride, Hq, Hkv, _ptr(pos),
+                                _ptr(tok_seq), _ptr(block_table), max_blocks, block_size, _ptr(out), scale, _ptr(cu),
+                                int(skip_prompts), _ptr(outs), spec, T, num_blocks, _ptr(workspace), workspace_bytes,
+                                _stream(stream)), "pkv_attn_verify")
 
 
 def attn_prefill(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks, block_size, out,
