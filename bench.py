@@ -39,11 +39,15 @@ class HipEvents:
         self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
         self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.pairs = []
         for _ in range(n):
             a, b = ctypes.c_void_p(), ctypes.c_void_p()
             assert self.hip.hipEventCreate(ctypes.byref(a)) == 0 and self.hip.hipEventCreate(ctypes.byref(b)) == 0
             self.pairs.append((a.value, b.value))
+
+    def record(self, ev, stream):
+        assert self.hip.hipEventRecord(ev, stream) == 0
 
     def elapsed_ms(self):
         import ctypes
@@ -80,6 +84,9 @@ def main():
                     help="only run a plain 2 GiB device copy (x3), to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--verify-kernel", action="store_true",
                     help="c2/c3 unfused through the verify kernels (pkv_attn_verify) instead of decode")
+    ap.add_argument("--refabi", action="store_true",
+                    help="c2/c3 through the reference-ABI code object (pkv_kernels.hsaco: attn_paged_g4 + attn_merge "
+                         "on the reference engine's grid) after pkv_append")
     ap.add_argument("--unfused", action="store_true",
                     help="append, key ranges and merge as three launches instead of the fused step")
     args = ap.parse_args()
@@ -149,8 +156,33 @@ def main():
     sp = stream.cuda_stream
 
 
-    def step_on(i, strm):
+    rk = None
+    if args.refabi:
+        from pkv import refabi
+        rk = refabi.RefKernels()
+        Z = refabi.split_ranges(B, Hkv, torch.cuda.get_device_properties(0).multi_processor_count)
+        part = torch.empty(B * Z * Hq * (D + 2), dtype=torch.float32, device=dev) if Z > 1 else None
+        P_, I_, F_ = refabi.P, refabi.I, refabi.F
+
+    def step_on(i, strm, ev=None):
         s_ = strm.cuda_stream
+        if args.refabi:
+            pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=s_)
+            if ev:
+                kev.record(ev[0], s_)
+            rk.launch("attn_paged_g4", (B, Hkv, Z), 256, 0,
+                      [P_(q), P_(kc), P_(vc), P_(None), P_(None), P_(qkv), I_(qstride), I_(Hq), I_(Hkv),
+                       P_(pos_d[i]), P_(ts), P_(bt), I_(meta.max_blocks), I_(BS), P_(out), F_(1 / 16), P_(None),
+                       P_(None), I_(0), I_(0), P_(cu), I_(0), I_(refabi.SPLIT_MIN_KEYS), P_(part), P_(None), I_(1)],
+                      stream=s_)
+            if ev:
+                kev.record(ev[1], s_)
+            if part is not None:
+                rk.launch("attn_merge", (B, Hq, 1), 256, 0,
+                          [P_(part), I_(Z), I_(refabi.SPLIT_MIN_KEYS), P_(qkv), I_(qstride), I_(Hq), P_(pos_d[i]),
+                           P_(ts), P_(cu), I_(0), P_(out), P_(None), P_(None), I_(0), I_(0), P_(None), I_(1)],
+                          stream=s_)
+            return
         if args.unfused:
             pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=s_)
             fn = pkv.attn_verify if args.verify_kernel else pkv.attn_decode
@@ -163,16 +195,16 @@ def main():
     def step(i, ev=None):
         # ev: the key-range kernel records these HIP events at its own start
         # and end (hipExtLaunchKernelGGL), so no dispatch gap is counted.
-        if ev:
+        if ev and not args.refabi:
             pkv.time_next_range_kernel(ev[0], ev[1])
-        step_on(i, stream)
+        step_on(i, stream, ev)
 
+    kev = HipEvents(args.steps)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
     # Timed region: K steps; events bracket the dominant kernel of each step
     # (the fused step kernel, or the key-range kernel with --unfused).
-    kev = HipEvents(args.steps)
     evs = kev.pairs
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -212,11 +244,12 @@ def main():
     step_bytes = [synth.algorithmic_bytes_decode(kk, B, Hq, Hkv) + synth.algorithmic_bytes_append(B, Hkv)
                   for kk in keys]
     gbs = sum(step_bytes) / (total_ms * 1e-3) / 1e9
-    if args.unfused:
+    if args.unfused or args.refabi:
         # key-range kernel: every key's K and V rows (all kv heads) + q; its
         # partials are overhead, not algorithmic.
         kern_bytes = [kk * Hkv * D * 2 * 2 + B * Hq * D * 2 for kk in keys]
-        kname = "verify_range_kernel" if args.verify_kernel else "decode_range_kernel<4,false>"
+        kname = ("attn_paged_g4 (reference ABI)" if args.refabi else
+                 "verify_range_kernel" if args.verify_kernel else "decode_range_kernel<4,false>")
     else:
         kern_bytes = step_bytes  # the fused kernel does the whole step
         kname = "decode_range_kernel<4,true> (fused append + attention + merge)"
@@ -246,7 +279,8 @@ def main():
         "config": {"workload": ("c3: batch-64 paged decode step (append 1 token/seq + paged decode attention)"
                                 if args.config == "c3" else
                                 "c2: single-sequence paged decode step at 4096 context (append + attention)"),
-                   "path": "unfused (append, key ranges, merge)" if args.unfused else "fused step (one launch)",
+                   "path": ("reference-ABI code object (append, attn_paged_g4, attn_merge)" if args.refabi else
+                            "unfused (append, key ranges, merge)" if args.unfused else "fused step (one launch)"),
                    "batch": B, "ctx": "U[512,8192]", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
                    "pool_pages": pages, "seed": seed, "mean_keys_per_step": round(float(np.mean(keys)), 1),
                    "parallelism": "single GPU"},

@@ -114,20 +114,20 @@ __device__ __forceinline__ uint2 gate4(float a0, float a1, float a2, float a3, f
     return make_uint2(pack2(y0, y1), pack2(y2, y3));
 }
 
-// Combines n partials of token t for query head h into its gated output:
-// partial i is row (base + i * stride) * Hq + h of part_ms / part_acc (max in
-// log2 units, sum, weighted values; reference attn_merge,
-// qwen35.cu:2255-2273, in exp2 units). One block of 256 threads: wave w
-// folds partials w, w + 4, .. into a running (max, sum, values) with 16
-// partials in flight per lane (4 dims per lane), then the 4 waves' results
-// are combined through LDS. Every thread reaches the block-wide syncs.
-__device__ __forceinline__ void merge_head(const DecodeParams& p, int t, int base, int stride, int n, int h) {
+// Combines n partial records of one (row, query head) into its gated
+// output: record i has its (max, sum) at ms_at(i) and its 256 weighted
+// values at acc_at(i); max is in log2 units times mscale (1 for this
+// library's records, log2 e for natural-log records). Same combination as
+// the reference's attn_merge (qwen35.cu:2255-2273). One block of 256
+// threads: wave w folds records w, w + 4, .. into a running (max, sum,
+// values) with 16 records in flight per lane (4 dims per lane), then the 4
+// waves' results are combined through LDS. Every thread reaches the sync.
+template <class MsAt, class AccAt>
+__device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccAt acc_at, const uint16_t* gate,
+                                           uint16_t* out) {
     constexpr int U = 16;
     __shared__ __align__(16) float sh_a[4][HEAD_DIM + 4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, d = 4 * lane;
-    const size_t step = (size_t)stride * p.Hq;  // rows from one partial to the next
-    const float* ms = p.part_ms + ((size_t)base * p.Hq + h) * 2;
-    const float* acc = p.part_acc + ((size_t)base * p.Hq + h) * HEAD_DIM + d;
     float M = -INFINITY, S = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
     for (int i0 = w; i0 < n; i0 += 4 * U) {
         float2 mu[U];
@@ -136,8 +136,11 @@ __device__ __forceinline__ void merge_head(const DecodeParams& p, int t, int bas
         for (int u = 0; u < U; u++) {
             const int i = i0 + 4 * u;
             if (i < n) {
-                mu[u] = *reinterpret_cast<const float2*>(ms + i * step * 2);
-                au[u] = *reinterpret_cast<const float4*>(acc + i * step * HEAD_DIM);
+                mu[u] = *reinterpret_cast<const float2*>(ms_at(i));
+                const float* a = acc_at(i) + d;  // 8-byte aligned
+                const float2 lo = *reinterpret_cast<const float2*>(a), hi = *reinterpret_cast<const float2*>(a + 2);
+                au[u] = make_float4(lo.x, lo.y, hi.x, hi.y);
+                mu[u].x *= mscale;
             } else {
                 mu[u] = make_float2(-INFINITY, 0.f);
                 au[u] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -156,7 +159,7 @@ __device__ __forceinline__ void merge_head(const DecodeParams& p, int t, int bas
         M = Mn;
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const float f = __builtin_amdgcn_exp2f(mu[u].x - M);  // 0 for an empty partial (-inf)
+            const float f = __builtin_amdgcn_exp2f(mu[u].x - M);  // 0 for an empty record (-inf)
             S += mu[u].y * f;
             A0 += au[u].x * f;
             A1 += au[u].y * f;
@@ -187,10 +190,19 @@ __device__ __forceinline__ void merge_head(const DecodeParams& p, int t, int bas
             a.w += b.w * f;
             s += sh_a[k][HEAD_DIM + 1] * f;
         }
-        const uint2 graw =
-            *reinterpret_cast<const uint2*>(p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d);
-        *reinterpret_cast<uint2*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + d) = gate4(a.x, a.y, a.z, a.w, 1.f / s, graw);
+        const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
+        *reinterpret_cast<uint2*>(out + d) = gate4(a.x, a.y, a.z, a.w, 1.f / s, graw);
     }
+}
+
+// Merges this library's partials of token t, query head h: record i is row
+// (base + i * stride) * Hq + h of part_ms / part_acc.
+__device__ __forceinline__ void merge_head(const DecodeParams& p, int t, int base, int stride, int n, int h) {
+    const size_t r0 = (size_t)base * p.Hq + h, step = (size_t)stride * p.Hq;
+    merge_rows(
+        n, 1.f, [&](int i) { return p.part_ms + (r0 + i * step) * 2; },
+        [&](int i) { return p.part_acc + (r0 + i * step) * HEAD_DIM; },
+        p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM, p.out + ((size_t)t * p.Hq + h) * HEAD_DIM);
 }
 
 // One wave: token t, kv head kvh, keys [j0, j1) of its sequence. With FRESH,
@@ -202,9 +214,13 @@ __device__ __forceinline__ void merge_head(const DecodeParams& p, int t, int bas
 // position P0 on) choose every K/V address per lane between the cache and
 // the source rows (no branch, so the loads stay pipelined); earlier pages of
 // the piece take the plain path.
-template <int G, bool FUSED>
+// The wave's results go to epi(g, acc[8], m, l, ch) on the lanes of the
+// first half-wave (ch = lane: dims 8 ch .. 8 ch + 7 of query head
+// kvh * G + g; m in log2 units, l the sum of weights; m = -inf, l = 0 when
+// no key of the piece is attended).
+template <int G, bool FUSED, class Epi>
 __device__ __forceinline__ void piece_body(const DecodeParams& p, const int* __restrict__ bt, WaveLds<G>& lds,
-                                           int t, int kvh, int j0, int j1, int L, int idx, int P0, int row0) {
+                                           int t, int kvh, int j0, int j1, int L, int P0, int row0, Epi epi) {
     static_assert(G == 4, "lane mapping assumes 4 keys x 4 heads per lane");
     const int lane = threadIdx.x & 63, sig = lane & 15, rho = lane >> 4;
     const int hv = lane >> 5, ch = lane & 31;
@@ -378,28 +394,35 @@ __device__ __forceinline__ void piece_body(const DecodeParams& p, const int* __r
     }
     wave_sync();
     if (hv != 0) return;
-    const bool direct = j0 == 0 && j1 == L;
 #pragma unroll
-    for (int g = 0; g < G; g++) {
+    for (int g = 0; g < G; g++) epi(g, acc[g], lds.ml[2 * g], lds.ml[2 * g + 1], ch);
+}
+
+// Writes a piece's result: the gated output when the piece holds all of the
+// token's keys, else the partial record at index idx.
+template <int G>
+struct DecodeEpi {
+    const DecodeParams& p;
+    int t, kvh, idx;
+    bool direct;
+    __device__ __forceinline__ void operator()(int g, const float (&acc)[8], float m, float l, int ch) const {
         const int h = kvh * G + g;
         if (direct) {
-            const float inv = 1.f / lds.ml[2 * g + 1];
+            const float inv = 1.f / l;
             const uint4 graw = *reinterpret_cast<const uint4*>(p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM +
                                                                HEAD_DIM + 8 * ch);
-            const uint2 lo = gate4(acc[g][0], acc[g][1], acc[g][2], acc[g][3], inv, make_uint2(graw.x, graw.y));
-            const uint2 hi = gate4(acc[g][4], acc[g][5], acc[g][6], acc[g][7], inv, make_uint2(graw.z, graw.w));
+            const uint2 lo = gate4(acc[0], acc[1], acc[2], acc[3], inv, make_uint2(graw.x, graw.y));
+            const uint2 hi = gate4(acc[4], acc[5], acc[6], acc[7], inv, make_uint2(graw.z, graw.w));
             *reinterpret_cast<uint4*>(p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + 8 * ch) =
                 make_uint4(lo.x, lo.y, hi.x, hi.y);
         } else {
             float* pa = p.part_acc + ((size_t)idx * p.Hq + h) * HEAD_DIM + 8 * ch;
-            *reinterpret_cast<float4*>(pa) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-            *reinterpret_cast<float4*>(pa + 4) = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-            if (ch == 0)
-                *reinterpret_cast<float2*>(p.part_ms + ((size_t)idx * p.Hq + h) * 2) =
-                    make_float2(lds.ml[2 * g], lds.ml[2 * g + 1]);
+            *reinterpret_cast<float4*>(pa) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            *reinterpret_cast<float4*>(pa + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+            if (ch == 0) *reinterpret_cast<float2*>(p.part_ms + ((size_t)idx * p.Hq + h) * 2) = make_float2(m, l);
         }
     }
-}
+};
 
 template <int G, bool FUSED>
 __device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* __restrict__ tok_seq,
@@ -408,12 +431,13 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* _
                                              int j1, int L, int idx) {
     const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
     const int* __restrict__ bt = block_table + (size_t)seq * p.max_blocks;
+    const DecodeEpi<G> epi{p, t, kvh, idx, j0 == 0 && j1 == L};
     if constexpr (FUSED) {
         const int row0 = __builtin_amdgcn_readfirstlane(cu[seq]);
         const int P0 = __builtin_amdgcn_readfirstlane(pos[row0]);
-        piece_body<G, true>(p, bt, lds, t, kvh, j0, j1, L, idx, P0, row0);
+        piece_body<G, true>(p, bt, lds, t, kvh, j0, j1, L, P0, row0, epi);
     } else {
-        piece_body<G, false>(p, bt, lds, t, kvh, j0, j1, L, idx, INT_MAX, 0);
+        piece_body<G, false>(p, bt, lds, t, kvh, j0, j1, L, INT_MAX, 0, epi);
     }
 }
 

@@ -8,22 +8,19 @@
 // bf16(rbf(O / l) * sigmoid(gate)).
 //
 // Tiling (this build's own). A workgroup takes 64 consecutive query
-// positions of one sequence and one kv head: 4 waves, wave w = query head w
-// of the group, each over both 32-query blocks. Keys stream in tiles of 32
-// (two pages) staged in LDS once for the 4 waves (GQA sharing): K row-major
-// [key][d] and V transposed [d][key]. Per tile and query block a wave computes
+// positions of one sequence and one kv head (32 for launches on a grid of
+// 32-query tiles): a wave per (query head of the group, block of 32
+// queries), 8 waves. Keys stream in tiles of 32 (two pages) staged in LDS
+// once for all waves (GQA sharing): K row-major [key][d] and V transposed
+// [d][key]. Per tile a wave computes
 //   S^T[32 keys][32 queries] = K Q^T     16 x v_mfma_f32_32x32x16_bf16
 //   O^T[256 d][32 queries] += V^T P^T    16 x v_mfma_f32_32x32x16_bf16
-// and every K / V^T fragment read from LDS feeds both blocks' MFMAs, which
-// halves LDS read traffic per MFMA (one fragment per MFMA would need the
-// whole 128 B/clk of LDS bandwidth at the MFMA peak).
 // Computing S transposed leaves each lane with one query's 16 scores (keys
 // 8 (r / 4) + 4 (lane / 32) + r % 4), so the online softmax is in-lane plus
 // one cross-half shuffle, and the probabilities are already the B operand of
 // the second product once the matching V^T rows are read (keys
-// 16 kk + 4 (lane / 32) + {0..3, 8..11}). q stays in registers (128 VGPRs
-// for the two blocks); O^T takes 256 accumulators (one wave per SIMD, so the
-// whole 512-register file). The next tile's K/V are loaded into registers
+// 16 kk + 4 (lane / 32) + {0..3, 8..11}). q stays in registers (64 VGPRs),
+// O^T takes 128 accumulators. The next tile's K/V are loaded into registers
 // while the current one is multiplied (double-buffered LDS).
 #include "pkv_common.h"
 
@@ -47,7 +44,6 @@ struct PrefillParams {
     long num_blocks;
 };
 
-constexpr int PF_BQ = 64;          // query positions per workgroup
 constexpr int PF_BK = 32;          // keys per tile
 constexpr int PF_KSTR = HEAD_DIM + 8;  // K tile row stride (elements)
 // V^T row stride: a multiple of 4 elements (8-byte operand reads) with
@@ -56,30 +52,31 @@ constexpr int PF_KSTR = HEAD_DIM + 8;  // K tile row stride (elements)
 constexpr int PF_VSTR = PF_BK + 4;
 constexpr int PF_K_ELEMS = PF_BK * PF_KSTR;
 constexpr int PF_V_ELEMS = HEAD_DIM * PF_VSTR;
-// 32-query blocks per wave: 2 halves LDS reads per MFMA but needs 128 q +
-// 256 accumulator registers per wave (spills at one wave per SIMD); 1 runs
-// 8 waves, two per SIMD.
-#ifndef PKV_PF_NQB
-#define PKV_PF_NQB 1
-#endif
-constexpr int PF_NQB = PKV_PF_NQB;
-constexpr int PF_WAVES = 4 * (PF_BQ / 32) / PF_NQB;
-constexpr int PF_THREADS = 64 * PF_WAVES;
+// Query positions per workgroup: 64 for the library's entry point (8 waves:
+// 4 query heads x 2 blocks of 32); 32 (4 waves) for launches that bring
+// their own grid of 32-query tiles.
+constexpr int PF_BQ = 64;
+constexpr int pf_threads(int bq) { return 64 * 4 * (bq / 32); }
+constexpr int PF_THREADS = pf_threads(PF_BQ);
+constexpr int PF_STAGE = PF_K_ELEMS + PF_V_ELEMS;
+constexpr size_t prefill_smem_bytes() { return (size_t)2 * PF_STAGE * 2; }
 
-__global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {
-    static_assert(PF_BK * HEAD_DIM / 8 % PF_THREADS == 0, "whole 16-byte chunks per thread");
-    extern __shared__ __align__(16) uint16_t pf_smem[];
+// The whole kernel for one workgroup; pf_smem holds prefill_smem_bytes().
+template <int BQ>
+__device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
+    constexpr int THREADS = pf_threads(BQ);
+    static_assert(PF_BK * HEAD_DIM / 8 % THREADS == 0, "whole 16-byte chunks per thread");
     // Buffer b: K tile at pf_smem + b * STAGE, V^T tile right after it.
-    constexpr int STAGE = PF_K_ELEMS + PF_V_ELEMS;
+    constexpr int STAGE = PF_STAGE;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, lh = lane >> 5;
     const int kvh = blockIdx.y;
-    const int G = 4, h = kvh * G + (wave & 3), qb0 = (wave >> 2) * PF_NQB;  // first query block
+    const int G = 4, h = kvh * G + (wave & 3), qb0 = wave >> 2;  // the wave's query block
     // Find this block's query tile among the prompt sequences.
     int s = -1, tile = blockIdx.x;
     for (int i = 0; i < p.seqs; i++) {
         const int n = p.cu[i + 1] - p.cu[i];
         if (n <= 1 || is_spec(p.outs, p.spec, i)) continue;
-        const int tiles = (n + PF_BQ - 1) / PF_BQ;
+        const int tiles = (n + BQ - 1) / BQ;
         if (tile < tiles) {
             s = i;
             break;
@@ -87,52 +84,45 @@ __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p)
         tile -= tiles;
     }
     if (s < 0) return;
-    const int tb = p.cu[s] + tile * PF_BQ, nb = min(PF_BQ, p.cu[s + 1] - tb);
+    const int tb = p.cu[s] + tile * BQ, nb = min(BQ, p.cu[s + 1] - tb);
     const int qp0 = p.pos[tb];
     const int L = qp0 + nb;  // keys this tile needs: 0 .. L - 1
     const int* bt = p.block_table + (size_t)s * p.max_blocks;
     const size_t row = (size_t)p.Hkv * HEAD_DIM;
 
-    // This wave's queries: blocks qb0 + qb of 32 (query (qb0 + qb) * 32 + lq
-    // of the tile), q^T operands scaled into log2 units.
-    bf16x8 qf[PF_NQB][16];
-    const float f = p.scale * LOG2E;
-#pragma unroll
-    for (int qb = 0; qb < PF_NQB; qb++) {
-        const int myq = (qb0 + qb) * 32 + lq;
+    // This wave's queries: query block qb0 (queries 32 qb0 + lq of the
+    // tile), q^T operands scaled into log2 units.
+    const int myq = qb0 * 32 + lq;
+    bf16x8 qf[16];
+    {
+        const float f = p.scale * LOG2E;
         const bool ok = myq < nb;
         const uint16_t* qrow = p.q + ((size_t)(tb + (ok ? myq : 0)) * p.Hq + h) * HEAD_DIM;
 #pragma unroll
         for (int kk = 0; kk < 16; kk++) {
             uint4 raw = ok ? *reinterpret_cast<const uint4*>(qrow + 16 * kk + 8 * lh) : make_uint4(0, 0, 0, 0);
+            // (outside the key loop: exact software rounding, NaN-preserving)
             raw = make_uint4(pack2(bf_lo(raw.x) * f, bf_hi(raw.x) * f), pack2(bf_lo(raw.y) * f, bf_hi(raw.y) * f),
                              pack2(bf_lo(raw.z) * f, bf_hi(raw.z) * f), pack2(bf_lo(raw.w) * f, bf_hi(raw.w) * f));
-            // (outside the key loop: exact software rounding, NaN-preserving)
-            qf[qb][kk] = as_bf16x8(raw);
+            qf[kk] = as_bf16x8(raw);
         }
     }
-    f32x16 o[PF_NQB][8];
+    f32x16 o[8];
 #pragma unroll
-    for (int qb = 0; qb < PF_NQB; qb++)
+    for (int db = 0; db < 8; db++)
 #pragma unroll
-        for (int db = 0; db < 8; db++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) o[qb][db][r] = 0.f;
-    float m[PF_NQB], l[PF_NQB];
-#pragma unroll
-    for (int qb = 0; qb < PF_NQB; qb++) {
-        m[qb] = -INFINITY;
-        l[qb] = 0.f;
-    }
-    const int last = qp0 + min(nb, (qb0 + PF_NQB) * 32) - 1;  // this wave's last query position
+        for (int r = 0; r < 16; r++) o[db][r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    const int qpw = qp0 + qb0 * 32;                      // the wave's first query position
+    const int last = qp0 + min(nb, (qb0 + 1) * 32) - 1;  // and its last
 
     // Tile loads: 32 keys x 256 dims of K and of V = 2 x 1024 chunks of 16 B,
-    // NCH + NCH per thread. K: chunk e = tid + PF_THREADS u is key e / 32,
+    // NCH + NCH per thread. K: chunk e = tid + THREADS u is key e / 32,
     // dims 8 (e % 32) (whole rows per 32 lanes). V: the thread takes keys
-    // 2 (tid % 16) and + 1 of chunks tid / 16 + (PF_THREADS / 16) i, so it can
+    // 2 (tid % 16) and + 1 of chunks tid / 16 + (THREADS / 16) i, so it can
     // store (key, key + 1) pairs of each dim as one word of the transposed
     // tile. Keys at or past L load zeros.
-    constexpr int NCH = PF_BK * HEAD_DIM / 8 / PF_THREADS;
+    constexpr int NCH = PF_BK * HEAD_DIM / 8 / THREADS;
     uint4 kr[NCH], vr[NCH];
     // Block size is a power of two (checked on the host): shifts, no division.
     const int bs_log2 = p.bs_log2, bs_mask = (1 << bs_log2) - 1;
@@ -144,9 +134,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p)
     auto load_tile = [&](int k0) {
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
-            const int e = tid + u * PF_THREADS, kp = k0 + (e >> 5);
+            const int e = tid + u * THREADS, kp = k0 + (e >> 5);
             kr[u] = kp < L ? *reinterpret_cast<const uint4*>(p.kc + slot_at(kp, (e & 31) * 8)) : make_uint4(0, 0, 0, 0);
-            const int vp = k0 + 2 * (tid & 15) + (u & 1), vc = ((tid >> 4) + (PF_THREADS / 16) * (u >> 1)) * 8;
+            const int vp = k0 + 2 * (tid & 15) + (u & 1), vc = ((tid >> 4) + (THREADS / 16) * (u >> 1)) * 8;
             vr[u] = vp < L ? *reinterpret_cast<const uint4*>(p.vc + slot_at(vp, vc)) : make_uint4(0, 0, 0, 0);
         }
     };
@@ -155,13 +145,13 @@ __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p)
         uint16_t* sv = sk + PF_K_ELEMS;
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
-            const int e = tid + u * PF_THREADS;
+            const int e = tid + u * THREADS;
             *reinterpret_cast<uint4*>(sk + (e >> 5) * PF_KSTR + (e & 31) * 8) = kr[u];
         }
         const int j = 2 * (tid & 15);
 #pragma unroll
         for (int half = 0; half < NCH / 2; half++) {
-            const int c = ((tid >> 4) + (PF_THREADS / 16) * half) * 8;
+            const int c = ((tid >> 4) + (THREADS / 16) * half) * 8;
             const uint4 va = vr[2 * half], vb = vr[2 * half + 1];
             const uint32_t a[4] = {va.x, va.y, va.z, va.w}, b[4] = {vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
@@ -183,66 +173,55 @@ __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p)
         if (k0 <= last) {
             const uint16_t* K = pf_smem + buf * STAGE;
             const uint16_t* Vt = K + PF_K_ELEMS;
-            // S^T = K Q^T for both query blocks; each K fragment feeds two
-            // MFMAs. Lane (lh, lq) ends with query (qb, lq)'s scores of keys
+            // S^T = K Q^T. Lane (lh, lq) ends with query lq's scores of keys
             // k0 + 8 (r / 4) + 4 lh + r % 4.
-            f32x16 st[PF_NQB];
+            f32x16 st;
 #pragma unroll
-            for (int qb = 0; qb < PF_NQB; qb++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) st[qb][r] = 0.f;
+            for (int r = 0; r < 16; r++) st[r] = 0.f;
 #pragma unroll
             for (int kk = 0; kk < 16; kk++) {
                 const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(K + lq * PF_KSTR + 16 * kk + 8 * lh));
-#pragma unroll
-                for (int qb = 0; qb < PF_NQB; qb++)
-                    st[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb][kk], st[qb], 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], st, 0, 0, 0);
             }
-            uint4 pb[PF_NQB][2];
-#pragma unroll
-            for (int qb = 0; qb < PF_NQB; qb++) {
-                const int qp = qp0 + (qb0 + qb) * 32 + lq;
-                if (k0 + PF_BK - 1 > qp0 + (qb0 + qb) * 32 || k0 + PF_BK > L) {
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int kp = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                        if (kp > qp || kp >= L) st[qb][r] = -INFINITY;
-                    }
-                }
-                float mx = m[qb];
-#pragma unroll
-                for (int r = 0; r < 16; r++) mx = fmaxf(mx, st[qb][r]);
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                // A query with no key yet keeps -inf; it subtracts 0 so exp2 gives 0.
-                const float bse = mx == -INFINITY ? 0.f : mx;
-                const float corr = __builtin_amdgcn_exp2f(m[qb] - bse);
-                float sum = 0.f;
+            const int qp = qpw + lq;
+            if (k0 + PF_BK - 1 > qpw || k0 + PF_BK > L) {
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    st[qb][r] = __builtin_amdgcn_exp2f(st[qb][r] - bse);
-                    sum += st[qb][r];
+                    const int kp = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    if (kp > qp || kp >= L) st[r] = -INFINITY;
                 }
-                sum += __shfl_xor(sum, 32, 64);
-                l[qb] = l[qb] * corr + sum;
-                m[qb] = mx;
-                // Rescale only when some query's max moved (rare after the
-                // first tiles).
-                if (__any(corr != 1.f)) {
-#pragma unroll
-                    for (int db = 0; db < 8; db++)
-#pragma unroll
-                        for (int r = 0; r < 16; r++) o[qb][db][r] *= corr;
-                }
-                // P^T (bf16) as the B operand: step kk, element e <-> key
-                // 16 kk + 8 (e / 4) + 4 lh + e % 4, i.e. register 8 kk + e.
-#pragma unroll
-                for (int kk = 0; kk < 2; kk++)
-                    pb[qb][kk] = make_uint4(pack2_hw(st[qb][8 * kk + 0], st[qb][8 * kk + 1]),
-                                            pack2_hw(st[qb][8 * kk + 2], st[qb][8 * kk + 3]),
-                                            pack2_hw(st[qb][8 * kk + 4], st[qb][8 * kk + 5]),
-                                            pack2_hw(st[qb][8 * kk + 6], st[qb][8 * kk + 7]));
             }
-            // O^T += V^T P^T: each V^T fragment feeds both query blocks.
+            float mx = m;
+#pragma unroll
+            for (int r = 0; r < 16; r++) mx = fmaxf(mx, st[r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            // A query with no key yet keeps -inf; it subtracts 0 so exp2 gives 0.
+            const float bse = mx == -INFINITY ? 0.f : mx;
+            const float corr = __builtin_amdgcn_exp2f(m - bse);
+            float sum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                st[r] = __builtin_amdgcn_exp2f(st[r] - bse);
+                sum += st[r];
+            }
+            sum += __shfl_xor(sum, 32, 64);
+            l = l * corr + sum;
+            m = mx;
+            // Rescale only when some query's max moved (rare after the first tiles).
+            if (__any(corr != 1.f)) {
+#pragma unroll
+                for (int db = 0; db < 8; db++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) o[db][r] *= corr;
+            }
+            // P^T (bf16) as the B operand: step kk, element e <-> key
+            // 16 kk + 8 (e / 4) + 4 lh + e % 4, i.e. register 8 kk + e.
+            uint4 pb[2];
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++)
+                pb[kk] = make_uint4(pack2_hw(st[8 * kk + 0], st[8 * kk + 1]), pack2_hw(st[8 * kk + 2], st[8 * kk + 3]),
+                                    pack2_hw(st[8 * kk + 4], st[8 * kk + 5]), pack2_hw(st[8 * kk + 6], st[8 * kk + 7]));
+            // O^T += V^T P^T
 #pragma unroll
             for (int kk = 0; kk < 2; kk++)
 #pragma unroll
@@ -251,9 +230,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p)
                     const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
                     const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
                     const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-#pragma unroll
-                    for (int qb = 0; qb < PF_NQB; qb++)
-                        o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pb[qb][kk]), o[qb][db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pb[kk]), o[db], 0, 0, 0);
                 }
         }
         if (it + 1 < ntiles) {
@@ -262,30 +239,29 @@ __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p)
             __syncthreads();
         }
     }
+    if (myq >= nb) return;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const size_t t = (size_t)tb + myq;
+    const uint16_t* gate = p.qkv + t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM;
+    uint16_t* orow = p.out + (t * p.Hq + h) * HEAD_DIM;
 #pragma unroll
-    for (int qb = 0; qb < PF_NQB; qb++) {
-        const int myq = (qb0 + qb) * 32 + lq;
-        if (myq >= nb) continue;
-        const float inv = l[qb] > 0.f ? 1.f / l[qb] : 0.f;
-        const size_t t = (size_t)tb + myq;
-        const uint16_t* gate = p.qkv + t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM;
-        uint16_t* orow = p.out + (t * p.Hq + h) * HEAD_DIM;
+    for (int db = 0; db < 8; db++)
 #pragma unroll
-        for (int db = 0; db < 8; db++)
-#pragma unroll
-            for (int g4 = 0; g4 < 4; g4++) {
-                const int d = 32 * db + 8 * g4 + 4 * lh;
-                const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
-                const f32x16& oo = o[qb][db];
-                *reinterpret_cast<uint2*>(orow + d) =
-                    make_uint2(pack2(rbf(oo[4 * g4] * inv) / (1.f + __expf(-bf_lo(graw.x))),
-                                     rbf(oo[4 * g4 + 1] * inv) / (1.f + __expf(-bf_hi(graw.x)))),
-                               pack2(rbf(oo[4 * g4 + 2] * inv) / (1.f + __expf(-bf_lo(graw.y))),
-                                     rbf(oo[4 * g4 + 3] * inv) / (1.f + __expf(-bf_hi(graw.y)))));
-            }
-    }
+        for (int g4 = 0; g4 < 4; g4++) {
+            const int d = 32 * db + 8 * g4 + 4 * lh;
+            const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
+            const f32x16& oo = o[db];
+            *reinterpret_cast<uint2*>(orow + d) =
+                make_uint2(pack2(rbf(oo[4 * g4] * inv) / (1.f + __expf(-bf_lo(graw.x))),
+                                 rbf(oo[4 * g4 + 1] * inv) / (1.f + __expf(-bf_hi(graw.x)))),
+                           pack2(rbf(oo[4 * g4 + 2] * inv) / (1.f + __expf(-bf_lo(graw.y))),
+                                 rbf(oo[4 * g4 + 3] * inv) / (1.f + __expf(-bf_hi(graw.y)))));
+        }
 }
 
-constexpr size_t prefill_smem_bytes() { return (size_t)2 * (PF_K_ELEMS + PF_V_ELEMS) * 2; }
+__global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {
+    extern __shared__ __align__(16) uint16_t pf_smem[];
+    prefill_body<PF_BQ>(p, pf_smem);
+}
 
 }  // namespace pkv

@@ -1,0 +1,219 @@
+// The reference's kernel ABI for the paged-attention path, as a gfx950 code
+// object (pkv_kernels.hsaco). The reference engine loads one code object with
+// hipModuleLoadData (src/gpu.rs:434-466), resolves kernels by name
+// (src/gpu.rs:552-566) and launches them with its own grids, blocks, dynamic
+// shared memory and argument slots (src/gpu.rs:903-930). The kernels below
+// carry the reference's names and signatures, accept exactly those launches
+// (src/model.rs:2366-2493) and compute the same results with this build's
+// kernel bodies:
+//
+//   attn_paged_g4   (qwen35.cu:1313-1334)  grid (T, Hkv, Z), 256 threads
+//   attn_merge      (qwen35.cu:2245-2249)  grid (T, Hq), 256 threads
+//   attn_groupr_g4_t2_k32 (qwen35.cu:1600-1616) grid (ceil(T/32) + seqs, Hkv),
+//                   256 threads: the prompt kernel a gfx950 device (compute
+//                   capability 9.5) selects (fa_shape, src/model.rs:58-79)
+//   attn_mfma_g4_t2 (amd/attention.cuh:137-142) the same grid, 512 threads:
+//                   the name gfx942 devices select
+//
+// Split decode follows the reference's contract so its buffer sizing holds:
+// range z of nz = split_parts(L, Z, min_chunk) covers keys [z c, z c + c),
+// c = ceil(L / nz), and leaves a record [M (natural log), S, A[256]] at
+// part[((s * spec + t - cu[s]) * Hq + h) * Z + z]; attn_merge combines the nz
+// records. Inside a block the 4 waves take a quarter of the range's pages each
+// (this build's decode wave body: dot2 + DPP reduce-scatter, online softmax,
+// one page in flight) and combine through LDS.
+//
+// Bounds of this ABI (the bf16 path): kscale / vscale must be null (an E4M3
+// cache uses the reference's attn_paged8_* names, not exported here); FP8
+// output copies (fmode != 0) are not produced; block_size 16 for decode, a
+// power of two for prompts; G = Hq / Hkv = 4. A launch outside these bounds
+// writes nothing. Page ids are not clamped (the reference ABI passes no pool
+// size).
+#include "pkv_decode.hip"
+#include "pkv_prefill.hip"
+
+#include <climits>
+
+namespace pkv {
+
+constexpr float LN2 = 0.69314718055994531f;
+constexpr long REF_NO_CLAMP = 1L << 40;  // no pool bound in the reference ABI
+
+// Key ranges of a decode token (reference split_parts, qwen35.cu:1139-1141).
+__device__ __forceinline__ int ref_split_parts(int L, int Z, int min_chunk) {
+    return max(1, min(Z, (L + min_chunk - 1) / max(1, min_chunk)));
+}
+
+__device__ __forceinline__ bool ref_prompt_row(int skip_prompts, const int* cu, int sq, const int* outs, int spec) {
+    return skip_prompts && cu[sq + 1] - cu[sq] > 1 && !is_spec(outs, spec, sq);
+}
+
+}  // namespace pkv
+
+using pkv::HEAD_DIM;
+
+extern "C" __global__ void __launch_bounds__(256)
+    attn_paged_g4(const uint16_t* __restrict__ q, const void* __restrict__ kcache, const void* __restrict__ vcache,
+                  const float* __restrict__ kscale, const float* __restrict__ vscale, const uint16_t* __restrict__ qkv,
+                  int qstride, int Hq, int Hkv, const int* __restrict__ pos, const int* __restrict__ tok_seq,
+                  const int* __restrict__ block_table, int max_blocks, int block_size, uint16_t* __restrict__ out,
+                  float scale, uint8_t* fq, void* fs, int fmode, int frows, const int* __restrict__ cu,
+                  int skip_prompts, int min_chunk, float* part, const int* __restrict__ outs, int spec) {
+    constexpr int G = 4, PAGE = pkv::PAGE;
+    __shared__ pkv::WaveLds<G> sh_w[4];
+    __shared__ float sh_acc[4][G][HEAD_DIM];
+    __shared__ float sh_ml[4][G][2];
+    if (blockDim.x != 256 || block_size != PAGE || Hq != G * Hkv || kscale || vscale) return;
+    const int t = blockIdx.x, kvh = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
+    const int sq = tok_seq[t];
+    if (pkv::ref_prompt_row(skip_prompts, cu, sq, outs, spec)) return;
+    const int L = pos[t] + 1;
+    const int parts = part ? pkv::ref_split_parts(L, gridDim.z, min_chunk) : 1;
+    if (z >= parts) return;
+    const int chunk = (L + parts - 1) / parts;
+    const int j0 = part ? z * chunk : 0, j1 = part ? min(L, j0 + chunk) : L;
+
+    pkv::DecodeParams p = {};
+    p.q = q;
+    p.kc = (uint16_t*)kcache;  // read only (the unfused body)
+    p.vc = (uint16_t*)vcache;
+    p.qkv = qkv;
+    p.qstride = qstride;
+    p.Hq = Hq;
+    p.Hkv = Hkv;
+    p.max_blocks = max_blocks;
+    p.out = out;
+    p.scale = scale;
+    p.num_blocks = pkv::REF_NO_CLAMP;
+
+    // The range's pages split over the 4 waves.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int a = j1, b = j1;
+    if (j0 < j1) {
+        const int pg0 = j0 / PAGE, np = (j1 - 1) / PAGE - pg0 + 1, per = (np + 3) / 4;
+        a = max(j0, (pg0 + wave * per) * PAGE);
+        b = min(j1, (pg0 + (wave + 1) * per) * PAGE);
+    }
+    if (a < b) {
+        const int* bt = block_table + (size_t)sq * max_blocks;
+        auto epi = [&](int g, const float (&acc)[8], float m, float l, int ch) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) sh_acc[wave][g][8 * ch + e] = acc[e];
+            if (ch == 0) {
+                sh_ml[wave][g][0] = m;
+                sh_ml[wave][g][1] = l;
+            }
+        };
+        pkv::piece_body<G, false>(p, bt, sh_w[wave], t, kvh, a, b, L, INT_MAX, 0, epi);
+    } else {
+        const int lane = tid & 63;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) sh_acc[wave][g][4 * lane + e] = 0.f;
+            if (lane == 0) {
+                sh_ml[wave][g][0] = -INFINITY;
+                sh_ml[wave][g][1] = 0.f;
+            }
+        }
+    }
+    __syncthreads();
+    // Combine the waves: thread d owns dimension d of every head.
+    const int d = tid;
+    for (int g = 0; g < G; g++) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, sh_ml[w][g][0]);
+        float S = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float f = sh_ml[w][g][0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sh_ml[w][g][0] - M);
+            S += sh_ml[w][g][1] * f;
+            A += sh_acc[w][g][d] * f;
+        }
+        const int h = kvh * G + g;
+        if (part) {
+            const size_t row = (size_t)sq * spec + (t - cu[sq]);
+            float* pp = part + ((row * Hq + h) * gridDim.z + z) * (HEAD_DIM + 2);
+            if (d == 0) {
+                pp[0] = M * pkv::LN2;  // natural-log units, as the reference's records
+                pp[1] = S;
+            }
+            pp[2 + d] = A;
+        } else {
+            const float gate = pkv::b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d]);
+            out[((size_t)t * Hq + h) * HEAD_DIM + d] =
+                (uint16_t)pkv::f2b_bits(pkv::rbf(A / S) / (1.f + __expf(-gate)));
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    attn_merge(const float* __restrict__ part, int Z, int min_chunk, const uint16_t* __restrict__ qkv, int qstride,
+               int Hq, const int* __restrict__ pos, const int* __restrict__ tok_seq, const int* __restrict__ cu,
+               int skip_prompts, uint16_t* __restrict__ out, uint8_t* fq, void* fs, int fmode, int frows,
+               const int* __restrict__ outs, int spec) {
+    if (blockDim.x != 256) return;
+    const int t = blockIdx.x, h = blockIdx.y;
+    const int sq = tok_seq[t];
+    if (pkv::ref_prompt_row(skip_prompts, cu, sq, outs, spec)) return;
+    const int nz = pkv::ref_split_parts(pos[t] + 1, Z, min_chunk);
+    const float* pp = part + (((size_t)sq * spec + (t - cu[sq])) * Hq + h) * Z * (HEAD_DIM + 2);
+    pkv::merge_rows(
+        nz, pkv::LOG2E, [&](int i) { return pp + (size_t)i * (HEAD_DIM + 2); },
+        [&](int i) { return pp + (size_t)i * (HEAD_DIM + 2) + 2; },
+        qkv + (size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM, out + ((size_t)t * Hq + h) * HEAD_DIM);
+}
+
+#define PKV_FLASH_ARGS                                                                                            \
+    const uint16_t *__restrict__ q, const void *__restrict__ kcache, const void *__restrict__ vcache,             \
+        const float *__restrict__ kscale, const float *__restrict__ vscale, const uint16_t *__restrict__ qkv,     \
+        int qstride, int Hq, int Hkv, const int *__restrict__ pos, const int *__restrict__ cu, int seqs,          \
+        const int *__restrict__ block_table, int max_blocks, int block_size, uint16_t *__restrict__ out,          \
+        float scale, const int *__restrict__ outs, int spec
+
+namespace pkv {
+
+// The prompt kernel on a grid of 32-query tiles (BQ = 32: one workgroup per
+// tile; BQ = 64: one per two tiles, the other blocks of the grid exit).
+// Stages in static LDS (the launch's dynamic shared memory is not used).
+template <int BQ>
+__device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
+    __shared__ __align__(16) uint16_t sm[2 * PF_STAGE];
+    if ((int)blockDim.x != pf_threads(BQ) || Hq != 4 * Hkv || kscale || vscale || block_size <= 0 ||
+        (block_size & (block_size - 1)))
+        return;
+    PrefillParams p;
+    p.q = q;
+    p.kc = (const uint16_t*)kcache;
+    p.vc = (const uint16_t*)vcache;
+    p.qkv = qkv;
+    p.qstride = qstride;
+    p.Hq = Hq;
+    p.Hkv = Hkv;
+    p.pos = pos;
+    p.cu = cu;
+    p.seqs = seqs;
+    p.block_table = block_table;
+    p.max_blocks = max_blocks;
+    p.block_size = block_size;
+    p.bs_log2 = __builtin_ctz((unsigned)block_size);
+    p.out = out;
+    p.scale = scale;
+    p.outs = outs;
+    p.spec = spec;
+    p.num_blocks = REF_NO_CLAMP;
+    prefill_body<BQ>(p, sm);
+}
+
+}  // namespace pkv
+
+extern "C" __global__ void __launch_bounds__(256, 1) attn_groupr_g4_t2_k32(PKV_FLASH_ARGS) {
+    pkv::flash_ref<32>(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
+                       max_blocks, block_size, out, scale, outs, spec);
+}
+
+extern "C" __global__ void __launch_bounds__(512, 1) attn_mfma_g4_t2(PKV_FLASH_ARGS) {
+    pkv::flash_ref<64>(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
+                       max_blocks, block_size, out, scale, outs, spec);
+}

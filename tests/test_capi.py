@@ -58,3 +58,32 @@ def test_workspace_grows_with_tokens():
     a, b = pkv.attn_decode_workspace(1, 16), pkv.attn_decode_workspace(64, 16)
     assert b > a > 0
     assert (b - a) >= 63 * 16 * 256 * 4
+
+
+def test_reference_abi_code_object_exports_the_reference_kernel_names(tmp_path):
+    """pkv_kernels.hsaco (a bundle for hipModuleLoadData) holds the gfx950
+    code object whose kernel symbols are the reference engine's names
+    (src/model.rs:1053-1061, fa_shape :58-79)."""
+    import subprocess
+    from pkv import refabi
+    bundler = "/opt/rocm/llvm/bin/clang-offload-bundler"
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    co = tmp_path / "gfx950.co"
+    subprocess.run([bundler, "--unbundle", "--type=o", f"--input={refabi.HSACO}", f"--output={co}",
+                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950"], check=True)
+    syms = subprocess.run([readelf, "--syms", "--wide", str(co)], check=True, capture_output=True, text=True).stdout
+    kernels = {line.split()[-1] for line in syms.splitlines() if " FUNC " in line and "GLOBAL" in line}
+    for name in ("attn_paged_g4", "attn_merge", "attn_groupr_g4_t2_k32", "attn_mfma_g4_t2"):
+        assert name in kernels, (name, sorted(kernels)[:20])
+
+
+def test_reference_launch_shapes():
+    """The restated host formulas the code object is launched with."""
+    from pkv import refabi
+    assert refabi.split_ranges(64, 4, 256) == 4       # config 3 on 256 CUs
+    assert refabi.split_ranges(1, 4, 256) == 64       # config 2: SPLIT_MAX
+    assert refabi.split_ranges(300, 4, 256) == 1
+    name, grid, threads, smem = refabi.flash_launch(100, 3, 4)
+    assert (name, grid, threads, smem) == ("attn_groupr_g4_t2_k32", (7, 4, 1), 256, 67584)
+    name, grid, threads, smem = refabi.flash_launch(100, 3, 4, mfma=True)
+    assert (name, grid, threads, smem) == ("attn_mfma_g4_t2", (7, 4, 1), 512, 37376)

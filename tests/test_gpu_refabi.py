@@ -1,0 +1,149 @@
+"""GPU parity of the reference-ABI code object (pkv_kernels.hsaco): its
+kernels, loaded by name with hipModuleLoadData and launched with the
+reference engine's grids, blocks, shared memory and 8-byte argument slots
+(src/model.rs:2366-2493, src/gpu.rs:903-930), against the oracle.
+
+Tolerance (north star): bf16 outputs within max-abs 2e-3 and relative 1e-2,
+|got - want| <= 2e-3 + 1e-2 * |want|. The split records are also merged on
+the host with the reference's own attn_merge formula (natural-log maxima,
+qwen35.cu:2255-2273), pinning the record format a mixed deployment would
+exchange."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _util import BS, D, bf16_bits, close, decode_case
+from pkv.refabi import F, I, P, RefKernels, SPLIT_MIN_KEYS, flash_launch, split_ranges
+from test_gpu_prefill import prefill_case
+from test_gpu_verify import verify_case
+
+pytestmark = pytest.mark.gpu
+SCALE = 1.0 / 16.0
+
+
+@pytest.fixture(scope="module")
+def rk():
+    return RefKernels()
+
+
+def i16(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+
+
+def i32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+
+
+def ref_decode(rk, c, dev, Z=None, spec=1, skip=0, outs=None, out_init=None, keep_part=False):
+    """attn_paged_g4 (+ attn_merge when split) as model.rs:2366-2437 launches them."""
+    T, Hq, Hkv = len(c["pos"]), c["Hq"], c["Hkv"]
+    sms = torch.cuda.get_device_properties(0).multi_processor_count
+    ranges = split_ranges(T, Hkv, sms) if Z is None else Z
+    seqs = len(c["cu"]) - 1
+    part = (torch.full((seqs * spec * ranges * Hq * (D + 2),), float("nan"), device=dev) if ranges > 1 else None)
+    q, kc, vc, qkv = (i16(c[k], dev) for k in ("q", "kc", "vc", "qkv"))
+    pos, ts, bt, cu = i32(c["pos"], dev), i32(c["tok_seq"], dev), i32(c["bt"], dev), i32(c["cu"], dev)
+    outs_d = None if outs is None else i32(outs, dev)
+    out = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev) if out_init is None else i16(out_init, dev)
+    rk.launch("attn_paged_g4", (T, Hkv, ranges), 256, 0,
+              [P(q), P(kc), P(vc), P(None), P(None), P(qkv), I(c["qstride"]), I(Hq), I(Hkv), P(pos), P(ts), P(bt),
+               I(c["max_blocks"]), I(BS), P(out), F(SCALE), P(None), P(None), I(0), I(0), P(cu), I(skip),
+               I(SPLIT_MIN_KEYS), P(part), P(outs_d), I(spec)])
+    if part is not None:
+        rk.launch("attn_merge", (T, Hq, 1), 256, 0,
+                  [P(part), I(ranges), I(SPLIT_MIN_KEYS), P(qkv), I(c["qstride"]), I(Hq), P(pos), P(ts), P(cu),
+                   I(skip), P(out), P(None), P(None), I(0), I(0), P(outs_d), I(spec)])
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    if keep_part:
+        return got, (None if part is None else part.cpu().numpy()), ranges
+    return got
+
+
+def oracle_decode(c, **kw):
+    out, _ = oracle.attn_decode(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], c["Hq"], c["Hkv"], c["pos"],
+                                c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"], **kw)
+    return out
+
+
+@pytest.mark.parametrize("lens,Hkv,seed,Z", [
+    ([1, 2, 15, 16, 17], 4, 0, None),          # page edges; 52 ranges offered, 1 used
+    ([4097], 4, 1, None),                      # config 2: 64 ranges of 65 keys
+    ([513, 8193, 1000, 4000, 777, 64], 4, 2, None),
+    ([300, 5000], 2, 3, None),                 # Hkv 2
+    ([900, 70, 4000], 4, 4, 1),                # no split: part = 0, gated output in place
+    ([200] * 300, 4, 5, None),                 # 300 tokens: split_ranges gives 1
+])
+def test_ref_decode_matches_oracle(dev, rk, lens, Hkv, seed, Z):
+    print(f"case refabi decode lens={lens[:6]} Hkv={Hkv} Z={Z}", flush=True)
+    c = decode_case(lens, 4 * Hkv, Hkv, seed)
+    ok, err = close(ref_decode(rk, c, dev, Z=Z), oracle_decode(c))
+    assert ok, f"max |diff| {err}"
+
+
+def test_ref_spec_rows_and_prompt_skip(dev, rk):
+    """Speculative rows (spec = 4 rows per sequence, partial rows indexed
+    s * spec + row) verified; a prompt sequence's rows skipped."""
+    print("case refabi spec rows", flush=True)
+    c = verify_case([(300, 4), (0, 9), (40, 4), (90, 1), (2000, 3)], 4, 6)
+    outs = np.zeros(5 * 4, np.int32)  # outs[s * spec] >= 0: sequence s verifies drafts
+    outs[1 * 4] = -1                   # sequence 1 (9 rows) is a prompt: skipped before any write
+    init = np.full((c["T"], 16, D), 0x5555, np.uint16)
+    got = ref_decode(rk, c, dev, spec=4, skip=1, outs=outs, out_init=init)
+    assert (got[4:13] == 0x5555).all()
+    want = oracle_decode(c, skip_prompts=1, outs=outs, spec=4, out=init.copy())
+    ok, err = close(got, want)
+    assert ok, err
+
+
+def test_ref_records_merge_with_reference_formula(dev, rk):
+    """The split records are the reference's: [M (natural log), S, A[256]] at
+    ((s * spec + t - cu[s]) * Hq + h) * Z + z. Merged on the host with
+    attn_merge's formula they give the kernel's output."""
+    print("case refabi records", flush=True)
+    c = decode_case([4097, 1500, 130], 16, 4, 7)
+    got, part, Z = ref_decode(rk, c, dev, keep_part=True)
+    assert Z > 1
+    T, Hq = 3, 16
+    rec = part.reshape(T, Hq, Z, D + 2).astype(np.float64)
+    for t, L in enumerate(c["pos"] + 1):
+        nz = max(1, min(Z, -(-int(L) // SPLIT_MIN_KEYS)))
+        r = rec[t, :, :nz]
+        assert np.isfinite(r).all()
+        M = r[:, :, 0].max(axis=1, keepdims=True)
+        f = np.exp(r[:, :, 0] - M)
+        S = (r[:, :, 1] * f).sum(axis=1)
+        A = (r[:, :, 2:] * f[:, :, None]).sum(axis=1) / S[:, None]
+        o = oracle.b2f(oracle.f2b(A.astype(np.float32)))
+        gate = oracle.b2f(c["qkv"][t][:Hq * 2 * D].reshape(Hq, 2, D)[:, 1]).astype(np.float64)
+        want = oracle.f2b((o / (1 + np.exp(-gate))).astype(np.float32))
+        ok, err = close(got[t], want)
+        assert ok, f"token {t}: {err}"
+
+
+@pytest.mark.parametrize("mfma", [False, True])
+@pytest.mark.parametrize("ctxs,chunks,Hkv,seed", [
+    ([0], [37], 4, 0),
+    ([100], [64], 4, 1),
+    ([16, 5], [130, 2], 1, 2),
+    ([1000, 33, 0], [70, 200, 65], 2, 3),
+])
+def test_ref_prefill_matches_oracle(dev, rk, mfma, ctxs, chunks, Hkv, seed):
+    print(f"case refabi prefill mfma={mfma} ctx={ctxs} chunk={chunks} Hkv={Hkv}", flush=True)
+    c = prefill_case(ctxs, chunks, Hkv, seed, decode_rows=1)
+    T, Hq = c["T"], c["Hq"]
+    name, grid, threads, smem = flash_launch(T, c["seqs"], Hkv, mfma=mfma)
+    init = np.full((T, Hq, D), 0x3333, np.uint16)
+    out = i16(init, dev)
+    rk.launch(name, grid, threads, smem,
+              [P(i16(c["q"], dev)), P(i16(c["kc"], dev)), P(i16(c["vc"], dev)), P(None), P(None),
+               P(i16(c["qkv"], dev)), I(c["qstride"]), I(Hq), I(Hkv), P(i32(c["pos"], dev)), P(i32(c["cu"], dev)),
+               I(c["seqs"]), P(i32(c["bt"], dev)), I(c["max_blocks"]), I(BS), P(out), F(SCALE), P(None), I(1)])
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    assert (got[0] == 0x3333).all()  # the decode row is left to decode attention
+    want = oracle.attn_prefill(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["cu"],
+                               c["seqs"], c["bt"], c["max_blocks"], BS, SCALE, out=init.copy())
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
