@@ -441,6 +441,74 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* _
     }
 }
 
+// The workgroup's key range [start, end) of the flattened key space (keys
+// of token t: lenf(t)), cut into equal ranges of R = max(min_range,
+// ceil(W / n_wg)) keys, and the token t0 holding key `start` at offset off0.
+// Workgroup (0, 0) also writes offs[t] (exclusive offsets), offs[T] = W and
+// offs[T + 1] = R for the merge. For T <= block size one scan serves both;
+// otherwise a first pass totals W and a second finds the offsets. Returns
+// false (for the whole workgroup) when the range is empty.
+template <class LenF>
+__device__ __forceinline__ bool find_range(const DecodeParams& p, LenF lenf, int* sh_scan, int* sh_t0, int& start,
+                                           int& end, int& t0, int& off0) {
+    const int T = p.T, nthr = blockDim.x, tid = threadIdx.x, b = blockIdx.x;
+    const bool writer = b == 0 && blockIdx.y == 0;
+    const bool one = T <= nthr;
+    int W = 0, myL = 0, myoff = 0;
+    if (one) {
+        myL = tid < T ? lenf(tid) : 0;
+        myoff = block_scan(myL, sh_scan, W);
+    } else {
+        for (int base = 0; base < T; base += nthr) {
+            const int t = base + tid;
+            const int L = t < T ? lenf(t) : 0;
+            int tot;
+            block_scan(L, sh_scan, tot);
+            W += tot;
+        }
+    }
+    W = __builtin_amdgcn_readfirstlane(W);  // block-uniform: keep it in scalar registers
+    const int R = max(p.min_range, (W + p.n_wg - 1) / p.n_wg);
+    start = b * R;
+    end = min(W, start + R);
+    if (writer && tid == 0) {
+        p.offs[T] = W;
+        p.offs[T + 1] = R;
+    }
+    if (one) {
+        if (tid < T) {
+            if (writer) p.offs[tid] = myoff;
+            if (myL > 0 && myoff <= start && start < myoff + myL) {
+                sh_t0[0] = tid;
+                sh_t0[1] = myoff;
+            }
+        }
+    } else {
+        if (start >= W && b != 0) return false;
+        int run = 0;
+        for (int base = 0; base < T; base += nthr) {
+            const int t = base + tid;
+            const int L = t < T ? lenf(t) : 0;
+            int tot;
+            const int off = run + block_scan(L, sh_scan, tot);
+            if (t < T) {
+                if (writer) p.offs[t] = off;
+                if (L > 0 && off <= start && start < off + L) {
+                    sh_t0[0] = t;
+                    sh_t0[1] = off;
+                }
+            }
+            run += tot;
+            if (b != 0 && run > start) break;  // uniform: every thread has the same run
+        }
+    }
+    if (start >= W) return false;
+    __syncthreads();
+    t0 = __builtin_amdgcn_readfirstlane(sh_t0[0]);
+    off0 = __builtin_amdgcn_readfirstlane(sh_t0[1]);
+    return true;
+}
+
 // Key-range kernel (FUSED = false) or fused step kernel (FUSED = true): one
 // workgroup per key range and group of up to 4 kv heads (blockIdx.y), a wave
 // per kv head. Block: 64 * min(Hkv, 4) threads (the host rejects Hkv > 4 that
@@ -471,45 +539,12 @@ __global__ void __launch_bounds__(256, 1)
             }
         }
     }
-    // Pass 1: total keys W.
-    int W = 0;
-    for (int base = 0; base < T; base += nthr) {
-        const int t = base + tid;
-        const int L = t < T ? decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec) : 0;
-        int tot;
-        block_scan(L, sh_scan, tot);
-        W += tot;
-    }
-    W = __builtin_amdgcn_readfirstlane(W);  // block-uniform: keep it in scalar registers
-    const int R = max(p.min_range, (W + p.n_wg - 1) / p.n_wg);
-    const int start = b * R, end = min(W, start + R);
-    if (b == 0 && blockIdx.y == 0 && tid == 0) {
-        p.offs[T] = W;
-        p.offs[T + 1] = R;
-    }
-    if (start >= W && b != 0) return;
-    // Pass 2: exclusive offsets (written by block 0 for decode_merge_kernel);
-    // find the token holding key `start`.
-    int run = 0;
-    for (int base = 0; base < T; base += nthr) {
-        const int t = base + tid;
-        const int L = t < T ? decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec) : 0;
-        int tot;
-        const int off = run + block_scan(L, sh_scan, tot);
-        if (t < T) {
-            if (b == 0 && blockIdx.y == 0) p.offs[t] = off;
-            if (L > 0 && off <= start && start < off + L) {
-                sh_t0[0] = t;
-                sh_t0[1] = off;
-            }
-        }
-        run += tot;
-        if (b != 0 && run > start) break;  // uniform: every thread has the same run
-    }
-    if (start >= W) return;
-    __syncthreads();
+    int start, end, t0, off0;
+    if (!find_range(p, [&](int t) { return decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec); }, sh_scan,
+                    sh_t0, start, end, t0, off0))
+        return;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = kv0 + wave;
-    int t = __builtin_amdgcn_readfirstlane(sh_t0[0]), off = __builtin_amdgcn_readfirstlane(sh_t0[1]);
+    int t = t0, off = off0;
     while (off < end && t < T) {
         const int L = decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec);
         if (L > 0) {

@@ -184,42 +184,13 @@ __global__ void __launch_bounds__(256, 1)
     __shared__ int sh_t0[2];
     __shared__ __align__(16) uint16_t sh_v[4][VF_LDS];
     const int T = p.T, nthr = blockDim.x, tid = threadIdx.x, b = blockIdx.x;
-    int W = 0, nr;
-    for (int base = 0; base < T; base += nthr) {
-        const int t = base + tid;
-        const int L = t < T ? seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr) : 0;
-        int tot;
-        block_scan(L, sh_scan, tot);
-        W += tot;
-    }
-    W = __builtin_amdgcn_readfirstlane(W);
-    const int R = max(p.min_range, (W + p.n_wg - 1) / p.n_wg);
-    const int start = b * R, end = min(W, start + R);
-    if (b == 0 && blockIdx.y == 0 && tid == 0) {
-        p.offs[T] = W;
-        p.offs[T + 1] = R;
-    }
-    if (start >= W && b != 0) return;
-    int run = 0;
-    for (int base = 0; base < T; base += nthr) {
-        const int t = base + tid;
-        const int L = t < T ? seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr) : 0;
-        int tot;
-        const int off = run + block_scan(L, sh_scan, tot);
-        if (t < T) {
-            if (b == 0 && blockIdx.y == 0) p.offs[t] = off;
-            if (L > 0 && off <= start && start < off + L) {
-                sh_t0[0] = t;
-                sh_t0[1] = off;
-            }
-        }
-        run += tot;
-        if (b != 0 && run > start) break;
-    }
-    if (start >= W) return;
-    __syncthreads();
+    int nr, start, end, t0, off0;
+    if (!find_range(
+            p, [&](int t) { return seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr); }, sh_scan,
+            sh_t0, start, end, t0, off0))
+        return;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = blockIdx.y * 4 + wave;
-    int t = __builtin_amdgcn_readfirstlane(sh_t0[0]), off = __builtin_amdgcn_readfirstlane(sh_t0[1]);
+    int t = t0, off = off0;
     while (off < end && t < T) {
         const int Ls = __builtin_amdgcn_readfirstlane(seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr));
         if (Ls > 0) {

@@ -9,7 +9,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libpkv.so")
+# PKV_LIBRARY selects another build of the same library (A/B measurements).
+LIB_PATH = os.environ.get("PKV_LIBRARY") or os.path.join(_HERE, "libpkv.so")
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(f"libpkv.so not built at {LIB_PATH}: run __graft_entry__.build()")
