@@ -193,6 +193,27 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
                      int64_t num_blocks, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Device: attention input preparation (the reference's append site)
+ * ------------------------------------------------------------------------- */
+
+/* The reference's attn_prep (src/kernels/qwen35.cu:1067-1128, launched at
+ * src/model.rs:2340-2365; same arguments plus T, num_slots and stream): for
+ * each token t < T and head of the qkv row [Hq x (q | gate) | k Hkv | v Hkv]
+ * (256 wide): q and k heads are RMS-normalised with the f32 weights q_norm /
+ * k_norm [256] (bf16(x * scale * w), scale = 1 / sqrt(sum x^2 / 256 + eps))
+ * and their dims 0..63 rotated as pairs (d, d + 32) by
+ * rope[axis * rope_stride + t] * inv_freq[d] (axis: height for d % 3 == 1
+ * below 3 sec_h, width for d % 3 == 2 below 3 sec_w, else time; bf16 cos/sin);
+ * q goes to qout [T][Hq][256], k to kcache and v (copied) to vcache at slot
+ * slot_map[t] (rows [slot][Hkv][256]); k/v are skipped for slots outside
+ * [0, num_slots). kscale / vscale (E4M3 cache) must be NULL here
+ * (PKV_ERR_UNSUPPORTED otherwise). */
+int pkv_attn_prep(const void* qkv, int qstride, int Hq, int Hkv, const float* q_norm, const float* k_norm,
+                  const int32_t* rope, int rope_stride, int sec_h, int sec_w, const int32_t* slot_map,
+                  const float* inv_freq, void* qout, void* kcache, void* vcache, const float* kscale,
+                  const float* vscale, float eps, int T, int64_t num_slots, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Host: block allocator (reference Scheduler.free_blocks / block_refs,
  * src/sched.rs:461-465, 515, 801-817)
  * ------------------------------------------------------------------------- */

@@ -51,6 +51,7 @@ _lib.orc_merge.argtypes = [_P, _P, _P, _I, _P]
 _lib.orc_attn_prefill.restype = _I
 _lib.orc_attn_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I]
 _lib.orc_mtp_slots.argtypes = [_P, _P, _P, _I, _I, _P, _I, _P, _P, _I]
+_lib.orc_attn_prep.argtypes = [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _F, _I, _L, _P, _P, _P]
 
 
 def _p(a):
@@ -166,3 +167,20 @@ def mtp_slots(rows, pos, block_table, max_blocks, block_size, limits, k):
     _lib.orc_mtp_slots(_p(rows), _p(pos), _p(block_table), max_blocks, block_size, _p(limits), k, _p(dpos),
                        _p(dslot), S)
     return dpos, dslot
+
+
+def attn_prep(qkv, qstride, Hq, Hkv, q_norm, k_norm, rope, rope_stride, sec_h, sec_w, slot_map, inv_freq, eps,
+              qout, kcache, vcache):
+    """Reference attn_prep restated (qwen35.cu:1067-1128); writes qout (uint16
+    [T][Hq][256]) and the k/v slots of kcache/vcache (uint16) in place."""
+    T = len(slot_map)
+    qkv = np.ascontiguousarray(qkv, np.uint16)
+    q_norm = np.ascontiguousarray(q_norm, np.float32)
+    k_norm = np.ascontiguousarray(k_norm, np.float32)
+    rope = _i32(rope)
+    slot_map = _i32(slot_map)
+    inv_freq = np.ascontiguousarray(inv_freq, np.float32)
+    num_slots = kcache.size // (max(Hkv, 1) * 256)
+    _lib.orc_attn_prep(_p(qkv), qstride, Hq, Hkv, _p(q_norm), _p(k_norm), _p(rope), rope_stride, sec_h, sec_w,
+                       _p(slot_map), _p(inv_freq), eps, T, num_slots, _p(qout),
+                       _p(kcache), _p(vcache))

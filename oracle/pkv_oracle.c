@@ -12,6 +12,8 @@
  *   - split-K partials and merge    (qwen35.cu:1137-1141, 1264-1288, 2242-2279)
  *   - chunked-prefill causal attention (qwen35.cu:1364-1585, amd/attention.cuh:12-136)
  *   - page copy (copy-on-write; build-defined: the reference has no CoW)
+ *   - attention input preparation: q/k RMSNorm, interleaved multimodal
+ *     rotary, q out, k/v to their cache slots (attn_prep, qwen35.cu:1067-1128)
  *
  * Pinning (what each function is checked against, in tests/test_oracle.py):
  *   append/gather/page_copy: closed forms, gather(append(x)) == x under
@@ -19,9 +21,14 @@
  *   attention: torch fp64 scaled_dot_product_attention golden fixtures
  *       (tests/golden/), closed forms (one key -> v; equal keys -> mean of v;
  *       a dominant key -> its v), split+merge == unsplit.
+ *   attn_prep: closed forms (constant rows normalise to the weights; position
+ *       0 leaves rows unrotated; a rotation keeps each pair's norm; the axis
+ *       rule picks height/width positions for exactly the frequencies
+ *       d % 3 == 1 / 2 below 3 sec_h / 3 sec_w), v copied bit for bit.
  *   Parity unpinned beyond the stated tolerance: the reference GPU kernels'
  *   exact bf16 rounding of P inside the prefill tiles (amd/attention.cuh:115)
- *   and expf vs exp2f last bits.
+ *   and expf vs exp2f last bits; in attn_prep the f32 order of the squared
+ *   sum and the last bits of cosf/sinf (1 bf16 ulp).
  *
  * Arithmetic: softmax and weighted sums in double; the epilogue follows the
  * reference exactly in f32: o = bf16_round(A / S); y = o / (1 + expf(-gate));
@@ -287,5 +294,62 @@ void orc_mtp_slots(const int* rows, const int* pos, const int* block_table, int 
         dpos[s] = p;
         dslot[s] = p <= limits[s] ? block_table[(size_t)s * max_blocks + p / block_size] * block_size + p % block_size
                                   : -1;
+    }
+}
+
+/* ---- attention input preparation (reference attn_prep, qwen35.cu:1067-1128):
+ * per token t and head: q heads (and k heads) are RMS-normalised with their
+ * f32 weights, y = bf16(x * scale * w), scale = 1 / sqrt(sum x^2 / 256 + eps)
+ * (sum in double here, rounded to f32), then dims 0..63 are rotated as pairs
+ * (d, d + 32) with bf16-rounded cos/sin of position * inv_freq[d]: lo' =
+ * bf16(bf16(lo c) - bf16(hi s)), hi' = bf16(bf16(hi c) + bf16(lo s)). The
+ * position of frequency d is rope[axis * rope_stride + t], axis = 1 (height)
+ * when d % 3 == 1 and d < 3 sec_h, 2 (width) when d % 3 == 2 and d < 3 sec_w,
+ * else 0 (time). q -> qout[t][h]; k -> kcache[slot][h]; v copied to
+ * vcache[slot][h]; k and v are skipped for slot < 0 (or >= num_slots). */
+#define ROPE_DIM 64
+void orc_attn_prep(const uint16_t* qkv, int qstride, int Hq, int Hkv, const float* q_norm, const float* k_norm,
+                   const int* rope, int rope_stride, int sec_h, int sec_w, const int* slot_map,
+                   const float* inv_freq, float eps, int T, long num_slots, uint16_t* qout, uint16_t* kcache,
+                   uint16_t* vcache) {
+    for (int t = 0; t < T; t++) {
+        const uint16_t* row = qkv + (size_t)t * qstride;
+        const long slot = slot_map[t];
+        const int has_slot = slot >= 0 && slot < num_slots;
+        for (int hh = 0; hh < Hq + 2 * Hkv; hh++) {
+            if (hh >= Hq + Hkv) {
+                if (!has_slot) continue;
+                const int vh = hh - Hq - Hkv;
+                memcpy(vcache + ((size_t)slot * Hkv + vh) * HEAD_DIM, row + (size_t)Hq * 2 * HEAD_DIM +
+                       (size_t)Hkv * HEAD_DIM + (size_t)vh * HEAD_DIM, HEAD_DIM * 2);
+                continue;
+            }
+            const int is_q = hh < Hq;
+            if (!is_q && !has_slot) continue;
+            const uint16_t* src = is_q ? row + (size_t)hh * 2 * HEAD_DIM : row + (size_t)Hq * 2 * HEAD_DIM +
+                                                                             (size_t)(hh - Hq) * HEAD_DIM;
+            const float* w = is_q ? q_norm : k_norm;
+            double ss = 0.0;
+            for (int d = 0; d < HEAD_DIM; d++) {
+                const double x = orc_b2f(src[d]);
+                ss += x * x;
+            }
+            const float scale = 1.f / sqrtf((float)ss / HEAD_DIM + eps);
+            float y[HEAD_DIM];
+            for (int d = 0; d < HEAD_DIM; d++) y[d] = rbf(orc_b2f(src[d]) * scale * w[d]);
+            float r[ROPE_DIM];
+            for (int d = 0; d < ROPE_DIM / 2; d++) {
+                const int axis = (d % 3 == 1 && d < 3 * sec_h) ? 1 : (d % 3 == 2 && d < 3 * sec_w) ? 2 : 0;
+                const float f = (float)rope[(size_t)axis * rope_stride + t] * inv_freq[d];
+                const float c = rbf(cosf(f)), sn = rbf(sinf(f));
+                const float lo = y[d], hi = y[d + ROPE_DIM / 2];
+                r[d] = rbf(rbf(lo * c) - rbf(hi * sn));
+                r[d + ROPE_DIM / 2] = rbf(rbf(hi * c) + rbf(lo * sn));
+            }
+            for (int d = 0; d < ROPE_DIM; d++) y[d] = r[d];
+            uint16_t* dst = is_q ? qout + ((size_t)t * Hq + hh) * HEAD_DIM
+                                 : kcache + ((size_t)slot * Hkv + (hh - Hq)) * HEAD_DIM;
+            for (int d = 0; d < HEAD_DIM; d++) dst[d] = orc_f2b(y[d]);
+        }
     }
 }

@@ -5,6 +5,7 @@
 #include "pkv_decode.hip"
 #include "pkv_prefill.hip"
 #include "pkv_verify.hip"
+#include "pkv_prep.hip"
 #include "../../include/pkv.h"
 
 #include <hip/hip_ext.h>
@@ -123,6 +124,41 @@ int pkv_page_copy(void* kcache, void* vcache, const int32_t* src, const int32_t*
     const int slices = (int)std::min<int64_t>(16, std::max<int64_t>(1, page_bytes / 4096));
     hipLaunchKernelGGL(pkv::page_copy_kernel, dim3(n, 2, slices), dim3(256), 0, (hipStream_t)stream,
                        (uint8_t*)kcache, (uint8_t*)vcache, src, dst, (long)page_bytes, (long)num_blocks, slices);
+    return launch_status();
+}
+
+int pkv_attn_prep(const void* qkv, int qstride, int Hq, int Hkv, const float* q_norm, const float* k_norm,
+                  const int32_t* rope, int rope_stride, int sec_h, int sec_w, const int32_t* slot_map,
+                  const float* inv_freq, void* qout, void* kcache, void* vcache, const float* kscale,
+                  const float* vscale, float eps, int T, int64_t num_slots, void* stream) {
+    if (T < 0 || Hq <= 0 || Hkv < 0 || num_slots < 0 || rope_stride < 0) return PKV_ERR_INVALID;
+    if (kscale || vscale) return PKV_ERR_UNSUPPORTED;  // E4M3 cache: not on this path
+    if (T == 0) return PKV_OK;
+    if (!qkv || !q_norm || !rope || !slot_map || !inv_freq || !qout) return PKV_ERR_INVALID;
+    if (Hkv > 0 && (!k_norm || !kcache || !vcache)) return PKV_ERR_INVALID;
+    if (rope_stride < T || qstride < (2 * Hq + 2 * Hkv) * pkv::HEAD_DIM || qstride % 4 != 0) return PKV_ERR_INVALID;
+    if (!aligned(qkv, 8) || !aligned(qout, 8) || !aligned(q_norm, 16) || (k_norm && !aligned(k_norm, 16)) ||
+        (kcache && !aligned(kcache, 8)) || (vcache && !aligned(vcache, 8)))
+        return PKV_ERR_INVALID;
+    pkv::PrepArgs a;
+    a.qkv = (const uint16_t*)qkv;
+    a.qstride = qstride;
+    a.Hq = Hq;
+    a.Hkv = Hkv;
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.rope = rope;
+    a.rope_stride = rope_stride;
+    a.sec_h = sec_h;
+    a.sec_w = sec_w;
+    a.slot_map = slot_map;
+    a.inv_freq = inv_freq;
+    a.qout = (uint16_t*)qout;
+    a.kcache = (uint16_t*)kcache;
+    a.vcache = (uint16_t*)vcache;
+    a.eps = eps;
+    a.num_slots = (long)num_slots;
+    hipLaunchKernelGGL(pkv::prep_kernel, dim3(T, (Hq + 2 * Hkv + 3) / 4), dim3(256), 0, (hipStream_t)stream, a);
     return launch_status();
 }
 

@@ -7,6 +7,7 @@
 // (src/model.rs:2366-2493) and compute the same results with this build's
 // kernel bodies:
 //
+//   attn_prep       (qwen35.cu:1076-1082)  grid (T, Hq + 2 Hkv), 128 threads
 //   attn_paged_g4   (qwen35.cu:1313-1334)  grid (T, Hkv, Z), 256 threads
 //   attn_merge      (qwen35.cu:2245-2249)  grid (T, Hq), 256 threads
 //   attn_groupr_g4_t2_k32 (qwen35.cu:1600-1616) grid (ceil(T/32) + seqs, Hkv),
@@ -31,6 +32,7 @@
 // size).
 #include "pkv_decode.hip"
 #include "pkv_prefill.hip"
+#include "pkv_prep.hip"
 
 #include <climits>
 
@@ -51,6 +53,36 @@ __device__ __forceinline__ bool ref_prompt_row(int skip_prompts, const int* cu, 
 }  // namespace pkv
 
 using pkv::HEAD_DIM;
+
+// One (token, head) per block as the reference launches it; the first wave
+// does the work (4 dims per lane), the second has none.
+extern "C" __global__ void __launch_bounds__(128)
+    attn_prep(const uint16_t* __restrict__ qkv, int qstride, int Hq, int Hkv, const float* __restrict__ q_norm,
+              const float* __restrict__ k_norm, const int* __restrict__ rope, int rope_stride, int sec_h, int sec_w,
+              const int* __restrict__ slot_map, const float* __restrict__ inv_freq, uint16_t* __restrict__ qout,
+              void* __restrict__ kcache, void* __restrict__ vcache, float* __restrict__ kscale,
+              float* __restrict__ vscale, float eps) {
+    if (threadIdx.x >= 64 || kscale || vscale) return;
+    pkv::PrepArgs a;
+    a.qkv = qkv;
+    a.qstride = qstride;
+    a.Hq = Hq;
+    a.Hkv = Hkv;
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.rope = rope;
+    a.rope_stride = rope_stride;
+    a.sec_h = sec_h;
+    a.sec_w = sec_w;
+    a.slot_map = slot_map;
+    a.inv_freq = inv_freq;
+    a.qout = qout;
+    a.kcache = (uint16_t*)kcache;
+    a.vcache = (uint16_t*)vcache;
+    a.eps = eps;
+    a.num_slots = pkv::REF_NO_CLAMP;
+    pkv::prep_head(a, blockIdx.x, blockIdx.y);
+}
 
 extern "C" __global__ void __launch_bounds__(256)
     attn_paged_g4(const uint16_t* __restrict__ q, const void* __restrict__ kcache, const void* __restrict__ vcache,

@@ -83,6 +83,8 @@ _SIGS = {
 }
 _SIGS["pkv_attn_decode_split"] = _SIGS["pkv_attn_decode"]
 _SIGS["pkv_attn_verify"] = _SIGS["pkv_attn_decode"]
+_SIGS["pkv_attn_prep"] = (_c_int, [_c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p,
+                                   _c_p, _c_p, _c_p, _c_p, _c_p, ctypes.c_float, _c_int, ctypes.c_int64, _c_p])
 _SIGS["pkv_attn_verify_workspace"] = _SIGS["pkv_attn_decode_workspace"]
 _SIGS["pkv_attn_decode_merge"] = _SIGS["pkv_attn_decode"]
 for _name, (_res, _args) in _SIGS.items():
@@ -206,6 +208,15 @@ def attn_verify(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_ta
                                 _ptr(tok_seq), _ptr(block_table), max_blocks, block_size, _ptr(out), scale, _ptr(cu),
                                 int(skip_prompts), _ptr(outs), spec, T, num_blocks, _ptr(workspace), workspace_bytes,
                                 _stream(stream)), "pkv_attn_verify")
+
+
+def attn_prep(qkv, qstride, Hq, Hkv, q_norm, k_norm, rope, rope_stride, sec_h, sec_w, slot_map, inv_freq, qout,
+              kcache, vcache, eps, T, num_slots, kscale=None, vscale=None, stream=None):
+    """Attention input preparation (reference attn_prep): q/k RMSNorm +
+    interleaved multimodal rotary, q to qout, k/v into their cache slots."""
+    _check(_lib.pkv_attn_prep(_ptr(qkv), qstride, Hq, Hkv, _ptr(q_norm), _ptr(k_norm), _ptr(rope), rope_stride, sec_h,
+                              sec_w, _ptr(slot_map), _ptr(inv_freq), _ptr(qout), _ptr(kcache), _ptr(vcache),
+                              _ptr(kscale), _ptr(vscale), eps, T, num_slots, _stream(stream)), "pkv_attn_prep")
 
 
 def attn_prefill(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks, block_size, out,

@@ -215,3 +215,94 @@ def test_mtp_slots_closed_form():
     dpos, dslot = oracle.mtp_slots([0, 1], [15, 3], bt, 3, BS, [47, 4], 2)
     assert list(dpos) == [17, 5]
     assert list(dslot) == [9 * 16 + 1, -1]
+
+
+# ---- attn_prep (reference qwen35.cu:1067-1128) ----
+
+def _prep_case(T, Hq, Hkv, rng, slots=None, sec=(11, 11, 10), theta=1e7):
+    qstride = (2 * Hq + 2 * Hkv) * 256
+    qkv = bf16_bits(rng.standard_normal((T, qstride)))
+    inv_freq = (1.0 / theta ** (2 * np.arange(32) / 64.0)).astype(np.float32)
+    return dict(qkv=qkv, qstride=qstride, Hq=Hq, Hkv=Hkv, q_norm=np.ones(256, np.float32),
+                k_norm=np.ones(256, np.float32), rope=np.zeros((3, T), np.int32), sec=sec, inv_freq=inv_freq,
+                slots=np.arange(T, dtype=np.int32) if slots is None else np.asarray(slots, np.int32))
+
+
+def _run_prep(c, eps=1e-6, pool=None):
+    T, Hq, Hkv = len(c["slots"]), c["Hq"], c["Hkv"]
+    pool = pool or max(T, 1)
+    qout = np.zeros((T, Hq, 256), np.uint16)
+    kc = np.full((pool, Hkv, 256), 0x7777, np.uint16)
+    vc = np.full((pool, Hkv, 256), 0x7777, np.uint16)
+    oracle.attn_prep(c["qkv"], c["qstride"], Hq, Hkv, c["q_norm"], c["k_norm"], c["rope"], T, c["sec"][1],
+                     c["sec"][2], c["slots"], c["inv_freq"], eps, qout, kc, vc)
+    return qout, kc, vc
+
+
+def test_prep_constant_rows_normalise_to_weights():
+    """A constant head row with eps = 0 normalises to exactly w (position 0:
+    no rotation): x * (1 / |x|) * w = w for w exact in bf16."""
+    rng = np.random.default_rng(0)
+    c = _prep_case(2, 4, 2, rng)
+    c["qkv"][:] = bf16_bits(np.full(c["qkv"].shape, 0.75))
+    c["q_norm"] = np.linspace(-2, 2, 256).astype(np.float32)
+    c["q_norm"] = oracle.b2f(bf16_bits(c["q_norm"]))
+    qout, kc, _ = _run_prep(c, eps=0.0)
+    assert np.array_equal(oracle.b2f(qout[0, 0]), c["q_norm"])
+    assert np.array_equal(oracle.b2f(kc[1, 1]), np.ones(256, np.float32))
+
+
+def test_prep_position_zero_is_plain_rmsnorm_and_v_is_copied():
+    rng = np.random.default_rng(1)
+    c = _prep_case(3, 4, 2, rng, slots=[5, -1, 2])
+    qout, kc, vc = _run_prep(c, pool=8)
+    x = oracle.b2f(c["qkv"][0, :256]).astype(np.float64)
+    y = x / np.sqrt((x * x).mean() + 1e-6)
+    got = oracle.b2f(qout[0, 0]).astype(np.float64)
+    assert np.abs(got - y).max() <= 2 ** -7 * np.abs(y).max()
+    # v rows bit for bit at their slots; slot -1 writes nothing (q still written)
+    voff = (2 * 4 + 2) * 256
+    assert np.array_equal(vc[5].reshape(-1), c["qkv"][0, voff:voff + 512])
+    assert np.array_equal(vc[2].reshape(-1), c["qkv"][2, voff:voff + 512])
+    untouched = [i for i in range(8) if i not in (5, 2)]
+    assert (vc[untouched] == 0x7777).all() and (kc[untouched] == 0x7777).all()
+    assert not (qout[1] == 0).all()
+
+
+def test_prep_rotation_keeps_pair_norms_and_angles():
+    """Each pair (d, d + 32) turns by pos * inv_freq[d]: against a complex
+    rotation of the position-0 result (within bf16 rounding)."""
+    rng = np.random.default_rng(2)
+    c = _prep_case(1, 1, 0, rng)
+    base, _, _ = _run_prep(c)
+    c["rope"][:] = 1234
+    rot, _, _ = _run_prep(c)
+    y0 = oracle.b2f(base[0, 0]).astype(np.float64)
+    y1 = oracle.b2f(rot[0, 0]).astype(np.float64)
+    ang = 1234.0 * c["inv_freq"].astype(np.float64)
+    z0 = y0[:32] + 1j * y0[32:64]
+    z1 = y1[:32] + 1j * y1[32:64]
+    want = z0 * np.exp(1j * ang)
+    assert np.abs(z1 - want).max() < 3 * 2 ** -8 * np.abs(z0).max()
+    assert np.array_equal(y1[64:], y0[64:])  # dims past 64 are not rotated
+
+
+def test_prep_axis_rule():
+    """Frequencies d % 3 == 1 below 3 sec_h take the height position, d % 3
+    == 2 below 3 sec_w the width position, the rest time (interleaved
+    multimodal rotary). Each frequency's angle identifies its axis."""
+    rng = np.random.default_rng(3)
+    c = _prep_case(1, 1, 0, rng, sec=(11, 5, 3))
+    base, _, _ = _run_prep(c)
+    c["rope"][:, 0] = [1000, 2000, 3000]
+    rot, _, _ = _run_prep(c)
+    y0 = oracle.b2f(base[0, 0]).astype(np.float64)
+    y1 = oracle.b2f(rot[0, 0]).astype(np.float64)
+    z0 = y0[:32] + 1j * y0[32:64]
+    z1 = y1[:32] + 1j * y1[32:64]
+    for d in range(32):
+        errs = [abs(z1[d] - z0[d] * np.exp(1j * p * float(c["inv_freq"][d]))) for p in (1000, 2000, 3000)]
+        axis = int(np.argmin(errs))
+        want = 1 if (d % 3 == 1 and d < 15) else 2 if (d % 3 == 2 and d < 9) else 0
+        if abs(z0[d]) > 0.05 and float(c["inv_freq"][d]) * 1000 > 1e-2:
+            assert axis == want, (d, errs)
