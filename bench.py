@@ -87,6 +87,10 @@ def main():
     ap.add_argument("--refabi", action="store_true",
                     help="c2/c3 through the reference-ABI code object (pkv_kernels.hsaco: attn_paged_g4 + attn_merge "
                          "on the reference engine's grid) after pkv_append")
+    ap.add_argument("--prefill-variant", type=int, default=None, help="c4: prefill kernel (pkv_attn_prefill_config)")
+    ap.add_argument("--with-prep", action="store_true",
+                    help="c2/c3: the step's append is pkv_attn_prep (q/k RMSNorm + rotary + K/V slot writes, the "
+                         "reference's attn_prep) on the raw qkv rows, followed by the key ranges and the merge")
     ap.add_argument("--unfused", action="store_true",
                     help="append, key ranges and merge as three launches instead of the fused step")
     args = ap.parse_args()
@@ -156,6 +160,12 @@ def main():
     sp = stream.cuda_stream
 
 
+    if args.with_prep:
+        args.unfused = True
+        qn = (1 + 0.1 * torch.randn(D, device=dev, generator=gen)).float()
+        kn = (1 + 0.1 * torch.randn(D, device=dev, generator=gen)).float()
+        inv_freq = (1.0 / 1e7 ** (torch.arange(32, device=dev, dtype=torch.float64) * 2 / 64)).float()
+        rope_d = pos_d.unsqueeze(1).expand(-1, 3, -1).contiguous()  # [steps][3][B]: text tokens
     rk = None
     if args.refabi:
         from pkv import refabi
@@ -183,7 +193,12 @@ def main():
                            P_(ts), P_(cu), I_(0), P_(out), P_(None), P_(None), I_(0), I_(0), P_(None), I_(1)],
                           stream=s_)
             return
-        if args.unfused:
+        if args.with_prep:
+            pkv.attn_prep(qkv, qstride, Hq, Hkv, qn, kn, rope_d[i], B, 11, 11, slot_d[i], inv_freq, q, kc, vc, 1e-6,
+                          B, pages * BS, stream=s_)
+            pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu,
+                            0, None, 1, B, pages, ws, stream=s_)
+        elif args.unfused:
             pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=s_)
             fn = pkv.attn_verify if args.verify_kernel else pkv.attn_decode
             fn(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu,
@@ -249,6 +264,7 @@ def main():
         # partials are overhead, not algorithmic.
         kern_bytes = [kk * Hkv * D * 2 * 2 + B * Hq * D * 2 for kk in keys]
         kname = ("attn_paged_g4 (reference ABI)" if args.refabi else
+                 "decode_range_kernel<4,false> (after attn_prep)" if args.with_prep else
                  "verify_range_kernel" if args.verify_kernel else "decode_range_kernel<4,false>")
     else:
         kern_bytes = step_bytes  # the fused kernel does the whole step
@@ -280,6 +296,7 @@ def main():
                                 if args.config == "c3" else
                                 "c2: single-sequence paged decode step at 4096 context (append + attention)"),
                    "path": ("reference-ABI code object (append, attn_paged_g4, attn_merge)" if args.refabi else
+                            "attn_prep (norm + rotary + append), key ranges, merge" if args.with_prep else
                             "unfused (append, key ranges, merge)" if args.unfused else "fused step (one launch)"),
                    "batch": B, "ctx": "U[512,8192]", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
                    "pool_pages": pages, "seed": seed, "mean_keys_per_step": round(float(np.mean(keys)), 1),
@@ -304,6 +321,8 @@ def bench_prefill(args):
 
     import pkv
 
+    if args.prefill_variant:
+        pkv.attn_prefill_config(args.prefill_variant)
     seed = args.seed if args.seed is not None else int(time.time()) % 100000
     dev = torch.device("cuda:0")
     Hq, Hkv, D, BS, B, P, N = 16, 4, 256, 16, 8, 16384, 2048

@@ -40,10 +40,10 @@ __device__ __forceinline__ uint32_t f2b_bits(float f) {
 __device__ __forceinline__ float rbf(float x) { return __uint_as_float(f2b_bits(x) << 16); }
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return f2b_bits(lo) | (f2b_bits(hi) << 16); }
 // Two finite floats to packed bf16 with the hardware's round-to-nearest-even
-// conversion (v_cvt_pk_bf16_f32); for values that are never NaN.
+// conversion (one v_cvt_pk_bf16_f32); for values that are never NaN.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack2_hw(float lo, float hi) {
-    return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)lo) |
-           ((uint32_t)__builtin_bit_cast(unsigned short, (__bf16)hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
 // Two bf16 products summed into c in f32 (v_dot2c_f32_bf16).

@@ -6,6 +6,7 @@
 // `row_bytes` = Hkv * head_bytes contiguous bytes, so a page is
 // block_size * row_bytes contiguous bytes. Every kernel copies whole slot
 // rows with 16-byte vector accesses when rows and pointers allow it.
+#pragma once
 #include "pkv_common.h"
 
 namespace pkv {

@@ -41,6 +41,7 @@
 // release/acquire fences per token piece, an L2 writeback and invalidate on
 // this multi-XCD part; measured at +45 us per batch-64 step, so the merge
 // stays a second launch.)
+#pragma once
 #include "pkv_common.h"
 
 #include <climits>

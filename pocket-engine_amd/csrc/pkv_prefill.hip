@@ -22,6 +22,7 @@
 // 16 kk + 4 (lane / 32) + {0..3, 8..11}). q stays in registers (64 VGPRs),
 // O^T takes 128 accumulators. The next tile's K/V are loaded into registers
 // while the current one is multiplied (double-buffered LDS).
+#pragma once
 #include "pkv_common.h"
 
 namespace pkv {
@@ -52,27 +53,28 @@ constexpr int PF_KSTR = HEAD_DIM + 8;  // K tile row stride (elements)
 constexpr int PF_VSTR = PF_BK + 4;
 constexpr int PF_K_ELEMS = PF_BK * PF_KSTR;
 constexpr int PF_V_ELEMS = HEAD_DIM * PF_VSTR;
-// Query positions per workgroup: 64 for the library's entry point (8 waves:
-// 4 query heads x 2 blocks of 32); 32 (4 waves) for launches that bring
-// their own grid of 32-query tiles.
+// Query positions per workgroup (BQ) and 32-query blocks per wave (NQB):
+// waves = 4 query heads x BQ / (32 NQB). NQB = 2 feeds every K / V^T
+// fragment read from LDS into two MFMAs (half the LDS traffic per MFMA) at
+// the cost of 128 q + 256 accumulator registers per wave (one wave per SIMD).
+#ifndef PKV_PF_NQB
+#define PKV_PF_NQB 1
+#endif
 constexpr int PF_BQ = 64;
-constexpr int pf_threads(int bq) { return 64 * 4 * (bq / 32); }
-constexpr int PF_THREADS = pf_threads(PF_BQ);
+constexpr int PF_NQB = PKV_PF_NQB;
+constexpr int pf_threads(int bq, int nqb) { return 64 * 4 * (bq / 32) / nqb; }
+constexpr int PF_THREADS = pf_threads(PF_BQ, PF_NQB);
 constexpr int PF_STAGE = PF_K_ELEMS + PF_V_ELEMS;
 constexpr size_t prefill_smem_bytes() { return (size_t)2 * PF_STAGE * 2; }
 
-// The whole kernel for one workgroup; pf_smem holds prefill_smem_bytes().
+// The query tile of this workgroup among the prompt sequences: tile
+// blockIdx.x of the concatenated BQ-query tiles of the prompt sequences
+// (sequences of more than one row that do not verify drafts). Returns false
+// if the grid has more blocks than tiles.
 template <int BQ>
-__device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
-    constexpr int THREADS = pf_threads(BQ);
-    static_assert(PF_BK * HEAD_DIM / 8 % THREADS == 0, "whole 16-byte chunks per thread");
-    // Buffer b: K tile at pf_smem + b * STAGE, V^T tile right after it.
-    constexpr int STAGE = PF_STAGE;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, lh = lane >> 5;
-    const int kvh = blockIdx.y;
-    const int G = 4, h = kvh * G + (wave & 3), qb0 = wave >> 2;  // the wave's query block
-    // Find this block's query tile among the prompt sequences.
-    int s = -1, tile = blockIdx.x;
+__device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s, int& tb, int& nb) {
+    int tile = blockIdx.x;
+    s = -1;
     for (int i = 0; i < p.seqs; i++) {
         const int n = p.cu[i + 1] - p.cu[i];
         if (n <= 1 || is_spec(p.outs, p.spec, i)) continue;
@@ -83,38 +85,63 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* p
         }
         tile -= tiles;
     }
-    if (s < 0) return;
-    const int tb = p.cu[s] + tile * BQ, nb = min(BQ, p.cu[s + 1] - tb);
+    if (s < 0) return false;
+    tb = p.cu[s] + tile * BQ;
+    nb = min(BQ, p.cu[s + 1] - tb);
+    return true;
+}
+
+// One workgroup's query tile (sequence s, rows tb .. tb + nb - 1, nb <= BQ);
+// pf_smem holds prefill_smem_bytes().
+template <int BQ, int NQB>
+__device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb) {
+    constexpr int THREADS = pf_threads(BQ, NQB);
+    static_assert(PF_BK * HEAD_DIM / 8 % THREADS == 0, "whole 16-byte chunks per thread");
+    // Buffer b: K tile at pf_smem + b * STAGE, V^T tile right after it.
+    constexpr int STAGE = PF_STAGE;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, lh = lane >> 5;
+    const int kvh = blockIdx.y;
+    const int G = 4, h = kvh * G + (wave & 3), qb0 = (wave >> 2) * NQB;  // the wave's first query block
     const int qp0 = p.pos[tb];
     const int L = qp0 + nb;  // keys this tile needs: 0 .. L - 1
     const int* bt = p.block_table + (size_t)s * p.max_blocks;
     const size_t row = (size_t)p.Hkv * HEAD_DIM;
 
-    // This wave's queries: query block qb0 (queries 32 qb0 + lq of the
+    // This wave's queries: blocks qb0 + qb (queries 32 (qb0 + qb) + lq of the
     // tile), q^T operands scaled into log2 units.
-    const int myq = qb0 * 32 + lq;
-    bf16x8 qf[16];
+    bf16x8 qf[NQB][16];
     {
         const float f = p.scale * LOG2E;
-        const bool ok = myq < nb;
-        const uint16_t* qrow = p.q + ((size_t)(tb + (ok ? myq : 0)) * p.Hq + h) * HEAD_DIM;
 #pragma unroll
-        for (int kk = 0; kk < 16; kk++) {
-            uint4 raw = ok ? *reinterpret_cast<const uint4*>(qrow + 16 * kk + 8 * lh) : make_uint4(0, 0, 0, 0);
-            // (outside the key loop: exact software rounding, NaN-preserving)
-            raw = make_uint4(pack2(bf_lo(raw.x) * f, bf_hi(raw.x) * f), pack2(bf_lo(raw.y) * f, bf_hi(raw.y) * f),
-                             pack2(bf_lo(raw.z) * f, bf_hi(raw.z) * f), pack2(bf_lo(raw.w) * f, bf_hi(raw.w) * f));
-            qf[kk] = as_bf16x8(raw);
+        for (int qb = 0; qb < NQB; qb++) {
+            const int myq = (qb0 + qb) * 32 + lq;
+            const bool ok = myq < nb;
+            const uint16_t* qrow = p.q + ((size_t)(tb + (ok ? myq : 0)) * p.Hq + h) * HEAD_DIM;
+#pragma unroll
+            for (int kk = 0; kk < 16; kk++) {
+                uint4 raw = ok ? *reinterpret_cast<const uint4*>(qrow + 16 * kk + 8 * lh) : make_uint4(0, 0, 0, 0);
+                // (outside the key loop: exact software rounding, NaN-preserving)
+                raw = make_uint4(pack2(bf_lo(raw.x) * f, bf_hi(raw.x) * f), pack2(bf_lo(raw.y) * f, bf_hi(raw.y) * f),
+                                 pack2(bf_lo(raw.z) * f, bf_hi(raw.z) * f), pack2(bf_lo(raw.w) * f, bf_hi(raw.w) * f));
+                qf[qb][kk] = as_bf16x8(raw);
+            }
         }
     }
-    f32x16 o[8];
+    f32x16 o[NQB][8];
 #pragma unroll
-    for (int db = 0; db < 8; db++)
+    for (int qb = 0; qb < NQB; qb++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) o[db][r] = 0.f;
-    float m = -INFINITY, l = 0.f;
-    const int qpw = qp0 + qb0 * 32;                      // the wave's first query position
-    const int last = qp0 + min(nb, (qb0 + 1) * 32) - 1;  // and its last
+        for (int db = 0; db < 8; db++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[qb][db][r] = 0.f;
+    float m[NQB], l[NQB];
+#pragma unroll
+    for (int qb = 0; qb < NQB; qb++) {
+        m[qb] = -INFINITY;
+        l[qb] = 0.f;
+    }
+    const int qpw = qp0 + qb0 * 32;                        // the wave's first query position
+    const int last = qp0 + min(nb, (qb0 + NQB) * 32) - 1;  // and its last
 
     // Tile loads: 32 keys x 256 dims of K and of V = 2 x 1024 chunks of 16 B,
     // NCH + NCH per thread. K: chunk e = tid + THREADS u is key e / 32,
@@ -173,55 +200,65 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* p
         if (k0 <= last) {
             const uint16_t* K = pf_smem + buf * STAGE;
             const uint16_t* Vt = K + PF_K_ELEMS;
-            // S^T = K Q^T. Lane (lh, lq) ends with query lq's scores of keys
+            // S^T = K Q^T; each K fragment feeds the wave's NQB blocks. Lane
+            // (lh, lq) ends with query lq's scores of keys
             // k0 + 8 (r / 4) + 4 lh + r % 4.
-            f32x16 st;
+            f32x16 st[NQB];
 #pragma unroll
-            for (int r = 0; r < 16; r++) st[r] = 0.f;
+            for (int qb = 0; qb < NQB; qb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) st[qb][r] = 0.f;
 #pragma unroll
             for (int kk = 0; kk < 16; kk++) {
                 const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(K + lq * PF_KSTR + 16 * kk + 8 * lh));
-                st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], st, 0, 0, 0);
+#pragma unroll
+                for (int qb = 0; qb < NQB; qb++)
+                    st[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb][kk], st[qb], 0, 0, 0);
             }
-            const int qp = qpw + lq;
-            if (k0 + PF_BK - 1 > qpw || k0 + PF_BK > L) {
+            uint4 pb[NQB][2];
+#pragma unroll
+            for (int qb = 0; qb < NQB; qb++) {
+                const int qb_first = qpw + qb * 32, qp = qb_first + lq;
+                if (k0 + PF_BK - 1 > qb_first || k0 + PF_BK > L) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int kp = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        if (kp > qp || kp >= L) st[qb][r] = -INFINITY;
+                    }
+                }
+                float mx = m[qb];
+#pragma unroll
+                for (int r = 0; r < 16; r++) mx = fmaxf(mx, st[qb][r]);
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                // A query with no key yet keeps -inf; it subtracts 0 so exp2 gives 0.
+                const float bse = mx == -INFINITY ? 0.f : mx;
+                const float corr = __builtin_amdgcn_exp2f(m[qb] - bse);
+                float sum = 0.f;
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int kp = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    if (kp > qp || kp >= L) st[r] = -INFINITY;
+                    st[qb][r] = __builtin_amdgcn_exp2f(st[qb][r] - bse);
+                    sum += st[qb][r];
                 }
+                sum += __shfl_xor(sum, 32, 64);
+                l[qb] = l[qb] * corr + sum;
+                m[qb] = mx;
+                // Rescale only when some query's max moved (rare after the first tiles).
+                if (__any(corr != 1.f)) {
+#pragma unroll
+                    for (int db = 0; db < 8; db++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) o[qb][db][r] *= corr;
+                }
+                // P^T (bf16) as the B operand: step kk, element e <-> key
+                // 16 kk + 8 (e / 4) + 4 lh + e % 4, i.e. register 8 kk + e.
+#pragma unroll
+                for (int kk = 0; kk < 2; kk++)
+                    pb[qb][kk] = make_uint4(pack2_hw(st[qb][8 * kk + 0], st[qb][8 * kk + 1]),
+                                            pack2_hw(st[qb][8 * kk + 2], st[qb][8 * kk + 3]),
+                                            pack2_hw(st[qb][8 * kk + 4], st[qb][8 * kk + 5]),
+                                            pack2_hw(st[qb][8 * kk + 6], st[qb][8 * kk + 7]));
             }
-            float mx = m;
-#pragma unroll
-            for (int r = 0; r < 16; r++) mx = fmaxf(mx, st[r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            // A query with no key yet keeps -inf; it subtracts 0 so exp2 gives 0.
-            const float bse = mx == -INFINITY ? 0.f : mx;
-            const float corr = __builtin_amdgcn_exp2f(m - bse);
-            float sum = 0.f;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                st[r] = __builtin_amdgcn_exp2f(st[r] - bse);
-                sum += st[r];
-            }
-            sum += __shfl_xor(sum, 32, 64);
-            l = l * corr + sum;
-            m = mx;
-            // Rescale only when some query's max moved (rare after the first tiles).
-            if (__any(corr != 1.f)) {
-#pragma unroll
-                for (int db = 0; db < 8; db++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) o[db][r] *= corr;
-            }
-            // P^T (bf16) as the B operand: step kk, element e <-> key
-            // 16 kk + 8 (e / 4) + 4 lh + e % 4, i.e. register 8 kk + e.
-            uint4 pb[2];
-#pragma unroll
-            for (int kk = 0; kk < 2; kk++)
-                pb[kk] = make_uint4(pack2_hw(st[8 * kk + 0], st[8 * kk + 1]), pack2_hw(st[8 * kk + 2], st[8 * kk + 3]),
-                                    pack2_hw(st[8 * kk + 4], st[8 * kk + 5]), pack2_hw(st[8 * kk + 6], st[8 * kk + 7]));
-            // O^T += V^T P^T
+            // O^T += V^T P^T; each V^T fragment feeds the wave's NQB blocks.
 #pragma unroll
             for (int kk = 0; kk < 2; kk++)
 #pragma unroll
@@ -230,7 +267,9 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* p
                     const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
                     const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
                     const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pb[kk]), o[db], 0, 0, 0);
+#pragma unroll
+                    for (int qb = 0; qb < NQB; qb++)
+                        o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pb[qb][kk]), o[qb][db], 0, 0, 0);
                 }
         }
         if (it + 1 < ntiles) {
@@ -239,29 +278,39 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* p
             __syncthreads();
         }
     }
-    if (myq >= nb) return;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const size_t t = (size_t)tb + myq;
-    const uint16_t* gate = p.qkv + t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM;
-    uint16_t* orow = p.out + (t * p.Hq + h) * HEAD_DIM;
 #pragma unroll
-    for (int db = 0; db < 8; db++)
+    for (int qb = 0; qb < NQB; qb++) {
+        const int myq = (qb0 + qb) * 32 + lq;
+        if (myq >= nb) continue;
+        const float inv = l[qb] > 0.f ? 1.f / l[qb] : 0.f;
+        const size_t t = (size_t)tb + myq;
+        const uint16_t* gate = p.qkv + t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM;
+        uint16_t* orow = p.out + (t * p.Hq + h) * HEAD_DIM;
 #pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) {
-            const int d = 32 * db + 8 * g4 + 4 * lh;
-            const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
-            const f32x16& oo = o[db];
-            *reinterpret_cast<uint2*>(orow + d) =
-                make_uint2(pack2(rbf(oo[4 * g4] * inv) / (1.f + __expf(-bf_lo(graw.x))),
-                                 rbf(oo[4 * g4 + 1] * inv) / (1.f + __expf(-bf_hi(graw.x)))),
-                           pack2(rbf(oo[4 * g4 + 2] * inv) / (1.f + __expf(-bf_lo(graw.y))),
-                                 rbf(oo[4 * g4 + 3] * inv) / (1.f + __expf(-bf_hi(graw.y)))));
-        }
+        for (int db = 0; db < 8; db++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const int d = 32 * db + 8 * g4 + 4 * lh;
+                const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
+                const f32x16& oo = o[qb][db];
+                *reinterpret_cast<uint2*>(orow + d) =
+                    make_uint2(pack2(rbf(oo[4 * g4] * inv) / (1.f + __expf(-bf_lo(graw.x))),
+                                     rbf(oo[4 * g4 + 1] * inv) / (1.f + __expf(-bf_hi(graw.x)))),
+                               pack2(rbf(oo[4 * g4 + 2] * inv) / (1.f + __expf(-bf_lo(graw.y))),
+                                     rbf(oo[4 * g4 + 3] * inv) / (1.f + __expf(-bf_hi(graw.y)))));
+            }
+    }
+}
+
+template <int BQ, int NQB>
+__device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
+    int s, tb, nb;
+    if (find_prefill_tile<BQ>(p, s, tb, nb)) prefill_tile<BQ, NQB>(p, pf_smem, s, tb, nb);
 }
 
 __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
-    prefill_body<PF_BQ>(p, pf_smem);
+    prefill_body<PF_BQ, PF_NQB>(p, pf_smem);
 }
 
 }  // namespace pkv

@@ -17,6 +17,7 @@
 // wave by shuffles, and each rotary pair's partner 8 lanes away inside the
 // same 16-lane row (dims 0..31 on lanes 0..7, 32..63 on lanes 8..15), fetched
 // with one DPP row rotate: no LDS, no barrier.
+#pragma once
 #include "pkv_common.h"
 
 namespace pkv {

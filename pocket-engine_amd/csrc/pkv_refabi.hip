@@ -212,7 +212,7 @@ namespace pkv {
 template <int BQ>
 __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
     __shared__ __align__(16) uint16_t sm[2 * PF_STAGE];
-    if ((int)blockDim.x != pf_threads(BQ) || Hq != 4 * Hkv || kscale || vscale || block_size <= 0 ||
+    if ((int)blockDim.x != pf_threads(BQ, 1) || Hq != 4 * Hkv || kscale || vscale || block_size <= 0 ||
         (block_size & (block_size - 1)))
         return;
     PrefillParams p;
@@ -235,7 +235,7 @@ __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
     p.outs = outs;
     p.spec = spec;
     p.num_blocks = REF_NO_CLAMP;
-    prefill_body<BQ>(p, sm);
+    prefill_body<BQ, 1>(p, sm);
 }
 
 }  // namespace pkv

@@ -30,6 +30,7 @@
 // (two cross-lane shuffles). The MFMA work per page is ~0.3 us of one SIMD's
 // time against the ~2.3 us the page's 16 KiB take at the HBM share of a
 // SIMD, so the kernel stays bandwidth-bound with the compute hidden.
+#pragma once
 #include "pkv_common.h"
 
 namespace pkv {
