@@ -87,7 +87,6 @@ def main():
     ap.add_argument("--refabi", action="store_true",
                     help="c2/c3 through the reference-ABI code object (pkv_kernels.hsaco: attn_paged_g4 + attn_merge "
                          "on the reference engine's grid) after pkv_append")
-    ap.add_argument("--prefill-variant", type=int, default=None, help="c4: prefill kernel (pkv_attn_prefill_config)")
     ap.add_argument("--with-prep", action="store_true",
                     help="c2/c3: the step's append is pkv_attn_prep (q/k RMSNorm + rotary + K/V slot writes, the "
                          "reference's attn_prep) on the raw qkv rows, followed by the key ranges and the merge")
@@ -321,8 +320,6 @@ def bench_prefill(args):
 
     import pkv
 
-    if args.prefill_variant:
-        pkv.attn_prefill_config(args.prefill_variant)
     seed = args.seed if args.seed is not None else int(time.time()) % 100000
     dev = torch.device("cuda:0")
     Hq, Hkv, D, BS, B, P, N = 16, 4, 256, 16, 8, 16384, 2048

@@ -155,14 +155,6 @@ int pkv_attn_verify(const void* q, const void* kcache, const void* vcache, const
                     const int32_t* outs, int spec, int T, int64_t num_blocks, void* workspace,
                     size_t workspace_bytes, void* stream);
 
-/* Selects the prefill kernel pkv_attn_prefill launches (process-wide):
- * 1 the kernel with register-staged tiles (any power-of-two block size);
- * 2 (default) and 3 the kernels with direct-to-LDS tiles, 32 (2) or 64 (3)
- * queries per wave, used for block sizes >= 16 and max_blocks <= 8192
- * (else 1). All compute the same function. No reference counterpart (a
- * measurement and test knob). */
-int pkv_attn_prefill_config(int variant);
-
 /* Measurement: the next key-range kernel this thread launches (the dominant
  * kernel of pkv_attn_decode / _split / _step / pkv_attn_verify) records start_event when it
  * starts executing and stop_event when it ends (hipExtLaunchKernelGGL), so

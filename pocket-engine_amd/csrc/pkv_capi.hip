@@ -6,7 +6,6 @@
 #include "pkv_prefill.hip"
 #include "pkv_verify.hip"
 #include "pkv_prep.hip"
-#include "pkv_prefill2.hip"
 #include "../../include/pkv.h"
 
 #include <hip/hip_ext.h>
@@ -47,7 +46,6 @@ int device_cus() {
 
 int g_wg_per_cu = 1;
 int g_min_range = 32;
-int g_prefill_variant = 1;  // 1: prefill_kernel; 2, 3: direct-to-LDS variants
 // Events the next key-range launch of this thread records at its start and
 // end (hipExtLaunchKernelGGL), then forgets.
 thread_local hipEvent_t t_ev_start = nullptr, t_ev_stop = nullptr;
@@ -207,18 +205,6 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
     p.num_blocks = (long)num_blocks;
     hipEvent_t e0 = t_pf_start, e1 = t_pf_stop;
     t_pf_start = t_pf_stop = nullptr;
-    if (block_size >= 16 && max_blocks <= pkv::P2_MAX_PAGES && g_prefill_variant >= 2) {
-        // direct-to-LDS tiles (block size >= 16: a tile spans <= 2 pages); variant 2: one 32-query
-        // block per wave (8 waves), 3: two (4 waves)
-        const int tiles = (T + pkv::P2_BQ - 1) / pkv::P2_BQ + seqs;
-        if (g_prefill_variant == 2)
-            hipExtLaunchKernelGGL(pkv::prefill2_q1_kernel, dim3(tiles, Hkv), dim3(pkv::p2_threads(1)), 0,
-                                  (hipStream_t)stream, e0, e1, 0, p, block_table);
-        else
-            hipExtLaunchKernelGGL(pkv::prefill2_q2_kernel, dim3(tiles, Hkv), dim3(pkv::p2_threads(2)), 0,
-                                  (hipStream_t)stream, e0, e1, 0, p, block_table);
-        return launch_status();
-    }
     // Upper bound on query tiles: each prompt sequence rounds up once.
     const int tiles = (T + pkv::PF_BQ - 1) / pkv::PF_BQ + seqs;
     hipExtLaunchKernelGGL(pkv::prefill_kernel, dim3(tiles, Hkv), dim3(pkv::PF_THREADS), smem, (hipStream_t)stream, e0,
@@ -235,12 +221,6 @@ int pkv_time_next_range_kernel(void* start_event, void* stop_event) {
 int pkv_time_next_prefill_kernel(void* start_event, void* stop_event) {
     t_pf_start = (hipEvent_t)start_event;
     t_pf_stop = (hipEvent_t)stop_event;
-    return PKV_OK;
-}
-
-int pkv_attn_prefill_config(int variant) {
-    if (variant < 1 || variant > 3) return PKV_ERR_INVALID;
-    g_prefill_variant = variant;
     return PKV_OK;
 }
 

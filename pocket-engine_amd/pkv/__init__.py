@@ -83,7 +83,6 @@ _SIGS = {
 }
 _SIGS["pkv_attn_decode_split"] = _SIGS["pkv_attn_decode"]
 _SIGS["pkv_attn_verify"] = _SIGS["pkv_attn_decode"]
-_SIGS["pkv_attn_prefill_config"] = (_c_int, [_c_int])
 _SIGS["pkv_attn_prep"] = (_c_int, [_c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p,
                                    _c_p, _c_p, _c_p, _c_p, _c_p, ctypes.c_float, _c_int, ctypes.c_int64, _c_p])
 _SIGS["pkv_attn_verify_workspace"] = _SIGS["pkv_attn_decode_workspace"]
@@ -166,10 +165,6 @@ def time_next_range_kernel(start_event, stop_event):
 def time_next_prefill_kernel(start_event, stop_event):
     h = lambda e: e if (e is None or isinstance(e, int)) else e.cuda_event
     _check(_lib.pkv_time_next_prefill_kernel(h(start_event), h(stop_event)), "pkv_time_next_prefill_kernel")
-
-
-def attn_prefill_config(variant=2):
-    _check(_lib.pkv_attn_prefill_config(variant), "pkv_attn_prefill_config")
 
 
 def attn_decode_config(wg_per_cu=1, min_range=32):
