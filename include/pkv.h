@@ -155,6 +155,20 @@ int pkv_attn_verify(const void* q, const void* kcache, const void* vcache, const
                     const int32_t* outs, int spec, int T, int64_t num_blocks, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* Decode (and draft-verify) attention over an E4M3 cache: the reference's
+ * attn_paged8_g<G> (src/kernels/qwen35.cu:1313-1334 with F8; kscale /
+ * vscale given) with the arguments of pkv_attn_decode plus the scales.
+ * kcache / vcache hold E4M3 bytes [blocks * 16][Hkv][256] and kscale /
+ * vscale one f32 per [slot][kv head] (written by pkv_attn_prep with
+ * scales): s_j = (q * scale) . k_j * kscale_j, out = bf16(bf16(sum_j p_j
+ * vscale_j v_j / sum_j p_j) * sigmoid(gate)). Rows group as in
+ * pkv_attn_verify (`cu` required); workspace: pkv_attn_verify_workspace. */
+int pkv_attn_decode_e4m3(const void* q, const void* kcache, const void* vcache, const float* kscale,
+                         const float* vscale, const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos,
+                         const int32_t* tok_seq, const int32_t* block_table, int max_blocks, int block_size,
+                         void* out, float scale, const int32_t* cu, int skip_prompts, const int32_t* outs, int spec,
+                         int T, int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Measurement: the next key-range kernel this thread launches (the dominant
  * kernel of pkv_attn_decode / _split / _step / pkv_attn_verify) records start_event when it
  * starts executing and stop_event when it ends (hipExtLaunchKernelGGL), so
@@ -206,8 +220,11 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
  * below 3 sec_h, width for d % 3 == 2 below 3 sec_w, else time; bf16 cos/sin);
  * q goes to qout [T][Hq][256], k to kcache and v (copied) to vcache at slot
  * slot_map[t] (rows [slot][Hkv][256]); k/v are skipped for slots outside
- * [0, num_slots). kscale / vscale (E4M3 cache) must be NULL here
- * (PKV_ERR_UNSUPPORTED otherwise). */
+ * [0, num_slots). With kscale / vscale (both or neither) the cache is E4M3:
+ * kcache / vcache hold bytes [slot][Hkv][256] and each k / v head row is
+ * stored as e4m3(v / s), s = amax / 448 (1 for an all-zero row) written to
+ * kscale / vscale [slot][Hkv] (the reference's store_e4m3,
+ * qwen35.cu:1055-1065). */
 int pkv_attn_prep(const void* qkv, int qstride, int Hq, int Hkv, const float* q_norm, const float* k_norm,
                   const int32_t* rope, int rope_stride, int sec_h, int sec_w, const int32_t* slot_map,
                   const float* inv_freq, void* qout, void* kcache, void* vcache, const float* kscale,

@@ -52,6 +52,14 @@ _lib.orc_attn_prefill.restype = _I
 _lib.orc_attn_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I]
 _lib.orc_mtp_slots.argtypes = [_P, _P, _P, _I, _I, _P, _I, _P, _P, _I]
 _lib.orc_attn_prep.argtypes = [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _F, _I, _L, _P, _P, _P]
+_lib.orc_e4m3_to_f.restype = _F
+_lib.orc_e4m3_to_f.argtypes = [ctypes.c_uint8]
+_lib.orc_f_to_e4m3.restype = ctypes.c_uint8
+_lib.orc_f_to_e4m3.argtypes = [_F]
+_lib.orc_store_e4m3.argtypes = [_P, _P, _P]
+_lib.orc_attn_prep8.argtypes = [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _F, _I, _L, _P, _P, _P, _P, _P]
+_lib.orc_attn_decode8.restype = _I
+_lib.orc_attn_decode8.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _F, _P, _I, _P, _I, _I]
 
 
 def _p(a):
@@ -184,3 +192,55 @@ def attn_prep(qkv, qstride, Hq, Hkv, q_norm, k_norm, rope, rope_stride, sec_h, s
     _lib.orc_attn_prep(_p(qkv), qstride, Hq, Hkv, _p(q_norm), _p(k_norm), _p(rope), rope_stride, sec_h, sec_w,
                        _p(slot_map), _p(inv_freq), eps, T, num_slots, _p(qout),
                        _p(kcache), _p(vcache))
+
+
+def e4m3_to_f(codes):
+    """E4M3FN bytes -> float32 (OCP: bias 7, max 448, 0x7F / 0xFF NaN)."""
+    codes = np.asarray(codes, np.uint8)
+    return np.array([_lib.orc_e4m3_to_f(int(c)) for c in codes.reshape(-1)], np.float32).reshape(codes.shape)
+
+
+def f_to_e4m3(x):
+    """float32 -> E4M3FN bytes, nearest-even, saturating to +-448."""
+    x = np.asarray(x, np.float32)
+    return np.array([_lib.orc_f_to_e4m3(float(v)) for v in x.reshape(-1)], np.uint8).reshape(x.shape)
+
+
+def store_e4m3(v):
+    """One head's 256 floats -> (bytes, scale) as the reference's store_e4m3."""
+    v = np.ascontiguousarray(v, np.float32)
+    out = np.zeros(256, np.uint8)
+    sc = np.zeros(1, np.float32)
+    _lib.orc_store_e4m3(_p(v), _p(out), _p(sc))
+    return out, float(sc[0])
+
+
+def attn_prep8(qkv, qstride, Hq, Hkv, q_norm, k_norm, rope, rope_stride, sec_h, sec_w, slot_map, inv_freq, eps,
+               qout, kcache8, vcache8, kscale, vscale):
+    """attn_prep with an E4M3 cache (bytes + f32 scale per slot and kv head)."""
+    T = len(slot_map)
+    qkv = np.ascontiguousarray(qkv, np.uint16)
+    q_norm = np.ascontiguousarray(q_norm, np.float32)
+    k_norm = np.ascontiguousarray(k_norm, np.float32)
+    rope = _i32(rope)
+    slot_map = _i32(slot_map)
+    inv_freq = np.ascontiguousarray(inv_freq, np.float32)
+    num_slots = kcache8.size // (max(Hkv, 1) * 256)
+    _lib.orc_attn_prep8(_p(qkv), qstride, Hq, Hkv, _p(q_norm), _p(k_norm), _p(rope), rope_stride, sec_h, sec_w,
+                        _p(slot_map), _p(inv_freq), eps, T, num_slots, _p(qout), _p(kcache8), _p(vcache8),
+                        _p(kscale), _p(vscale))
+
+
+def attn_decode8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks,
+                 block_size, scale, cu=None, skip_prompts=0, outs=None, spec=1, out=None):
+    """Decode attention over an E4M3 cache (reference attn_paged8 semantics)."""
+    T = len(pos)
+    if out is None:
+        out = np.zeros((T, Hq, 256), np.uint16)
+    cu, outs, pos, tok_seq, block_table = _i32(cu), _i32(outs), _i32(pos), _i32(tok_seq), _i32(block_table)
+    kscale = np.ascontiguousarray(kscale, np.float32)
+    vscale = np.ascontiguousarray(vscale, np.float32)
+    _lib.orc_attn_decode8(_p(q), _p(kcache8), _p(vcache8), _p(kscale), _p(vscale), _p(qkv), qstride, Hq, Hkv,
+                          _p(pos), _p(tok_seq), _p(block_table), max_blocks, block_size, _p(out), scale, _p(cu),
+                          skip_prompts, _p(outs), spec, T)
+    return out

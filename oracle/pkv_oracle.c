@@ -14,6 +14,10 @@
  *   - page copy (copy-on-write; build-defined: the reference has no CoW)
  *   - attention input preparation: q/k RMSNorm, interleaved multimodal
  *     rotary, q out, k/v to their cache slots (attn_prep, qwen35.cu:1067-1128)
+ *   - the E4M3 cache: per-(slot, head) scale amax / 448 and saturating
+ *     round-to-nearest-even E4M3 (OCP "E4M3FN": bias 7, max 448, NaN 0x7F /
+ *     0xFF, no infinities) bytes (store_e4m3, qwen35.cu:1055-1065), and
+ *     decode attention over it (attn_paged8_g*, qwen35.cu:1146-1309 with F8)
  *
  * Pinning (what each function is checked against, in tests/test_oracle.py):
  *   append/gather/page_copy: closed forms, gather(append(x)) == x under
@@ -21,6 +25,11 @@
  *   attention: torch fp64 scaled_dot_product_attention golden fixtures
  *       (tests/golden/), closed forms (one key -> v; equal keys -> mean of v;
  *       a dominant key -> its v), split+merge == unsplit.
+ *   E4M3: decoding of all 256 codes and rounding of random and tie values
+ *       against torch.float8_e4m3fn (which agrees in range; the reference
+ *       saturates where torch gives NaN: closed-form checks at +-448);
+ *       decode8 closed forms (one key -> its scaled value, equal keys -> the
+ *       mean) and decode8 == bf16 decode on values the E4M3 grid holds.
  *   attn_prep: closed forms (constant rows normalise to the weights; position
  *       0 leaves rows unrotated; a rotation keeps each pair's norm; the axis
  *       rule picks height/width positions for exactly the frequencies
@@ -352,4 +361,126 @@ void orc_attn_prep(const uint16_t* qkv, int qstride, int Hq, int Hkv, const floa
             for (int d = 0; d < HEAD_DIM; d++) dst[d] = orc_f2b(y[d]);
         }
     }
+}
+
+/* ---- E4M3 (OCP E4M3FN) ---- */
+float orc_e4m3_to_f(uint8_t b) {
+    const int sign = b >> 7, e = (b >> 3) & 15, m = b & 7;
+    float v;
+    if (e == 15 && m == 7) return NAN;
+    if (e == 0)
+        v = ldexpf((float)m, -9);  /* subnormal: m / 8 * 2^-6 */
+    else
+        v = ldexpf(1.f + m / 8.f, e - 7);
+    return sign ? -v : v;
+}
+
+/* Round to nearest, ties to even, saturating to +-448; NaN -> 0x7F. */
+uint8_t orc_f_to_e4m3(float x) {
+    if (isnan(x)) return 0x7F;
+    const uint8_t sign = signbit(x) ? 0x80 : 0;
+    double a = fabs((double)x);
+    if (a >= 448.0) return sign | 0x7E;
+    /* the E4M3 grid below 448: exhaustive nearest search with ties to even */
+    int best = 0;
+    double bd = a;
+    for (int c = 1; c <= 0x7E; c++) {
+        const double v = orc_e4m3_to_f((uint8_t)c);
+        const double d = fabs(v - a);
+        if (d < bd || (d == bd && (c & 1) == 0 && (best & 1) == 1)) {
+            bd = d;
+            best = c;
+        }
+    }
+    return sign | (uint8_t)best;
+}
+
+/* One head's 256 values as E4M3 with scale amax / 448 (1 if all zero):
+ * bytes = e4m3(v * (1 / scale)) (reference store_e4m3, qwen35.cu:1055-1065). */
+void orc_store_e4m3(const float* v, uint8_t* dst, float* scale) {
+    float amax = 0.f;
+    for (int d = 0; d < HEAD_DIM; d++) amax = fmaxf(amax, fabsf(v[d]));
+    const float sc = amax > 0.f ? amax / 448.f : 1.f;
+    const float inv = 1.f / sc;
+    for (int d = 0; d < HEAD_DIM; d++) dst[d] = orc_f_to_e4m3(v[d] * inv);
+    *scale = sc;
+}
+
+/* attn_prep with an E4M3 cache: as orc_attn_prep, but k (normed, rotated,
+ * bf16-rounded) and v (as read) go to kcache8 / vcache8 bytes with their
+ * per-(slot, head) scales in kscale / vscale. */
+void orc_attn_prep8(const uint16_t* qkv, int qstride, int Hq, int Hkv, const float* q_norm, const float* k_norm,
+                    const int* rope, int rope_stride, int sec_h, int sec_w, const int* slot_map,
+                    const float* inv_freq, float eps, int T, long num_slots, uint16_t* qout, uint8_t* kcache8,
+                    uint8_t* vcache8, float* kscale, float* vscale) {
+    uint16_t* kbf = (uint16_t*)malloc((size_t)(num_slots > 0 ? num_slots : 1) * Hkv * HEAD_DIM * 2);
+    uint16_t* vbf = (uint16_t*)malloc((size_t)(num_slots > 0 ? num_slots : 1) * Hkv * HEAD_DIM * 2);
+    orc_attn_prep(qkv, qstride, Hq, Hkv, q_norm, k_norm, rope, rope_stride, sec_h, sec_w, slot_map, inv_freq, eps, T,
+                  num_slots, qout, kbf, vbf);
+    for (int t = 0; t < T; t++) {
+        const long slot = slot_map[t];
+        if (slot < 0 || slot >= num_slots) continue;
+        for (int h = 0; h < Hkv; h++) {
+            const size_t at = (size_t)slot * Hkv + h;
+            float kv[HEAD_DIM], vv[HEAD_DIM];
+            for (int d = 0; d < HEAD_DIM; d++) {
+                kv[d] = orc_b2f(kbf[at * HEAD_DIM + d]);
+                vv[d] = orc_b2f(vbf[at * HEAD_DIM + d]);
+            }
+            orc_store_e4m3(kv, kcache8 + at * HEAD_DIM, kscale + at);
+            orc_store_e4m3(vv, vcache8 + at * HEAD_DIM, vscale + at);
+        }
+    }
+    free(kbf);
+    free(vbf);
+}
+
+/* Paged decode attention over an E4M3 cache (reference attn_body<F8>,
+ * qwen35.cu:1146-1309): s_j = (q * scale) . k8_j * kscale_j, p_j = e^(s_j -
+ * max), out = bf16(bf16(sum p_j vscale_j v8_j / sum p_j) * sigmoid(gate));
+ * softmax and sums in double. Same metadata rules as orc_attn_decode. */
+int orc_attn_decode8(const uint16_t* q, const uint8_t* kcache8, const uint8_t* vcache8, const float* kscale,
+                     const float* vscale, const uint16_t* qkv, int qstride, int Hq, int Hkv, const int* pos,
+                     const int* tok_seq, const int* block_table, int max_blocks, int block_size, uint16_t* out,
+                     float scale, const int* cu, int skip_prompts, const int* outs, int spec, int T) {
+    const int G = Hq / Hkv;
+    double* s = NULL;
+    size_t cap = 0;
+    for (int t = 0; t < T; t++) {
+        const int sq = tok_seq[t];
+        if (skip_prompts && cu[sq + 1] - cu[sq] > 1 && !is_spec(outs, spec, sq)) continue;
+        const int L = pos[t] + 1;
+        if ((size_t)L > cap) {
+            cap = (size_t)L;
+            s = (double*)realloc(s, cap * sizeof(double));
+        }
+        const int* bt = block_table + (size_t)sq * max_blocks;
+        for (int h = 0; h < Hq; h++) {
+            const int kvh = h / G;
+            double mx = -INFINITY;
+            for (int j = 0; j < L; j++) {
+                const size_t at = ((size_t)bt[j / block_size] * block_size + j % block_size) * Hkv + kvh;
+                double d = 0.0;
+                for (int e = 0; e < HEAD_DIM; e++)
+                    d += (double)orc_b2f(q[((size_t)t * Hq + h) * HEAD_DIM + e]) * scale *
+                         orc_e4m3_to_f(kcache8[at * HEAD_DIM + e]);
+                s[j] = d * kscale[at];
+                if (s[j] > mx) mx = s[j];
+            }
+            double S = 0.0, A[HEAD_DIM];
+            for (int e = 0; e < HEAD_DIM; e++) A[e] = 0.0;
+            for (int j = 0; j < L; j++) {
+                const size_t at = ((size_t)bt[j / block_size] * block_size + j % block_size) * Hkv + kvh;
+                const double p = exp(s[j] - mx);
+                S += p;
+                for (int e = 0; e < HEAD_DIM; e++) A[e] += p * vscale[at] * orc_e4m3_to_f(vcache8[at * HEAD_DIM + e]);
+            }
+            for (int e = 0; e < HEAD_DIM; e++) {
+                const float gate = orc_b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + e]);
+                out[((size_t)t * Hq + h) * HEAD_DIM + e] = gated(A[e] / S, gate);
+            }
+        }
+    }
+    free(s);
+    return 0;
 }

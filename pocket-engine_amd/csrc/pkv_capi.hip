@@ -132,13 +132,14 @@ int pkv_attn_prep(const void* qkv, int qstride, int Hq, int Hkv, const float* q_
                   const float* inv_freq, void* qout, void* kcache, void* vcache, const float* kscale,
                   const float* vscale, float eps, int T, int64_t num_slots, void* stream) {
     if (T < 0 || Hq <= 0 || Hkv < 0 || num_slots < 0 || rope_stride < 0) return PKV_ERR_INVALID;
-    if (kscale || vscale) return PKV_ERR_UNSUPPORTED;  // E4M3 cache: not on this path
+    if ((kscale == nullptr) != (vscale == nullptr)) return PKV_ERR_INVALID;  // both (E4M3 cache) or neither
     if (T == 0) return PKV_OK;
     if (!qkv || !q_norm || !rope || !slot_map || !inv_freq || !qout) return PKV_ERR_INVALID;
     if (Hkv > 0 && (!k_norm || !kcache || !vcache)) return PKV_ERR_INVALID;
     if (rope_stride < T || qstride < (2 * Hq + 2 * Hkv) * pkv::HEAD_DIM || qstride % 4 != 0) return PKV_ERR_INVALID;
     if (!aligned(qkv, 8) || !aligned(qout, 8) || !aligned(q_norm, 16) || (k_norm && !aligned(k_norm, 16)) ||
-        (kcache && !aligned(kcache, 8)) || (vcache && !aligned(vcache, 8)))
+        (kcache && !aligned(kcache, 8)) || (vcache && !aligned(vcache, 8)) || (kscale && !aligned(kscale, 4)) ||
+        (vscale && !aligned(vscale, 4)))
         return PKV_ERR_INVALID;
     pkv::PrepArgs a;
     a.qkv = (const uint16_t*)qkv;
@@ -156,6 +157,8 @@ int pkv_attn_prep(const void* qkv, int qstride, int Hq, int Hkv, const float* q_
     a.qout = (uint16_t*)qout;
     a.kcache = (uint16_t*)kcache;
     a.vcache = (uint16_t*)vcache;
+    a.kscale = (float*)kscale;
+    a.vscale = (float*)vscale;
     a.eps = eps;
     a.num_slots = (long)num_slots;
     hipLaunchKernelGGL(pkv::prep_kernel, dim3(T, (Hq + 2 * Hkv + 3) / 4), dim3(256), 0, (hipStream_t)stream, a);
@@ -259,7 +262,7 @@ struct AppendArgs {
 // kernel with the step's append fused in (needs `app`); bit 8: the verify
 // kernels (rows grouped by sequence, 4 per page pass) instead of per-token
 // decode (with bits 1 and 2).
-int attn_decode_phases(int phases, const AppendArgs* app, const void* q, const void* kcache, const void* vcache,
+int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, const float* vscale, const void* q, const void* kcache, const void* vcache,
                        const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos, const int32_t* tok_seq,
                        const int32_t* block_table, int max_blocks, int block_size, void* out, float scale,
                        const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
@@ -273,6 +276,8 @@ int attn_decode_phases(int phases, const AppendArgs* app, const void* q, const v
     if ((skip_prompts || (phases & 8)) && !cu) return PKV_ERR_INVALID;
     const bool verify = phases & 8;
     if (verify && (phases & 4)) return PKV_ERR_INVALID;
+    const bool f8 = kscale != nullptr;
+    if (f8 && (!verify || !vscale || !aligned(kscale, 4) || !aligned(vscale, 4))) return PKV_ERR_INVALID;
     if (qstride < 2 * Hq * pkv::HEAD_DIM || qstride % 8 != 0) return PKV_ERR_INVALID;
     if (!aligned(q, 16) || !aligned(kcache, 16) || !aligned(vcache, 16) || !aligned(qkv, 16) || !aligned(out, 16) ||
         !aligned(workspace, 256))
@@ -311,13 +316,18 @@ int attn_decode_phases(int phases, const AppendArgs* app, const void* q, const v
     p.k_rows = app ? (const uint16_t*)app->k_rows : nullptr;
     p.v_rows = app ? (const uint16_t*)app->v_rows : nullptr;
     p.row_stride = app ? (long)(app->row_stride / 2) : 0;
+    p.kscale = kscale;
+    p.vscale = vscale;
     const int32_t* slot_map = app ? app->slot_map : nullptr;
     if (phases & 5) {
         hipEvent_t e0 = t_ev_start, e1 = t_ev_stop;
         t_ev_start = t_ev_stop = nullptr;
-        if (verify)
-            hipExtLaunchKernelGGL(pkv::verify_range_kernel, dim3(n_wg, groups), dim3(threads), 0, (hipStream_t)stream,
-                                  e0, e1, 0, p, pos, tok_seq, block_table, cu, outs);
+        if (verify && f8)
+            hipExtLaunchKernelGGL((pkv::verify_range_kernel<true>), dim3(n_wg, groups), dim3(threads), 0,
+                                  (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs);
+        else if (verify)
+            hipExtLaunchKernelGGL((pkv::verify_range_kernel<false>), dim3(n_wg, groups), dim3(threads), 0,
+                                  (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs);
         else if (phases & 4)
             hipExtLaunchKernelGGL((pkv::decode_range_kernel<4, true>), dim3(n_wg, groups), dim3(threads), 0,
                                   (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs, slot_map);
@@ -352,16 +362,29 @@ extern "C" {
     q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, out, scale, cu,  \
         skip_prompts, outs, spec, T, num_blocks, workspace, workspace_bytes, stream
 
-int pkv_attn_decode(PKV_DECODE_ARGS) { return attn_decode_phases(3, nullptr, PKV_DECODE_PASS); }
-int pkv_attn_decode_split(PKV_DECODE_ARGS) { return attn_decode_phases(1, nullptr, PKV_DECODE_PASS); }
-int pkv_attn_decode_merge(PKV_DECODE_ARGS) { return attn_decode_phases(2, nullptr, PKV_DECODE_PASS); }
+int pkv_attn_decode(PKV_DECODE_ARGS) { return attn_decode_phases(3, nullptr, nullptr, nullptr, PKV_DECODE_PASS); }
+int pkv_attn_decode_split(PKV_DECODE_ARGS) {
+    return attn_decode_phases(1, nullptr, nullptr, nullptr, PKV_DECODE_PASS);
+}
+int pkv_attn_decode_merge(PKV_DECODE_ARGS) {
+    return attn_decode_phases(2, nullptr, nullptr, nullptr, PKV_DECODE_PASS);
+}
 
-int pkv_attn_verify(PKV_DECODE_ARGS) { return attn_decode_phases(8 | 3, nullptr, PKV_DECODE_PASS); }
+int pkv_attn_verify(PKV_DECODE_ARGS) { return attn_decode_phases(8 | 3, nullptr, nullptr, nullptr, PKV_DECODE_PASS); }
+
+int pkv_attn_decode_e4m3(const void* q, const void* kcache, const void* vcache, const float* kscale,
+                         const float* vscale, const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos,
+                         const int32_t* tok_seq, const int32_t* block_table, int max_blocks, int block_size, void* out,
+                         float scale, const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T,
+                         int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!kscale || !vscale) return PKV_ERR_INVALID;
+    return attn_decode_phases(8 | 3, nullptr, kscale, vscale, PKV_DECODE_PASS);
+}
 
 int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map,
                          PKV_DECODE_ARGS) {
     const AppendArgs app{k_rows, v_rows, row_stride, slot_map};
-    return attn_decode_phases(4 | 2, &app, PKV_DECODE_PASS);
+    return attn_decode_phases(4 | 2, &app, nullptr, nullptr, PKV_DECODE_PASS);
 }
 
 }  // extern "C"

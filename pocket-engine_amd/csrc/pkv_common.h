@@ -46,6 +46,26 @@ __device__ __forceinline__ uint32_t pack2_hw(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
+// E4M3 (OCP E4M3FN on gfx950: bias 7, max 448, NaN 0x7F) conversions.
+// Two E4M3 bytes (the low or high half of w) to two bf16 (exact: bf16 holds
+// every E4M3 value).
+template <bool HI>
+__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+}
+// Eight E4M3 bytes (two words) to eight bf16 (an MFMA operand).
+__device__ __forceinline__ uint4 e4m3x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+    return make_uint4(e4m3x2_to_bf16x2<false>(w0), e4m3x2_to_bf16x2<true>(w0), e4m3x2_to_bf16x2<false>(w1),
+                      e4m3x2_to_bf16x2<true>(w1));
+}
+// Four floats to four E4M3 bytes, round to nearest even (values within the
+// E4M3 range; callers scale to |v| <= 448).
+__device__ __forceinline__ uint32_t f32x4_to_e4m3x4(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return (uint32_t)w;
+}
+
 // Two bf16 products summed into c in f32 (v_dot2c_f32_bf16).
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);

@@ -10,7 +10,9 @@
 //     3 sec_h, 2 (width) for d % 3 == 2 below 3 sec_w, else 0 (time);
 //     q goes to qout[t][hh], k to kcache[slot][hh - Hq];
 //   v heads: copied bit for bit to vcache[slot];
-//   k and v are skipped for slot_map[t] < 0 (padding rows); q is always written.
+//   k and v are skipped for slot_map[t] < 0 (padding rows); q is always written;
+//   with an E4M3 cache (kscale / vscale given) k and v are stored as E4M3
+//   bytes with an f32 scale per (slot, kv head) (store_e4m3_wave).
 //
 // Layout (this build's own): one wave per (token, head), 4 consecutive dims
 // per lane (one 8-byte load and store), the squared sum reduced across the
@@ -36,9 +38,25 @@ struct PrepArgs {
     uint16_t* qout;
     uint16_t* kcache;
     uint16_t* vcache;
+    float* kscale;  // non-null: an E4M3 cache (bytes in kcache / vcache, f32 scale per slot and kv head)
+    float* vscale;
     float eps;
     long num_slots;
 };
+
+// One head's 256 values (4 per lane) as E4M3 with scale amax / 448 (1 if
+// all zero): bytes = e4m3(v * (1 / scale)) (reference store_e4m3,
+// qwen35.cu:1055-1065).
+__device__ __forceinline__ void store_e4m3_wave(const float (&v)[4], uint8_t* dst, float* scale) {
+    const int lane = threadIdx.x & 63;
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float sc = amax > 0.f ? amax / 448.f : 1.f;
+    const float inv = 1.f / sc;
+    *reinterpret_cast<uint32_t*>(dst + 4 * lane) = f32x4_to_e4m3x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+    if (lane == 0) *scale = sc;
+}
 
 // One wave: token t, head hh (q heads, then k heads, then v heads).
 __device__ __forceinline__ void prep_head(const PrepArgs& a, int t, int hh) {
@@ -50,8 +68,14 @@ __device__ __forceinline__ void prep_head(const PrepArgs& a, int t, int hh) {
         if (!has_slot) return;
         const int vh = hh - a.Hq - a.Hkv;
         const uint16_t* src = row + (size_t)a.Hq * 2 * HEAD_DIM + (size_t)(a.Hkv + vh) * HEAD_DIM;
-        *reinterpret_cast<uint2*>(a.vcache + ((size_t)slot * a.Hkv + vh) * HEAD_DIM + 4 * lane) =
-            *reinterpret_cast<const uint2*>(src + 4 * lane);
+        const size_t at = (size_t)slot * a.Hkv + vh;
+        const uint2 raw = *reinterpret_cast<const uint2*>(src + 4 * lane);
+        if (a.vscale) {
+            const float x[4] = {bf_lo(raw.x), bf_hi(raw.x), bf_lo(raw.y), bf_hi(raw.y)};
+            store_e4m3_wave(x, reinterpret_cast<uint8_t*>(a.vcache) + at * HEAD_DIM, a.vscale + at);
+        } else {
+            *reinterpret_cast<uint2*>(a.vcache + at * HEAD_DIM + 4 * lane) = raw;
+        }
         return;
     }
     const bool is_q = hh < a.Hq;
@@ -81,6 +105,11 @@ __device__ __forceinline__ void prep_head(const PrepArgs& a, int t, int hh) {
             const float lo = lo_half ? y[e] : yp[e], hi = lo_half ? yp[e] : y[e];
             y[e] = lo_half ? rbf(rbf(lo * c) - rbf(hi * s)) : rbf(rbf(hi * c) + rbf(lo * s));
         }
+    }
+    if (!is_q && a.kscale) {
+        const size_t at = (size_t)slot * a.Hkv + (hh - a.Hq);
+        store_e4m3_wave(y, reinterpret_cast<uint8_t*>(a.kcache) + at * HEAD_DIM, a.kscale + at);
+        return;
     }
     uint16_t* dst = is_q ? a.qout + ((size_t)t * a.Hq + hh) * HEAD_DIM
                          : a.kcache + ((size_t)slot * a.Hkv + (hh - a.Hq)) * HEAD_DIM;

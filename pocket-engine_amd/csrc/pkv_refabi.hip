@@ -62,7 +62,7 @@ extern "C" __global__ void __launch_bounds__(128)
               const int* __restrict__ slot_map, const float* __restrict__ inv_freq, uint16_t* __restrict__ qout,
               void* __restrict__ kcache, void* __restrict__ vcache, float* __restrict__ kscale,
               float* __restrict__ vscale, float eps) {
-    if (threadIdx.x >= 64 || kscale || vscale) return;
+    if (threadIdx.x >= 64 || (kscale == nullptr) != (vscale == nullptr)) return;
     pkv::PrepArgs a;
     a.qkv = qkv;
     a.qstride = qstride;
@@ -79,6 +79,8 @@ extern "C" __global__ void __launch_bounds__(128)
     a.qout = qout;
     a.kcache = (uint16_t*)kcache;
     a.vcache = (uint16_t*)vcache;
+    a.kscale = kscale;
+    a.vscale = vscale;
     a.eps = eps;
     a.num_slots = pkv::REF_NO_CLAMP;
     pkv::prep_head(a, blockIdx.x, blockIdx.y);

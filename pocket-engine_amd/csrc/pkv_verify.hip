@@ -55,6 +55,12 @@ __device__ __forceinline__ int seg_len(int t, int T, const int* __restrict__ pos
 
 // One wave: segment headed by token t (rows t + r, r < 4, attending Lr[r]
 // keys; Lr = 0 for absent rows), kv head kvh, keys [j0, j1).
+// F8: an E4M3 cache (bytes [slot][Hkv][256], f32 kscale / vscale per slot and
+// kv head; reference attn_paged8, qwen35.cu:1146-1309 with F8): K and V bytes
+// are converted to bf16 in registers (exact), each score is multiplied by its
+// key's kscale, and each weight by its key's vscale before P.V (the softmax
+// sum takes the unscaled weights).
+template <bool F8>
 __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* __restrict__ bt, uint16_t* vl, int t,
                                              int kvh, int j0, int j1, int Ls, int L0, int L1, int L2, int L3,
                                              int idx) {
@@ -62,32 +68,65 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
     const int r_me = c16 >> 2, g_me = c16 & 3;
     const int myL = r_me == 0 ? L0 : r_me == 1 ? L1 : r_me == 2 ? L2 : L3;
     const float sl2 = p.scale * LOG2E;
-    const size_t row_elems = (size_t)p.Hkv * HEAD_DIM;
+    const size_t row_elems = (size_t)p.Hkv * HEAD_DIM;  // slot row: elements (bf16) or bytes (E4M3)
 
+    // q.k over the 256 dims in 8 steps of 32: step c, lane group gq takes
+    // dims dim0(c) .. + 7 (the same for q and k).
+    auto dim0 = [&](int c) { return F8 ? 64 * gq + 16 * (c >> 1) + 8 * (c & 1) : 32 * c + 8 * gq; };
     bf16x8 qf[8];
     if (myL > 0) {
-        const uint16_t* qrow = p.q + ((size_t)(t + r_me) * p.Hq + kvh * 4 + g_me) * HEAD_DIM + 8 * gq;
+        const uint16_t* qrow = p.q + ((size_t)(t + r_me) * p.Hq + kvh * 4 + g_me) * HEAD_DIM;
 #pragma unroll
-        for (int c = 0; c < 8; c++) qf[c] = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + 32 * c));
+        for (int c = 0; c < 8; c++) qf[c] = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + dim0(c)));
     } else {
 #pragma unroll
         for (int c = 0; c < 8; c++) qf[c] = as_bf16x8(make_uint4(0, 0, 0, 0));
     }
-    auto page_base = [&](int pi) -> size_t {
-        long pg = bt[pi];
-        pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
-        return (size_t)pg * PAGE * row_elems + (size_t)kvh * HEAD_DIM;
+    auto page_of = [&](int pi) -> long {
+        const long pg = bt[pi];
+        return pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
     };
-    uint4 kb[8], vb[8];
-    auto load_k = [&](size_t base) {
-        const uint16_t* r = p.kc + base + (size_t)c16 * row_elems + 8 * gq;
+    auto page_base = [&](int pi) -> size_t { return (size_t)page_of(pi) * PAGE * row_elems + (size_t)kvh * HEAD_DIM; };
+    constexpr int NK = F8 ? 4 : 8, NV = F8 ? 4 : 8;  // 16-byte loads per lane per page
+    uint4 kb[NK], vb[NV];
+    float ksc[4], vsc[4];  // E4M3: scales of this lane's keys 4 gq + i
+    auto load_k = [&](size_t base, int pi) {
+        if constexpr (F8) {
+            const uint8_t* r = reinterpret_cast<const uint8_t*>(p.kc) + base + (size_t)c16 * row_elems + 64 * gq;
 #pragma unroll
-        for (int c = 0; c < 8; c++) kb[c] = load_nt(r + 32 * c);
+            for (int c = 0; c < NK; c++) kb[c] = load_nt(r + 16 * c);
+            const size_t s0 = ((size_t)page_of(pi) * PAGE + 4 * gq) * p.Hkv + kvh;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                ksc[i] = p.kscale[s0 + (size_t)i * p.Hkv];
+                vsc[i] = p.vscale[s0 + (size_t)i * p.Hkv];
+            }
+        } else {
+            const uint16_t* r = p.kc + base + (size_t)c16 * row_elems + 8 * gq;
+#pragma unroll
+            for (int c = 0; c < NK; c++) kb[c] = load_nt(r + 32 * c);
+        }
     };
     auto load_v = [&](size_t base) {
-        const uint16_t* r = p.vc + base + (size_t)(lane >> 5) * row_elems + 8 * (lane & 31);
+        if constexpr (F8) {
+            // keys 4 k + lane / 16, bytes 16 (lane % 16) .. + 15
+            const uint8_t* r = reinterpret_cast<const uint8_t*>(p.vc) + base + (size_t)(lane >> 4) * row_elems + 16 * c16;
 #pragma unroll
-        for (int k = 0; k < 8; k++) vb[k] = load_nt(r + (size_t)(2 * k) * row_elems);
+            for (int k = 0; k < NV; k++) vb[k] = load_nt(r + (size_t)(4 * k) * row_elems);
+        } else {
+            const uint16_t* r = p.vc + base + (size_t)(lane >> 5) * row_elems + 8 * (lane & 31);
+#pragma unroll
+            for (int k = 0; k < NV; k++) vb[k] = load_nt(r + (size_t)(2 * k) * row_elems);
+        }
+    };
+    // A operand of step c: K dims dim0(c) .. + 7 of key c16
+    auto k_frag = [&](int c) -> bf16x8 {
+        if constexpr (F8) {
+            const uint4 w = kb[c >> 1];
+            return as_bf16x8((c & 1) ? e4m3x8_to_bf16x8(w.z, w.w) : e4m3x8_to_bf16x8(w.x, w.y));
+        } else {
+            return as_bf16x8(kb[c]);
+        }
     };
 
     f32x4 acc[16];
@@ -102,11 +141,27 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
     auto page = [&](int pi, size_t next, bool prefetch) {
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < 8; c++) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kb[c]), qf[c], s, 0, 0, 0);
+        for (int c = 0; c < 8; c++) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_frag(c), qf[c], s, 0, 0, 0);
+        float ks_cur[4], vs_cur[4];
+        if constexpr (F8) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) *reinterpret_cast<uint4*>(st + 2 * k * VF_VSTR) = vb[k];
+            for (int i = 0; i < 4; i++) {
+                ks_cur[i] = ksc[i];
+                vs_cur[i] = vsc[i];
+            }
+            // V rows to LDS as bf16: row 4 k + lane / 16, dims 16 (lane % 16) .. + 15
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                uint16_t* d = vl + (4 * k + (lane >> 4)) * VF_VSTR + 16 * c16;
+                *reinterpret_cast<uint4*>(d) = e4m3x8_to_bf16x8(vb[k].x, vb[k].y);
+                *reinterpret_cast<uint4*>(d + 8) = e4m3x8_to_bf16x8(vb[k].z, vb[k].w);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < NV; k++) *reinterpret_cast<uint4*>(st + 2 * k * VF_VSTR) = vb[k];
+        }
         if (prefetch) {
-            load_k(next);
+            load_k(next, pi + 1);
             load_v(next);
         }
         const int k0 = pi * PAGE + 4 * gq;
@@ -114,7 +169,8 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int kp = k0 + i;
-            sc[i] = (kp >= j0 && kp < j1 && kp < myL) ? s[i] * sl2 : -INFINITY;
+            const float v = F8 ? s[i] * ks_cur[i] : s[i];
+            sc[i] = (kp >= j0 && kp < j1 && kp < myL) ? v * sl2 : -INFINITY;
             mx = fmaxf(mx, sc[i]);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -122,29 +178,48 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
         const float mn = fmaxf(m, mx);
         const float mref = mn == -INFINITY ? 0.f : mn;  // a column with no key yet keeps zeros
         const float corr = __builtin_amdgcn_exp2f(m - mref);
-        const uint32_t p01 = pack2_hw(__builtin_amdgcn_exp2f(sc[0] - mref), __builtin_amdgcn_exp2f(sc[1] - mref));
-        const uint32_t p23 = pack2_hw(__builtin_amdgcn_exp2f(sc[2] - mref), __builtin_amdgcn_exp2f(sc[3] - mref));
-        // the denominator sums the same bf16 weights P.V uses
-        l = l * corr + ((bf_lo(p01) + bf_hi(p01)) + (bf_lo(p23) + bf_hi(p23)));
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) pr[i] = __builtin_amdgcn_exp2f(sc[i] - mref);
+        uint32_t p01, p23, r01 = 0, r23 = 0;
+        if constexpr (F8) {
+            // The sum takes the weights, P.V the weights times vscale, as a
+            // bf16 high part plus a bf16 remainder (two MFMAs: ~16 mantissa
+            // bits, where one bf16 would add 2^-9 relative error per weight
+            // to values the reference keeps in f32).
+            l = l * corr + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+            const float w0 = pr[0] * vs_cur[0], w1 = pr[1] * vs_cur[1], w2 = pr[2] * vs_cur[2], w3 = pr[3] * vs_cur[3];
+            p01 = pack2_hw(w0, w1);
+            p23 = pack2_hw(w2, w3);
+            r01 = pack2_hw(w0 - bf_lo(p01), w1 - bf_hi(p01));
+            r23 = pack2_hw(w2 - bf_lo(p23), w3 - bf_hi(p23));
+        } else {
+            p01 = pack2_hw(pr[0], pr[1]);
+            p23 = pack2_hw(pr[2], pr[3]);
+            // the denominator sums the same bf16 weights P.V uses
+            l = l * corr + ((bf_lo(p01) + bf_hi(p01)) + (bf_lo(p23) + bf_hi(p23)));
+        }
         m = mn;
         if (__any(corr != 1.f)) {
 #pragma unroll
             for (int db = 0; db < 16; db++) acc[db] *= corr;
         }
         const s16x4 pb = __builtin_bit_cast(s16x4, make_uint2(p01, p23));
+        const s16x4 pr_lo = __builtin_bit_cast(s16x4, make_uint2(r01, r23));
         wave_sync();  // V staged
 #pragma unroll
         for (int db = 0; db < 16; db++) {
             const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) s16x4*)(tr + 16 * db));
             acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb, acc[db], 0, 0, 0);
+            if constexpr (F8) acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pr_lo, acc[db], 0, 0, 0);
         }
         wave_sync();  // reads done before the next page is staged
     };
     const int pg0 = j0 / PAGE, pg1 = (j1 - 1) / PAGE;
     {
         const size_t b0 = page_base(pg0);
-        load_k(b0);
+        load_k(b0, pg0);
         load_v(b0);
     }
     for (int pi = pg0; pi < pg1; pi++) page(pi, page_base(pi + 1), true);
@@ -177,6 +252,7 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
 // threads. Same range split as decode_range_kernel with segment lengths in
 // place of token lengths; block 0 writes offs[t] (segment offsets by head
 // token, equal neighbours for other tokens), offs[T] = W, offs[T + 1] = R.
+template <bool F8>
 __global__ void __launch_bounds__(256, 1)
     verify_range_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                         const int* __restrict__ block_table, const int* __restrict__ cu,
@@ -204,8 +280,8 @@ __global__ void __launch_bounds__(256, 1)
                                : 0;
             const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
             const int j0 = max(start, off) - off, j1 = min(end, off + Ls) - off;
-            verify_piece(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Ls, Lr[0], Lr[1],
-                         Lr[2], Lr[3], t + b);
+            verify_piece<F8>(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Ls, Lr[0],
+                             Lr[1], Lr[2], Lr[3], t + b);
             off += Ls;
         }
         t++;
@@ -230,5 +306,10 @@ __global__ void __launch_bounds__(256)
     if (b0 == b1) return;
     merge_head(p, t, (th + b0) * VF_ROWS + r, VF_ROWS, b1 - b0 + 1, blockIdx.y);
 }
+
+template __global__ void verify_range_kernel<false>(DecodeParams, const int*, const int*, const int*, const int*,
+                                                    const int*);
+template __global__ void verify_range_kernel<true>(DecodeParams, const int*, const int*, const int*, const int*,
+                                                   const int*);
 
 }  // namespace pkv

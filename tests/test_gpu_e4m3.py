@@ -1,0 +1,163 @@
+"""GPU parity of the E4M3 KV cache: pkv_attn_prep with scales (the
+reference's store_e4m3 in attn_prep, qwen35.cu:1055-1128) and
+pkv_attn_decode_e4m3 (attn_paged8_g4, qwen35.cu:1146-1334 with F8) against
+the oracle (oracle/pkv_oracle.c orc_attn_prep8 / orc_attn_decode8).
+
+Bars: v bytes and scales bit-exact (quantised from the exact bf16 inputs);
+k bytes within one E4M3 code (the normed / rotated bf16 inputs may differ by
+one bf16 ulp, see test_gpu_prep.py) with scales within 1 %; attention
+outputs within max-abs 2e-3 and relative 1e-2 of the oracle. The hardware
+conversions are OCP E4M3FN on gfx950; the oracle's are pinned against
+torch.float8_e4m3fn in tests/test_oracle.py."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import pkv
+from _util import BS, D, bf16_bits, close, decode_case
+from test_gpu_prep import case as prep_case
+from test_gpu_verify import verify_case
+
+pytestmark = pytest.mark.gpu
+SCALE = 1.0 / 16.0
+
+
+def t_(a, dev):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to(dev)
+
+
+def test_prep_stores_e4m3(dev):
+    print("case prep e4m3", flush=True)
+    T, Hq, Hkv = 37, 16, 4
+    c = prep_case(T, Hq, Hkv, 11, pool=64)
+    pool = c["pool"]
+    kc8 = np.full((pool, Hkv, D), 0x33, np.uint8)
+    vc8 = np.full((pool, Hkv, D), 0x33, np.uint8)
+    ks = np.full((pool, Hkv), -1.0, np.float32)
+    vs = np.full((pool, Hkv), -1.0, np.float32)
+    qout = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev)
+    kd, vd, ksd, vsd = t_(kc8, dev), t_(vc8, dev), t_(ks, dev), t_(vs, dev)
+    pkv.attn_prep(t_(c["qkv"], dev), c["qstride"], Hq, Hkv, t_(c["q_norm"], dev), t_(c["k_norm"], dev),
+                  t_(c["rope"], dev), T, 11, 11, t_(c["slots"], dev), t_(c["inv_freq"], dev), qout, kd, vd, 1e-6, T, pool,
+                  kscale=ksd, vscale=vsd)
+    torch.cuda.synchronize()
+    wq = np.zeros((T, Hq, D), np.uint16)
+    wk8, wv8, wks, wvs = kc8.copy(), vc8.copy(), ks.copy(), vs.copy()
+    oracle.attn_prep8(c["qkv"], c["qstride"], Hq, Hkv, c["q_norm"], c["k_norm"], c["rope"], T, 11, 11, c["slots"],
+                      c["inv_freq"], 1e-6, wq, wk8, wv8, wks, wvs)
+    gk8, gv8, gks, gvs = kd.cpu().numpy(), vd.cpu().numpy(), ksd.cpu().numpy(), vsd.cpu().numpy()
+    assert np.array_equal(gv8, wv8) and np.array_equal(gvs, wvs)  # untouched slots included
+    written = np.zeros(pool, bool)
+    written[c["slots"][c["slots"] >= 0]] = True
+    assert np.array_equal(gk8[~written], wk8[~written]) and np.array_equal(gks[~written], wks[~written])
+    assert np.allclose(gks[written], wks[written], rtol=1e-2)
+    a, b = gk8[written].astype(np.int32), wk8[written].astype(np.int32)
+    same_sign = (a >> 7) == (b >> 7)
+    assert (np.abs(a - b)[same_sign] <= 1).all() and same_sign.mean() > 0.999
+    assert (a == b).mean() > 0.97
+
+
+def e4m3_cache(shape, rng):
+    """Random E4M3 bytes (no NaN codes) and positive scales per slot row head."""
+    b = rng.integers(0, 0x7F, size=shape).astype(np.uint8)  # 0x00 .. 0x7E
+    return b | (rng.integers(0, 2, size=shape).astype(np.uint8) << 7)
+
+
+def run_decode8(c, k8, v8, ks, vs, dev, skip=0, outs=None, spec=1, out_init=None):
+    T, Hq = len(c["pos"]), c["Hq"]
+    out = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev) if out_init is None else t_(out_init, dev)
+    ws = torch.empty(pkv.attn_verify_workspace(T, Hq), dtype=torch.uint8, device=dev)
+    pkv.attn_decode_e4m3(t_(c["q"], dev), t_(k8, dev), t_(v8, dev), t_(ks, dev), t_(vs, dev), t_(c["qkv"], dev),
+                         c["qstride"], Hq, c["Hkv"], t_(c["pos"].astype(np.int32), dev),
+                         t_(c["tok_seq"].astype(np.int32), dev), t_(c["bt"], dev), c["max_blocks"], BS, out, SCALE,
+                         t_(c["cu"].astype(np.int32), dev), skip, None if outs is None else t_(outs, dev), spec, T,
+                         c["pages"], ws)
+    torch.cuda.synchronize()
+    return out.cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("lens,Hkv,seed,min_range", [
+    ([1, 2, 15, 16, 17], 4, 0, 32),
+    ([513, 8193, 1000, 4000, 777, 64], 4, 1, 32),
+    ([300, 5000], 2, 2, 32),
+    ([900, 2000], 8, 3, 1 << 20),
+])
+def test_decode_e4m3_matches_oracle(dev, lens, Hkv, seed, min_range):
+    print(f"case decode e4m3 lens={lens} Hkv={Hkv} min_range={min_range}", flush=True)
+    pkv.attn_decode_config(1, min_range)
+    try:
+        c = decode_case(lens, 4 * Hkv, Hkv, seed)
+        rng = np.random.default_rng(seed + 50)
+        k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+        ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)  # |k| up to ~9
+        vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+        got = run_decode8(c, k8, v8, ks, vs, dev)
+        want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], c["Hq"], Hkv, c["pos"],
+                                   c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
+        ok, err = close(got, want)
+        assert ok, f"max |diff| {err}"
+    finally:
+        pkv.attn_decode_config(1, 32)
+
+
+def test_verify_e4m3_rows_and_prompt_skip(dev):
+    """Verify rows over the E4M3 cache (4 rows per pass), a skipped prompt."""
+    print("case verify e4m3", flush=True)
+    c = verify_case([(300, 4), (0, 9), (40, 4), (90, 1), (2000, 3)], 4, 12)
+    rng = np.random.default_rng(12)
+    k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+    ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+    vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+    outs = np.zeros(5, np.int32)
+    outs[1] = -1
+    init = np.full((c["T"], 16, D), 0x5555, np.uint16)
+    got = run_decode8(c, k8, v8, ks, vs, dev, skip=1, outs=outs, out_init=init)
+    assert (got[4:13] == 0x5555).all()
+    want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], 16, 4, c["pos"], c["tok_seq"], c["bt"],
+                               c["max_blocks"], BS, SCALE, cu=c["cu"], skip_prompts=1, outs=outs, out=init.copy())
+    ok, err = close(got, want)
+    assert ok, err
+
+
+def test_decode_e4m3_equals_bf16_decode_on_grid_values(dev):
+    """Config-3-like batch (64 sequences, 512..8192 keys): with unit scales
+    the E4M3 cache holds exactly the bf16 cache's values, so E4M3 decode
+    and bf16 decode agree (within the tolerance: different kernels)."""
+    print("case decode e4m3 vs bf16 c3", flush=True)
+    from pkv import synth
+    lens = synth.c3_lengths(4, batch=64)
+    meta = synth.decode_meta(lens - 1, 64 * 520, steps=1, seed=4)
+    st = meta.step(0)
+    Hq, Hkv = 16, 4
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    n = meta.num_pages * BS * Hkv * D
+    k8 = torch.randint(0, 0x60, (n,), device=dev, generator=gen, dtype=torch.int32).to(torch.uint8)
+    v8 = torch.randint(0, 0x60, (n,), device=dev, generator=gen, dtype=torch.int32).to(torch.uint8)
+    k8 |= (torch.randint(0, 2, (n,), device=dev, generator=gen, dtype=torch.int32) << 7).to(torch.uint8)
+    v8 |= (torch.randint(0, 2, (n,), device=dev, generator=gen, dtype=torch.int32) << 7).to(torch.uint8)
+    kbf = k8.view(torch.float8_e4m3fn).to(torch.bfloat16).view(-1, Hkv, D)
+    vbf = v8.view(torch.float8_e4m3fn).to(torch.bfloat16).view(-1, Hkv, D)
+    ones = torch.ones(meta.num_pages * BS * Hkv, device=dev)
+    B = len(lens)
+    q = (torch.randn(B, Hq, D, device=dev, generator=gen) * 0.05).to(torch.bfloat16)
+    qstride = synth.qkv_stride(Hq, Hkv)
+    qkv = torch.randn(B, qstride, device=dev, generator=gen).to(torch.bfloat16)
+    pos, ts, cu = (torch.from_numpy(st[k]).to(dev) for k in ("pos", "tok_seq", "cu"))
+    bt = torch.from_numpy(meta.block_table).to(dev)
+    o8 = torch.zeros(B, Hq, D, dtype=torch.bfloat16, device=dev)
+    ob = torch.zeros_like(o8)
+    ws = torch.empty(max(pkv.attn_verify_workspace(B, Hq), pkv.attn_decode_workspace(B, Hq)), dtype=torch.uint8,
+                     device=dev)
+    pkv.attn_decode_e4m3(q, k8, v8, ones, ones, qkv, qstride, Hq, Hkv, pos, ts, bt, meta.max_blocks, BS, o8, SCALE, cu,
+                         0, None, 1, B, meta.num_pages, ws)
+    pkv.attn_decode(q, kbf, vbf, qkv, qstride, Hq, Hkv, pos, ts, bt, meta.max_blocks, BS, ob, SCALE, cu, 0, None, 1, B,
+                    meta.num_pages, ws)
+    torch.cuda.synchronize()
+    bits = lambda x: x.cpu().view(torch.int16).numpy().view(np.uint16)
+    ok, err = close(bits(o8), bits(ob))
+    assert ok, err

@@ -306,3 +306,69 @@ def test_prep_axis_rule():
         want = 1 if (d % 3 == 1 and d < 15) else 2 if (d % 3 == 2 and d < 9) else 0
         if abs(z0[d]) > 0.05 and float(c["inv_freq"][d]) * 1000 > 1e-2:
             assert axis == want, (d, errs)
+
+
+# ---- E4M3 cache (reference store_e4m3 / attn_paged8, qwen35.cu:1055-1065, 1146-1309) ----
+
+def test_e4m3_decode_all_codes_match_torch():
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = oracle.e4m3_to_f(codes)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert set(np.flatnonzero(nan)) == {0x7F, 0xFF}
+
+
+def test_e4m3_encode_matches_torch_in_range_and_saturates():
+    import torch
+    rng = np.random.default_rng(0)
+    grid = oracle.e4m3_to_f(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)
+    mids = (grid[:-1] + grid[1:]) / 2  # exact ties
+    x = np.concatenate([rng.standard_normal(4000) * 50, rng.standard_normal(2000) * 0.01, mids, -mids,
+                        [0.0, -0.0, 448.0, -448.0, 2 ** -9, 2 ** -10, 3 * 2 ** -10]]).astype(np.float32)
+    x = x[np.abs(x) < 464]  # torch overflows to NaN past the largest tie; the reference saturates
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.f_to_e4m3(x), want)
+    assert list(oracle.f_to_e4m3(np.array([500.0, -1e9, 464.0], np.float32))) == [0x7E, 0xFE, 0x7E]
+    assert oracle.f_to_e4m3(np.array([np.nan], np.float32))[0] == 0x7F
+
+
+def test_e4m3_store_scale_and_zero_row():
+    rng = np.random.default_rng(1)
+    v = (rng.standard_normal(256) * 3).astype(np.float32)
+    b, sc = oracle.store_e4m3(v)
+    assert sc == np.float32(np.abs(v).max()) / np.float32(448.0)
+    assert np.abs(oracle.e4m3_to_f(b)).max() == 448.0  # the largest maps to E4M3's largest
+    assert np.allclose(oracle.e4m3_to_f(b) * sc, v, rtol=2 ** -3, atol=sc * 2 ** -9)
+    b0, sc0 = oracle.store_e4m3(np.zeros(256, np.float32))
+    assert sc0 == 1.0 and not b0.any()
+
+
+def test_decode8_equals_bf16_decode_on_the_e4m3_grid():
+    """K and V whose values sit on the E4M3 grid (scale 1): E4M3 decode ==
+    bf16 decode; a single key gives its scaled value."""
+    from _util import decode_case
+    c = decode_case([1, 37, 150], 16, 4, 5)
+    rng = np.random.default_rng(5)
+    grid = oracle.e4m3_to_f(np.arange(0x60, dtype=np.uint8))  # |v| < 16
+    n = c["kc"].size
+    k8 = rng.integers(0, 0x60, size=n).astype(np.uint8) | (rng.integers(0, 2, size=n).astype(np.uint8) << 7)
+    v8 = rng.integers(0, 0x60, size=n).astype(np.uint8) | (rng.integers(0, 2, size=n).astype(np.uint8) << 7)
+    kbf = bf16_bits(oracle.e4m3_to_f(k8)).reshape(c["kc"].shape)
+    vbf = bf16_bits(oracle.e4m3_to_f(v8)).reshape(c["vc"].shape)
+    slots = c["kc"].shape[0] * c["kc"].shape[1]
+    ones = np.ones(slots, np.float32)
+    got = oracle.attn_decode8(c["q"], k8, v8, ones, ones, c["qkv"], c["qstride"], 16, 4, c["pos"], c["tok_seq"],
+                              c["bt"], c["max_blocks"], 16, 1 / 16)
+    want, _ = oracle.attn_decode(c["q"], kbf, vbf, c["qkv"], c["qstride"], 16, 4, c["pos"], c["tok_seq"], c["bt"],
+                                 c["max_blocks"], 16, 1 / 16)
+    assert np.array_equal(got, want)
+    # one key: output is its value times its scale, gated
+    vs = np.full(slots, 0.5, np.float32)
+    got1 = oracle.attn_decode8(c["q"], k8, v8, ones, vs, c["qkv"], c["qstride"], 16, 4, c["pos"], c["tok_seq"],
+                               c["bt"], c["max_blocks"], 16, 1 / 16)
+    want1, _ = oracle.attn_decode(c["q"], kbf, bf16_bits(oracle.b2f(vbf) * 0.5), c["qkv"], c["qstride"], 16, 4,
+                                  c["pos"], c["tok_seq"], c["bt"], c["max_blocks"], 16, 1 / 16)
+    assert np.array_equal(got1, want1)
