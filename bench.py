@@ -87,6 +87,8 @@ def main():
     ap.add_argument("--refabi", action="store_true",
                     help="c2/c3 through the reference-ABI code object (pkv_kernels.hsaco: attn_paged_g4 + attn_merge "
                          "on the reference engine's grid) after pkv_append")
+    ap.add_argument("--kv", default="bf16", choices=["bf16", "e4m3"],
+                    help="c2/c3 cache type; e4m3: the step is pkv_attn_prep (E4M3 store) + pkv_attn_decode_e4m3")
     ap.add_argument("--with-prep", action="store_true",
                     help="c2/c3: the step's append is pkv_attn_prep (q/k RMSNorm + rotary + K/V slot writes, the "
                          "reference's attn_prep) on the raw qkv rows, followed by the key ranges and the merge")
@@ -134,11 +136,22 @@ def main():
     meta = synth.decode_meta(lens, pages, steps=S, seed=seed)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    kc = torch.empty(pages * BS, Hkv, D, dtype=torch.bfloat16, device=dev)
-    vc = torch.empty_like(kc)
-    for t in (kc, vc):  # N(0,1) * 0.5, in slices to bound temporaries
-        for i in range(0, t.shape[0], 1 << 18):
-            t[i:i + (1 << 18)] = torch.randn(t[i:i + (1 << 18)].shape, device=dev, generator=gen) * 0.5
+    e4m3 = args.kv == "e4m3"
+    if e4m3:
+        # random E4M3 bytes (NaN codes replaced) and scales amax/448-like
+        kc = torch.randint(0, 256, (pages * BS, Hkv, D), device=dev, generator=gen, dtype=torch.int32).to(torch.uint8)
+        vc = torch.randint(0, 256, (pages * BS, Hkv, D), device=dev, generator=gen, dtype=torch.int32).to(torch.uint8)
+        for t in (kc, vc):
+            t[(t & 0x7F) == 0x7F] = 0x7E
+        kscale = torch.rand(pages * BS, Hkv, device=dev, generator=gen) * 0.004 + 0.001
+        vscale = torch.rand(pages * BS, Hkv, device=dev, generator=gen) * 0.004 + 0.001
+        args.with_prep = True
+    else:
+        kc = torch.empty(pages * BS, Hkv, D, dtype=torch.bfloat16, device=dev)
+        vc = torch.empty_like(kc)
+        for t in (kc, vc):  # N(0,1) * 0.5, in slices to bound temporaries
+            for i in range(0, t.shape[0], 1 << 18):
+                t[i:i + (1 << 18)] = torch.randn(t[i:i + (1 << 18)].shape, device=dev, generator=gen) * 0.5
     q = (torch.randn(B, Hq, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
     qstride = synth.qkv_stride(Hq, Hkv)
     qkv = (torch.randn(B, qstride, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
@@ -192,7 +205,12 @@ def main():
                            P_(ts), P_(cu), I_(0), P_(out), P_(None), P_(None), I_(0), I_(0), P_(None), I_(1)],
                           stream=s_)
             return
-        if args.with_prep:
+        if e4m3:
+            pkv.attn_prep(qkv, qstride, Hq, Hkv, qn, kn, rope_d[i], B, 11, 11, slot_d[i], inv_freq, q, kc, vc, 1e-6,
+                          B, pages * BS, kscale=kscale, vscale=vscale, stream=s_)
+            pkv.attn_decode_e4m3(q, kc, vc, kscale, vscale, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks,
+                                 BS, out, 1 / 16, cu, 0, None, 1, B, pages, ws, stream=s_)
+        elif args.with_prep:
             pkv.attn_prep(qkv, qstride, Hq, Hkv, qn, kn, rope_d[i], B, 11, 11, slot_d[i], inv_freq, q, kc, vc, 1e-6,
                           B, pages * BS, stream=s_)
             pkv.attn_decode(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt, meta.max_blocks, BS, out, 1 / 16, cu,
@@ -255,14 +273,19 @@ def main():
         graph_us = 1e3 * g0.elapsed_time(g1) / args.steps
 
     keys = [meta.keys(args.warmup + k) for k in range(args.steps)]
-    step_bytes = [synth.algorithmic_bytes_decode(kk, B, Hq, Hkv) + synth.algorithmic_bytes_append(B, Hkv)
-                  for kk in keys]
+    if e4m3:
+        step_bytes = [synth.algorithmic_bytes_decode(kk, B, Hq, Hkv, kv="e4m3") + synth.algorithmic_bytes_append(
+            B, Hkv, kv="e4m3") for kk in keys]
+    else:
+        step_bytes = [synth.algorithmic_bytes_decode(kk, B, Hq, Hkv) + synth.algorithmic_bytes_append(B, Hkv)
+                      for kk in keys]
     gbs = sum(step_bytes) / (total_ms * 1e-3) / 1e9
     if args.unfused or args.refabi:
         # key-range kernel: every key's K and V rows (all kv heads) + q; its
         # partials are overhead, not algorithmic.
-        kern_bytes = [kk * Hkv * D * 2 * 2 + B * Hq * D * 2 for kk in keys]
-        kname = ("attn_paged_g4 (reference ABI)" if args.refabi else
+        kern_bytes = [kk * Hkv * (D + 4 if e4m3 else D * 2) * 2 + B * Hq * D * 2 for kk in keys]
+        kname = ("verify_range_kernel<true> (E4M3 cache, after attn_prep)" if e4m3 else
+                 "attn_paged_g4 (reference ABI)" if args.refabi else
                  "decode_range_kernel<4,false> (after attn_prep)" if args.with_prep else
                  "verify_range_kernel" if args.verify_kernel else "decode_range_kernel<4,false>")
     else:
@@ -294,7 +317,9 @@ def main():
         "config": {"workload": ("c3: batch-64 paged decode step (append 1 token/seq + paged decode attention)"
                                 if args.config == "c3" else
                                 "c2: single-sequence paged decode step at 4096 context (append + attention)"),
-                   "path": ("reference-ABI code object (append, attn_paged_g4, attn_merge)" if args.refabi else
+                   "kv": args.kv,
+                   "path": ("attn_prep (E4M3 store), key ranges over the E4M3 cache, merge" if e4m3 else
+                            "reference-ABI code object (append, attn_paged_g4, attn_merge)" if args.refabi else
                             "attn_prep (norm + rotary + append), key ranges, merge" if args.with_prep else
                             "unfused (append, key ranges, merge)" if args.unfused else "fused step (one launch)"),
                    "batch": B, "ctx": "U[512,8192]", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,

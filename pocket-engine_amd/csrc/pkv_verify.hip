@@ -33,6 +33,8 @@
 #pragma once
 #include "pkv_common.h"
 
+#include <type_traits>
+
 namespace pkv {
 
 constexpr int VF_ROWS = 4;                // query rows per segment
@@ -88,44 +90,47 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
     };
     auto page_base = [&](int pi) -> size_t { return (size_t)page_of(pi) * PAGE * row_elems + (size_t)kvh * HEAD_DIM; };
     constexpr int NK = F8 ? 4 : 8, NV = F8 ? 4 : 8;  // 16-byte loads per lane per page
-    uint4 kb[NK], vb[NV];
-    float ksc[4], vsc[4];  // E4M3: scales of this lane's keys 4 gq + i
-    auto load_k = [&](size_t base, int pi) {
+    // One page's loads: K and V rows (E4M3: plus this lane's keys' scales).
+    struct Buf {
+        uint4 kb[NK], vb[NV];
+        float ksc[4], vsc[4];  // E4M3: scales of keys 4 gq + i
+    };
+    auto load_k = [&](Buf& B, size_t base, int pi) {
         if constexpr (F8) {
             const uint8_t* r = reinterpret_cast<const uint8_t*>(p.kc) + base + (size_t)c16 * row_elems + 64 * gq;
 #pragma unroll
-            for (int c = 0; c < NK; c++) kb[c] = load_nt(r + 16 * c);
+            for (int c = 0; c < NK; c++) B.kb[c] = load_nt(r + 16 * c);
             const size_t s0 = ((size_t)page_of(pi) * PAGE + 4 * gq) * p.Hkv + kvh;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                ksc[i] = p.kscale[s0 + (size_t)i * p.Hkv];
-                vsc[i] = p.vscale[s0 + (size_t)i * p.Hkv];
+                B.ksc[i] = p.kscale[s0 + (size_t)i * p.Hkv];
+                B.vsc[i] = p.vscale[s0 + (size_t)i * p.Hkv];
             }
         } else {
             const uint16_t* r = p.kc + base + (size_t)c16 * row_elems + 8 * gq;
 #pragma unroll
-            for (int c = 0; c < NK; c++) kb[c] = load_nt(r + 32 * c);
+            for (int c = 0; c < NK; c++) B.kb[c] = load_nt(r + 32 * c);
         }
     };
-    auto load_v = [&](size_t base) {
+    auto load_v = [&](Buf& B, size_t base) {
         if constexpr (F8) {
             // keys 4 k + lane / 16, bytes 16 (lane % 16) .. + 15
             const uint8_t* r = reinterpret_cast<const uint8_t*>(p.vc) + base + (size_t)(lane >> 4) * row_elems + 16 * c16;
 #pragma unroll
-            for (int k = 0; k < NV; k++) vb[k] = load_nt(r + (size_t)(4 * k) * row_elems);
+            for (int k = 0; k < NV; k++) B.vb[k] = load_nt(r + (size_t)(4 * k) * row_elems);
         } else {
             const uint16_t* r = p.vc + base + (size_t)(lane >> 5) * row_elems + 8 * (lane & 31);
 #pragma unroll
-            for (int k = 0; k < NV; k++) vb[k] = load_nt(r + (size_t)(2 * k) * row_elems);
+            for (int k = 0; k < NV; k++) B.vb[k] = load_nt(r + (size_t)(2 * k) * row_elems);
         }
     };
     // A operand of step c: K dims dim0(c) .. + 7 of key c16
-    auto k_frag = [&](int c) -> bf16x8 {
+    auto k_frag = [&](const Buf& B, int c) -> bf16x8 {
         if constexpr (F8) {
-            const uint4 w = kb[c >> 1];
+            const uint4 w = B.kb[c >> 1];
             return as_bf16x8((c & 1) ? e4m3x8_to_bf16x8(w.z, w.w) : e4m3x8_to_bf16x8(w.x, w.y));
         } else {
-            return as_bf16x8(kb[c]);
+            return as_bf16x8(B.kb[c]);
         }
     };
 
@@ -138,31 +143,35 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
     const uint16_t* tr = vl + (4 * gq + (c16 >> 2)) * VF_VSTR + 4 * (c16 & 3);
     uint16_t* st = vl + (lane >> 5) * VF_VSTR + 8 * (lane & 31);
 
-    auto page = [&](int pi, size_t next, bool prefetch) {
+    // One page from buffer B; with PREFETCH, B is refilled with page nxt as
+    // soon as its K and V have been consumed.
+    auto page = [&](Buf& B, int pi, int nxt, auto prefetch) {
+        constexpr bool PREFETCH = decltype(prefetch)::value;
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < 8; c++) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_frag(c), qf[c], s, 0, 0, 0);
+        for (int c = 0; c < 8; c++) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_frag(B, c), qf[c], s, 0, 0, 0);
         float ks_cur[4], vs_cur[4];
         if constexpr (F8) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                ks_cur[i] = ksc[i];
-                vs_cur[i] = vsc[i];
+                ks_cur[i] = B.ksc[i];
+                vs_cur[i] = B.vsc[i];
             }
             // V rows to LDS as bf16: row 4 k + lane / 16, dims 16 (lane % 16) .. + 15
 #pragma unroll
             for (int k = 0; k < NV; k++) {
                 uint16_t* d = vl + (4 * k + (lane >> 4)) * VF_VSTR + 16 * c16;
-                *reinterpret_cast<uint4*>(d) = e4m3x8_to_bf16x8(vb[k].x, vb[k].y);
-                *reinterpret_cast<uint4*>(d + 8) = e4m3x8_to_bf16x8(vb[k].z, vb[k].w);
+                *reinterpret_cast<uint4*>(d) = e4m3x8_to_bf16x8(B.vb[k].x, B.vb[k].y);
+                *reinterpret_cast<uint4*>(d + 8) = e4m3x8_to_bf16x8(B.vb[k].z, B.vb[k].w);
             }
         } else {
 #pragma unroll
-            for (int k = 0; k < NV; k++) *reinterpret_cast<uint4*>(st + 2 * k * VF_VSTR) = vb[k];
+            for (int k = 0; k < NV; k++) *reinterpret_cast<uint4*>(st + 2 * k * VF_VSTR) = B.vb[k];
         }
-        if (prefetch) {
-            load_k(next, pi + 1);
-            load_v(next);
+        if constexpr (PREFETCH) {
+            const size_t next = page_base(nxt);
+            load_k(B, next, nxt);
+            load_v(B, next);
         }
         const int k0 = pi * PAGE + 4 * gq;
         float sc[4], mx = -INFINITY;
@@ -216,14 +225,14 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
         }
         wave_sync();  // reads done before the next page is staged
     };
+    using NOPF = std::integral_constant<bool, false>;
+    using PF = std::integral_constant<bool, true>;
     const int pg0 = j0 / PAGE, pg1 = (j1 - 1) / PAGE;
-    {
-        const size_t b0 = page_base(pg0);
-        load_k(b0, pg0);
-        load_v(b0);
-    }
-    for (int pi = pg0; pi < pg1; pi++) page(pi, page_base(pi + 1), true);
-    page(pg1, 0, false);
+    Buf A;
+    load_k(A, page_base(pg0), pg0);
+    load_v(A, page_base(pg0));
+    for (int pi = pg0; pi < pg1; pi++) page(A, pi, pi + 1, PF{});
+    page(A, pg1, 0, NOPF{});
 
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
