@@ -206,6 +206,17 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
                      int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec, int T,
                      int64_t num_blocks, void* stream);
 
+/* Chunked-prefill attention over an E4M3 cache: the reference's
+ * attn_group8_g<G> (src/kernels/qwen35.cu:1364-1585 with F8, selected for
+ * st.kv_fp8 at src/model.rs:2441-2446): the arguments of pkv_attn_prefill
+ * plus kscale / vscale; each loaded K / V row is dequantised to
+ * bf16(v * scale) (qwen35.cu:1424-1436), the rest as pkv_attn_prefill. */
+int pkv_attn_prefill_e4m3(const void* q, const void* kcache, const void* vcache, const float* kscale,
+                          const float* vscale, const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos,
+                          const int32_t* cu, int seqs, const int32_t* block_table, int max_blocks, int block_size,
+                          void* out, float scale, const int32_t* outs, int spec, int T, int64_t num_blocks,
+                          void* stream);
+
 /* ---------------------------------------------------------------------------
  * Device: attention input preparation (the reference's append site)
  * ------------------------------------------------------------------------- */

@@ -58,6 +58,8 @@ _lib.orc_f_to_e4m3.restype = ctypes.c_uint8
 _lib.orc_f_to_e4m3.argtypes = [_F]
 _lib.orc_store_e4m3.argtypes = [_P, _P, _P]
 _lib.orc_attn_prep8.argtypes = [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _F, _I, _L, _P, _P, _P, _P, _P]
+_lib.orc_attn_prefill8.restype = _I
+_lib.orc_attn_prefill8.argtypes = [_P, _P, _P, _P, _P, _L, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F]
 _lib.orc_attn_decode8.restype = _I
 _lib.orc_attn_decode8.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _F, _P, _I, _P, _I, _I]
 
@@ -243,4 +245,19 @@ def attn_decode8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, pos
     _lib.orc_attn_decode8(_p(q), _p(kcache8), _p(vcache8), _p(kscale), _p(vscale), _p(qkv), qstride, Hq, Hkv,
                           _p(pos), _p(tok_seq), _p(block_table), max_blocks, block_size, _p(out), scale, _p(cu),
                           skip_prompts, _p(outs), spec, T)
+    return out
+
+
+def attn_prefill8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,
+                  block_size, scale, out=None):
+    """Chunked prefill over an E4M3 cache (reference attn_group8)."""
+    T = len(pos)
+    if out is None:
+        out = np.zeros((T, Hq, 256), np.uint16)
+    pos, cu, block_table = _i32(pos), _i32(cu), _i32(block_table)
+    kscale = np.ascontiguousarray(kscale, np.float32)
+    vscale = np.ascontiguousarray(vscale, np.float32)
+    num_slots = kcache8.size // (Hkv * 256)
+    _lib.orc_attn_prefill8(_p(q), _p(kcache8), _p(vcache8), _p(kscale), _p(vscale), num_slots, _p(qkv), qstride, Hq,
+                           Hkv, _p(pos), _p(cu), seqs, _p(block_table), max_blocks, block_size, _p(out), scale)
     return out

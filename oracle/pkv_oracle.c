@@ -484,3 +484,26 @@ int orc_attn_decode8(const uint16_t* q, const uint8_t* kcache8, const uint8_t* v
     free(s);
     return 0;
 }
+
+/* Chunked-prefill attention over an E4M3 cache (reference attn_group8,
+ * qwen35.cu:1364-1585 with F8): every K / V row is dequantised to
+ * bf16(e4m3 * scale) as the reference loads its tiles (qwen35.cu:1424-1436),
+ * then orc_attn_prefill. num_slots rows of Hkv heads. */
+int orc_attn_prefill8(const uint16_t* q, const uint8_t* kcache8, const uint8_t* vcache8, const float* kscale,
+                      const float* vscale, long num_slots, const uint16_t* qkv, int qstride, int Hq, int Hkv,
+                      const int* pos, const int* cu, int seqs, const int* block_table, int max_blocks,
+                      int block_size, uint16_t* out, float scale) {
+    const size_t n = (size_t)num_slots * Hkv;
+    uint16_t* kb = (uint16_t*)malloc(n * HEAD_DIM * 2);
+    uint16_t* vb = (uint16_t*)malloc(n * HEAD_DIM * 2);
+    for (size_t r = 0; r < n; r++)
+        for (int d = 0; d < HEAD_DIM; d++) {
+            kb[r * HEAD_DIM + d] = orc_f2b(orc_e4m3_to_f(kcache8[r * HEAD_DIM + d]) * kscale[r]);
+            vb[r * HEAD_DIM + d] = orc_f2b(orc_e4m3_to_f(vcache8[r * HEAD_DIM + d]) * vscale[r]);
+        }
+    const int rc = orc_attn_prefill(q, kb, vb, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,
+                                    block_size, out, scale, NULL, 1);
+    free(kb);
+    free(vb);
+    return rc;
+}

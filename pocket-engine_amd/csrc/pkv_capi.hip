@@ -165,10 +165,14 @@ int pkv_attn_prep(const void* qkv, int qstride, int Hq, int Hkv, const float* q_
     return launch_status();
 }
 
-int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
-                     int Hkv, const int32_t* pos, const int32_t* cu, int seqs, const int32_t* block_table,
-                     int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec, int T,
-                     int64_t num_blocks, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int attn_prefill(const void* q, const void* kcache, const void* vcache, const float* kscale, const float* vscale,
+                 const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos, const int32_t* cu, int seqs,
+                 const int32_t* block_table, int max_blocks, int block_size, void* out, float scale,
+                 const int32_t* outs, int spec, int T, int64_t num_blocks, void* stream) {
     if (T < 0 || seqs < 0 || Hq <= 0 || Hkv <= 0 || max_blocks <= 0 || block_size <= 0 || num_blocks <= 0 ||
         spec < 1)
         return PKV_ERR_INVALID;
@@ -178,12 +182,15 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
     if (qstride < 2 * Hq * pkv::HEAD_DIM || qstride % 8 != 0) return PKV_ERR_INVALID;
     if (!aligned(q, 16) || !aligned(kcache, 16) || !aligned(vcache, 16) || !aligned(qkv, 16) || !aligned(out, 16))
         return PKV_ERR_INVALID;
-    static bool attr_set = false;  // per process: the kernel's LDS above the 64 KiB default
+    const bool f8 = kscale != nullptr;
+    if (f8 && (!vscale || !aligned(kscale, 4) || !aligned(vscale, 4))) return PKV_ERR_INVALID;
+    static bool attr_set = false;  // per process: the kernels' LDS above the 64 KiB default
     const size_t smem = pkv::prefill_smem_bytes();
     if (!attr_set) {
-        const int st = status_of(
-            hipFuncSetAttribute((const void*)pkv::prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-        if (st != PKV_OK) return st;
+        for (const void* k : {(const void*)pkv::prefill_kernel, (const void*)pkv::prefill_e4m3_kernel}) {
+            const int st = status_of(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+            if (st != PKV_OK) return st;
+        }
         attr_set = true;
     }
     pkv::PrefillParams p;
@@ -206,14 +213,40 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
     p.outs = outs;
     p.spec = spec;
     p.num_blocks = (long)num_blocks;
+    p.kscale = kscale;
+    p.vscale = vscale;
     hipEvent_t e0 = t_pf_start, e1 = t_pf_stop;
     t_pf_start = t_pf_stop = nullptr;
     // Upper bound on query tiles: each prompt sequence rounds up once.
     const int tiles = (T + pkv::PF_BQ - 1) / pkv::PF_BQ + seqs;
-    hipExtLaunchKernelGGL(pkv::prefill_kernel, dim3(tiles, Hkv), dim3(pkv::PF_THREADS), smem, (hipStream_t)stream, e0,
-                          e1, 0, p);
+    hipExtLaunchKernelGGL(f8 ? pkv::prefill_e4m3_kernel : pkv::prefill_kernel, dim3(tiles, Hkv),
+                          dim3(pkv::PF_THREADS), smem, (hipStream_t)stream, e0, e1, 0, p);
     return launch_status();
 }
+
+}  // namespace
+
+extern "C" {
+
+int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
+                     int Hkv, const int32_t* pos, const int32_t* cu, int seqs, const int32_t* block_table,
+                     int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec, int T,
+                     int64_t num_blocks, void* stream) {
+    return attn_prefill(q, kcache, vcache, nullptr, nullptr, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
+                        max_blocks, block_size, out, scale, outs, spec, T, num_blocks, stream);
+}
+
+int pkv_attn_prefill_e4m3(const void* q, const void* kcache, const void* vcache, const float* kscale,
+                          const float* vscale, const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos,
+                          const int32_t* cu, int seqs, const int32_t* block_table, int max_blocks, int block_size,
+                          void* out, float scale, const int32_t* outs, int spec, int T, int64_t num_blocks,
+                          void* stream) {
+    if (!kscale || !vscale) return PKV_ERR_INVALID;
+    return attn_prefill(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
+                        max_blocks, block_size, out, scale, outs, spec, T, num_blocks, stream);
+}
+
+
 
 int pkv_time_next_range_kernel(void* start_event, void* stop_event) {
     t_ev_start = (hipEvent_t)start_event;

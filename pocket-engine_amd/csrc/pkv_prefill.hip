@@ -43,6 +43,10 @@ struct PrefillParams {
     const int* outs;
     int spec;
     long num_blocks;
+    // E4M3 cache (prefill_tile<.., true>): kc / vc hold bytes, one f32 scale
+    // per (slot, kv head)
+    const float* kscale;
+    const float* vscale;
 };
 
 constexpr int PF_BK = 32;          // keys per tile
@@ -92,8 +96,10 @@ __device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s
 }
 
 // One workgroup's query tile (sequence s, rows tb .. tb + nb - 1, nb <= BQ);
-// pf_smem holds prefill_smem_bytes().
-template <int BQ, int NQB>
+// pf_smem holds prefill_smem_bytes(). F8: an E4M3 cache, dequantised while
+// the tiles load as the reference's attn_group8 does (qwen35.cu:1424-1436):
+// K' = bf16(k * kscale), V' = bf16(v * vscale); the rest is unchanged.
+template <int BQ, int NQB, bool F8 = false>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb) {
     constexpr int THREADS = pf_threads(BQ, NQB);
     static_assert(PF_BK * HEAD_DIM / 8 % THREADS == 0, "whole 16-byte chunks per thread");
@@ -158,13 +164,28 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
         return (((size_t)pg << bs_log2) + (kp & bs_mask)) * row + (size_t)kvh * HEAD_DIM + c;
     };
+    // 8 values at element offset `at` of a pool: bf16 as stored, or E4M3
+    // bytes times the slot's scale, rounded to bf16.
+    auto load8 = [&](const uint16_t* pool, const float* scales, size_t at, size_t scale_at) -> uint4 {
+        if constexpr (F8) {
+            const uint2 w = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(pool) + at);
+            const float sc = scales[scale_at];
+            const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, true);
+            const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, true);
+            return make_uint4(pack2_hw(a.x * sc, a.y * sc), pack2_hw(b.x * sc, b.y * sc), pack2_hw(c.x * sc, c.y * sc),
+                              pack2_hw(d.x * sc, d.y * sc));
+        } else {
+            return *reinterpret_cast<const uint4*>(pool + at);
+        }
+    };
     auto load_tile = [&](int k0) {
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
             const int e = tid + u * THREADS, kp = k0 + (e >> 5);
-            kr[u] = kp < L ? *reinterpret_cast<const uint4*>(p.kc + slot_at(kp, (e & 31) * 8)) : make_uint4(0, 0, 0, 0);
+            kr[u] = kp < L ? load8(p.kc, p.kscale, slot_at(kp, (e & 31) * 8), slot_at(kp, 0) / HEAD_DIM)
+                           : make_uint4(0, 0, 0, 0);
             const int vp = k0 + 2 * (tid & 15) + (u & 1), vc = ((tid >> 4) + (THREADS / 16) * (u >> 1)) * 8;
-            vr[u] = vp < L ? *reinterpret_cast<const uint4*>(p.vc + slot_at(vp, vc)) : make_uint4(0, 0, 0, 0);
+            vr[u] = vp < L ? load8(p.vc, p.vscale, slot_at(vp, vc), slot_at(vp, 0) / HEAD_DIM) : make_uint4(0, 0, 0, 0);
         }
     };
     auto store_tile = [&](int buf) {
@@ -302,15 +323,21 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     }
 }
 
-template <int BQ, int NQB>
+template <int BQ, int NQB, bool F8 = false>
 __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
     int s, tb, nb;
-    if (find_prefill_tile<BQ>(p, s, tb, nb)) prefill_tile<BQ, NQB>(p, pf_smem, s, tb, nb);
+    if (find_prefill_tile<BQ>(p, s, tb, nb)) prefill_tile<BQ, NQB, F8>(p, pf_smem, s, tb, nb);
 }
 
 __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
     prefill_body<PF_BQ, PF_NQB>(p, pf_smem);
+}
+
+// The same over an E4M3 cache (p.kscale / p.vscale set).
+__global__ void __launch_bounds__(PF_THREADS, 1) prefill_e4m3_kernel(PrefillParams p) {
+    extern __shared__ __align__(16) uint16_t pf_smem[];
+    prefill_body<PF_BQ, PF_NQB, true>(p, pf_smem);
 }
 
 }  // namespace pkv

@@ -15,6 +15,9 @@
 //                   capability 9.5) selects (fa_shape, src/model.rs:58-79)
 //   attn_mfma_g4_t2 (amd/attention.cuh:137-142) the same grid, 512 threads:
 //                   the name gfx942 devices select
+//   attn_group8_g4_t2_k16 (qwen35.cu:1593-1608) the same grid, 256 threads,
+//                   over an E4M3 cache (kscale / vscale): gfx950's choice
+//                   for an E4M3 cache
 //
 // Split decode follows the reference's contract so its buffer sizing holds:
 // range z of nz = split_parts(L, Z, min_chunk) covers keys [z c, z c + c),
@@ -24,8 +27,8 @@
 // (this build's decode wave body: dot2 + DPP reduce-scatter, online softmax,
 // one page in flight) and combine through LDS.
 //
-// Bounds of this ABI (the bf16 path): kscale / vscale must be null (an E4M3
-// cache uses the reference's attn_paged8_* names, not exported here); FP8
+// Bounds of this ABI: the decode kernels take a bf16 cache (kscale / vscale
+// null; the reference's attn_paged8_* names are not exported here); FP8
 // output copies (fmode != 0) are not produced; block_size 16 for decode, a
 // power of two for prompts; G = Hq / Hkv = 4. A launch outside these bounds
 // writes nothing. Page ids are not clamped (the reference ABI passes no pool
@@ -237,6 +240,8 @@ __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
     p.outs = outs;
     p.spec = spec;
     p.num_blocks = REF_NO_CLAMP;
+    p.kscale = nullptr;
+    p.vscale = nullptr;
     prefill_body<BQ, 1>(p, sm);
 }
 
@@ -245,6 +250,40 @@ __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
 extern "C" __global__ void __launch_bounds__(256, 1) attn_groupr_g4_t2_k32(PKV_FLASH_ARGS) {
     pkv::flash_ref<32>(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
                        max_blocks, block_size, out, scale, outs, spec);
+}
+
+// The E4M3 prompt kernel a gfx950 device selects for an E4M3 cache
+// (fa_shape(4, 95, true): attn_group8_g4_t2_k16, 256 threads, grid of
+// 32-query tiles, 101,376 bytes of dynamic shared memory, which holds this
+// kernel's two 34.5 KiB stages).
+extern "C" __global__ void __launch_bounds__(256, 1) attn_group8_g4_t2_k16(PKV_FLASH_ARGS) {
+    extern __shared__ __align__(16) uint16_t g8_smem[];
+    if ((int)blockDim.x != pkv::pf_threads(32, 1) || Hq != 4 * Hkv || !kscale || !vscale || block_size <= 0 ||
+        (block_size & (block_size - 1)))
+        return;
+    pkv::PrefillParams p;
+    p.q = q;
+    p.kc = (const uint16_t*)kcache;
+    p.vc = (const uint16_t*)vcache;
+    p.qkv = qkv;
+    p.qstride = qstride;
+    p.Hq = Hq;
+    p.Hkv = Hkv;
+    p.pos = pos;
+    p.cu = cu;
+    p.seqs = seqs;
+    p.block_table = block_table;
+    p.max_blocks = max_blocks;
+    p.block_size = block_size;
+    p.bs_log2 = __builtin_ctz((unsigned)block_size);
+    p.out = out;
+    p.scale = scale;
+    p.outs = outs;
+    p.spec = spec;
+    p.num_blocks = pkv::REF_NO_CLAMP;
+    p.kscale = kscale;
+    p.vscale = vscale;
+    pkv::prefill_body<32, 1, true>(p, g8_smem);
 }
 
 extern "C" __global__ void __launch_bounds__(512, 1) attn_mfma_g4_t2(PKV_FLASH_ARGS) {

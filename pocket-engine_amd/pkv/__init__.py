@@ -83,6 +83,7 @@ _SIGS = {
 }
 _SIGS["pkv_attn_decode_split"] = _SIGS["pkv_attn_decode"]
 _SIGS["pkv_attn_verify"] = _SIGS["pkv_attn_decode"]
+_SIGS["pkv_attn_prefill_e4m3"] = (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p] + _SIGS["pkv_attn_prefill"][1][3:])
 _SIGS["pkv_attn_decode_e4m3"] = (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p] + _SIGS["pkv_attn_decode"][1][3:])
 _SIGS["pkv_attn_prep"] = (_c_int, [_c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p,
                                    _c_p, _c_p, _c_p, _c_p, _c_p, ctypes.c_float, _c_int, ctypes.c_int64, _c_p])
@@ -230,6 +231,15 @@ def attn_decode_e4m3(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, p
                                      Hq, Hkv, _ptr(pos), _ptr(tok_seq), _ptr(block_table), max_blocks, block_size,
                                      _ptr(out), scale, _ptr(cu), int(skip_prompts), _ptr(outs), spec, T, num_blocks,
                                      _ptr(workspace), workspace_bytes, _stream(stream)), "pkv_attn_decode_e4m3")
+
+
+def attn_prefill_e4m3(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,
+                      block_size, out, scale, outs, spec, T, num_blocks, stream=None):
+    """Causal chunked-prefill attention over an E4M3 cache (reference attn_group8)."""
+    _check(_lib.pkv_attn_prefill_e4m3(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(kscale), _ptr(vscale), _ptr(qkv),
+                                      qstride, Hq, Hkv, _ptr(pos), _ptr(cu), seqs, _ptr(block_table), max_blocks,
+                                      block_size, _ptr(out), scale, _ptr(outs), spec, T, num_blocks, _stream(stream)),
+           "pkv_attn_prefill_e4m3")
 
 
 def attn_prefill(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks, block_size, out,

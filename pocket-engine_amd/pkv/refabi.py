@@ -22,12 +22,17 @@ def split_ranges(t, hkv, sms):
     return max(1, min(SPLIT_MAX, -(-(4 * sms) // (t * hkv))))
 
 
-def flash_launch(t, s, hkv, g=4, mfma=False):
+def flash_launch(t, s, hkv, g=4, mfma=False, fp8=False):
     """(name, grid, threads, dynamic smem) of the prompt kernel: fa_shape for
     a bf16 cache on gfx950 (compute capability 9.5: attn_groupr_g4_t2_k32) or
-    gfx942 (attn_mfma_g4_t2), model.rs:58-79, 112-141, 2455-2463."""
+    gfx942 (attn_mfma_g4_t2), or for an E4M3 cache on either
+    (attn_group8_g4_t2_k16), model.rs:58-79, 112-141, 2455-2463."""
     tiles, keys = 2, 32
-    if mfma:
+    if fp8:
+        keys = 16
+        name, threads = f"attn_group8_g{g}_t{tiles}_k{keys}", 32 * g * tiles
+        smem = (g * 16 * tiles + 4 * keys) * (HEAD_DIM + 8) * 2
+    elif mfma:
         name, threads = f"attn_mfma_g{g}_t{tiles}", 64 * g * tiles
         smem = (keys * (HEAD_DIM + 8) + HEAD_DIM * (keys + 8)) * 2
     else:

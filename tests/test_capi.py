@@ -73,7 +73,8 @@ def test_reference_abi_code_object_exports_the_reference_kernel_names(tmp_path):
                     "--targets=hipv4-amdgcn-amd-amdhsa--gfx950"], check=True)
     syms = subprocess.run([readelf, "--syms", "--wide", str(co)], check=True, capture_output=True, text=True).stdout
     kernels = {line.split()[-1] for line in syms.splitlines() if " FUNC " in line and "GLOBAL" in line}
-    for name in ("attn_prep", "attn_paged_g4", "attn_merge", "attn_groupr_g4_t2_k32", "attn_mfma_g4_t2"):
+    for name in ("attn_prep", "attn_paged_g4", "attn_merge", "attn_groupr_g4_t2_k32", "attn_mfma_g4_t2",
+                 "attn_group8_g4_t2_k16"):
         assert name in kernels, (name, sorted(kernels)[:20])
 
 
@@ -87,3 +88,5 @@ def test_reference_launch_shapes():
     assert (name, grid, threads, smem) == ("attn_groupr_g4_t2_k32", (7, 4, 1), 256, 67584)
     name, grid, threads, smem = refabi.flash_launch(100, 3, 4, mfma=True)
     assert (name, grid, threads, smem) == ("attn_mfma_g4_t2", (7, 4, 1), 512, 37376)
+    name, grid, threads, smem = refabi.flash_launch(100, 3, 4, fp8=True)
+    assert (name, grid, threads, smem) == ("attn_group8_g4_t2_k16", (7, 4, 1), 256, 101376)

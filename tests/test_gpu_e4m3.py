@@ -161,3 +161,43 @@ def test_decode_e4m3_equals_bf16_decode_on_grid_values(dev):
     bits = lambda x: x.cpu().view(torch.int16).numpy().view(np.uint16)
     ok, err = close(bits(o8), bits(ob))
     assert ok, err
+
+
+@pytest.mark.parametrize("refabi_kernel", [False, True])
+@pytest.mark.parametrize("ctxs,chunks,Hkv,seed", [
+    ([0], [37], 4, 0),
+    ([100, 16], [64, 130], 4, 1),
+    ([1000, 33, 0], [70, 200, 65], 2, 3),
+])
+def test_prefill_e4m3_matches_oracle(dev, refabi_kernel, ctxs, chunks, Hkv, seed):
+    """Chunked prefill over an E4M3 cache, through pkv_attn_prefill_e4m3 or
+    the code object's attn_group8_g4_t2_k16 launched as the engine does."""
+    print(f"case prefill e4m3 refabi={refabi_kernel} ctx={ctxs} chunk={chunks}", flush=True)
+    from test_gpu_prefill import prefill_case
+    from pkv.refabi import F, I, P, RefKernels, flash_launch
+    c = prefill_case(ctxs, chunks, Hkv, seed, decode_rows=1)
+    rng = np.random.default_rng(seed + 70)
+    k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+    ks = (rng.random(c["kc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+    vs = (rng.random(c["vc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+    T, Hq = c["T"], c["Hq"]
+    init = np.full((T, Hq, D), 0x3333, np.uint16)
+    out = t_(init, dev)
+    args = [t_(c["q"], dev), t_(k8, dev), t_(v8, dev), t_(ks, dev), t_(vs, dev), t_(c["qkv"], dev)]
+    pos, cu, bt = t_(c["pos"], dev), t_(c["cu"], dev), t_(c["bt"], dev)
+    if refabi_kernel:
+        name, grid, threads, smem = flash_launch(T, c["seqs"], Hkv, fp8=True)
+        RefKernels().launch(name, grid, threads, smem,
+                            [P(args[0]), P(args[1]), P(args[2]), P(args[3]), P(args[4]), P(args[5]), I(c["qstride"]),
+                             I(Hq), I(Hkv), P(pos), P(cu), I(c["seqs"]), P(bt), I(c["max_blocks"]), I(BS), P(out),
+                             F(SCALE), P(None), I(1)])
+    else:
+        pkv.attn_prefill_e4m3(*args, c["qstride"], Hq, Hkv, pos, cu, c["seqs"], bt, c["max_blocks"], BS, out, SCALE,
+                              None, 1, T, c["pages"])
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    assert (got[0] == 0x3333).all()  # the decode row is left to decode attention
+    want = oracle.attn_prefill8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["cu"], c["seqs"],
+                                c["bt"], c["max_blocks"], BS, SCALE, out=init.copy())
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"

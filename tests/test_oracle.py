@@ -372,3 +372,27 @@ def test_decode8_equals_bf16_decode_on_the_e4m3_grid():
     want1, _ = oracle.attn_decode(c["q"], kbf, bf16_bits(oracle.b2f(vbf) * 0.5), c["qkv"], c["qstride"], 16, 4,
                                   c["pos"], c["tok_seq"], c["bt"], c["max_blocks"], 16, 1 / 16)
     assert np.array_equal(got1, want1)
+
+
+def test_prefill8_is_prefill_of_the_dequantised_cache():
+    """E4M3 prefill == bf16 prefill of bf16(e4m3 * scale) rows, and with
+    unit scales on grid values == bf16 prefill of the same values."""
+    from _util import decode_case
+    rng = np.random.default_rng(8)
+    c = decode_case([40, 70], 8, 2, 8)
+    T = 12
+    pos = np.concatenate([np.arange(28, 34), np.arange(64, 70)]).astype(np.int32)
+    cu = np.array([0, 6, 12], np.int32)
+    q = bf16_bits(rng.standard_normal((T, 8, 256)) * 0.5)
+    qkv = bf16_bits(rng.standard_normal((T, c["qstride"])))
+    k8 = rng.integers(0, 0x60, size=c["kc"].shape).astype(np.uint8)
+    v8 = rng.integers(0, 0x60, size=c["vc"].shape).astype(np.uint8) | 0x80
+    ks = rng.random(c["kc"].shape[:2]).astype(np.float32) * 0.1
+    vs = rng.random(c["kc"].shape[:2]).astype(np.float32) * 0.1
+    got = oracle.attn_prefill8(q, k8, v8, ks, vs, qkv, c["qstride"], 8, 2, pos, cu, 2, c["bt"], c["max_blocks"], 16,
+                               1 / 16)
+    kb = bf16_bits(oracle.e4m3_to_f(k8) * ks[:, :, None])
+    vb = bf16_bits(oracle.e4m3_to_f(v8) * vs[:, :, None])
+    want = oracle.attn_prefill(q, kb, vb, qkv, c["qstride"], 8, 2, pos, cu, 2, c["bt"], c["max_blocks"], 16, 1 / 16)
+    assert np.array_equal(got, want)
+    assert not (got == 0).all()
