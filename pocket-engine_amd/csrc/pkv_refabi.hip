@@ -9,6 +9,7 @@
 //
 //   attn_prep       (qwen35.cu:1076-1082)  grid (T, Hq + 2 Hkv), 128 threads
 //   attn_paged_g4   (qwen35.cu:1313-1334)  grid (T, Hkv, Z), 256 threads
+//   attn_paged8_g4  the same over an E4M3 cache (kscale / vscale)
 //   attn_merge      (qwen35.cu:2245-2249)  grid (T, Hq), 256 threads
 //   attn_groupr_g4_t2_k32 (qwen35.cu:1600-1616) grid (ceil(T/32) + seqs, Hkv),
 //                   256 threads: the prompt kernel a gfx950 device (compute
@@ -27,8 +28,7 @@
 // (this build's decode wave body: dot2 + DPP reduce-scatter, online softmax,
 // one page in flight) and combine through LDS.
 //
-// Bounds of this ABI: the decode kernels take a bf16 cache (kscale / vscale
-// null; the reference's attn_paged8_* names are not exported here); FP8
+// Bounds of this ABI: FP8
 // output copies (fmode != 0) are not produced; block_size 16 for decode, a
 // power of two for prompts; G = Hq / Hkv = 4. A launch outside these bounds
 // writes nothing. Page ids are not clamped (the reference ABI passes no pool
@@ -36,6 +36,7 @@
 #include "pkv_decode.hip"
 #include "pkv_prefill.hip"
 #include "pkv_prep.hip"
+#include "pkv_verify.hip"
 
 #include <climits>
 
@@ -89,30 +90,39 @@ extern "C" __global__ void __launch_bounds__(128)
     pkv::prep_head(a, blockIdx.x, blockIdx.y);
 }
 
-extern "C" __global__ void __launch_bounds__(256)
-    attn_paged_g4(const uint16_t* __restrict__ q, const void* __restrict__ kcache, const void* __restrict__ vcache,
-                  const float* __restrict__ kscale, const float* __restrict__ vscale, const uint16_t* __restrict__ qkv,
-                  int qstride, int Hq, int Hkv, const int* __restrict__ pos, const int* __restrict__ tok_seq,
-                  const int* __restrict__ block_table, int max_blocks, int block_size, uint16_t* __restrict__ out,
-                  float scale, uint8_t* fq, void* fs, int fmode, int frows, const int* __restrict__ cu,
-                  int skip_prompts, int min_chunk, float* part, const int* __restrict__ outs, int spec) {
-    constexpr int G = 4, PAGE = pkv::PAGE;
-    __shared__ pkv::WaveLds<G> sh_w[4];
+namespace pkv {
+
+// attn_paged_g4 / attn_paged8_g4 on the reference's grid (token t, kv head,
+// range z): the range's pages split over the 4 waves (bf16: the decode wave
+// body; E4M3: the MFMA verify body with one row), combined through LDS.
+template <bool F8>
+__device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache, const void* vcache,
+                                          const float* kscale, const float* vscale, const uint16_t* qkv, int qstride,
+                                          int Hq, int Hkv, const int* __restrict__ pos,
+                                          const int* __restrict__ tok_seq, const int* __restrict__ block_table,
+                                          int max_blocks, int block_size, uint16_t* out, float scale,
+                                          const int* __restrict__ cu, int skip_prompts, int min_chunk, float* part,
+                                          const int* __restrict__ outs, int spec) {
+    constexpr int G = 4;
+    __shared__ WaveLds<G> sh_w[F8 ? 1 : 4];
+    __shared__ __align__(16) uint16_t sh_v[F8 ? 4 : 1][F8 ? VF_LDS : 8];
     __shared__ float sh_acc[4][G][HEAD_DIM];
     __shared__ float sh_ml[4][G][2];
-    if (blockDim.x != 256 || block_size != PAGE || Hq != G * Hkv || kscale || vscale) return;
+    if (blockDim.x != 256 || block_size != PAGE || Hq != G * Hkv || (kscale != nullptr) != F8 ||
+        (vscale != nullptr) != F8)
+        return;
     const int t = blockIdx.x, kvh = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
     const int sq = tok_seq[t];
-    if (pkv::ref_prompt_row(skip_prompts, cu, sq, outs, spec)) return;
+    if (ref_prompt_row(skip_prompts, cu, sq, outs, spec)) return;
     const int L = pos[t] + 1;
-    const int parts = part ? pkv::ref_split_parts(L, gridDim.z, min_chunk) : 1;
+    const int parts = part ? ref_split_parts(L, gridDim.z, min_chunk) : 1;
     if (z >= parts) return;
     const int chunk = (L + parts - 1) / parts;
     const int j0 = part ? z * chunk : 0, j1 = part ? min(L, j0 + chunk) : L;
 
-    pkv::DecodeParams p = {};
+    DecodeParams p = {};
     p.q = q;
-    p.kc = (uint16_t*)kcache;  // read only (the unfused body)
+    p.kc = (uint16_t*)kcache;  // read only
     p.vc = (uint16_t*)vcache;
     p.qkv = qkv;
     p.qstride = qstride;
@@ -121,9 +131,10 @@ extern "C" __global__ void __launch_bounds__(256)
     p.max_blocks = max_blocks;
     p.out = out;
     p.scale = scale;
-    p.num_blocks = pkv::REF_NO_CLAMP;
+    p.num_blocks = REF_NO_CLAMP;
+    p.kscale = kscale;
+    p.vscale = vscale;
 
-    // The range's pages split over the 4 waves.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int a = j1, b = j1;
     if (j0 < j1) {
@@ -131,18 +142,9 @@ extern "C" __global__ void __launch_bounds__(256)
         a = max(j0, (pg0 + wave * per) * PAGE);
         b = min(j1, (pg0 + (wave + 1) * per) * PAGE);
     }
-    if (a < b) {
-        const int* bt = block_table + (size_t)sq * max_blocks;
-        auto epi = [&](int g, const float (&acc)[8], float m, float l, int ch) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) sh_acc[wave][g][8 * ch + e] = acc[e];
-            if (ch == 0) {
-                sh_ml[wave][g][0] = m;
-                sh_ml[wave][g][1] = l;
-            }
-        };
-        pkv::piece_body<G, false>(p, bt, sh_w[wave], t, kvh, a, b, L, INT_MAX, 0, epi);
-    } else {
+    // every lane first clears its wave's record (rows a wave does not reach
+    // stay empty), then the wave's piece overwrites it
+    {
         const int lane = tid & 63;
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -152,6 +154,33 @@ extern "C" __global__ void __launch_bounds__(256)
                 sh_ml[wave][g][0] = -INFINITY;
                 sh_ml[wave][g][1] = 0.f;
             }
+        }
+        wave_sync();
+    }
+    if (a < b) {
+        const int* bt = block_table + (size_t)sq * max_blocks;
+        if constexpr (F8) {
+            auto epi = [&](int r, int g, int gq, const f32x4 (&acc)[16], float m, float l) {
+#pragma unroll
+                for (int db = 0; db < 16; db++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sh_acc[wave][g][16 * db + 4 * gq + i] = acc[db][i];
+                if (gq == 0) {
+                    sh_ml[wave][g][0] = m;
+                    sh_ml[wave][g][1] = l;
+                }
+            };
+            verify_piece<true>(p, bt, sh_v[wave], t, kvh, a, b, L, 0, 0, 0, epi);
+        } else {
+            auto epi = [&](int g, const float (&acc)[8], float m, float l, int ch) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) sh_acc[wave][g][8 * ch + e] = acc[e];
+                if (ch == 0) {
+                    sh_ml[wave][g][0] = m;
+                    sh_ml[wave][g][1] = l;
+                }
+            };
+            piece_body<G, false>(p, bt, sh_w[wave], t, kvh, a, b, L, INT_MAX, 0, epi);
         }
     }
     __syncthreads();
@@ -173,17 +202,34 @@ extern "C" __global__ void __launch_bounds__(256)
             const size_t row = (size_t)sq * spec + (t - cu[sq]);
             float* pp = part + ((row * Hq + h) * gridDim.z + z) * (HEAD_DIM + 2);
             if (d == 0) {
-                pp[0] = M * pkv::LN2;  // natural-log units, as the reference's records
+                pp[0] = M * LN2;  // natural-log units, as the reference's records
                 pp[1] = S;
             }
             pp[2 + d] = A;
         } else {
-            const float gate = pkv::b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d]);
-            out[((size_t)t * Hq + h) * HEAD_DIM + d] =
-                (uint16_t)pkv::f2b_bits(pkv::rbf(A / S) / (1.f + __expf(-gate)));
+            const float gate = b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d]);
+            out[((size_t)t * Hq + h) * HEAD_DIM + d] = (uint16_t)f2b_bits(rbf(A / S) / (1.f + __expf(-gate)));
         }
     }
 }
+
+}  // namespace pkv
+
+#define PKV_PAGED_ARGS                                                                                           \
+    const uint16_t *__restrict__ q, const void *__restrict__ kcache, const void *__restrict__ vcache,            \
+        const float *__restrict__ kscale, const float *__restrict__ vscale, const uint16_t *__restrict__ qkv,    \
+        int qstride, int Hq, int Hkv, const int *__restrict__ pos, const int *__restrict__ tok_seq,              \
+        const int *__restrict__ block_table, int max_blocks, int block_size, uint16_t *__restrict__ out,         \
+        float scale, uint8_t *fq, void *fs, int fmode, int frows, const int *__restrict__ cu, int skip_prompts,   \
+        int min_chunk, float *part, const int *__restrict__ outs, int spec
+#define PKV_PAGED_PASS                                                                                           \
+    q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, \
+        out, scale, cu, skip_prompts, min_chunk, part, outs, spec
+
+extern "C" __global__ void __launch_bounds__(256) attn_paged_g4(PKV_PAGED_ARGS) { pkv::paged_ref<false>(PKV_PAGED_PASS); }
+
+// The same over an E4M3 cache (kscale / vscale given).
+extern "C" __global__ void __launch_bounds__(256) attn_paged8_g4(PKV_PAGED_ARGS) { pkv::paged_ref<true>(PKV_PAGED_PASS); }
 
 extern "C" __global__ void __launch_bounds__(256)
     attn_merge(const float* __restrict__ part, int Z, int min_chunk, const uint16_t* __restrict__ qkv, int qstride,

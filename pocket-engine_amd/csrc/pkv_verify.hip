@@ -62,10 +62,13 @@ __device__ __forceinline__ int seg_len(int t, int T, const int* __restrict__ pos
 // are converted to bf16 in registers (exact), each score is multiplied by its
 // key's kscale, and each weight by its key's vscale before P.V (the softmax
 // sum takes the unscaled weights).
-template <bool F8>
+// The result goes to epi(r, g, gq, acc, m, l) on the lanes of attending rows:
+// row r, query head kvh * 4 + g, dims 16 db + 4 gq + i in acc[db][i]; m in
+// log2 units, l the sum of weights (m = -inf, l = 0 when the piece has no
+// key for the row).
+template <bool F8, class Epi>
 __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* __restrict__ bt, uint16_t* vl, int t,
-                                             int kvh, int j0, int j1, int Ls, int L0, int L1, int L2, int L3,
-                                             int idx) {
+                                             int kvh, int j0, int j1, int L0, int L1, int L2, int L3, Epi epi) {
     const int lane = threadIdx.x & 63, c16 = lane & 15, gq = lane >> 4;
     const int r_me = c16 >> 2, g_me = c16 & 3;
     const int myL = r_me == 0 ? L0 : r_me == 1 ? L1 : r_me == 2 ? L2 : L3;
@@ -237,25 +240,38 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
     if (myL == 0) return;
-    const int h = kvh * 4 + g_me, tr_row = t + r_me;
-    if (j0 == 0 && j1 == Ls) {
-        const float inv = 1.f / l;
-        const uint16_t* gate = p.qkv + (size_t)tr_row * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + 4 * gq;
-        uint16_t* o = p.out + ((size_t)tr_row * p.Hq + h) * HEAD_DIM + 4 * gq;
-#pragma unroll
-        for (int db = 0; db < 16; db++) {
-            const uint2 graw = *reinterpret_cast<const uint2*>(gate + 16 * db);
-            *reinterpret_cast<uint2*>(o + 16 * db) = gate4(acc[db][0], acc[db][1], acc[db][2], acc[db][3], inv, graw);
-        }
-    } else {
-        const size_t row = ((size_t)idx * VF_ROWS + r_me) * p.Hq + h;
-        float* pa = p.part_acc + row * HEAD_DIM + 4 * gq;
-#pragma unroll
-        for (int db = 0; db < 16; db++)
-            *reinterpret_cast<float4*>(pa + 16 * db) = make_float4(acc[db][0], acc[db][1], acc[db][2], acc[db][3]);
-        if (gq == 0) *reinterpret_cast<float2*>(p.part_ms + row * 2) = make_float2(m, l);
-    }
+    epi(r_me, g_me, gq, acc, m, l);
 }
+
+// Writes a verify piece's result for the lanes of (row r, head g): the gated
+// output when the piece holds all of the segment's keys, else the partial
+// record at index idx.
+struct VerifyEpi {
+    const DecodeParams& p;
+    int t, kvh, idx;
+    bool direct;
+    __device__ __forceinline__ void operator()(int r, int g, int gq, const f32x4 (&acc)[16], float m, float l) const {
+        const int h = kvh * 4 + g, row_t = t + r;
+        if (direct) {
+            const float inv = 1.f / l;
+            const uint16_t* gate = p.qkv + (size_t)row_t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + 4 * gq;
+            uint16_t* o = p.out + ((size_t)row_t * p.Hq + h) * HEAD_DIM + 4 * gq;
+#pragma unroll
+            for (int db = 0; db < 16; db++) {
+                const uint2 graw = *reinterpret_cast<const uint2*>(gate + 16 * db);
+                *reinterpret_cast<uint2*>(o + 16 * db) =
+                    gate4(acc[db][0], acc[db][1], acc[db][2], acc[db][3], inv, graw);
+            }
+        } else {
+            const size_t row = ((size_t)idx * VF_ROWS + r) * p.Hq + h;
+            float* pa = p.part_acc + row * HEAD_DIM + 4 * gq;
+#pragma unroll
+            for (int db = 0; db < 16; db++)
+                *reinterpret_cast<float4*>(pa + 16 * db) = make_float4(acc[db][0], acc[db][1], acc[db][2], acc[db][3]);
+            if (gq == 0) *reinterpret_cast<float2*>(p.part_ms + row * 2) = make_float2(m, l);
+        }
+    }
+};
 
 // Key-range kernel over segments; grid (n_wg, ceil(Hkv / 4)), 64 * min(Hkv, 4)
 // threads. Same range split as decode_range_kernel with segment lengths in
@@ -289,8 +305,9 @@ __global__ void __launch_bounds__(256, 1)
                                : 0;
             const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
             const int j0 = max(start, off) - off, j1 = min(end, off + Ls) - off;
-            verify_piece<F8>(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Ls, Lr[0],
-                             Lr[1], Lr[2], Lr[3], t + b);
+            const VerifyEpi epi{p, t, kvh, t + b, j0 == 0 && j1 == Ls};
+            verify_piece<F8>(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Lr[0], Lr[1],
+                             Lr[2], Lr[3], epi);
             off += Ls;
         }
         t++;

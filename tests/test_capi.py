@@ -74,7 +74,7 @@ def test_reference_abi_code_object_exports_the_reference_kernel_names(tmp_path):
     syms = subprocess.run([readelf, "--syms", "--wide", str(co)], check=True, capture_output=True, text=True).stdout
     kernels = {line.split()[-1] for line in syms.splitlines() if " FUNC " in line and "GLOBAL" in line}
     for name in ("attn_prep", "attn_paged_g4", "attn_merge", "attn_groupr_g4_t2_k32", "attn_mfma_g4_t2",
-                 "attn_group8_g4_t2_k16"):
+                 "attn_group8_g4_t2_k16", "attn_paged8_g4"):
         assert name in kernels, (name, sorted(kernels)[:20])
 
 

@@ -201,3 +201,39 @@ def test_prefill_e4m3_matches_oracle(dev, refabi_kernel, ctxs, chunks, Hkv, seed
                                 c["bt"], c["max_blocks"], BS, SCALE, out=init.copy())
     ok, err = close(got, want)
     assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("lens,Z", [([1, 2, 15, 16, 17], None), ([4097], None), ([513, 8193, 1000, 64], None),
+                                    ([900, 70], 1)])
+def test_reference_named_paged8(dev, lens, Z):
+    """attn_paged8_g4 (+ attn_merge when split) of the code object, launched
+    as model.rs:2366-2437 does for an E4M3 cache, against the oracle."""
+    print(f"case refabi paged8 lens={lens} Z={Z}", flush=True)
+    from pkv.refabi import F, I, P, RefKernels, SPLIT_MIN_KEYS, split_ranges
+    rk = RefKernels()
+    c = decode_case(lens, 16, 4, 21)
+    rng = np.random.default_rng(21)
+    k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+    ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+    vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+    T, Hq, Hkv = len(c["pos"]), 16, 4
+    sms = torch.cuda.get_device_properties(0).multi_processor_count
+    ranges = split_ranges(T, Hkv, sms) if Z is None else Z
+    part = torch.full((T * ranges * Hq * (D + 2),), float("nan"), device=dev) if ranges > 1 else None
+    q, qkv = t_(c["q"], dev), t_(c["qkv"], dev)
+    pos, ts, bt, cu = (t_(c[k].astype(np.int32), dev) for k in ("pos", "tok_seq", "bt", "cu"))
+    out = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev)
+    rk.launch("attn_paged8_g4", (T, Hkv, ranges), 256, 0,
+              [P(q), P(t_(k8, dev)), P(t_(v8, dev)), P(t_(ks, dev)), P(t_(vs, dev)), P(qkv), I(c["qstride"]), I(Hq),
+               I(Hkv), P(pos), P(ts), P(bt), I(c["max_blocks"]), I(BS), P(out), F(SCALE), P(None), P(None), I(0), I(0),
+               P(cu), I(0), I(SPLIT_MIN_KEYS), P(part), P(None), I(1)])
+    if part is not None:
+        rk.launch("attn_merge", (T, Hq, 1), 256, 0,
+                  [P(part), I(ranges), I(SPLIT_MIN_KEYS), P(qkv), I(c["qstride"]), I(Hq), P(pos), P(ts), P(cu), I(0),
+                   P(out), P(None), P(None), I(0), I(0), P(None), I(1)])
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["tok_seq"],
+                               c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
