@@ -11,15 +11,17 @@
 // positions of one sequence and one kv head (32 for launches on a grid of
 // 32-query tiles): a wave per (query head of the group, block of 32
 // queries), 8 waves. Keys stream in tiles of 32 (two pages) staged in LDS
-// once for all waves (GQA sharing): K row-major [key][d] and V transposed
-// [d][key]. Per tile a wave computes
+// once for all waves (GQA sharing), K and V both row-major [key][d]. Per
+// tile a wave computes
 //   S^T[32 keys][32 queries] = K Q^T     16 x v_mfma_f32_32x32x16_bf16
 //   O^T[256 d][32 queries] += V^T P^T    16 x v_mfma_f32_32x32x16_bf16
 // Computing S transposed leaves each lane with one query's 16 scores (keys
 // 8 (r / 4) + 4 (lane / 32) + r % 4), so the online softmax is in-lane plus
 // one cross-half shuffle, and the probabilities are already the B operand of
-// the second product once the matching V^T rows are read (keys
-// 16 kk + 4 (lane / 32) + {0..3, 8..11}). q stays in registers (64 VGPRs),
+// the second product once the matching V^T fragments are read (keys
+// 16 kk + 4 (lane / 32) + {0..3, 8..11}; transposed on the LDS read by
+// ds_read_b64_tr_b16). Page ids of full tiles are uniform loads, so the
+// staging costs a handful of ALU instructions per tile. q stays in registers (64 VGPRs),
 // O^T takes 128 accumulators. The next tile's K/V are loaded into registers
 // while the current one is multiplied (double-buffered LDS).
 #pragma once
@@ -51,12 +53,12 @@ struct PrefillParams {
 
 constexpr int PF_BK = 32;          // keys per tile
 constexpr int PF_KSTR = HEAD_DIM + 8;  // K tile row stride (elements)
-// V^T row stride: a multiple of 4 elements (8-byte operand reads) with
-// 4 * stride = 16 (mod 64 banks), so the transposed stores of a wave's four
-// dim chunks land on distinct banks.
-constexpr int PF_VSTR = PF_BK + 4;
+// V tile row stride (row-major [key][d]): 576 bytes = 64 (mod 256), so the
+// 4 rows x 64 bytes a half-wave's transposing reads touch fall on distinct
+// banks.
+constexpr int PF_VSTR = HEAD_DIM + 32;
 constexpr int PF_K_ELEMS = PF_BK * PF_KSTR;
-constexpr int PF_V_ELEMS = HEAD_DIM * PF_VSTR;
+constexpr int PF_V_ELEMS = PF_BK * PF_VSTR;
 // Query positions per workgroup (BQ) and 32-query blocks per wave (NQB):
 // waves = 4 query heads x BQ / (32 NQB). NQB = 2 feeds every K / V^T
 // fragment read from LDS into two MFMAs (half the LDS traffic per MFMA) at
@@ -96,14 +98,15 @@ __device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s
 }
 
 // One workgroup's query tile (sequence s, rows tb .. tb + nb - 1, nb <= BQ);
-// pf_smem holds prefill_smem_bytes(). F8: an E4M3 cache, dequantised while
+// pf_smem holds prefill_smem_bytes(). UPAGE: every page holds at least
+// THREADS / 32 keys. F8: an E4M3 cache, dequantised while
 // the tiles load as the reference's attn_group8 does (qwen35.cu:1424-1436):
 // K' = bf16(k * kscale), V' = bf16(v * vscale); the rest is unchanged.
-template <int BQ, int NQB, bool F8 = false>
+template <int BQ, int NQB, bool F8, bool UPAGE>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb) {
     constexpr int THREADS = pf_threads(BQ, NQB);
     static_assert(PF_BK * HEAD_DIM / 8 % THREADS == 0, "whole 16-byte chunks per thread");
-    // Buffer b: K tile at pf_smem + b * STAGE, V^T tile right after it.
+    // Buffer b: K tile at pf_smem + b * STAGE, V tile right after it.
     constexpr int STAGE = PF_STAGE;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, lh = lane >> 5;
     const int kvh = blockIdx.y;
@@ -149,71 +152,103 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     const int qpw = qp0 + qb0 * 32;                        // the wave's first query position
     const int last = qp0 + min(nb, (qb0 + NQB) * 32) - 1;  // and its last
 
-    // Tile loads: 32 keys x 256 dims of K and of V = 2 x 1024 chunks of 16 B,
-    // NCH + NCH per thread. K: chunk e = tid + THREADS u is key e / 32,
-    // dims 8 (e % 32) (whole rows per 32 lanes). V: the thread takes keys
-    // 2 (tid % 16) and + 1 of chunks tid / 16 + (THREADS / 16) i, so it can
-    // store (key, key + 1) pairs of each dim as one word of the transposed
-    // tile. Keys at or past L load zeros.
-    constexpr int NCH = PF_BK * HEAD_DIM / 8 / THREADS;
+    // Tile loads: 32 keys x 256 dims of K and of V, both row-major in LDS,
+    // NCH 16-byte chunks of each per thread: chunk u is key KPU u + kl0 of
+    // the tile (KPU = THREADS / 32 consecutive keys per u), dims c8 .. c8 + 7.
+    // When a page holds at least KPU keys, each u reads one page: its id is a
+    // uniform (scalar) load and the lane's part of the address is the same
+    // for every tile. Every load is issued unconditionally from a valid
+    // address (page index clamped to the sequence's last key); keys at or
+    // past L are zeroed when the tile is stored to LDS, so no load result is
+    // overwritten while in flight.
+    constexpr int KPU = THREADS / 32;
+    constexpr int NCH = PF_BK / KPU;
+    const int kl0 = tid >> 5, c8 = (tid & 31) * 8;
     uint4 kr[NCH], vr[NCH];
     // Block size is a power of two (checked on the host): shifts, no division.
     const int bs_log2 = p.bs_log2, bs_mask = (1 << bs_log2) - 1;
-    auto slot_at = [&](int kp, int c) -> size_t {
-        long pg = bt[kp >> bs_log2];
+    const int last_pi = (L - 1) >> bs_log2;
+    auto page_id = [&](int pi) -> size_t {
+        long pg = bt[min(pi, last_pi)];
         pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
-        return (((size_t)pg << bs_log2) + (kp & bs_mask)) * row + (size_t)kvh * HEAD_DIM + c;
+        return (size_t)pg;
     };
-    // 8 values at element offset `at` of a pool: bf16 as stored, or E4M3
-    // bytes times the slot's scale, rounded to bf16.
-    auto load8 = [&](const uint16_t* pool, const float* scales, size_t at, size_t scale_at) -> uint4 {
+    // 8 values at element `at` of a pool: bf16 as stored, or E4M3 bytes times
+    // the slot's scale (at `scale_at`), rounded to bf16.
+    // `slot` is the key's cache slot, or (fast path) the uniform slot of the
+    // KPU-key group with the lane's key offset folded into at / scale_at.
+    auto load8 = [&](const uint16_t* pool, const float* scales, size_t slot, uint32_t at, uint32_t scale_at) -> uint4 {
         if constexpr (F8) {
-            const uint2 w = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(pool) + at);
-            const float sc = scales[scale_at];
+            const uint8_t* base = reinterpret_cast<const uint8_t*>(pool) + slot * row;
+            const uint2 w = *reinterpret_cast<const uint2*>(base + at);
+            const float sc = (scales + slot * p.Hkv)[scale_at];
             const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, true);
             const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, true);
             return make_uint4(pack2_hw(a.x * sc, a.y * sc), pack2_hw(b.x * sc, b.y * sc), pack2_hw(c.x * sc, c.y * sc),
                               pack2_hw(d.x * sc, d.y * sc));
         } else {
-            return *reinterpret_cast<const uint4*>(pool + at);
+            return *reinterpret_cast<const uint4*>((pool + slot * row) + at);
         }
+    };
+    const uint32_t lane_at = (uint32_t)(kl0 * row + kvh * HEAD_DIM + c8);  // lane part of an element offset
+    const uint32_t lane_sc = (uint32_t)(kl0 * p.Hkv + kvh);               // and of a scale index
+    // UPAGE: the page ids of the tile loaded next (uniform), fetched one
+    // tile ahead so their latency hides behind a whole tile of work (the
+    // block-table reads are vector loads: the barriers keep the compiler
+    // from using the scalar cache).
+    int ids[NCH];
+    auto fetch_ids = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < NCH; u++) ids[u] = bt[min((k0 + u * KPU) >> bs_log2, last_pi)];
     };
     auto load_tile = [&](int k0) {
+        if constexpr (UPAGE) {
 #pragma unroll
-        for (int u = 0; u < NCH; u++) {
-            const int e = tid + u * THREADS, kp = k0 + (e >> 5);
-            kr[u] = kp < L ? load8(p.kc, p.kscale, slot_at(kp, (e & 31) * 8), slot_at(kp, 0) / HEAD_DIM)
-                           : make_uint4(0, 0, 0, 0);
-            const int vp = k0 + 2 * (tid & 15) + (u & 1), vc = ((tid >> 4) + (THREADS / 16) * (u >> 1)) * 8;
-            vr[u] = vp < L ? load8(p.vc, p.vscale, slot_at(vp, vc), slot_at(vp, 0) / HEAD_DIM) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store_tile = [&](int buf) {
-        uint16_t* sk = pf_smem + buf * STAGE;
-        uint16_t* sv = sk + PF_K_ELEMS;
+            for (int u = 0; u < NCH; u++) {
+                const int kg = k0 + u * KPU;
+                long pg = __builtin_amdgcn_readfirstlane(ids[u]);
+                pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
+                const size_t slot = ((size_t)pg << bs_log2) + (kg & bs_mask);  // uniform
+                kr[u] = load8(p.kc, p.kscale, slot, lane_at, lane_sc);
+                vr[u] = load8(p.vc, p.vscale, slot, lane_at, lane_sc);
+            }
+            fetch_ids(k0 + PF_BK);
+        } else {
 #pragma unroll
-        for (int u = 0; u < NCH; u++) {
-            const int e = tid + u * THREADS;
-            *reinterpret_cast<uint4*>(sk + (e >> 5) * PF_KSTR + (e & 31) * 8) = kr[u];
-        }
-        const int j = 2 * (tid & 15);
-#pragma unroll
-        for (int half = 0; half < NCH / 2; half++) {
-            const int c = ((tid >> 4) + (THREADS / 16) * half) * 8;
-            const uint4 va = vr[2 * half], vb = vr[2 * half + 1];
-            const uint32_t a[4] = {va.x, va.y, va.z, va.w}, b[4] = {vb.x, vb.y, vb.z, vb.w};
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-                // dims c + 2d (low halves) and c + 2d + 1 (high halves) of keys j, j + 1
-                *reinterpret_cast<uint32_t*>(sv + (c + 2 * d) * PF_VSTR + j) = (a[d] & 0xffffu) | (b[d] << 16);
-                *reinterpret_cast<uint32_t*>(sv + (c + 2 * d + 1) * PF_VSTR + j) = (a[d] >> 16) | (b[d] & 0xffff0000u);
+            for (int u = 0; u < NCH; u++) {
+                const int kp = k0 + u * KPU + kl0;
+                const size_t slot = (page_id(kp >> bs_log2) << bs_log2) + (kp & bs_mask);
+                kr[u] = load8(p.kc, p.kscale, slot, kvh * HEAD_DIM + c8, kvh);
+                vr[u] = load8(p.vc, p.vscale, slot, kvh * HEAD_DIM + c8, kvh);
             }
         }
     };
+    auto store_tile = [&](int buf, int k0) {
+        uint16_t* sk = pf_smem + buf * STAGE;
+        uint16_t* sv = sk + PF_K_ELEMS;
+        if (k0 + PF_BK > L) {
+#pragma unroll
+            for (int u = 0; u < NCH; u++)
+                if (k0 + u * KPU + kl0 >= L) kr[u] = vr[u] = make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < NCH; u++) {
+            *reinterpret_cast<uint4*>(sk + (u * KPU + kl0) * PF_KSTR + c8) = kr[u];
+            *reinterpret_cast<uint4*>(sv + (u * KPU + kl0) * PF_VSTR + c8) = vr[u];
+        }
+    };
+    // V^T fragments (A operand of O^T += V^T P^T, dims 32 db + lq, keys
+    // 16 kk + 8 h + 4 lh + e) come from the row-major V tile through
+    // ds_read_b64_tr_b16: in each 16-lane group, result lane i element e is
+    // element i % 4 of what lane i / 4 + 4 e read, so lane s of the group
+    // reads row 4 lh + s / 4 (+ 16 kk + 8 h), dims 16 (group & 1) + 4 (s % 4)
+    // (+ 32 db).
+    const int tr_at = (4 * lh + ((lane & 15) >> 2)) * PF_VSTR + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     const int ntiles = (L + PF_BK - 1) / PF_BK;
+    if constexpr (UPAGE) fetch_ids(0);
     load_tile(0);
-    store_tile(0);
+    store_tile(0, 0);
     __syncthreads();
     for (int it = 0; it < ntiles; it++) {
         const int buf = it & 1, k0 = it * PF_BK;
@@ -280,14 +315,17 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                                             pack2_hw(st[qb][8 * kk + 6], st[qb][8 * kk + 7]));
             }
             // O^T += V^T P^T; each V^T fragment feeds the wave's NQB blocks.
+            typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+            const uint16_t* vtr = Vt + tr_at;
 #pragma unroll
             for (int kk = 0; kk < 2; kk++)
 #pragma unroll
                 for (int db = 0; db < 8; db++) {
-                    const uint16_t* vrow = Vt + (32 * db + lq) * PF_VSTR + 16 * kk + 4 * lh;
-                    const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
-                    const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4*)(vtr + (16 * kk) * PF_VSTR + 32 * db));
+                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4*)(vtr + (16 * kk + 8) * PF_VSTR + 32 * db));
+                    const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
                     for (int qb = 0; qb < NQB; qb++)
                         o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pb[qb][kk]), o[qb][db], 0, 0, 0);
@@ -295,7 +333,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         }
         if (it + 1 < ntiles) {
             __syncthreads();  // everyone is done with the buffer two tiles back
-            store_tile(buf ^ 1);
+            store_tile(buf ^ 1, k0 + PF_BK);
             __syncthreads();
         }
     }
@@ -326,7 +364,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
 template <int BQ, int NQB, bool F8 = false>
 __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
     int s, tb, nb;
-    if (find_prefill_tile<BQ>(p, s, tb, nb)) prefill_tile<BQ, NQB, F8>(p, pf_smem, s, tb, nb);
+    if (!find_prefill_tile<BQ>(p, s, tb, nb)) return;
+    // Pages of at least THREADS / 32 keys: uniform page ids per chunk.
+    if (p.bs_log2 >= __builtin_ctz(pf_threads(BQ, NQB) / 32))
+        prefill_tile<BQ, NQB, F8, true>(p, pf_smem, s, tb, nb);
+    else
+        prefill_tile<BQ, NQB, F8, false>(p, pf_smem, s, tb, nb);
 }
 
 __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {
