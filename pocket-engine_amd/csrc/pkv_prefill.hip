@@ -51,6 +51,15 @@ struct PrefillParams {
     const float* vscale;
 };
 
+// 16 bytes at byte offset `off` of `base` (a uniform address) by a raw
+// buffer load: the descriptor holds the base, the offset stays one VGPR.
+__device__ __forceinline__ uint4 buf_load16(const void* base, uint32_t off) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                                                       0x00020000);
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 constexpr int PF_BK = 32;          // keys per tile
 constexpr int PF_KSTR = HEAD_DIM + 8;  // K tile row stride (elements)
 // V tile row stride (row-major [key][d]): 576 bytes = 64 (mod 256), so the
@@ -179,7 +188,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     // KPU-key group with the lane's key offset folded into at / scale_at.
     auto load8 = [&](const uint16_t* pool, const float* scales, size_t slot, uint32_t at, uint32_t scale_at) -> uint4 {
         if constexpr (F8) {
-            const uint8_t* base = reinterpret_cast<const uint8_t*>(pool) + slot * row;
+            const uint8_t* base = reinterpret_cast<const uint8_t*>(pool) + slot * row;  // uniform on the fast path
             const uint2 w = *reinterpret_cast<const uint2*>(base + at);
             const float sc = (scales + slot * p.Hkv)[scale_at];
             const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, true);
@@ -187,7 +196,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             return make_uint4(pack2_hw(a.x * sc, a.y * sc), pack2_hw(b.x * sc, b.y * sc), pack2_hw(c.x * sc, c.y * sc),
                               pack2_hw(d.x * sc, d.y * sc));
         } else {
-            return *reinterpret_cast<const uint4*>((pool + slot * row) + at);
+            // uniform base + 32-bit lane byte offset (the saddr addressing form)
+            const uint8_t* base = reinterpret_cast<const uint8_t*>(pool + slot * row);
+            return *reinterpret_cast<const uint4*>(base + 2 * at);
         }
     };
     const uint32_t lane_at = (uint32_t)(kl0 * row + kvh * HEAD_DIM + c8);  // lane part of an element offset
@@ -209,8 +220,15 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                 long pg = __builtin_amdgcn_readfirstlane(ids[u]);
                 pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
                 const size_t slot = ((size_t)pg << bs_log2) + (kg & bs_mask);  // uniform
-                kr[u] = load8(p.kc, p.kscale, slot, lane_at, lane_sc);
-                vr[u] = load8(p.vc, p.vscale, slot, lane_at, lane_sc);
+                if constexpr (F8) {
+                    kr[u] = load8(p.kc, p.kscale, slot, lane_at, lane_sc);
+                    vr[u] = load8(p.vc, p.vscale, slot, lane_at, lane_sc);
+                } else {
+                    // buffer loads: uniform base in the descriptor, the lane's
+                    // 32-bit byte offset in one VGPR shared by K and V
+                    kr[u] = buf_load16(p.kc + slot * row, 2 * lane_at);
+                    vr[u] = buf_load16(p.vc + slot * row, 2 * lane_at);
+                }
             }
             fetch_ids(k0 + PF_BK);
         } else {
