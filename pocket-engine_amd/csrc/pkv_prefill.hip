@@ -80,7 +80,10 @@ constexpr int PF_NQB = PKV_PF_NQB;
 constexpr int pf_threads(int bq, int nqb) { return 64 * 4 * (bq / 32) / nqb; }
 constexpr int PF_THREADS = pf_threads(PF_BQ, PF_NQB);
 constexpr int PF_STAGE = PF_K_ELEMS + PF_V_ELEMS;
-constexpr size_t prefill_smem_bytes() { return (size_t)2 * PF_STAGE * 2; }
+// LDS stages of K / V tiles: 3 (one barrier per tile) unless the launch's
+// shared memory only holds 2 (two barriers per tile).
+constexpr int PF_NST = 3;
+constexpr size_t prefill_smem_bytes(int nst = PF_NST) { return (size_t)nst * PF_STAGE * 2; }
 
 // The query tile of this workgroup among the prompt sequences: tile
 // blockIdx.x of the concatenated BQ-query tiles of the prompt sequences
@@ -107,11 +110,11 @@ __device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s
 }
 
 // One workgroup's query tile (sequence s, rows tb .. tb + nb - 1, nb <= BQ);
-// pf_smem holds prefill_smem_bytes(). UPAGE: every page holds at least
+// pf_smem holds prefill_smem_bytes(NST). UPAGE: every page holds at least
 // THREADS / 32 keys. F8: an E4M3 cache, dequantised while
 // the tiles load as the reference's attn_group8 does (qwen35.cu:1424-1436):
 // K' = bf16(k * kscale), V' = bf16(v * vscale); the rest is unchanged.
-template <int BQ, int NQB, bool F8, bool UPAGE>
+template <int BQ, int NQB, bool F8, bool UPAGE, int NST>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb) {
     constexpr int THREADS = pf_threads(BQ, NQB);
     static_assert(PF_BK * HEAD_DIM / 8 % THREADS == 0, "whole 16-byte chunks per thread");
@@ -265,12 +268,26 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
 
     const int ntiles = (L + PF_BK - 1) / PF_BK;
     if constexpr (UPAGE) fetch_ids(0);
+    // NST 3: iteration i stores tile i + 1 (loaded during iteration i - 1)
+    // into the stage tile i - 2 used, requests tile i + 2, computes tile i,
+    // then one barrier. NST 2: iteration i requests tile i + 1, computes
+    // tile i, and stores between two barriers.
+    static_assert(NST == 2 || NST == 3, "2 or 3 stages");
     load_tile(0);
     store_tile(0, 0);
+    if (NST == 3 && ntiles > 1) load_tile(PF_BK);
     __syncthreads();
+    int buf = 0;
     for (int it = 0; it < ntiles; it++) {
-        const int buf = it & 1, k0 = it * PF_BK;
-        if (it + 1 < ntiles) load_tile(k0 + PF_BK);
+        const int k0 = it * PF_BK;
+        if constexpr (NST == 3) {
+            if (it + 1 < ntiles) {
+                store_tile(buf == 2 ? 0 : buf + 1, k0 + PF_BK);
+                if (it + 2 < ntiles) load_tile(k0 + 2 * PF_BK);
+            }
+        } else {
+            if (it + 1 < ntiles) load_tile(k0 + PF_BK);
+        }
         if (k0 <= last) {
             const uint16_t* K = pf_smem + buf * STAGE;
             const uint16_t* Vt = K + PF_K_ELEMS;
@@ -349,10 +366,14 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                         o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pb[qb][kk]), o[qb][db], 0, 0, 0);
                 }
         }
-        if (it + 1 < ntiles) {
+        if constexpr (NST == 3) {
+            if (it + 1 < ntiles) __syncthreads();  // tile i + 1 stored; tile i's stage free after the next store
+            buf = buf == 2 ? 0 : buf + 1;
+        } else if (it + 1 < ntiles) {
             __syncthreads();  // everyone is done with the buffer two tiles back
             store_tile(buf ^ 1, k0 + PF_BK);
             __syncthreads();
+            buf ^= 1;
         }
     }
 #pragma unroll
@@ -379,15 +400,15 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     }
 }
 
-template <int BQ, int NQB, bool F8 = false>
+template <int BQ, int NQB, bool F8 = false, int NST = PF_NST>
 __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
     int s, tb, nb;
     if (!find_prefill_tile<BQ>(p, s, tb, nb)) return;
     // Pages of at least THREADS / 32 keys: uniform page ids per chunk.
     if (p.bs_log2 >= __builtin_ctz(pf_threads(BQ, NQB) / 32))
-        prefill_tile<BQ, NQB, F8, true>(p, pf_smem, s, tb, nb);
+        prefill_tile<BQ, NQB, F8, true, NST>(p, pf_smem, s, tb, nb);
     else
-        prefill_tile<BQ, NQB, F8, false>(p, pf_smem, s, tb, nb);
+        prefill_tile<BQ, NQB, F8, false, NST>(p, pf_smem, s, tb, nb);
 }
 
 __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {

@@ -259,7 +259,9 @@ namespace pkv {
 
 // The prompt kernel on a grid of 32-query tiles (BQ = 32: one workgroup per
 // tile; BQ = 64: one per two tiles, the other blocks of the grid exit).
-// Stages in static LDS (the launch's dynamic shared memory is not used).
+// Stages in static LDS (the launch's dynamic shared memory is not used, but
+// it is still allocated: up to 67,584 bytes for attn_groupr, so the static
+// part stays at two stages, 70,656 bytes, within the CU's 160 KiB).
 template <int BQ>
 __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
     __shared__ __align__(16) uint16_t sm[2 * PF_STAGE];
@@ -288,7 +290,7 @@ __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
     p.num_blocks = REF_NO_CLAMP;
     p.kscale = nullptr;
     p.vscale = nullptr;
-    prefill_body<BQ, 1>(p, sm);
+    prefill_body<BQ, 1, false, 2>(p, sm);
 }
 
 }  // namespace pkv
@@ -301,7 +303,7 @@ extern "C" __global__ void __launch_bounds__(256, 1) attn_groupr_g4_t2_k32(PKV_F
 // The E4M3 prompt kernel a gfx950 device selects for an E4M3 cache
 // (fa_shape(4, 95, true): attn_group8_g4_t2_k16, 256 threads, grid of
 // 32-query tiles, 101,376 bytes of dynamic shared memory, which holds this
-// kernel's two 34.5 KiB stages).
+// kernel's two 34.5 KiB stages: the 2-stage loop).
 extern "C" __global__ void __launch_bounds__(256, 1) attn_group8_g4_t2_k16(PKV_FLASH_ARGS) {
     extern __shared__ __align__(16) uint16_t g8_smem[];
     if ((int)blockDim.x != pkv::pf_threads(32, 1) || Hq != 4 * Hkv || !kscale || !vscale || block_size <= 0 ||
@@ -329,7 +331,7 @@ extern "C" __global__ void __launch_bounds__(256, 1) attn_group8_g4_t2_k16(PKV_F
     p.num_blocks = pkv::REF_NO_CLAMP;
     p.kscale = kscale;
     p.vscale = vscale;
-    pkv::prefill_body<32, 1, true>(p, g8_smem);
+    pkv::prefill_body<32, 1, true, 2>(p, g8_smem);
 }
 
 extern "C" __global__ void __launch_bounds__(512, 1) attn_mfma_g4_t2(PKV_FLASH_ARGS) {

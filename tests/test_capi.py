@@ -90,3 +90,28 @@ def test_reference_launch_shapes():
     assert (name, grid, threads, smem) == ("attn_mfma_g4_t2", (7, 4, 1), 512, 37376)
     name, grid, threads, smem = refabi.flash_launch(100, 3, 4, fp8=True)
     assert (name, grid, threads, smem) == ("attn_group8_g4_t2_k16", (7, 4, 1), 256, 101376)
+
+
+def test_reference_prompt_kernels_fit_lds(tmp_path):
+    """Static LDS of each prompt kernel of the code object plus the dynamic
+    shared memory the engine's launch passes (flash_launch, model.rs:58-79)
+    fits one CU's 160 KiB; otherwise the dispatch is rejected."""
+    import re
+    import subprocess
+    from pkv import refabi
+    bundler = "/opt/rocm/llvm/bin/clang-offload-bundler"
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    co = tmp_path / "gfx950.co"
+    subprocess.run([bundler, "--unbundle", "--type=o", f"--input={refabi.HSACO}", f"--output={co}",
+                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950"], check=True)
+    notes = subprocess.run([readelf, "--notes", str(co)], check=True, capture_output=True, text=True).stdout
+    static = {}
+    for item in notes.split("\n  - ")[1:]:
+        name = re.search(r"\.name:\s+(\S+)", item)
+        lds = re.search(r"\.group_segment_fixed_size:\s+(\d+)", item)
+        if name and lds:
+            static[name.group(1)] = int(lds.group(1))
+    for kw in ({}, {"mfma": True}, {"fp8": True}):
+        name, _, _, smem = refabi.flash_launch(100, 3, 4, **kw)
+        assert name in static, (name, sorted(static))
+        assert static[name] + smem <= 160 * 1024, (name, static[name], smem)
