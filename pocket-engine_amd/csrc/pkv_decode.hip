@@ -344,6 +344,16 @@ __device__ __forceinline__ void piece_body(const DecodeParams& p, const int* __r
 #pragma unroll
                 for (int e = 0; e < 8; e++) acc[g][e] *= cg[g];
         }
+        // Keys outside [j0, j1) on a partial page (the piece's first or
+        // last) carry weight 0; their V is zeroed too, since a stale slot
+        // may hold NaN.
+        if (pi * PAGE < j0 || pi * PAGE + PAGE > j1) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int kp = pi * PAGE + 8 * hv + k;
+                if (kp < j0 || kp >= j1) vb[k] = make_uint4(0, 0, 0, 0);
+            }
+        }
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const float4 pk = *reinterpret_cast<const float4*>(&lds.p[(8 * hv + k) * G]);

@@ -60,14 +60,50 @@ __device__ __forceinline__ uint4 buf_load16(const void* base, uint32_t off) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-constexpr int PF_BK = 32;          // keys per tile
-constexpr int PF_KSTR = HEAD_DIM + 8;  // K tile row stride (elements)
-// V tile row stride (row-major [key][d]): 576 bytes = 64 (mod 256), so the
-// 4 rows x 64 bytes a half-wave's transposing reads touch fall on distinct
-// banks.
-constexpr int PF_VSTR = HEAD_DIM + 32;
-constexpr int PF_K_ELEMS = PF_BK * PF_KSTR;
-constexpr int PF_V_ELEMS = PF_BK * PF_VSTR;
+constexpr int PF_BK = 32;  // keys per tile
+// Tile layout in LDS (K and V alike, row-major [key][d]): keys r and r + 16
+// are one 1,024-byte pair (one 64-lane global_load_lds_dwordx4 fills it) and
+// pairs are padded: K pairs every 1,040 bytes, so the 16 rows a quarter-wave
+// reads with ds_read_b128 start 16 bytes apart modulo 256 (distinct banks);
+// V pairs every 1,088 bytes (64 modulo 256), so the 4 rows x 64 bytes of a
+// half-wave's transposing ds_read_b64_tr_b16 land on distinct banks.
+constexpr int PF_KPAIR = 520;  // elements
+constexpr int PF_VPAIR = 544;
+constexpr int PF_K_ELEMS = 16 * PF_KPAIR;
+constexpr int PF_V_ELEMS = 16 * PF_VPAIR;
+// Element offset of row r (0..31) of a K or V tile.
+__device__ __forceinline__ constexpr int pf_krow(int r) { return (r & 15) * PF_KPAIR + (r >> 4) * HEAD_DIM; }
+__device__ __forceinline__ constexpr int pf_vrow(int r) { return (r & 15) * PF_VPAIR + (r >> 4) * HEAD_DIM; }
+
+// LDS byte address of a shared-memory pointer (the M0 operand of LDS DMA).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+// LDS DMA (global_load_lds_dwordx4 / _dword): every active lane reads 16
+// (4) bytes at its own global address and the data lands at LDS address
+// m0 + 16 (4) x lane (m0 must be wave-uniform). Issued from inline assembly so the compiler neither
+// waits for it nor counts it: the caller waits on vmcnt itself (the
+// compiler's own vmcnt waits stay correct, only stricter, since counts are
+// of operations newer than the one awaited).
+__device__ __forceinline__ void dma16(const void* src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(m0))
+                 : "memory");
+}
+__device__ __forceinline__ void dma4(const void* src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(m0))
+                 : "memory");
+}
+// s_waitcnt vmcnt(N) (N < 16) that leaves the other counters alone.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 16, "vmcnt 0..15");
+    __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xF << 8));
+}
+
 // Query positions per workgroup (BQ) and 32-query blocks per wave (NQB):
 // waves = 4 query heads x BQ / (32 NQB). NQB = 2 feeds every K / V^T
 // fragment read from LDS into two MFMAs (half the LDS traffic per MFMA) at
@@ -83,7 +119,9 @@ constexpr int PF_STAGE = PF_K_ELEMS + PF_V_ELEMS;
 // LDS stages of K / V tiles: 3 (one barrier per tile) unless the launch's
 // shared memory only holds 2 (two barriers per tile).
 constexpr int PF_NST = 3;
-constexpr size_t prefill_smem_bytes(int nst = PF_NST) { return (size_t)nst * PF_STAGE * 2; }
+// The DMA path's page-id ring after the stages: per wave 4 slots x 4 ids.
+constexpr int PF_IDS_BYTES = (PF_THREADS / 64) * 4 * 4 * 4;
+constexpr size_t prefill_smem_bytes(int nst = PF_NST) { return (size_t)nst * PF_STAGE * 2 + PF_IDS_BYTES; }
 
 // The query tile of this workgroup among the prompt sequences: tile
 // blockIdx.x of the concatenated BQ-query tiles of the prompt sequences
@@ -114,13 +152,14 @@ __device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s
 // THREADS / 32 keys. F8: an E4M3 cache, dequantised while
 // the tiles load as the reference's attn_group8 does (qwen35.cu:1424-1436):
 // K' = bf16(k * kscale), V' = bf16(v * vscale); the rest is unchanged.
-template <int BQ, int NQB, bool F8, bool UPAGE, int NST>
+template <int BQ, int NQB, bool F8, bool UPAGE, int NST, bool DMA>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb) {
     constexpr int THREADS = pf_threads(BQ, NQB);
     static_assert(PF_BK * HEAD_DIM / 8 % THREADS == 0, "whole 16-byte chunks per thread");
     // Buffer b: K tile at pf_smem + b * STAGE, V tile right after it.
     constexpr int STAGE = PF_STAGE;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, lh = lane >> 5;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31,
+              lh = lane >> 5;
     const int kvh = blockIdx.y;
     const int G = 4, h = kvh * G + (wave & 3), qb0 = (wave >> 2) * NQB;  // the wave's first query block
     const int qp0 = p.pos[tb];
@@ -254,40 +293,21 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         }
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
-            *reinterpret_cast<uint4*>(sk + (u * KPU + kl0) * PF_KSTR + c8) = kr[u];
-            *reinterpret_cast<uint4*>(sv + (u * KPU + kl0) * PF_VSTR + c8) = vr[u];
+            *reinterpret_cast<uint4*>(sk + pf_krow(u * KPU + kl0) + c8) = kr[u];
+            *reinterpret_cast<uint4*>(sv + pf_vrow(u * KPU + kl0) + c8) = vr[u];
         }
     };
     // V^T fragments (A operand of O^T += V^T P^T, dims 32 db + lq, keys
     // 16 kk + 8 h + 4 lh + e) come from the row-major V tile through
     // ds_read_b64_tr_b16: in each 16-lane group, result lane i element e is
     // element i % 4 of what lane i / 4 + 4 e read, so lane s of the group
-    // reads row 4 lh + s / 4 (+ 16 kk + 8 h), dims 16 (group & 1) + 4 (s % 4)
-    // (+ 32 db).
-    const int tr_at = (4 * lh + ((lane & 15) >> 2)) * PF_VSTR + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    // reads row 16 kk + 8 h + 4 lh + s / 4, dims 32 db + 16 (group & 1) +
+    // 4 (s % 4) (row 16 kk + x sits at pf_vrow(x) + 256 kk).
+    const int tr_at = (4 * lh + ((lane & 15) >> 2)) * PF_VPAIR + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     const int ntiles = (L + PF_BK - 1) / PF_BK;
-    if constexpr (UPAGE) fetch_ids(0);
-    // NST 3: iteration i stores tile i + 1 (loaded during iteration i - 1)
-    // into the stage tile i - 2 used, requests tile i + 2, computes tile i,
-    // then one barrier. NST 2: iteration i requests tile i + 1, computes
-    // tile i, and stores between two barriers.
-    static_assert(NST == 2 || NST == 3, "2 or 3 stages");
-    load_tile(0);
-    store_tile(0, 0);
-    if (NST == 3 && ntiles > 1) load_tile(PF_BK);
-    __syncthreads();
-    int buf = 0;
-    for (int it = 0; it < ntiles; it++) {
-        const int k0 = it * PF_BK;
-        if constexpr (NST == 3) {
-            if (it + 1 < ntiles) {
-                store_tile(buf == 2 ? 0 : buf + 1, k0 + PF_BK);
-                if (it + 2 < ntiles) load_tile(k0 + 2 * PF_BK);
-            }
-        } else {
-            if (it + 1 < ntiles) load_tile(k0 + PF_BK);
-        }
+    // Tile k0 from stage buf: S^T, online softmax, O^T update.
+    auto compute = [&](int buf, int k0) __attribute__((always_inline)) {
         if (k0 <= last) {
             const uint16_t* K = pf_smem + buf * STAGE;
             const uint16_t* Vt = K + PF_K_ELEMS;
@@ -299,9 +319,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             for (int qb = 0; qb < NQB; qb++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) st[qb][r] = 0.f;
+            const uint16_t* krow = K + pf_krow(lq) + 8 * lh;
 #pragma unroll
             for (int kk = 0; kk < 16; kk++) {
-                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(K + lq * PF_KSTR + 16 * kk + 8 * lh));
+                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 16 * kk));
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++)
                     st[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb][kk], st[qb], 0, 0, 0);
@@ -357,15 +378,115 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
 #pragma unroll
                 for (int db = 0; db < 8; db++) {
                     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_s16x4*)(vtr + (16 * kk) * PF_VSTR + 32 * db));
+                        (lds_s16x4*)(vtr + 256 * kk + 32 * db));
                     const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_s16x4*)(vtr + (16 * kk + 8) * PF_VSTR + 32 * db));
+                        (lds_s16x4*)(vtr + 8 * PF_VPAIR + 256 * kk + 32 * db));
                     const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
                     for (int qb = 0; qb < NQB; qb++)
                         o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pb[qb][kk]), o[qb][db], 0, 0, 0);
                 }
         }
+    };
+    static_assert(NST == 2 || NST == 3, "2 or 3 stages");
+    if constexpr (DMA) {
+        // Iteration i requests tile i + 2 (stage (i + 2) % 3, freed by the
+        // barrier that ended iteration i - 1) and the page ids of tile i + 4,
+        // computes tile i, waits for its own DMA of tile i + 1 (everything
+        // but this iteration's requests), then one barrier publishes tile
+        // i + 1 to all waves. Each wave DMAs pair rows 2 w and 2 w + 1 of K
+        // and of V (keys 2 w, 2 w + 1, 2 w + 16, 2 w + 17) and reads their
+        // page ids from its own 4-slot ring, filled 4 tiles ahead by its own
+        // DMA, so the loop issues no other vector memory reads.
+        static_assert(!F8 && NST == 3 && THREADS == PF_THREADS, "bf16, 3 stages, 8 waves");
+        int* ring = reinterpret_cast<int*>(pf_smem + NST * STAGE) + wave * 16;
+        const int hi = lane >> 5;
+        auto dma_ids = [&](int k0, int slot) __attribute__((always_inline)) {
+            if (lane < 4) {
+                const int r = 2 * wave + (lane & 1) + 16 * (lane >> 1);
+                dma4(bt + min((k0 + r) >> bs_log2, last_pi), lds_addr(ring + 4 * slot));
+            }
+        };
+        auto dma_tile = [&](int k0, int buf, int slot) __attribute__((always_inline)) {
+            const int4 idv = *reinterpret_cast<const int4*>(ring + 4 * slot);
+            const int id[4] = {__builtin_amdgcn_readfirstlane(idv.x), __builtin_amdgcn_readfirstlane(idv.y),
+                               __builtin_amdgcn_readfirstlane(idv.z), __builtin_amdgcn_readfirstlane(idv.w)};
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int r = 2 * wave + j, kp = k0 + r + 16 * hi;
+                long pg = hi ? id[2 + j] : id[j];
+                pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
+                const size_t at = (((size_t)pg << bs_log2) + (kp & bs_mask)) * row + kvh * HEAD_DIM + 8 * (lane & 31);
+                uint16_t* st = pf_smem + buf * STAGE;
+                dma16(p.kc + at, lds_addr(st + pf_krow(r)));
+                dma16(p.vc + at, lds_addr(st + PF_K_ELEMS + pf_vrow(r)));
+            }
+        };
+        // V rows of keys at or past L (partial last tile) read stale slots:
+        // the wave zeroes its own rows once its DMA has landed (P is 0 there,
+        // but 0 x a stale NaN would not be).
+        auto zero_tail = [&](int k0, int buf) __attribute__((always_inline)) {
+            if (k0 + PF_BK <= L) return;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int r = 2 * wave + j;
+                if (k0 + r + 16 * hi >= L)
+                    *reinterpret_cast<uint4*>(pf_smem + buf * STAGE + PF_K_ELEMS + pf_vrow(r + 16 * hi) +
+                                              8 * (lane & 31)) = make_uint4(0, 0, 0, 0);
+            }
+        };
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            if (t < ntiles) dma_ids(t * PF_BK, t);
+        wait_vm<0>();
+        dma_tile(0, 0, 0);
+        if (ntiles > 1) {
+            dma_tile(PF_BK, 1, 1);
+            wait_vm<4>();
+        } else {
+            wait_vm<0>();
+        }
+        zero_tail(0, 0);
+        __syncthreads();
+        int buf = 0;
+        for (int it = 0; it < ntiles; it++) {
+            const int k0 = it * PF_BK;
+            const bool more2 = it + 2 < ntiles, more4 = it + 4 < ntiles;
+            if (more2) dma_tile(k0 + 2 * PF_BK, buf == 0 ? 2 : buf - 1, (it + 2) & 3);
+            if (more4) dma_ids(k0 + 4 * PF_BK, it & 3);
+            compute(buf, k0);
+            if (it + 1 < ntiles) {
+                // tile i + 1 landed: all but this iteration's requests
+                if (more4) wait_vm<5>();
+                else if (more2) wait_vm<4>();
+                else wait_vm<0>();
+                buf = buf == 2 ? 0 : buf + 1;
+                zero_tail(k0 + PF_BK, buf);
+                __syncthreads();
+            }
+        }
+    } else {
+    if constexpr (UPAGE) fetch_ids(0);
+    // NST 3: iteration i stores tile i + 1 (loaded during iteration i - 1)
+    // into the stage tile i - 2 used, requests tile i + 2, computes tile i,
+    // then one barrier. NST 2: iteration i requests tile i + 1, computes
+    // tile i, and stores between two barriers.
+    load_tile(0);
+    store_tile(0, 0);
+    if (NST == 3 && ntiles > 1) load_tile(PF_BK);
+    __syncthreads();
+    int buf = 0;
+    for (int it = 0; it < ntiles; it++) {
+        const int k0 = it * PF_BK;
+        if constexpr (NST == 3) {
+            if (it + 1 < ntiles) {
+                store_tile(buf == 2 ? 0 : buf + 1, k0 + PF_BK);
+                if (it + 2 < ntiles) load_tile(k0 + 2 * PF_BK);
+            }
+        } else {
+            if (it + 1 < ntiles) load_tile(k0 + PF_BK);
+        }
+        compute(buf, k0);
         if constexpr (NST == 3) {
             if (it + 1 < ntiles) __syncthreads();  // tile i + 1 stored; tile i's stage free after the next store
             buf = buf == 2 ? 0 : buf + 1;
@@ -375,6 +496,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             __syncthreads();
             buf ^= 1;
         }
+    }
     }
 #pragma unroll
     for (int qb = 0; qb < NQB; qb++) {
@@ -404,11 +526,16 @@ template <int BQ, int NQB, bool F8 = false, int NST = PF_NST>
 __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
     int s, tb, nb;
     if (!find_prefill_tile<BQ>(p, s, tb, nb)) return;
-    // Pages of at least THREADS / 32 keys: uniform page ids per chunk.
-    if (p.bs_log2 >= __builtin_ctz(pf_threads(BQ, NQB) / 32))
-        prefill_tile<BQ, NQB, F8, true, NST>(p, pf_smem, s, tb, nb);
+    // bf16 with 3 stages and 8 waves: tiles by LDS DMA; otherwise through
+    // registers, with uniform page ids per chunk when pages hold at least
+    // THREADS / 32 keys.
+    constexpr bool DMA = !F8 && NST == 3 && pf_threads(BQ, NQB) == PF_THREADS;
+    if constexpr (DMA)
+        prefill_tile<BQ, NQB, F8, true, NST, true>(p, pf_smem, s, tb, nb);
+    else if (p.bs_log2 >= __builtin_ctz(pf_threads(BQ, NQB) / 32))
+        prefill_tile<BQ, NQB, F8, true, NST, false>(p, pf_smem, s, tb, nb);
     else
-        prefill_tile<BQ, NQB, F8, false, NST>(p, pf_smem, s, tb, nb);
+        prefill_tile<BQ, NQB, F8, false, NST, false>(p, pf_smem, s, tb, nb);
 }
 
 __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {

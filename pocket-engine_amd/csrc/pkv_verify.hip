@@ -157,19 +157,28 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
         if constexpr (F8) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
+                const int kp = pi * PAGE + 4 * gq + i;
                 ks_cur[i] = B.ksc[i];
-                vs_cur[i] = B.vsc[i];
+                vs_cur[i] = (kp >= j0 && kp < j1) ? B.vsc[i] : 0.f;  // a stale scale may be NaN
             }
             // V rows to LDS as bf16: row 4 k + lane / 16, dims 16 (lane % 16) .. + 15
 #pragma unroll
             for (int k = 0; k < NV; k++) {
                 uint16_t* d = vl + (4 * k + (lane >> 4)) * VF_VSTR + 16 * c16;
-                *reinterpret_cast<uint4*>(d) = e4m3x8_to_bf16x8(B.vb[k].x, B.vb[k].y);
-                *reinterpret_cast<uint4*>(d + 8) = e4m3x8_to_bf16x8(B.vb[k].z, B.vb[k].w);
+                const int kp = pi * PAGE + 4 * k + (lane >> 4);
+                const bool in = kp >= j0 && kp < j1;
+                *reinterpret_cast<uint4*>(d) = in ? e4m3x8_to_bf16x8(B.vb[k].x, B.vb[k].y) : make_uint4(0, 0, 0, 0);
+                *reinterpret_cast<uint4*>(d + 8) = in ? e4m3x8_to_bf16x8(B.vb[k].z, B.vb[k].w) : make_uint4(0, 0, 0, 0);
             }
         } else {
+            // rows of keys outside [j0, j1) as zeros: their weight is 0, and
+            // a stale slot may hold NaN
 #pragma unroll
-            for (int k = 0; k < NV; k++) *reinterpret_cast<uint4*>(st + 2 * k * VF_VSTR) = B.vb[k];
+            for (int k = 0; k < NV; k++) {
+                const int kp = pi * PAGE + 2 * k + (lane >> 5);
+                *reinterpret_cast<uint4*>(st + 2 * k * VF_VSTR) =
+                    (kp >= j0 && kp < j1) ? B.vb[k] : make_uint4(0, 0, 0, 0);
+            }
         }
         if constexpr (PREFETCH) {
             const size_t next = page_base(nxt);

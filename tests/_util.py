@@ -56,3 +56,24 @@ def close(got_bits, want_bits, atol=2e-3, rtol=1e-2):
     err = np.abs(g - w)
     ok = err <= atol + rtol * np.abs(w)
     return bool(ok.all()), float(err.max()) if err.size else 0.0
+
+
+def used_slots(c, lens):
+    """Slots holding a key of a sequence (sequence s has keys
+    0 .. lens[s] - 1 through block table row s)."""
+    used = np.zeros(c["kc"].shape[0], bool)
+    for s, L in enumerate(lens):
+        for k in range(int(L)):
+            used[c["bt"][s][k // BS] * BS + k % BS] = True
+    return used
+
+
+def nan_stale(c, lens):
+    """K / V caches of case c with every slot that holds no key of a
+    sequence set to bf16 NaN: stale or never-written slots must not reach
+    any output."""
+    used = used_slots(c, lens)
+    kc, vc = c["kc"].copy(), c["vc"].copy()
+    kc[~used] = 0x7FC0
+    vc[~used] = 0x7FC0
+    return dict(c, kc=kc, vc=vc)

@@ -11,7 +11,7 @@ import torch
 
 import oracle
 import pkv
-from _util import BS, D, bf16_bits, close, decode_case, hash_bf16
+from _util import BS, D, bf16_bits, close, decode_case, hash_bf16, nan_stale
 from pkv import synth
 
 pytestmark = pytest.mark.gpu
@@ -65,6 +65,20 @@ def default_config():
 def test_decode_matches_oracle(dev, lens, Hkv, seed):
     print(f"case decode lens={lens[:6]} Hkv={Hkv} seed={seed}", flush=True)
     c = decode_case(lens, 4 * Hkv, Hkv, seed)
+    got = run_gpu(c, dev)
+    want = run_oracle(c)
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("lens,wg,mr", [([1, 2, 15, 17, 33], 1, 32), ([4097, 40], 4, 16), ([513, 8193, 1000], 1, 32)])
+def test_decode_stale_slots_are_nan(dev, lens, wg, mr):
+    """Slots holding no key (past each length in its last page, unused
+    pages) are NaN in K and V; masked keys must not reach the output, not
+    even as 0 x NaN, whole-token or split over ranges."""
+    print(f"case decode NaN stale slots lens={lens} wg={wg} mr={mr}", flush=True)
+    pkv.attn_decode_config(wg, mr)
+    c = nan_stale(decode_case(lens, 16, 4, 12), lens)
     got = run_gpu(c, dev)
     want = run_oracle(c)
     ok, err = close(got, want)

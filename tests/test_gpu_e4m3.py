@@ -237,3 +237,78 @@ def test_reference_named_paged8(dev, lens, Z):
                                c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
     ok, err = close(got, want)
     assert ok, f"max |diff| {err}"
+
+
+def nan_stale8(c, lens, k8, v8, ks, vs):
+    """E4M3 bytes 0x7F (NaN) and NaN scales in every slot holding no key."""
+    from _util import used_slots
+    used = used_slots(c, lens)
+    k8, v8, ks, vs = k8.copy(), v8.copy(), ks.copy(), vs.copy()
+    k8[~used] = 0x7F
+    v8[~used] = 0x7F
+    ks[~used] = np.nan
+    vs[~used] = np.nan
+    return k8, v8, ks, vs
+
+
+@pytest.mark.parametrize("kind", ["decode", "decode_split", "verify"])
+def test_e4m3_stale_slots_are_nan(dev, kind):
+    """Decode / verify over an E4M3 cache whose slots holding no key are NaN
+    bytes with NaN scales: no NaN reaches the outputs."""
+    print(f"case e4m3 NaN stale slots {kind}", flush=True)
+    pkv.attn_decode_config(1, 16 if kind == "decode_split" else 32)
+    try:
+        if kind == "verify":
+            groups = [(12, 4), (301, 3), (0, 2)]
+            c = verify_case(groups, 4, 14)
+            lens = [L0 + n for L0, n in groups]
+        else:
+            lens = [1, 2, 15, 17, 33, 4097]
+            c = decode_case(lens, 16, 4, 14)
+        rng = np.random.default_rng(14)
+        k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+        ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+        vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+        k8, v8, ks, vs = nan_stale8(c, lens, k8, v8, ks, vs)
+        got = run_decode8(c, k8, v8, ks, vs, dev)
+        want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], c["Hq"], 4, c["pos"],
+                                   c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
+        ok, err = close(got, want)
+        assert ok, f"max |diff| {err}"
+    finally:
+        pkv.attn_decode_config(1, 32)
+
+
+@pytest.mark.parametrize("refabi_kernel", [False, True])
+def test_prefill_e4m3_stale_slots_are_nan(dev, refabi_kernel):
+    """Chunked prefill over an E4M3 cache with NaN bytes and scales in every
+    slot holding no key."""
+    print(f"case prefill e4m3 NaN stale slots refabi={refabi_kernel}", flush=True)
+    from test_gpu_prefill import prefill_case
+    from pkv.refabi import F, I, P, RefKernels, flash_launch
+    c = prefill_case([100, 5], [45, 130], 4, 15)
+    rng = np.random.default_rng(15)
+    k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+    ks = (rng.random(c["kc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+    vs = (rng.random(c["vc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+    lens = [int(c["pos"][c["cu"][s + 1] - 1]) + 1 for s in range(c["seqs"])]
+    k8, v8, ks, vs = nan_stale8(c, lens, k8, v8, ks, vs)
+    T, Hq, Hkv = c["T"], c["Hq"], 4
+    out = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev)
+    args = [t_(c["q"], dev), t_(k8, dev), t_(v8, dev), t_(ks, dev), t_(vs, dev), t_(c["qkv"], dev)]
+    pos, cu, bt = t_(c["pos"], dev), t_(c["cu"], dev), t_(c["bt"], dev)
+    if refabi_kernel:
+        name, grid, threads, smem = flash_launch(T, c["seqs"], Hkv, fp8=True)
+        RefKernels().launch(name, grid, threads, smem,
+                            [P(args[0]), P(args[1]), P(args[2]), P(args[3]), P(args[4]), P(args[5]), I(c["qstride"]),
+                             I(Hq), I(Hkv), P(pos), P(cu), I(c["seqs"]), P(bt), I(c["max_blocks"]), I(BS), P(out),
+                             F(SCALE), P(None), I(1)])
+    else:
+        pkv.attn_prefill_e4m3(*args, c["qstride"], Hq, Hkv, pos, cu, c["seqs"], bt, c["max_blocks"], BS, out, SCALE,
+                              None, 1, T, c["pages"])
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    want = oracle.attn_prefill8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["cu"], c["seqs"],
+                                c["bt"], c["max_blocks"], BS, SCALE)
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"

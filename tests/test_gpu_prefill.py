@@ -15,7 +15,7 @@ import torch
 
 import oracle
 import pkv
-from _util import BS, D, bf16_bits, close, decode_case
+from _util import BS, D, bf16_bits, close, decode_case, nan_stale
 
 pytestmark = pytest.mark.gpu
 SCALE = 1.0 / 16.0
@@ -100,6 +100,21 @@ def test_prefill_late_dominant_key(dev):
     kc = c["kc"].copy()
     kc[slot, 0] = bf16_bits(16 * u)  # its score: 16 |u|^2 / 16 * log2 e = 92 (log2 units) above ~0
     c = dict(c, kc=kc, q=q)
+    got = run_prefill(c, dev)
+    want = oracle.attn_prefill(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], c["Hq"], c["Hkv"], c["pos"], c["cu"],
+                               c["seqs"], c["bt"], c["max_blocks"], BS, SCALE)
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("ctxs,chunks", [([0], [37]), ([100], [45]), ([16, 5], [130, 2])])
+def test_prefill_stale_slots_are_nan(dev, ctxs, chunks):
+    """Every cache slot that holds no key of a sequence (past its length in
+    its last page, unused pages) is NaN in K and V: keys at or past the
+    length must not reach the output, not even as 0 x NaN."""
+    print(f"case prefill NaN stale slots ctx={ctxs} chunk={chunks}", flush=True)
+    c = prefill_case(ctxs, chunks, 4, 11)
+    c = nan_stale(c, [int(c["pos"][c["cu"][s + 1] - 1]) + 1 for s in range(c["seqs"])])
     got = run_prefill(c, dev)
     want = oracle.attn_prefill(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], c["Hq"], c["Hkv"], c["pos"], c["cu"],
                                c["seqs"], c["bt"], c["max_blocks"], BS, SCALE)

@@ -14,7 +14,7 @@ import torch
 
 import oracle
 import pkv
-from _util import BS, D, bf16_bits, close
+from _util import BS, D, bf16_bits, close, nan_stale
 
 pytestmark = pytest.mark.gpu
 SCALE = 1.0 / 16.0
@@ -94,6 +94,21 @@ def test_verify_matches_oracle(dev, groups, Hkv, seed, min_range):
     print(f"case verify groups={groups} Hkv={Hkv} min_range={min_range}", flush=True)
     pkv.attn_decode_config(1, min_range)
     c = verify_case(groups, Hkv, seed)
+    got = run_verify(c, dev)
+    want = run_oracle(c)
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("groups,min_range", [([(12, 4), (29, 3), (0, 2)], 32), ([(5000, 4), (301, 4)], 32)])
+def test_verify_stale_slots_are_nan(dev, groups, min_range):
+    """Slots holding no key of a sequence are NaN in K and V (the drafts'
+    own later keys are real keys, masked causally): no NaN reaches the
+    outputs."""
+    print(f"case verify NaN stale slots groups={groups}", flush=True)
+    pkv.attn_decode_config(1, min_range)
+    c = verify_case(groups, 4, 13)
+    c = nan_stale(c, [L0 + n for L0, n in groups])
     got = run_verify(c, dev)
     want = run_oracle(c)
     ok, err = close(got, want)
