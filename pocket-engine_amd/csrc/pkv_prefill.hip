@@ -71,6 +71,13 @@ constexpr int PF_KPAIR = 520;  // elements
 constexpr int PF_VPAIR = 544;
 constexpr int PF_K_ELEMS = 16 * PF_KPAIR;
 constexpr int PF_V_ELEMS = 16 * PF_VPAIR;
+// Rows hold keys in the order key_of_row(r) = (r & 7) + 16 ((r >> 3) & 1) +
+// 8 (r >> 4): the two rows of a pair (r, r + 16) are keys j and j + 8 of the
+// same 16-key half, i.e. the same page whenever pages hold 16 keys or more,
+// so one DMA of a pair reads from one page. (P and V^T share the row order,
+// so only key positions, for masking, depend on it.)
+__device__ __forceinline__ constexpr int pf_key_of_row(int r) { return (r & 7) + 16 * ((r >> 3) & 1) + 8 * (r >> 4); }
+__device__ __forceinline__ constexpr int pf_row_of_key(int j) { return (j & 7) + 8 * ((j >> 4) & 1) + 16 * ((j >> 3) & 1); }
 // Element offset of row r (0..31) of a K or V tile.
 __device__ __forceinline__ constexpr int pf_krow(int r) { return (r & 15) * PF_KPAIR + (r >> 4) * HEAD_DIM; }
 __device__ __forceinline__ constexpr int pf_vrow(int r) { return (r & 15) * PF_VPAIR + (r >> 4) * HEAD_DIM; }
@@ -102,6 +109,13 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 16, "vmcnt 0..15");
     __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xF << 8));
+}
+// The same LDS DMA from a uniform base plus a 32-bit lane byte offset.
+__device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(off), "s"(base), "s"(__builtin_amdgcn_readfirstlane(m0))
+                 : "memory");
 }
 
 // Query positions per workgroup (BQ) and 32-query blocks per wave (NQB):
@@ -293,8 +307,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         }
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
-            *reinterpret_cast<uint4*>(sk + pf_krow(u * KPU + kl0) + c8) = kr[u];
-            *reinterpret_cast<uint4*>(sv + pf_vrow(u * KPU + kl0) + c8) = vr[u];
+            const int r = pf_row_of_key(u * KPU + kl0);
+            *reinterpret_cast<uint4*>(sk + pf_krow(r) + c8) = kr[u];
+            *reinterpret_cast<uint4*>(sv + pf_vrow(r) + c8) = vr[u];
         }
     };
     // V^T fragments (A operand of O^T += V^T P^T, dims 32 db + lq, keys
@@ -334,7 +349,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                 if (k0 + PF_BK - 1 > qb_first || k0 + PF_BK > L) {
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
-                        const int kp = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        const int kp = k0 + pf_key_of_row(8 * (r >> 2) + 4 * lh + (r & 3));
                         if (kp > qp || kp >= L) st[qb][r] = -INFINITY;
                     }
                 }
@@ -394,32 +409,34 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         // barrier that ended iteration i - 1) and the page ids of tile i + 4,
         // computes tile i, waits for its own DMA of tile i + 1 (everything
         // but this iteration's requests), then one barrier publishes tile
-        // i + 1 to all waves. Each wave DMAs pair rows 2 w and 2 w + 1 of K
-        // and of V (keys 2 w, 2 w + 1, 2 w + 16, 2 w + 17) and reads their
-        // page ids from its own 4-slot ring, filled 4 tiles ahead by its own
-        // DMA, so the loop issues no other vector memory reads.
-        static_assert(!F8 && NST == 3 && THREADS == PF_THREADS, "bf16, 3 stages, 8 waves");
+        // i + 1 to all waves. Wave w DMAs pairs 2 w and 2 w + 1 of K and of
+        // V (keys key_of_row(r) and + 8, one page: pages hold 16 keys or
+        // more on this path) and reads their page ids from its own 4-slot
+        // ring, filled 4 tiles ahead by its own DMA, so the loop issues no
+        // other vector memory reads.
+        static_assert(!F8 && UPAGE && NST == 3 && THREADS == PF_THREADS, "bf16, 16-key pages, 3 stages, 8 waves");
         int* ring = reinterpret_cast<int*>(pf_smem + NST * STAGE) + wave * 16;
         const int hi = lane >> 5;
+        // lane byte offset inside a pair's page: key + 8 for the upper half
+        const uint32_t lane_off = (uint32_t)(hi * 8 * row + kvh * HEAD_DIM + 8 * (lane & 31)) * 2;
         auto dma_ids = [&](int k0, int slot) __attribute__((always_inline)) {
-            if (lane < 4) {
-                const int r = 2 * wave + (lane & 1) + 16 * (lane >> 1);
-                dma4(bt + min((k0 + r) >> bs_log2, last_pi), lds_addr(ring + 4 * slot));
+            if (lane < 2) {
+                const int j = pf_key_of_row(2 * wave + lane);
+                dma4(bt + min((k0 + j) >> bs_log2, last_pi), lds_addr(ring + 4 * slot));
             }
         };
         auto dma_tile = [&](int k0, int buf, int slot) __attribute__((always_inline)) {
-            const int4 idv = *reinterpret_cast<const int4*>(ring + 4 * slot);
-            const int id[4] = {__builtin_amdgcn_readfirstlane(idv.x), __builtin_amdgcn_readfirstlane(idv.y),
-                               __builtin_amdgcn_readfirstlane(idv.z), __builtin_amdgcn_readfirstlane(idv.w)};
+            const int2 idv = *reinterpret_cast<const int2*>(ring + 4 * slot);
+            const int id[2] = {__builtin_amdgcn_readfirstlane(idv.x), __builtin_amdgcn_readfirstlane(idv.y)};
+            uint16_t* st = pf_smem + buf * STAGE;
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                const int r = 2 * wave + j, kp = k0 + r + 16 * hi;
-                long pg = hi ? id[2 + j] : id[j];
+                const int r = 2 * wave + j, kp = k0 + pf_key_of_row(r);
+                long pg = id[j];
                 pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
-                const size_t at = (((size_t)pg << bs_log2) + (kp & bs_mask)) * row + kvh * HEAD_DIM + 8 * (lane & 31);
-                uint16_t* st = pf_smem + buf * STAGE;
-                dma16(p.kc + at, lds_addr(st + pf_krow(r)));
-                dma16(p.vc + at, lds_addr(st + PF_K_ELEMS + pf_vrow(r)));
+                const size_t slot_at = (((size_t)pg << bs_log2) + (kp & bs_mask)) * row;  // uniform
+                dma16_s(p.kc + slot_at, lane_off, lds_addr(st + pf_krow(r)));
+                dma16_s(p.vc + slot_at, lane_off, lds_addr(st + PF_K_ELEMS + pf_vrow(r)));
             }
         };
         // V rows of keys at or past L (partial last tile) read stale slots:
@@ -429,10 +446,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             if (k0 + PF_BK <= L) return;
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                const int r = 2 * wave + j;
-                if (k0 + r + 16 * hi >= L)
-                    *reinterpret_cast<uint4*>(pf_smem + buf * STAGE + PF_K_ELEMS + pf_vrow(r + 16 * hi) +
-                                              8 * (lane & 31)) = make_uint4(0, 0, 0, 0);
+                const int r = 2 * wave + j + 16 * hi;
+                if (k0 + pf_key_of_row(r) >= L)
+                    *reinterpret_cast<uint4*>(pf_smem + buf * STAGE + PF_K_ELEMS + pf_vrow(r) + 8 * (lane & 31)) =
+                        make_uint4(0, 0, 0, 0);
             }
         };
 #pragma unroll
@@ -526,12 +543,13 @@ template <int BQ, int NQB, bool F8 = false, int NST = PF_NST>
 __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
     int s, tb, nb;
     if (!find_prefill_tile<BQ>(p, s, tb, nb)) return;
-    // bf16 with 3 stages and 8 waves: tiles by LDS DMA; otherwise through
+    // bf16 with 3 stages, 8 waves and pages of 16 keys or more: tiles by LDS
+    // DMA; otherwise through
     // registers, with uniform page ids per chunk when pages hold at least
     // THREADS / 32 keys.
     constexpr bool DMA = !F8 && NST == 3 && pf_threads(BQ, NQB) == PF_THREADS;
-    if constexpr (DMA)
-        prefill_tile<BQ, NQB, F8, true, NST, true>(p, pf_smem, s, tb, nb);
+    if (DMA && p.bs_log2 >= 4)
+        prefill_tile<BQ, NQB, F8, true, NST, DMA>(p, pf_smem, s, tb, nb);
     else if (p.bs_log2 >= __builtin_ctz(pf_threads(BQ, NQB) / 32))
         prefill_tile<BQ, NQB, F8, true, NST, false>(p, pf_smem, s, tb, nb);
     else
