@@ -91,6 +91,42 @@ __device__ __forceinline__ float dpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
+// LDS byte address of a shared-memory pointer (the M0 operand of LDS DMA).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+// LDS DMA (global_load_lds_dwordx4 / _dword): every active lane reads 16
+// (4) bytes at its own global address and the data lands at LDS address
+// m0 + 16 (4) x lane (m0 must be wave-uniform). Issued from inline assembly so the compiler neither
+// waits for it nor counts it: the caller waits on vmcnt itself (the
+// compiler's own vmcnt waits stay correct, only stricter, since counts are
+// of operations newer than the one awaited).
+__device__ __forceinline__ void dma16(const void* src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(m0))
+                 : "memory");
+}
+__device__ __forceinline__ void dma4(const void* src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(m0))
+                 : "memory");
+}
+// s_waitcnt vmcnt(N) (N < 64: bits 3:0 and 15:14) that leaves the other
+// counters alone.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt 0..63");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+// The same LDS DMA from a uniform base plus a 32-bit lane byte offset.
+__device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(off), "s"(base), "s"(__builtin_amdgcn_readfirstlane(m0))
+                 : "memory");
+}
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
