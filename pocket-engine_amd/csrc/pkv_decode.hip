@@ -439,20 +439,15 @@ struct DecodeEpi {
 };
 
 template <int G, bool FUSED>
-__device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* __restrict__ tok_seq,
-                                             const int* __restrict__ block_table, const int* __restrict__ pos,
-                                             const int* __restrict__ cu, WaveLds<G>& lds, int t, int kvh, int j0,
-                                             int j1, int L, int idx) {
-    const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
+__device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* __restrict__ block_table, WaveLds<G>& lds,
+                                             int t, int seq, int row0, int P0, int kvh, int j0, int j1, int L,
+                                             int idx) {
     const int* __restrict__ bt = block_table + (size_t)seq * p.max_blocks;
     const DecodeEpi<G> epi{p, t, kvh, idx, j0 == 0 && j1 == L};
-    if constexpr (FUSED) {
-        const int row0 = __builtin_amdgcn_readfirstlane(cu[seq]);
-        const int P0 = __builtin_amdgcn_readfirstlane(pos[row0]);
+    if constexpr (FUSED)
         piece_body<G, true>(p, bt, lds, t, kvh, j0, j1, L, P0, row0, epi);
-    } else {
+    else
         piece_body<G, false>(p, bt, lds, t, kvh, j0, j1, L, INT_MAX, 0, epi);
-    }
 }
 
 // The workgroup's key range [start, end) of the flattened key space (keys
@@ -535,35 +530,80 @@ __global__ void __launch_bounds__(256, 1)
     __shared__ int sh_scan[16];
     __shared__ int sh_t0[2];
     __shared__ WaveLds<G> sh_w[4];
+    // pos and tok_seq of every token (T <= block size): a piece's sequence,
+    // first row and first position come from LDS, not from dependent global
+    // loads at every piece start.
+    __shared__ int sh_pos[256], sh_seq[256];
     const int T = p.T, nthr = blockDim.x, tid = threadIdx.x, b = blockIdx.x;
     const int nkv = nthr >> 6, kv0 = blockIdx.y * 4;
+    const bool tab = T <= nthr;
+    // FUSED: this block appends the step's rows of its kv heads for tokens
+    // b, b + n_wg, .. (no range reads these slots from the cache in this
+    // launch). The first token's loads are issued now and stored after the
+    // range search, so their latency overlaps it.
+    const int per_row = nkv * HEAD_DIM / 8;  // uint4 per K (or V) row slice; 2 per_row == nthr
+    long app_slot = -1;
+    uint4 app_val;
+    auto app_src = [&](int t, int i) {
+        const bool is_v = i >= per_row;
+        return reinterpret_cast<const uint4*>((is_v ? p.v_rows : p.k_rows) + (size_t)t * p.row_stride +
+                                              (size_t)kv0 * HEAD_DIM)[is_v ? i - per_row : i];
+    };
+    auto app_store = [&](int t, long slot, int i, uint4 v) {
+        const bool is_v = i >= per_row;
+        reinterpret_cast<uint4*>((is_v ? p.vc : p.kc) + ((size_t)slot * p.Hkv + kv0) * HEAD_DIM)[is_v ? i - per_row : i] =
+            v;
+    };
     if constexpr (FUSED) {
-        // Append the step's rows of this block's kv heads: tokens b, b + n_wg, ..
-        // (no range reads these slots from the cache in this launch).
-        const int per_row = nkv * HEAD_DIM / 8;  // uint4 per K (or V) row slice
-        for (int t = b; t < T; t += p.n_wg) {
-            const long slot = slot_map[t];
-            if (slot < 0 || slot >= p.num_blocks * PAGE) continue;
-            for (int i = tid; i < 2 * per_row; i += nthr) {
-                const bool is_v = i >= per_row;
-                const int j = is_v ? i - per_row : i;
-                const uint16_t* s = (is_v ? p.v_rows : p.k_rows) + (size_t)t * p.row_stride + (size_t)kv0 * HEAD_DIM;
-                uint16_t* d = (is_v ? p.vc : p.kc) + ((size_t)slot * p.Hkv + kv0) * HEAD_DIM;
-                reinterpret_cast<uint4*>(d)[j] = reinterpret_cast<const uint4*>(s)[j];
-            }
+        if (b < T) {
+            app_slot = slot_map[b];
+            app_val = app_src(b, tid);
         }
     }
     int start, end, t0, off0;
-    if (!find_range(p, [&](int t) { return decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec); }, sh_scan,
-                    sh_t0, start, end, t0, off0))
-        return;
+    const bool any = find_range(
+        p,
+        [&](int t) {
+            const int L = decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec);
+            if (tab) {
+                sh_pos[t] = pos[t];
+                sh_seq[t] = tok_seq[t];
+            }
+            return L;
+        },
+        sh_scan, sh_t0, start, end, t0, off0);
+    if constexpr (FUSED) {
+        if (app_slot >= 0 && app_slot < p.num_blocks * PAGE) app_store(b, app_slot, tid, app_val);
+        for (int t = b + p.n_wg; t < T; t += p.n_wg) {
+            const long slot = slot_map[t];
+            if (slot >= 0 && slot < p.num_blocks * PAGE) app_store(t, slot, tid, app_src(t, tid));
+        }
+    }
+    if (!any) return;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = kv0 + wave;
     int t = t0, off = off0;
     while (off < end && t < T) {
-        const int L = decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec);
+        const int L = !tab || p.skip_prompts ? decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec)
+                                             : sh_pos[t] + 1;
         if (L > 0) {
             const int j0 = max(start, off) - off, j1 = min(end, off + L) - off;
-            decode_piece<G, FUSED>(p, tok_seq, block_table, pos, cu, sh_w[wave], t, kvh, j0, j1, L, t + b);
+            int seq, row0 = t, P0 = 0;
+            if (tab) {
+                // the sequence's rows of this step are the run of equal
+                // tok_seq around t; its first row's position is P0
+                seq = __builtin_amdgcn_readfirstlane(sh_seq[t]);
+                if constexpr (FUSED) {
+                    while (row0 > 0 && sh_seq[row0 - 1] == seq) row0--;
+                    P0 = __builtin_amdgcn_readfirstlane(sh_pos[row0]);
+                }
+            } else {
+                seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
+                if constexpr (FUSED) {
+                    row0 = __builtin_amdgcn_readfirstlane(cu[seq]);
+                    P0 = __builtin_amdgcn_readfirstlane(pos[row0]);
+                }
+            }
+            decode_piece<G, FUSED>(p, block_table, sh_w[wave], t, seq, row0, P0, kvh, j0, j1, L, t + b);
             off += L;
         }
         t++;
