@@ -73,6 +73,17 @@ int pkv_gather(const void* kcache, const void* vcache, const int32_t* bt_row, in
 int pkv_page_copy(void* kcache, void* vcache, const int32_t* src, const int32_t* dst, int n, int64_t page_bytes,
                   int64_t num_blocks, void* stream);
 
+/* Draft-pass metadata: replaces mtp_next (qwen35.cu:2633-2650, launched per
+ * MTP draft pass k >= 1). For sequence s < S with step row rows[s]:
+ * dpos[s] = pos[rows[s]] + k; dslot[s] = block_table[s * max_blocks +
+ * dpos / block_size] * block_size + dpos % block_size while dpos[s] <=
+ * limits[s], else -1 (also -1 when the page index reaches max_blocks);
+ * drope[axis * S + s] = rope[axis * rope_stride + rows[s]] + k for the 3
+ * rotary axes. All arrays are device int32. */
+int pkv_mtp_next(const int32_t* rows, const int32_t* pos, const int32_t* rope, int rope_stride,
+                 const int32_t* block_table, int max_blocks, int block_size, const int32_t* limits, int k,
+                 int32_t* dpos, int32_t* dslot, int32_t* drope, int S, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Device: paged decode attention (bf16, head_dim 256, block_size 16, G = 4)
  * ------------------------------------------------------------------------- */

@@ -51,6 +51,7 @@ _lib.orc_merge.argtypes = [_P, _P, _P, _I, _P]
 _lib.orc_attn_prefill.restype = _I
 _lib.orc_attn_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I]
 _lib.orc_mtp_slots.argtypes = [_P, _P, _P, _I, _I, _P, _I, _P, _P, _I]
+_lib.orc_mtp_next.argtypes = [_P, _P, _P, _I, _P, _I, _I, _P, _I, _P, _P, _P, _I]
 _lib.orc_attn_prep.argtypes = [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _F, _I, _L, _P, _P, _P]
 _lib.orc_e4m3_to_f.restype = _F
 _lib.orc_e4m3_to_f.argtypes = [ctypes.c_uint8]
@@ -177,6 +178,18 @@ def mtp_slots(rows, pos, block_table, max_blocks, block_size, limits, k):
     _lib.orc_mtp_slots(_p(rows), _p(pos), _p(block_table), max_blocks, block_size, _p(limits), k, _p(dpos),
                        _p(dslot), S)
     return dpos, dslot
+
+
+def mtp_next(rows, pos, rope, rope_stride, block_table, max_blocks, block_size, limits, k):
+    """(dpos, dslot, drope [3, S]) of draft pass k (qwen35.cu:2633-2650)."""
+    S = len(rows)
+    dpos = np.zeros(S, np.int32)
+    dslot = np.zeros(S, np.int32)
+    drope = np.zeros((3, S), np.int32)
+    rows, pos, rope, block_table, limits = _i32(rows), _i32(pos), _i32(rope), _i32(block_table), _i32(limits)
+    _lib.orc_mtp_next(_p(rows), _p(pos), _p(rope), rope_stride, _p(block_table), max_blocks, block_size, _p(limits), k,
+                      _p(dpos), _p(dslot), _p(drope), S)
+    return dpos, dslot, drope
 
 
 def attn_prep(qkv, qstride, Hq, Hkv, q_norm, k_norm, rope, rope_stride, sec_h, sec_w, slot_map, inv_freq, eps,

@@ -306,6 +306,16 @@ void orc_mtp_slots(const int* rows, const int* pos, const int* block_table, int 
     }
 }
 
+/* mtp_next in full (qwen35.cu:2633-2650): the slots above plus the three
+ * rotary position rows of the draft pass, drope[axis * S + s] =
+ * rope[axis * rope_stride + rows[s]] + k. */
+void orc_mtp_next(const int* rows, const int* pos, const int* rope, int rope_stride, const int* block_table,
+                  int max_blocks, int block_size, const int* limits, int k, int* dpos, int* dslot, int* drope, int S) {
+    orc_mtp_slots(rows, pos, block_table, max_blocks, block_size, limits, k, dpos, dslot, S);
+    for (int s = 0; s < S; s++)
+        for (int axis = 0; axis < 3; axis++) drope[axis * S + s] = rope[(size_t)axis * rope_stride + rows[s]] + k;
+}
+
 /* ---- attention input preparation (reference attn_prep, qwen35.cu:1067-1128):
  * per token t and head: q heads (and k heads) are RMS-normalised with their
  * f32 weights, y = bf16(x * scale * w), scale = 1 / sqrt(sum x^2 / 256 + eps)

@@ -127,6 +127,17 @@ int pkv_page_copy(void* kcache, void* vcache, const int32_t* src, const int32_t*
     return launch_status();
 }
 
+int pkv_mtp_next(const int32_t* rows, const int32_t* pos, const int32_t* rope, int rope_stride,
+                 const int32_t* block_table, int max_blocks, int block_size, const int32_t* limits, int k,
+                 int32_t* dpos, int32_t* dslot, int32_t* drope, int S, void* stream) {
+    if (S < 0 || max_blocks <= 0 || block_size <= 0 || rope_stride < 0) return PKV_ERR_INVALID;
+    if (S == 0) return PKV_OK;
+    if (!rows || !pos || !rope || !block_table || !limits || !dpos || !dslot || !drope) return PKV_ERR_INVALID;
+    hipLaunchKernelGGL(pkv::mtp_next_kernel, dim3((S + 255) / 256), dim3(256), 0, (hipStream_t)stream, rows, pos, rope,
+                       rope_stride, block_table, max_blocks, block_size, limits, k, dpos, dslot, drope, S);
+    return launch_status();
+}
+
 int pkv_attn_prep(const void* qkv, int qstride, int Hq, int Hkv, const float* q_norm, const float* k_norm,
                   const int32_t* rope, int rope_stride, int sec_h, int sec_w, const int32_t* slot_map,
                   const float* inv_freq, void* qout, void* kcache, void* vcache, const float* kscale,

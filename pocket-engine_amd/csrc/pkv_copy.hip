@@ -85,4 +85,37 @@ __global__ void __launch_bounds__(256) page_copy_kernel(uint8_t* __restrict__ kc
     for (long k = b + threadIdx.x; k < e; k += blockDim.x) dp[k] = sp[k];
 }
 
+// Draft-pass metadata (reference mtp_next, qwen35.cu:2633-2650): for
+// sequence s (step row rows[s]) and draft pass k, the position p =
+// pos[rows[s]] + k, its cache slot through the block table while p <=
+// limits[s] (-1 past the limit: the draft layer writes no KV there), and the
+// three rotary position rows shifted by k. One thread per sequence. A page
+// index past max_blocks maps to -1 (the reference reads past the row there).
+__device__ __forceinline__ void mtp_next_one(int s, const int* __restrict__ rows, const int* __restrict__ pos,
+                                             const int* __restrict__ rope, int rope_stride,
+                                             const int* __restrict__ block_table, int max_blocks, int block_size,
+                                             const int* __restrict__ limits, int k, int* __restrict__ dpos,
+                                             int* __restrict__ dslot, int* __restrict__ drope, int S) {
+    const int r = rows[s], p = pos[r] + k;
+    dpos[s] = p;
+    const int pi = p / block_size;
+    dslot[s] = p <= limits[s] && pi < max_blocks
+                   ? block_table[(size_t)s * max_blocks + pi] * block_size + p % block_size
+                   : -1;
+#pragma unroll
+    for (int axis = 0; axis < 3; axis++) drope[axis * S + s] = rope[(size_t)axis * rope_stride + r] + k;
+}
+
+__global__ void __launch_bounds__(256) mtp_next_kernel(const int* __restrict__ rows, const int* __restrict__ pos,
+                                                       const int* __restrict__ rope, int rope_stride,
+                                                       const int* __restrict__ block_table, int max_blocks,
+                                                       int block_size, const int* __restrict__ limits, int k,
+                                                       int* __restrict__ dpos, int* __restrict__ dslot,
+                                                       int* __restrict__ drope, int S) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s < S)
+        mtp_next_one(s, rows, pos, rope, rope_stride, block_table, max_blocks, block_size, limits, k, dpos, dslot,
+                     drope, S);
+}
+
 }  // namespace pkv

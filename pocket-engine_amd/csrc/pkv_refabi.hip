@@ -33,6 +33,7 @@
 // power of two for prompts; G = Hq / Hkv = 4. A launch outside these bounds
 // writes nothing. Page ids are not clamped (the reference ABI passes no pool
 // size).
+#include "pkv_copy.hip"
 #include "pkv_decode.hip"
 #include "pkv_prefill.hip"
 #include "pkv_prep.hip"
@@ -337,4 +338,16 @@ extern "C" __global__ void __launch_bounds__(256, 1) attn_group8_g4_t2_k16(PKV_F
 extern "C" __global__ void __launch_bounds__(512, 1) attn_mfma_g4_t2(PKV_FLASH_ARGS) {
     pkv::flash_ref<64>(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
                        max_blocks, block_size, out, scale, outs, spec);
+}
+
+// The draft passes' slot mapping under the reference's name and signature
+// (qwen35.cu:2633-2650; grid ceil(S / 128) x 128 threads).
+extern "C" __global__ void __launch_bounds__(256)
+    mtp_next(const int* __restrict__ rows, const int* __restrict__ pos, const int* __restrict__ rope, int rope_stride,
+             const int* __restrict__ block_table, int max_blocks, int block_size, const int* __restrict__ limits, int k,
+             int* __restrict__ dpos, int* __restrict__ dslot, int* __restrict__ drope, int S) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s < S && block_size > 0)
+        pkv::mtp_next_one(s, rows, pos, rope, rope_stride, block_table, max_blocks, block_size, limits, k, dpos,
+                          dslot, drope, S);
 }

@@ -37,6 +37,8 @@ _SIGS = {
     "pkv_append": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_i64, _c_p]),
     "pkv_gather": (_c_int, [_c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_p, _c_p, _c_p]),
     "pkv_page_copy": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_i64, _c_i64, _c_p]),
+    "pkv_mtp_next": (_c_int, [_c_p, _c_p, _c_p, _c_int, _c_p, _c_int, _c_int, _c_p, _c_int, _c_p, _c_p, _c_p, _c_int,
+                              _c_p]),
     "pkv_attn_decode_workspace": (_c_int, [_c_int, _c_int, ctypes.POINTER(_c_sz)]),
     "pkv_attn_decode": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_p, _c_int, _c_int,
                                  _c_p, _c_f, _c_p, _c_int, _c_p, _c_int, _c_int, _c_i64, _c_p, _c_sz, _c_p]),
@@ -143,6 +145,15 @@ def gather(kcache, vcache, bt_row, L, block_size, Hkv, head_bytes, num_blocks, k
 def page_copy(kcache, vcache, src, dst, n, page_bytes, num_blocks, stream=None):
     _check(_lib.pkv_page_copy(_ptr(kcache), _ptr(vcache), _ptr(src), _ptr(dst), n, page_bytes, num_blocks,
                               _stream(stream)), "pkv_page_copy")
+
+
+def mtp_next(rows, pos, rope, rope_stride, block_table, max_blocks, block_size, limits, k, dpos, dslot, drope, S,
+             stream=None):
+    """Draft pass k's positions, KV slots (-1 past limits) and rotary rows
+    (reference mtp_next, qwen35.cu:2633-2650); device int32 arrays."""
+    _check(_lib.pkv_mtp_next(_ptr(rows), _ptr(pos), _ptr(rope), rope_stride, _ptr(block_table), max_blocks, block_size,
+                             _ptr(limits), k, _ptr(dpos), _ptr(dslot), _ptr(drope), S, _stream(stream)),
+           "pkv_mtp_next")
 
 
 def attn_decode_workspace(T, Hq):

@@ -52,6 +52,9 @@ def test_invalid_and_unsupported_arguments_return_before_launch():
     assert L.pkv_page_copy(16, 16, 16, 16, 1, 100, 10, None) == pkv.ERR_INVALID  # page bytes % 16
     assert L.pkv_gather(16, 16, 16, -1, 16, 4, 512, 10, 16, 16, None) == pkv.ERR_INVALID
     assert L.pkv_attn_decode_config(0, 32) == pkv.ERR_INVALID
+    assert L.pkv_mtp_next(16, 16, 16, 4, 16, 0, 16, 16, 1, 16, 16, 16, 2, None) == pkv.ERR_INVALID  # max_blocks
+    assert L.pkv_mtp_next(None, 16, 16, 4, 16, 4, 16, 16, 1, 16, 16, 16, 2, None) == pkv.ERR_INVALID
+    assert L.pkv_mtp_next(None, None, None, 0, None, 4, 16, None, 1, None, None, None, 0, None) == pkv.OK
 
 
 def test_workspace_grows_with_tokens():
@@ -74,7 +77,7 @@ def test_reference_abi_code_object_exports_the_reference_kernel_names(tmp_path):
     syms = subprocess.run([readelf, "--syms", "--wide", str(co)], check=True, capture_output=True, text=True).stdout
     kernels = {line.split()[-1] for line in syms.splitlines() if " FUNC " in line and "GLOBAL" in line}
     for name in ("attn_prep", "attn_paged_g4", "attn_merge", "attn_groupr_g4_t2_k32", "attn_mfma_g4_t2",
-                 "attn_group8_g4_t2_k16", "attn_paged8_g4"):
+                 "attn_group8_g4_t2_k16", "attn_paged8_g4", "mtp_next"):
         assert name in kernels, (name, sorted(kernels)[:20])
 
 

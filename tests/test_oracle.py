@@ -217,6 +217,19 @@ def test_mtp_slots_closed_form():
     assert list(dslot) == [9 * 16 + 1, -1]
 
 
+def test_mtp_next_closed_form():
+    """Draft pass k = 2 over two sequences (rows 3 and 0 of the step): slot
+    of position pos + 2 through the block table while within the limit (-1
+    past it), rotary rows shifted by k per axis (rope_stride 5)."""
+    bt = np.array([[5, 9, 2], [7, 1, 0]], np.int32)
+    pos = np.array([3, 0, 0, 15], np.int32)      # rows 0..3
+    rope = np.arange(15, dtype=np.int32) * 10    # 3 axes x stride 5
+    dpos, dslot, drope = oracle.mtp_next([3, 0], pos, rope, 5, bt, 3, BS, [47, 4], 2)
+    assert list(dpos) == [17, 5]
+    assert list(dslot) == [9 * 16 + 1, -1]      # 17 <= 47: page 1 of row 0; 5 > 4
+    assert drope.tolist() == [[32, 2], [82, 52], [132, 102]]
+
+
 # ---- attn_prep (reference qwen35.cu:1067-1128) ----
 
 def _prep_case(T, Hq, Hkv, rng, slots=None, sec=(11, 11, 10), theta=1e7):
