@@ -350,6 +350,22 @@ int64_t pkv_kv_blocks(pkv_kv* kv, int seq_id, uint32_t* out, int64_t cap);
 int pkv_kv_fill(pkv_kv* kv, const int* seq_ids, const int* ntok, int nrows, int max_tokens, int max_blocks,
                 int32_t* pos, int32_t* slot_map, int32_t* tok_seq, int32_t* cu, int32_t* limits,
                 int32_t* block_table);
+/* The reference's per-step metadata buffer (Meta, model.rs:1245-1354): one
+ * int32 device buffer holding every per-step array at a fixed offset, so a
+ * step captured into a HIP graph replays against fixed pointers while the
+ * host rewrites the contents (engine.rs:704-720; Scheduler::fill / pad write
+ * it). Offsets in int32 words for capacities max_tokens (a multiple of 4 in
+ * the engine), max_seqs, max_blocks and spec (tokens a verifying sequence
+ * feeds; 1 without drafts); words is the buffer's length. This path reads
+ * pos, slot_map, tok_seq, rope, cu, outs, limits and block_table: pass
+ * buffer + offset to pkv_kv_fill / pkv_kv_pad and to the device entry
+ * points. */
+typedef struct {
+    int64_t ids, pos, slot_map, tok_seq, emb_src, rope, mtp_ids, mtp_src, cu, slots, fresh, outs, ocu, last, temps,
+        seeds, top_ks, top_ps, min_ps, pen_cu, limits, snaps, block_table, lora, masks, words;
+} pkv_meta;
+int pkv_meta_layout(int64_t max_tokens, int64_t max_seqs, int64_t max_blocks, int64_t spec, pkv_meta* out);
+
 /* Padding rows [from, to) of n tokens each for a graph bucket (Scheduler::pad,
  * sched.rs:1219-1261): pos = k, slot_map = -1 (no KV write), tok_seq = row,
  * cu advancing by n, limits = -1, block_table rows 0. Arrays hold max_rows

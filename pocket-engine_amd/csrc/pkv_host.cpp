@@ -414,6 +414,43 @@ int pkv_kv_fill(pkv_kv* kv, const int* seq_ids, const int* ntok, int nrows, int 
     return PKV_OK;
 }
 
+int pkv_meta_layout(int64_t max_tokens, int64_t max_seqs, int64_t max_blocks, int64_t spec, pkv_meta* out) {
+    if (max_tokens <= 0 || max_seqs <= 0 || max_blocks <= 0 || spec <= 0 || !out) return PKV_ERR_INVALID;
+    const int64_t T = max_tokens, S = max_seqs, outs = max_seqs * spec;
+    const int64_t lora_tiles = max_tokens / 16 + max_seqs;  // adapter tiles of 16 tokens (lora.rs:18)
+    pkv_meta m;
+    // per token: ids, pos, slot_map, tok_seq, emb_src, rope (3 rows), mtp_ids, mtp_src
+    m.ids = 0;
+    m.pos = T;
+    m.slot_map = 2 * T;
+    m.tok_seq = 3 * T;
+    m.emb_src = 4 * T;
+    m.rope = 5 * T;
+    m.mtp_ids = 8 * T;
+    m.mtp_src = 9 * T;
+    // per sequence: cu (S + 1), slots, fresh; per output row: outs
+    m.cu = 10 * T;
+    m.slots = m.cu + S + 1;
+    m.fresh = m.slots + S;
+    m.outs = m.fresh + S;
+    m.ocu = m.outs + outs;  // S + 1
+    m.last = m.ocu + S + 1;
+    m.temps = m.last + outs;
+    m.seeds = m.temps + outs;
+    m.top_ks = m.seeds + outs;
+    m.top_ps = m.top_ks + outs;
+    m.min_ps = m.top_ps + outs;
+    m.pen_cu = m.min_ps + outs;  // outs + 1
+    m.limits = m.pen_cu + outs + 1;
+    m.snaps = m.limits + S;  // 4 per sequence
+    m.block_table = m.snaps + 4 * S;
+    m.lora = m.block_table + S * max_blocks;  // 1 + 3 per tile
+    m.masks = m.lora + 1 + 3 * lora_tiles;
+    m.words = m.masks + outs;
+    *out = m;
+    return PKV_OK;
+}
+
 int pkv_kv_pad(int from, int to, int n, int max_rows, int max_tokens, int max_blocks, int32_t* pos,
                int32_t* slot_map, int32_t* tok_seq, int32_t* cu, int32_t* limits, int32_t* block_table) {
     if (from < 0 || to < from || n < 1 || max_blocks <= 0 || to > max_rows || (int64_t)to * n > max_tokens || !pos ||

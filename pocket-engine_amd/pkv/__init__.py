@@ -82,6 +82,7 @@ _SIGS = {
     "pkv_kv_fill": (_c_int, [_c_p, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), _c_int, _c_int, _c_int] +
                     [ctypes.POINTER(ctypes.c_int32)] * 6),
     "pkv_kv_pad": (_c_int, [_c_int] * 6 + [ctypes.POINTER(ctypes.c_int32)] * 6),
+    "pkv_meta_layout": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
 }
 _SIGS["pkv_attn_decode_split"] = _SIGS["pkv_attn_decode"]
 _SIGS["pkv_attn_verify"] = _SIGS["pkv_attn_decode"]
@@ -424,6 +425,19 @@ class Kv:
         _check(_lib.pkv_kv_fill(self._h, ids, nt, nrows, max_tokens, max_blocks, *args), "pkv_kv_fill")
         out["block_table"] = out["block_table"].reshape(-1, max_blocks)
         return out
+
+
+_META_FIELDS = ("ids", "pos", "slot_map", "tok_seq", "emb_src", "rope", "mtp_ids", "mtp_src", "cu", "slots", "fresh",
+                "outs", "ocu", "last", "temps", "seeds", "top_ks", "top_ps", "min_ps", "pen_cu", "limits", "snaps",
+                "block_table", "lora", "masks", "words")
+
+
+def meta_layout(max_tokens, max_seqs, max_blocks, spec=1):
+    """Offsets (int32 words) of the reference's per-step metadata buffer
+    (Meta, model.rs:1245-1354), and its length as "words"."""
+    arr = (ctypes.c_int64 * len(_META_FIELDS))()
+    _check(_lib.pkv_meta_layout(max_tokens, max_seqs, max_blocks, spec, ctypes.byref(arr)), "pkv_meta_layout")
+    return dict(zip(_META_FIELDS, arr))
 
 
 def pad_rows(meta, frm, to, n):

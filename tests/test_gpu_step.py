@@ -175,3 +175,97 @@ def test_step_graph_replay_matches_eager(dev):
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy().view(np.uint16), eager_out), f"replay {r}"
         assert np.array_equal(kc.cpu().numpy().view(np.uint16), eager_kc)
+
+
+def test_padded_bucket_graph_replay_through_meta_buffer(dev):
+    """Graph-bucket integration (engine.rs:704-720): the step's arrays live in
+    one int32 buffer at the reference's Meta offsets (pkv_meta_layout,
+    model.rs:1245-1354); a step of 5 sequences is padded to the bucket of 8
+    with Scheduler::pad's rows (pkv_kv_pad: slot -1, position 0, block table
+    row 0), captured once into a HIP graph and replayed for two different
+    steps with the buffer's contents rewritten. Real rows match the oracle;
+    padding rows write no KV (caches equal the oracle's append bit for bit)."""
+    print("case padded bucket graph replay", flush=True)
+    Hkv, Hq, bucket, maxb = 4, 16, 8, 600
+    lay = pkv.meta_layout(bucket, bucket, maxb, 1)
+    meta_d = torch.zeros(lay["words"], dtype=torch.int32, device=dev)
+    ptr = lambda name: meta_d.data_ptr() + 4 * lay[name]
+    lens0 = [4000, 900, 6000, 33, 1500]
+    base = decode_case([L + 1 for L in lens0], Hq, Hkv, 21, pages=2400)
+    kc, vc = i16(base["kc"], dev), i16(base["vc"], dev)
+    kc_ref, vc_ref = base["kc"].copy(), base["vc"].copy()
+    qstride = base["qstride"]
+    q_d = torch.zeros(bucket, Hq, D, dtype=torch.int16, device=dev)
+    qkv_d = torch.zeros(bucket, qstride, dtype=torch.int16, device=dev)
+    out = torch.zeros(bucket, Hq, D, dtype=torch.int16, device=dev)
+    ws = torch.empty(pkv.attn_decode_workspace(bucket, Hq), dtype=torch.uint8, device=dev)
+    k_rows = qkv_d.data_ptr() + 2 * (2 * Hq * D)
+    v_rows = k_rows + 2 * Hkv * D
+
+    def host_step(k):
+        """Step k: every sequence feeds token lens0 + k; arrays padded to the bucket."""
+        lens = [L + k + 1 for L in lens0]
+        m = {n: np.zeros(sz, np.int32) for n, sz in (("pos", bucket), ("slot_map", bucket), ("tok_seq", bucket),
+                                                     ("cu", bucket + 1), ("limits", bucket))}
+        m["block_table"] = np.zeros((bucket, maxb), np.int32)
+        for s, L in enumerate(lens):
+            p = L - 1
+            m["pos"][s] = p
+            m["tok_seq"][s] = s
+            m["cu"][s + 1] = s + 1
+            m["block_table"][s, :base["max_blocks"]] = base["bt"][s]
+            m["slot_map"][s] = base["bt"][s][p // BS] * BS + p % BS
+            m["limits"][s] = ((L + BS - 1) // BS) * BS - 1
+        pkv.pad_rows(m, len(lens), bucket, 1)
+        rng = np.random.default_rng(100 + k)
+        q = bf16_bits(rng.standard_normal((bucket, Hq, D)) * 0.5)
+        qkv = bf16_bits(rng.standard_normal((bucket, qstride)) * 0.5)
+        return lens, m, q, qkv
+
+    def upload(m, q, qkv):
+        staging = np.zeros(lay["words"], np.int32)
+        for n in ("pos", "slot_map", "tok_seq", "cu", "limits"):
+            staging[lay[n]:lay[n] + len(m[n])] = m[n]
+        staging[lay["block_table"]:lay["block_table"] + m["block_table"].size] = m["block_table"].ravel()
+        meta_d.copy_(torch.from_numpy(staging))
+        q_d.copy_(i16(q, dev))
+        qkv_d.copy_(i16(qkv, dev))
+
+    def launch():
+        pkv.attn_decode_step(k_rows, v_rows, qstride * 2, ptr("slot_map"), q_d, kc, vc, qkv_d, qstride, Hq, Hkv,
+                             ptr("pos"), ptr("tok_seq"), ptr("block_table"), maxb, BS, out, SCALE, ptr("cu"), 0, None,
+                             1, bucket, base["pages"], ws)
+
+    def check(k):
+        lens, m, q, qkv = host_step(k)
+        S = len(lens)
+        # the oracle's append of the real rows, then attention over the updated cache
+        for s in range(S):
+            slot = m["slot_map"][s]
+            kc_ref[slot] = qkv[s, 2 * Hq * D:2 * Hq * D + Hkv * D].reshape(Hkv, D)
+            vc_ref[slot] = qkv[s, 2 * Hq * D + Hkv * D:2 * Hq * D + 2 * Hkv * D].reshape(Hkv, D)
+        want, _ = oracle.attn_decode(q[:S], kc_ref, vc_ref, qkv[:S], qstride, Hq, Hkv, m["pos"][:S],
+                                     m["tok_seq"][:S], m["block_table"][:S], maxb, BS, SCALE)
+        got = out.cpu().numpy().view(np.uint16)[:S]
+        ok, err = close(got, want)
+        assert ok, f"step {k}: max |diff| {err}"
+        assert np.array_equal(kc.cpu().numpy().view(np.uint16), kc_ref), f"step {k}: K cache"
+        assert np.array_equal(vc.cpu().numpy().view(np.uint16), vc_ref), f"step {k}: V cache"
+
+    upload(*host_step(0)[1:])
+    s_ = torch.cuda.Stream()
+    s_.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_):
+        launch()  # warm-up outside capture (step 0, eager)
+    torch.cuda.current_stream().wait_stream(s_)
+    torch.cuda.synchronize()
+    check(0)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch()
+    for k in (1, 2):
+        upload(*host_step(k)[1:])
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        check(k)

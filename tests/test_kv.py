@@ -186,3 +186,28 @@ def test_random_operations_keep_refcounts_consistent():
     while kv.evict_one():
         pass
     assert kv.free_count() == 256
+
+
+def test_meta_layout_regions_follow_the_reference_order():
+    """pkv_meta_layout: the regions of Meta (model.rs:1245-1354) in order,
+    each as long as the reference documents (per token: ids, pos, slot_map,
+    tok_seq, emb_src, 3 rope rows, mtp_ids, mtp_src; cu and ocu: seqs + 1;
+    per output row (seqs x spec): outs, last, temps, seeds, top_ks, top_ps,
+    min_ps, masks, pen_cu + 1; snaps 4 per sequence; lora 1 + 3 per tile of
+    16 tokens), laid end to end from 0 to words."""
+    for T, S, B, spec in ((256, 64, 512, 1), (260, 32, 8192, 5), (4, 1, 1, 1)):
+        lay = pkv.meta_layout(T, S, B, spec)
+        O = S * spec
+        tiles = T // 16 + S
+        regions = [("ids", T), ("pos", T), ("slot_map", T), ("tok_seq", T), ("emb_src", T), ("rope", 3 * T),
+                   ("mtp_ids", T), ("mtp_src", T), ("cu", S + 1), ("slots", S), ("fresh", S), ("outs", O),
+                   ("ocu", S + 1), ("last", O), ("temps", O), ("seeds", O), ("top_ks", O), ("top_ps", O),
+                   ("min_ps", O), ("pen_cu", O + 1), ("limits", S), ("snaps", 4 * S), ("block_table", S * B),
+                   ("lora", 1 + 3 * tiles), ("masks", O)]
+        at = 0
+        for name, n in regions:
+            assert lay[name] == at, (T, S, B, spec, name)
+            at += n
+        assert lay["words"] == at
+    with pytest.raises(RuntimeError):
+        pkv.meta_layout(0, 1, 1, 1)
