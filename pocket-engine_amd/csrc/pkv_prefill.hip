@@ -373,29 +373,32 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         // barrier that ended iteration i - 1) and the page ids of tile i + 4,
         // computes tile i, waits for its own DMA of tile i + 1 (everything
         // but this iteration's requests), then one barrier publishes tile
-        // i + 1 to all waves. Wave w DMAs pairs 2 w and 2 w + 1 of K and of
-        // V (keys key_of_row(r) and + 8, one page: pages hold 16 keys or
-        // more on this path) and reads their page ids from its own 4-slot
+        // i + 1 to all waves. Wave w DMAs pairs NPW w .. NPW w + NPW - 1 of K
+        // and of V (keys key_of_row(r) and + 8, one page: pages hold 16 keys
+        // or more on this path) and reads their page ids from its own 4-slot
         // ring, filled 4 tiles ahead by its own DMA, so the loop issues no
         // other vector memory reads.
-        static_assert(!F8 && UPAGE && NST == 3 && THREADS == PF_THREADS, "bf16, 16-key pages, 3 stages, 8 waves");
+        static_assert(!F8 && UPAGE && NST == 3 && THREADS == PF_THREADS, "bf16, 16-key pages, 3 stages");
+        constexpr int NPW = 16 / (THREADS / 64);  // pairs per wave (2 with 8 waves, 4 with 4)
+        static_assert(NPW <= 4, "page-id ring slots hold 4 ids");
         int* ring = reinterpret_cast<int*>(pf_smem + NST * STAGE) + wave * 16;
         const int hi = lane >> 5;
         // lane byte offset inside a pair's page: key + 8 for the upper half
         const uint32_t lane_off = (uint32_t)(hi * 8 * row + kvh * HEAD_DIM + 8 * (lane & 31)) * 2;
         auto dma_ids = [&](int k0, int slot) __attribute__((always_inline)) {
-            if (lane < 2) {
-                const int j = pf_key_of_row(2 * wave + lane);
+            if (lane < NPW) {
+                const int j = pf_key_of_row(NPW * wave + lane);
                 dma4(bt + min((k0 + j) >> bs_log2, last_pi), lds_addr(ring + 4 * slot));
             }
         };
         auto dma_tile = [&](int k0, int buf, int slot) __attribute__((always_inline)) {
-            const int2 idv = *reinterpret_cast<const int2*>(ring + 4 * slot);
-            const int id[2] = {__builtin_amdgcn_readfirstlane(idv.x), __builtin_amdgcn_readfirstlane(idv.y)};
+            const int4 idv = *reinterpret_cast<const int4*>(ring + 4 * slot);
+            const int id[4] = {__builtin_amdgcn_readfirstlane(idv.x), __builtin_amdgcn_readfirstlane(idv.y),
+                               __builtin_amdgcn_readfirstlane(idv.z), __builtin_amdgcn_readfirstlane(idv.w)};
             uint16_t* st = pf_smem + buf * STAGE;
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int r = 2 * wave + j, kp = k0 + pf_key_of_row(r);
+            for (int j = 0; j < NPW; j++) {
+                const int r = NPW * wave + j, kp = k0 + pf_key_of_row(r);
                 long pg = id[j];
                 pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
                 const size_t slot_at = (((size_t)pg << bs_log2) + (kp & bs_mask)) * row;  // uniform
@@ -409,8 +412,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         auto zero_tail = [&](int k0, int buf) __attribute__((always_inline)) {
             if (k0 + PF_BK <= L) return;
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int r = 2 * wave + j + 16 * hi;
+            for (int j = 0; j < NPW; j++) {
+                const int r = NPW * wave + j + 16 * hi;
                 if (k0 + pf_key_of_row(r) >= L)
                     *reinterpret_cast<uint4*>(pf_smem + buf * STAGE + PF_K_ELEMS + pf_vrow(r) + 8 * (lane & 31)) =
                         make_uint4(0, 0, 0, 0);
@@ -423,7 +426,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         dma_tile(0, 0, 0);
         if (ntiles > 1) {
             dma_tile(PF_BK, 1, 1);
-            wait_vm<4>();
+            wait_vm<2 * NPW>();
         } else {
             wait_vm<0>();
         }
@@ -438,8 +441,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             compute(buf, k0);
             if (it + 1 < ntiles) {
                 // tile i + 1 landed: all but this iteration's requests
-                if (more4) wait_vm<5>();
-                else if (more2) wait_vm<4>();
+                if (more4) wait_vm<2 * NPW + 1>();
+                else if (more2) wait_vm<2 * NPW>();
                 else wait_vm<0>();
                 buf = buf == 2 ? 0 : buf + 1;
                 zero_tail(k0 + PF_BK, buf);
