@@ -288,7 +288,7 @@ def main():
         # key-range kernel: every key's K and V rows (all kv heads) + q; its
         # partials are overhead, not algorithmic.
         kern_bytes = [kk * Hkv * (D + 4 if e4m3 else D * 2) * 2 + B * Hq * D * 2 for kk in keys]
-        kname = ("verify_range_kernel<true> (E4M3 cache, after attn_prep)" if e4m3 else
+        kname = ("decode_range8_kernel (E4M3 cache, after attn_prep)" if e4m3 else
                  "attn_paged_g4 (reference ABI)" if args.refabi else
                  "decode_range_kernel<4,false> (after attn_prep)" if args.with_prep else
                  "verify_range_kernel" if args.verify_kernel else "decode_range_kernel<4,false>")

@@ -166,22 +166,32 @@ int pkv_attn_verify(const void* q, const void* kcache, const void* vcache, const
                     const int32_t* outs, int spec, int T, int64_t num_blocks, void* workspace,
                     size_t workspace_bytes, void* stream);
 
-/* Decode (and draft-verify) attention over an E4M3 cache: the reference's
- * attn_paged8_g<G> (src/kernels/qwen35.cu:1313-1334 with F8; kscale /
- * vscale given) with the arguments of pkv_attn_decode plus the scales.
- * kcache / vcache hold E4M3 bytes [blocks * 16][Hkv][256] and kscale /
- * vscale one f32 per [slot][kv head] (written by pkv_attn_prep with
- * scales): s_j = (q * scale) . k_j * kscale_j, out = bf16(bf16(sum_j p_j
- * vscale_j v_j / sum_j p_j) * sigmoid(gate)). Rows group as in
- * pkv_attn_verify (`cu` required); workspace: pkv_attn_verify_workspace. */
+/* Decode attention over an E4M3 cache: the reference's attn_paged8_g<G>
+ * + attn_merge (src/kernels/qwen35.cu:1313-1334 with F8, kscale / vscale
+ * given; launched as attn_paged_g<G> at src/model.rs:2366-2437) with the
+ * arguments of pkv_attn_decode plus the scales. kcache / vcache hold E4M3
+ * bytes [blocks * 16][Hkv][256] and kscale / vscale one f32 per [slot][kv
+ * head] (written by pkv_attn_prep with scales): s_j = (q * scale) . k_j *
+ * kscale_j, out = bf16(bf16(sum_j p_j vscale_j v_j / sum_j p_j) *
+ * sigmoid(gate)). Rows as pkv_attn_decode (`cu` only with skip_prompts);
+ * workspace: pkv_attn_decode_workspace bytes. */
 int pkv_attn_decode_e4m3(const void* q, const void* kcache, const void* vcache, const float* kscale,
                          const float* vscale, const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos,
                          const int32_t* tok_seq, const int32_t* block_table, int max_blocks, int block_size,
                          void* out, float scale, const int32_t* cu, int skip_prompts, const int32_t* outs, int spec,
                          int T, int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same over an E4M3 cache with the rows of a sequence grouped as in
+ * pkv_attn_verify (`cu` required; workspace: pkv_attn_verify_workspace):
+ * the reference's attn_paged8_g<G> for speculative rows. */
+int pkv_attn_verify_e4m3(const void* q, const void* kcache, const void* vcache, const float* kscale,
+                         const float* vscale, const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos,
+                         const int32_t* tok_seq, const int32_t* block_table, int max_blocks, int block_size,
+                         void* out, float scale, const int32_t* cu, int skip_prompts, const int32_t* outs, int spec,
+                         int T, int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Measurement: the next key-range kernel this thread launches (the dominant
- * kernel of pkv_attn_decode / _split / _step / pkv_attn_verify) records start_event when it
+ * kernel of pkv_attn_decode / _split / _step / _e4m3 / pkv_attn_verify) records start_event when it
  * starts executing and stop_event when it ends (hipExtLaunchKernelGGL), so
  * hipEventElapsedTime gives its own duration without dispatch gaps, like the
  * reference's Gpu::time_us event timing (src/gpu.rs:1461-1510). Events are

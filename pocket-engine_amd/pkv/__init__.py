@@ -88,6 +88,7 @@ _SIGS["pkv_attn_decode_split"] = _SIGS["pkv_attn_decode"]
 _SIGS["pkv_attn_verify"] = _SIGS["pkv_attn_decode"]
 _SIGS["pkv_attn_prefill_e4m3"] = (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p] + _SIGS["pkv_attn_prefill"][1][3:])
 _SIGS["pkv_attn_decode_e4m3"] = (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p] + _SIGS["pkv_attn_decode"][1][3:])
+_SIGS["pkv_attn_verify_e4m3"] = _SIGS["pkv_attn_decode_e4m3"]
 _SIGS["pkv_attn_prep"] = (_c_int, [_c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p,
                                    _c_p, _c_p, _c_p, _c_p, _c_p, ctypes.c_float, _c_int, ctypes.c_int64, _c_p])
 _SIGS["pkv_attn_verify_workspace"] = _SIGS["pkv_attn_decode_workspace"]
@@ -233,16 +234,34 @@ def attn_prep(qkv, qstride, Hq, Hkv, q_norm, k_norm, rope, rope_stride, sec_h, s
                               _ptr(kscale), _ptr(vscale), eps, T, num_slots, _stream(stream)), "pkv_attn_prep")
 
 
+def _e4m3_call(name, q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks,
+               block_size, out, scale, cu, skip_prompts, outs, spec, T, num_blocks, workspace, workspace_bytes, stream):
+    if workspace_bytes is None:
+        workspace_bytes = workspace.numel() * workspace.element_size()
+    _check(getattr(_lib, name)(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(kscale), _ptr(vscale), _ptr(qkv), qstride,
+                               Hq, Hkv, _ptr(pos), _ptr(tok_seq), _ptr(block_table), max_blocks, block_size,
+                               _ptr(out), scale, _ptr(cu), int(skip_prompts), _ptr(outs), spec, T, num_blocks,
+                               _ptr(workspace), workspace_bytes, _stream(stream)), name)
+
+
 def attn_decode_e4m3(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks,
                      block_size, out, scale, cu, skip_prompts, outs, spec, T, num_blocks, workspace,
                      workspace_bytes=None, stream=None):
-    """Decode / verify attention over an E4M3 cache (reference attn_paged8)."""
-    if workspace_bytes is None:
-        workspace_bytes = workspace.numel() * workspace.element_size()
-    _check(_lib.pkv_attn_decode_e4m3(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(kscale), _ptr(vscale), _ptr(qkv), qstride,
-                                     Hq, Hkv, _ptr(pos), _ptr(tok_seq), _ptr(block_table), max_blocks, block_size,
-                                     _ptr(out), scale, _ptr(cu), int(skip_prompts), _ptr(outs), spec, T, num_blocks,
-                                     _ptr(workspace), workspace_bytes, _stream(stream)), "pkv_attn_decode_e4m3")
+    """Per-token decode attention over an E4M3 cache (reference attn_paged8 +
+    attn_merge); workspace: attn_decode_workspace(T, Hq) bytes."""
+    _e4m3_call("pkv_attn_decode_e4m3", q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq,
+               block_table, max_blocks, block_size, out, scale, cu, skip_prompts, outs, spec, T, num_blocks,
+               workspace, workspace_bytes, stream)
+
+
+def attn_verify_e4m3(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks,
+                     block_size, out, scale, cu, skip_prompts, outs, spec, T, num_blocks, workspace,
+                     workspace_bytes=None, stream=None):
+    """The same with each sequence's rows sharing one pass over its pages
+    (as attn_verify; `cu` required); workspace: attn_verify_workspace(T, Hq)."""
+    _e4m3_call("pkv_attn_verify_e4m3", q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq,
+               block_table, max_blocks, block_size, out, scale, cu, skip_prompts, outs, spec, T, num_blocks,
+               workspace, workspace_bytes, stream)
 
 
 def attn_prefill_e4m3(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,

@@ -43,6 +43,14 @@ def test_invalid_and_unsupported_arguments_return_before_launch():
                              16, None) == pkv.ERR_INVALID
     assert L.pkv_attn_decode(18, 16, 16, 16, 10240, 16, 4, 16, 16, 16, 4, 16, 16, 0.1, 16, 0, None, 1, 3, 10, 256,
                              1 << 30, None) == pkv.ERR_INVALID
+    # E4M3 decode / verify: scales required; verify needs cu; no fused append
+    for fn in (L.pkv_attn_decode_e4m3, L.pkv_attn_verify_e4m3):
+        assert fn(16, 16, 16, None, None, 16, 10240, 16, 4, 16, 16, 16, 4, 16, 16, 0.1, 16, 0, None, 1, 3, 10, 256,
+                  1 << 30, None) == pkv.ERR_INVALID
+    assert L.pkv_attn_verify_e4m3(16, 16, 16, 16, 16, 16, 10240, 16, 4, 16, 16, 16, 4, 16, 16, 0.1, None, 0, None, 1,
+                                  3, 10, 256, 1 << 30, None) == pkv.ERR_INVALID
+    assert L.pkv_attn_decode_e4m3(16, 16, 16, 16, 16, 16, 10240, 16, 4, 16, 16, 16, 4, 16, 16, 0.1, None, 0, None, 1,
+                                  3, 10, 256, 16, None) == pkv.ERR_INVALID  # short workspace
     # zero tokens is a no-op
     assert L.pkv_attn_decode(None, None, None, None, 10240, 16, 4, None, None, None, 4, 16, None, 0.1, None, 0, None,
                              1, 0, 10, None, 0, None) == pkv.OK

@@ -1,7 +1,7 @@
 """GPU parity of the E4M3 KV cache: pkv_attn_prep with scales (the
 reference's store_e4m3 in attn_prep, qwen35.cu:1055-1128) and
-pkv_attn_decode_e4m3 (attn_paged8_g4, qwen35.cu:1146-1334 with F8) against
-the oracle (oracle/pkv_oracle.c orc_attn_prep8 / orc_attn_decode8).
+pkv_attn_decode_e4m3 / pkv_attn_verify_e4m3 (attn_paged8_g4,
+qwen35.cu:1146-1334 with F8) against the oracle (oracle/pkv_oracle.c orc_attn_prep8 / orc_attn_decode8).
 
 Bars: v bytes and scales bit-exact (quantised from the exact bf16 inputs);
 k bytes within one E4M3 code (the normed / rotated bf16 inputs may differ by
@@ -67,11 +67,15 @@ def e4m3_cache(shape, rng):
     return b | (rng.integers(0, 2, size=shape).astype(np.uint8) << 7)
 
 
-def run_decode8(c, k8, v8, ks, vs, dev, skip=0, outs=None, spec=1, out_init=None):
+def run_decode8(c, k8, v8, ks, vs, dev, skip=0, outs=None, spec=1, out_init=None, entry="decode"):
+    """pkv_attn_decode_e4m3 (per-token ranges) or pkv_attn_verify_e4m3 (rows
+    of a sequence grouped), each with its own workspace size."""
     T, Hq = len(c["pos"]), c["Hq"]
     out = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev) if out_init is None else t_(out_init, dev)
-    ws = torch.empty(pkv.attn_verify_workspace(T, Hq), dtype=torch.uint8, device=dev)
-    pkv.attn_decode_e4m3(t_(c["q"], dev), t_(k8, dev), t_(v8, dev), t_(ks, dev), t_(vs, dev), t_(c["qkv"], dev),
+    fn, wsf = ((pkv.attn_decode_e4m3, pkv.attn_decode_workspace) if entry == "decode" else
+               (pkv.attn_verify_e4m3, pkv.attn_verify_workspace))
+    ws = torch.empty(wsf(T, Hq), dtype=torch.uint8, device=dev)
+    fn(t_(c["q"], dev), t_(k8, dev), t_(v8, dev), t_(ks, dev), t_(vs, dev), t_(c["qkv"], dev),
                          c["qstride"], Hq, c["Hkv"], t_(c["pos"].astype(np.int32), dev),
                          t_(c["tok_seq"].astype(np.int32), dev), t_(c["bt"], dev), c["max_blocks"], BS, out, SCALE,
                          t_(c["cu"].astype(np.int32), dev), skip, None if outs is None else t_(outs, dev), spec, T,
@@ -80,14 +84,16 @@ def run_decode8(c, k8, v8, ks, vs, dev, skip=0, outs=None, spec=1, out_init=None
     return out.cpu().numpy().view(np.uint16)
 
 
+@pytest.mark.parametrize("entry", ["decode", "verify"])
 @pytest.mark.parametrize("lens,Hkv,seed,min_range", [
     ([1, 2, 15, 16, 17], 4, 0, 32),
     ([513, 8193, 1000, 4000, 777, 64], 4, 1, 32),
     ([300, 5000], 2, 2, 32),
     ([900, 2000], 8, 3, 1 << 20),
+    ([31, 32, 33, 47, 48, 49, 95], 4, 5, 16),
 ])
-def test_decode_e4m3_matches_oracle(dev, lens, Hkv, seed, min_range):
-    print(f"case decode e4m3 lens={lens} Hkv={Hkv} min_range={min_range}", flush=True)
+def test_decode_e4m3_matches_oracle(dev, entry, lens, Hkv, seed, min_range):
+    print(f"case {entry} e4m3 lens={lens} Hkv={Hkv} min_range={min_range}", flush=True)
     pkv.attn_decode_config(1, min_range)
     try:
         c = decode_case(lens, 4 * Hkv, Hkv, seed)
@@ -95,7 +101,7 @@ def test_decode_e4m3_matches_oracle(dev, lens, Hkv, seed, min_range):
         k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
         ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)  # |k| up to ~9
         vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
-        got = run_decode8(c, k8, v8, ks, vs, dev)
+        got = run_decode8(c, k8, v8, ks, vs, dev, entry=entry)
         want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], c["Hq"], Hkv, c["pos"],
                                    c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
         ok, err = close(got, want)
@@ -104,9 +110,11 @@ def test_decode_e4m3_matches_oracle(dev, lens, Hkv, seed, min_range):
         pkv.attn_decode_config(1, 32)
 
 
-def test_verify_e4m3_rows_and_prompt_skip(dev):
-    """Verify rows over the E4M3 cache (4 rows per pass), a skipped prompt."""
-    print("case verify e4m3", flush=True)
+@pytest.mark.parametrize("entry", ["decode", "verify"])
+def test_verify_e4m3_rows_and_prompt_skip(dev, entry):
+    """Verify rows over the E4M3 cache (per token, or 4 rows per pass), a
+    skipped prompt."""
+    print(f"case verify rows e4m3 {entry}", flush=True)
     c = verify_case([(300, 4), (0, 9), (40, 4), (90, 1), (2000, 3)], 4, 12)
     rng = np.random.default_rng(12)
     k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
@@ -115,7 +123,7 @@ def test_verify_e4m3_rows_and_prompt_skip(dev):
     outs = np.zeros(5, np.int32)
     outs[1] = -1
     init = np.full((c["T"], 16, D), 0x5555, np.uint16)
-    got = run_decode8(c, k8, v8, ks, vs, dev, skip=1, outs=outs, out_init=init)
+    got = run_decode8(c, k8, v8, ks, vs, dev, skip=1, outs=outs, out_init=init, entry=entry)
     assert (got[4:13] == 0x5555).all()
     want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], 16, 4, c["pos"], c["tok_seq"], c["bt"],
                                c["max_blocks"], BS, SCALE, cu=c["cu"], skip_prompts=1, outs=outs, out=init.copy())
@@ -153,14 +161,16 @@ def test_decode_e4m3_equals_bf16_decode_on_grid_values(dev):
     ob = torch.zeros_like(o8)
     ws = torch.empty(max(pkv.attn_verify_workspace(B, Hq), pkv.attn_decode_workspace(B, Hq)), dtype=torch.uint8,
                      device=dev)
-    pkv.attn_decode_e4m3(q, k8, v8, ones, ones, qkv, qstride, Hq, Hkv, pos, ts, bt, meta.max_blocks, BS, o8, SCALE, cu,
-                         0, None, 1, B, meta.num_pages, ws)
     pkv.attn_decode(q, kbf, vbf, qkv, qstride, Hq, Hkv, pos, ts, bt, meta.max_blocks, BS, ob, SCALE, cu, 0, None, 1, B,
                     meta.num_pages, ws)
-    torch.cuda.synchronize()
     bits = lambda x: x.cpu().view(torch.int16).numpy().view(np.uint16)
-    ok, err = close(bits(o8), bits(ob))
-    assert ok, err
+    for fn in (pkv.attn_decode_e4m3, pkv.attn_verify_e4m3):
+        o8.zero_()
+        fn(q, k8, v8, ones, ones, qkv, qstride, Hq, Hkv, pos, ts, bt, meta.max_blocks, BS, o8, SCALE, cu, 0, None, 1, B,
+           meta.num_pages, ws)
+        torch.cuda.synchronize()
+        ok, err = close(bits(o8), bits(ob))
+        assert ok, (fn.__name__, err)
 
 
 @pytest.mark.parametrize("refabi_kernel", [False, True])
@@ -251,14 +261,14 @@ def nan_stale8(c, lens, k8, v8, ks, vs):
     return k8, v8, ks, vs
 
 
-@pytest.mark.parametrize("kind", ["decode", "decode_split", "verify"])
+@pytest.mark.parametrize("kind", ["decode", "decode_split", "verify", "verify_rows_per_token"])
 def test_e4m3_stale_slots_are_nan(dev, kind):
     """Decode / verify over an E4M3 cache whose slots holding no key are NaN
     bytes with NaN scales: no NaN reaches the outputs."""
     print(f"case e4m3 NaN stale slots {kind}", flush=True)
     pkv.attn_decode_config(1, 16 if kind == "decode_split" else 32)
     try:
-        if kind == "verify":
+        if kind.startswith("verify"):
             groups = [(12, 4), (301, 3), (0, 2)]
             c = verify_case(groups, 4, 14)
             lens = [L0 + n for L0, n in groups]
@@ -270,7 +280,7 @@ def test_e4m3_stale_slots_are_nan(dev, kind):
         ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
         vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
         k8, v8, ks, vs = nan_stale8(c, lens, k8, v8, ks, vs)
-        got = run_decode8(c, k8, v8, ks, vs, dev)
+        got = run_decode8(c, k8, v8, ks, vs, dev, entry="verify" if kind == "verify" else "decode")
         want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], c["Hq"], 4, c["pos"],
                                    c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
         ok, err = close(got, want)
