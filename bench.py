@@ -301,6 +301,7 @@ def main():
     kern_avg_us = 1e3 * sum(kern_ms) / len(kern_ms)
     kern_gbs = sum(kern_bytes) / (sum(kern_ms) * 1e-3) / 1e9
 
+    copy_gbs, read_gbs = hbm_copy_probe(dev)
     cpu = None
     if not args.no_cpu and args.config == "c3":
         cpu = cpu_baseline(kc, vc, q, qkv, meta, steps[args.warmup], Hq, Hkv, qstride, dev)
@@ -336,7 +337,10 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(kern_gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
-                     "avg_us": round(kern_avg_us, 2), "traffic": None,
+                     "avg_us": round(kern_avg_us, 2), "median_us": round(1e3 * float(np.median(kern_ms)), 2),
+                     "hbm_copy_probe_gbs": round(copy_gbs, 1), "hbm_read_probe_gbs": round(read_gbs, 1),
+                     "frac_of_read_probe": round(kern_gbs / read_gbs, 4),
+                     "traffic": None,
                      "traffic_profiled": None if (e4m3 or args.refabi or args.with_prep or args.unfused) else {
                          "source": "profiles/decode_step_c3_batch64.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, "
                                    "copy-calibrated, seed 1)",
@@ -556,6 +560,41 @@ def bench_verify(args):
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
+
+
+def hbm_copy_probe(dev):
+    """A plain device copy of 2 GiB (read 2 GiB + write 2 GiB) timed with
+    events over 10 copies after 2 warm-up copies (a copy kernel on the
+    current stream), and a read-mostly reduction over the same bytes: the
+    HBM GB/s plain library kernels reach on this box, beside the 8 TB/s
+    spec figure."""
+    import torch
+
+    src = torch.ones(1 << 30, dtype=torch.int16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record()
+    e1.synchronize()
+    gbs = 10 * 2 * (2 << 30) / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    # read-mostly: an integer sum over the same 2 GiB (reads only, a few
+    # bytes written), the access decode makes
+    words = src.view(torch.int64)
+    for _ in range(2):
+        words.sum()
+    e0.record()
+    for _ in range(10):
+        words.sum()
+    e1.record()
+    e1.synchronize()
+    read_gbs = 10 * (2 << 30) / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, dst, words
+    torch.cuda.empty_cache()
+    return gbs, read_gbs
 
 
 def cpu_baseline(kc, vc, q, qkv, meta, st, Hq, Hkv, qstride, dev):
