@@ -395,7 +395,12 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
         return launch_status();
     }
     if (phases & 2) {
-        hipLaunchKernelGGL(pkv::decode_merge_kernel, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p);
+        // fewer (token, head) blocks than CUs: 16 waves per block, so a
+        // head's records (up to one per range) load in one round
+        if ((int64_t)T * Hq < device_cus())
+            hipLaunchKernelGGL(pkv::decode_merge_kernel<16>, dim3(T, Hq), dim3(1024), 0, (hipStream_t)stream, p);
+        else
+            hipLaunchKernelGGL(pkv::decode_merge_kernel<4>, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p);
         return launch_status();
     }
     return PKV_OK;

@@ -122,23 +122,26 @@ __device__ __forceinline__ uint2 gate4(float a0, float a1, float a2, float a3, f
 // output: record i has its (max, sum) at ms_at(i) and its 256 weighted
 // values at acc_at(i); max is in log2 units times mscale (1 for this
 // library's records, log2 e for natural-log records). Same combination as
-// the reference's attn_merge (qwen35.cu:2255-2273). One block of 256
-// threads: wave w folds records w, w + 4, .. into a running (max, sum,
-// values) with 16 records in flight per lane (4 dims per lane), then the 4
-// waves' results are combined through LDS. Every thread reaches the sync.
-template <class MsAt, class AccAt>
+// the reference's attn_merge (qwen35.cu:2255-2273). One block of 64 NW
+// threads: wave w folds records w, w + NW, .. into a running (max, sum,
+// values) with U records in flight per lane (4 dims per lane; U = 16, or 10
+// for NW = 16 within its 128 VGPRs), then the NW waves' results are combined
+// through LDS. Every thread reaches the sync. (NW = 16 folds up to 160
+// records in one round of loads: launches with few (row, head) blocks and
+// many records each.)
+template <int NW = 4, class MsAt, class AccAt>
 __device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccAt acc_at, const uint16_t* gate,
                                            uint16_t* out) {
-    constexpr int U = 16;
-    __shared__ __align__(16) float sh_a[4][HEAD_DIM + 4];
+    constexpr int U = NW >= 16 ? 10 : 16;
+    __shared__ __align__(16) float sh_a[NW][HEAD_DIM + 4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, d = 4 * lane;
     float M = -INFINITY, S = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
-    for (int i0 = w; i0 < n; i0 += 4 * U) {
+    for (int i0 = w; i0 < n; i0 += NW * U) {
         float2 mu[U];
         float4 au[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int i = i0 + 4 * u;
+            const int i = i0 + NW * u;
             if (i < n) {
                 mu[u] = *reinterpret_cast<const float2*>(ms_at(i));
                 const float* a = acc_at(i) + d;  // 8-byte aligned
@@ -180,11 +183,11 @@ __device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccA
     if (w == 0) {
         float Mt = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < 4; k++) Mt = fmaxf(Mt, sh_a[k][HEAD_DIM]);
+        for (int k = 0; k < NW; k++) Mt = fmaxf(Mt, sh_a[k][HEAD_DIM]);
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
         float s = 0.f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < NW; k++) {
             const float mk = sh_a[k][HEAD_DIM];
             const float f = mk == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mk - Mt);
             const float4 b = *reinterpret_cast<const float4*>(&sh_a[k][d]);
@@ -201,9 +204,10 @@ __device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccA
 
 // Merges this library's partials of token t, query head h: record i is row
 // (base + i * stride) * Hq + h of part_ms / part_acc.
+template <int NW = 4>
 __device__ __forceinline__ void merge_head(const DecodeParams& p, int t, int base, int stride, int n, int h) {
     const size_t r0 = (size_t)base * p.Hq + h, step = (size_t)stride * p.Hq;
-    merge_rows(
+    merge_rows<NW>(
         n, 1.f, [&](int i) { return p.part_ms + (r0 + i * step) * 2; },
         [&](int i) { return p.part_acc + (r0 + i * step) * HEAD_DIM; },
         p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM, p.out + ((size_t)t * p.Hq + h) * HEAD_DIM);
@@ -611,16 +615,19 @@ __global__ void __launch_bounds__(256, 1)
 }
 
 // Combines the partials of tokens split over several ranges (after
-// decode_range_kernel). One 256-thread block per (token, query head).
-__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
+// decode_range_kernel). One block of 64 NW threads per (token, query head).
+template <int NW>
+__global__ void __launch_bounds__(64 * NW) decode_merge_kernel(DecodeParams p) {
     const int t = blockIdx.x, T = p.T;
     const int o0 = p.offs[t], o1 = p.offs[t + 1];  // offs[T] = W
     if (o1 <= o0) return;
     const int R = p.offs[T + 1];
     const int b0 = o0 / R, b1 = (o1 - 1) / R;
     if (b0 == b1) return;  // finished in place by its range
-    merge_head(p, t, t + b0, 1, b1 - b0 + 1, blockIdx.y);
+    merge_head<NW>(p, t, t + b0, 1, b1 - b0 + 1, blockIdx.y);
 }
+template __global__ void decode_merge_kernel<4>(DecodeParams);
+template __global__ void decode_merge_kernel<16>(DecodeParams);
 
 template __global__ void decode_range_kernel<4, false>(DecodeParams, const int*, const int*, const int*, const int*,
                                                        const int*, const int*);
