@@ -10,25 +10,25 @@
 // (pkv_decode.hip). What changes is the inner loop: an E4M3 page holds half
 // the bytes of a bf16 page, so a wave walks two pages (32 keys, 8 KiB of K
 // and V for its kv head) per step, which keeps the same bytes in flight per
-// wave as the bf16 kernel and the same register footprint:
-//   K: lane (row r = lane / 16, sub s = lane % 16) loads the 16-byte chunk s
-//      (dims 16 s .. 16 s + 15) of keys 4 p + r, p = 0..7 (keys 0..15 from
-//      the first page, 16..31 from the second): 8 loads, each row of 16 lanes
-//      reading one 256-byte key row. The bytes become bf16 pairs
-//      (v_cvt_scalef32_pk_bf16_fp8, exact) and meet q in v_dot2c_f32_bf16.
-//      A reduce-scatter over the 16 lanes of a row (xor 8, xor 7, xor 2,
-//      xor 1) leaves lane s with the scores of key 4 (s / 2) + r for heads
-//      2 (s % 2) and 2 (s % 2) + 1.
-//   softmax: per head over the 8 lanes of a row that share s % 2 (DPP row
-//      rotates by 2, 4, 8) and the 4 rows (two shuffles); exp2 domain.
-//   V: lane (quarter u = lane / 16, chunk c = lane % 16) loads dims
+// wave as the bf16 kernel:
+//   q.k on MFMA: per page S[16 keys][16 columns] in 8 steps of
+//      v_mfma_f32_16x16x32_bf16. Lane (column s = lane % 16, group
+//      r = lane / 16) loads 64 contiguous bytes of key s (dims 16 r + 64 c,
+//      c = 0..3: 4 loads per page) and converts them to bf16 (exact,
+//      v_cvt_scalef32_pk_bf16_fp8) as the A operand; the B operand is query
+//      head s (columns 4..15 zero) over the same dims. The lane ends with the
+//      scores of keys 4 r .. 4 r + 3 of the page for head s.
+//   softmax: per head over the lane's 8 keys and its 4 lane groups (two
+//      shuffles); exp2 domain; kscale / vscale of the unit's 32 keys come
+//      through 256 bytes of LDS (one 4-byte load per lane).
+//   V on VALU: lane (quarter u = lane / 16, chunk c = lane % 16) loads dims
 //      16 c .. 16 c + 15 of keys 8 u .. 8 u + 7 (16 bytes each), converts
-//      them to f32 (v_cvt_pk_f32_fp8) and accumulates 16 dims x 4 heads;
-//      the four quarters are summed at the end of a piece.
-// kscale / vscale of the lane's key are loaded with the K bytes (4 bytes
-// per lane). Keys outside the piece get score -inf and weight 0 by select,
-// and their V bytes are zeroed, so a stale slot (NaN bytes or scales)
-// contributes nothing.
+//      them to f32 (v_cvt_pk_f32_fp8) and accumulates 16 dims x 4 heads with
+//      f32 FMAs of weight x vscale (the reference's f32 products); the four
+//      quarters are summed at the end of a piece.
+// Keys outside the piece get score -inf and weight 0 by select, and their V
+// bytes are zeroed, so a stale slot (NaN bytes or scales) contributes
+// nothing.
 #pragma once
 #include "pkv_decode.hip"
 
@@ -39,6 +39,7 @@ constexpr int UNIT8 = 2 * PAGE;      // keys per step of the E4M3 kernel
 
 struct WaveLds8 {
     float p[UNIT8 * 4];  // weight x vscale, [key][head]
+    float sc[64];        // the unit's kscale [key], then vscale [key]
     float c[4];          // rescale factor per head
     float ml[8];         // final (max, sum) per head
 };
@@ -61,12 +62,19 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     const uint8_t* kc = reinterpret_cast<const uint8_t*>(p.kc);
     const uint8_t* vc = reinterpret_cast<const uint8_t*>(p.vc);
 
-    uint4 qr[G][2];  // q dims 16 sig .. 16 sig + 15 of the group's heads
+    // q.k on MFMA: S[16 keys][16 columns] = K Q^T per page, 8 steps of
+    // v_mfma_f32_16x16x32_bf16 over the 256 dims. Lane (column sig, group
+    // rho) supplies, in step s = 2 c + h, dims 64 c + 16 rho + 8 h .. + 7 of
+    // key sig (A, from the E4M3 bytes) and of query head sig (B; columns
+    // 4..15 are zero), and ends with the scores of keys 4 rho .. 4 rho + 3 of
+    // the page for head sig.
+    bf16x8 qf[8];
+    {
+        const uint16_t* qrow = p.q + ((size_t)t * p.Hq + kvh * G + (sig & 3)) * HEAD_DIM + 16 * rho;
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        const uint16_t* qrow = p.q + ((size_t)t * p.Hq + kvh * G + g) * HEAD_DIM + 16 * sig;
-        qr[g][0] = *reinterpret_cast<const uint4*>(qrow);
-        qr[g][1] = *reinterpret_cast<const uint4*>(qrow + 8);
+        for (int s = 0; s < 8; s++)
+            qf[s] = as_bf16x8(sig < G ? *reinterpret_cast<const uint4*>(qrow + 64 * (s >> 1) + 8 * (s & 1))
+                                      : make_uint4(0, 0, 0, 0));
     }
     const size_t row_bytes = (size_t)Hkv * HEAD_DIM;  // one slot row (all kv heads), bytes
     auto page_id = [&](int pi) -> long {
@@ -79,19 +87,19 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
         pg_a = page_id(2 * u);
         pg_b = UNIT8 * u + PAGE < j1 ? page_id(2 * u + 1) : pg_a;
     };
-    uint4 kb[8], vb[8];
-    float ks, vs;  // scales of this lane's score key
-    const int skey = 4 * (sig >> 1) + rho;  // the key whose scores this lane ends with
+    uint4 kb[2][4], vb[8];
+    float sc_ld;  // kscale (lanes 0..31) or vscale (lanes 32..63) of unit key lane % 32
     auto load_k = [&](long pg_a, long pg_b) {
 #pragma unroll
-        for (int pp = 0; pp < 8; pp++) {
-            const long pg = pp < 4 ? pg_a : pg_b;
-            const int key = (4 * pp + rho) & (PAGE - 1);
-            kb[pp] = load_nt(kc + ((size_t)pg * PAGE + key) * row_bytes + (size_t)kvh * HEAD_DIM + 16 * sig);
+        for (int pg = 0; pg < 2; pg++) {
+            const uint8_t* r = kc + ((size_t)(pg ? pg_b : pg_a) * PAGE + sig) * row_bytes + (size_t)kvh * HEAD_DIM +
+                               16 * rho;
+#pragma unroll
+            for (int c = 0; c < 4; c++) kb[pg][c] = load_nt(r + 64 * c);
         }
-        const size_t at = ((size_t)(skey < PAGE ? pg_a : pg_b) * PAGE + (skey & (PAGE - 1))) * Hkv + kvh;
-        ks = p.kscale[at];
-        vs = p.vscale[at];
+        const int key = lane & 31;
+        const size_t at = ((size_t)(key < PAGE ? pg_a : pg_b) * PAGE + (key & (PAGE - 1))) * Hkv + kvh;
+        sc_ld = (lane < 32 ? p.kscale : p.vscale)[at];
     };
     auto load_v = [&](long pg_a, long pg_b) {
 #pragma unroll
@@ -103,7 +111,7 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
         }
     };
 
-    float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;  // heads 2 (sig & 1) + e
+    float m = -INFINITY, l = 0.f;  // head sig (lanes with sig < 4)
     float acc[G][16];
 #pragma unroll
     for (int g = 0; g < G; g++)
@@ -115,71 +123,54 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
         constexpr bool PREFETCH = decltype(prefetch)::value != 0;
         long na = 0, nb = 0;
         if constexpr (PREFETCH) unit_pages(next_u, na, nb);
-        // q . k partials: v[pp * 4 + g] over this lane's 16 dims.
-        float v[32];
+        f32x4 sacc[2];
 #pragma unroll
-        for (int pp = 0; pp < 8; pp++) {
-            uint4 lo, hi;
-            e4m3x16_to_bf16(kb[pp], lo, hi);
+        for (int pg = 0; pg < 2; pg++) {
+            sacc[pg] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int g = 0; g < G; g++) v[pp * 4 + g] = dot8(qr[g][1], hi, dot8(qr[g][0], lo, 0.f));
+            for (int s = 0; s < 8; s++) {
+                const uint4 w = kb[pg][s >> 1];
+                const bf16x8 a = as_bf16x8((s & 1) ? e4m3x8_to_bf16x8(w.z, w.w) : e4m3x8_to_bf16x8(w.x, w.y));
+                sacc[pg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[s], sacc[pg], 0, 0, 0);
+            }
         }
-        const float ks_u = ks, vs_u = vs;
+        lds.sc[lane] = sc_ld;  // kscale [0, 32), vscale [32, 64) of the unit's keys
         if constexpr (PREFETCH) load_k(na, nb);
-        // Reduce-scatter across the row's 16 lanes: the value index ends up
-        // as 2 sig + e (bit 4 from sig bit 3, .., bit 1 from sig bit 0).
-        {
-            const bool b3 = sig & 8;
+        wave_sync();
+        // Lane (sig, rho): keys 16 pg + 4 rho + i of the unit, head sig.
+        float sc[8], mx = -INFINITY;
 #pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const float keep = b3 ? v[k + 16] : v[k], send = b3 ? v[k] : v[k + 16];
-                v[k] = keep + dpp<DPP_ROW_ROR8>(send);
-            }
-            const bool b2 = sig & 4;
+        for (int pg = 0; pg < 2; pg++) {
+            const float4 ks4 = *reinterpret_cast<const float4*>(&lds.sc[16 * pg + 4 * rho]);
+            const float ks[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float keep = b2 ? v[k + 8] : v[k], send = b2 ? v[k] : v[k + 8];
-                v[k] = keep + dpp<DPP_ROW_HALF_MIRROR>(send);
-            }
-            const bool b1 = sig & 2;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const float keep = b1 ? v[k + 4] : v[k], send = b1 ? v[k] : v[k + 4];
-                v[k] = keep + dpp<DPP_QUAD_XOR2>(send);
-            }
-            const bool b0 = sig & 1;
-#pragma unroll
-            for (int k = 0; k < 2; k++) {
-                const float keep = b0 ? v[k + 2] : v[k], send = b0 ? v[k] : v[k + 2];
-                v[k] = keep + dpp<DPP_QUAD_XOR1>(send);
+            for (int i = 0; i < 4; i++) {
+                const int kpos = UNIT8 * u + 16 * pg + 4 * rho + i;
+                sc[4 * pg + i] = kpos >= j0 && kpos < j1 ? sacc[pg][i] * ks[i] * sl2 : -INFINITY;
+                mx = fmaxf(mx, sc[4 * pg + i]);
             }
         }
-        // Lane (sig, rho): key skey, heads 2 (sig & 1) + e in v[e].
-        const int kpos = UNIT8 * u + skey;
-        const bool in = kpos >= j0 && kpos < j1;
-        const float f = ks_u * sl2;
-        const float sc0 = in ? v[0] * f : -INFINITY, sc1 = in ? v[1] * f : -INFINITY;
-        auto rowmax = [&](float x) {
-            x = fmaxf(x, dpp<DPP_ROW_ROR2>(x));
-            x = fmaxf(x, dpp<DPP_ROW_ROR4>(x));
-            x = fmaxf(x, dpp<DPP_ROW_ROR8>(x));
-            x = fmaxf(x, shfl_xor(x, 16));
-            return fmaxf(x, shfl_xor(x, 32));
-        };
-        const float mn0 = fmaxf(m0, rowmax(sc0)), mn1 = fmaxf(m1, rowmax(sc1));
-        const float c0 = __builtin_amdgcn_exp2f(m0 - mn0), c1 = __builtin_amdgcn_exp2f(m1 - mn1);
-        const float p0 = __builtin_amdgcn_exp2f(sc0 - mn0), p1 = __builtin_amdgcn_exp2f(sc1 - mn1);
-        l0 = l0 * c0 + p0;
-        l1 = l1 * c1 + p1;
-        m0 = mn0;
-        m1 = mn1;
-        const int hb = 2 * (sig & 1);
-        lds.p[skey * G + hb] = in ? p0 * vs_u : 0.f;
-        lds.p[skey * G + hb + 1] = in ? p1 * vs_u : 0.f;
-        if (lane < 2) {
-            lds.c[hb] = c0;
-            lds.c[hb + 1] = c1;
+        mx = fmaxf(mx, shfl_xor(mx, 16));
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float cr_me = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first unit (m = -inf)
+        float psum = 0.f;
+#pragma unroll
+        for (int pg = 0; pg < 2; pg++) {
+            const float4 vs4 = *reinterpret_cast<const float4*>(&lds.sc[32 + 16 * pg + 4 * rho]);
+            const float vs[4] = {vs4.x, vs4.y, vs4.z, vs4.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int kk = 16 * pg + 4 * rho + i;
+                const float pr = __builtin_amdgcn_exp2f(sc[4 * pg + i] - mn);  // 0 for a masked key
+                psum += pr;
+                // a masked key's weight is 0 by select: its vscale may be NaN
+                if (sig < G) lds.p[kk * G + sig] = sc[4 * pg + i] == -INFINITY ? 0.f : pr * vs[i];
+            }
         }
+        l = l * cr_me + psum;
+        m = mn;
+        if (rho == 0 && sig < G) lds.c[sig] = cr_me;
         wave_sync();
         const float4 cr = *reinterpret_cast<const float4*>(lds.c);
         const float cg[4] = {cr.x, cr.y, cr.z, cr.w};
@@ -213,7 +204,7 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
                     for (int g = 0; g < G; g++) acc[g][4 * e4 + i] = fmaf(pg[g], x[i], acc[g][4 * e4 + i]);
             }
         }
-        wave_sync();  // lds.p / lds.c are rewritten for the next unit
+        wave_sync();  // lds.p / lds.c / lds.sc are rewritten for the next unit
         if constexpr (PREFETCH) load_v(na, nb);
     };
     using NONE = std::integral_constant<int, 0>;
@@ -226,17 +217,9 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     }
     for (int u = u0; u < u1; u++) unit(u, u + 1, PF{});
     unit(u1, u1, NONE{});
-    // Totals: a head's sum over the 8 lanes of each row sharing sig & 1 and
-    // the 4 rows; values over the 4 quarters.
-    auto rowsum = [&](float x) {
-        x += dpp<DPP_ROW_ROR2>(x);
-        x += dpp<DPP_ROW_ROR4>(x);
-        x += dpp<DPP_ROW_ROR8>(x);
-        x += shfl_xor(x, 16);
-        return x + shfl_xor(x, 32);
-    };
-    l0 = rowsum(l0);
-    l1 = rowsum(l1);
+    // Totals: a head's sum over its 4 lane groups; values over the 4 quarters.
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
@@ -244,12 +227,9 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
             acc[g][e] += shfl_xor(acc[g][e], 16);
             acc[g][e] += shfl_xor(acc[g][e], 32);
         }
-    if (lane < 2) {
-        const int hb = 2 * lane;
-        lds.ml[2 * hb] = m0;
-        lds.ml[2 * hb + 1] = l0;
-        lds.ml[2 * hb + 2] = m1;
-        lds.ml[2 * hb + 3] = l1;
+    if (lane < G) {
+        lds.ml[2 * lane] = m;
+        lds.ml[2 * lane + 1] = l;
     }
     wave_sync();
     if (lane >= 16) return;
