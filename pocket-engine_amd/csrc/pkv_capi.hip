@@ -53,9 +53,10 @@ thread_local hipEvent_t t_ev_start = nullptr, t_ev_stop = nullptr;
 thread_local hipEvent_t t_pf_start = nullptr, t_pf_stop = nullptr;  // same for the prefill kernel
 
 int decode_n_wg() { return device_cus() * g_wg_per_cu; }
-// The E4M3 decode kernel runs two workgroups per CU (250 VGPRs: two waves
-// per SIMD), so one wave's conversions and FMAs overlap the other's loads
-// (measured at C3: 129-131 us against 130-134 with one).
+// The E4M3 decode kernel runs two workgroups per CU (252 VGPRs and 72.8 KB
+// of LDS each: two waves per SIMD), so one wave's conversions and MFMAs
+// overlap the other's loads (measured at C3: 111-112 us against 117-121
+// with one).
 constexpr int F8_WG_PER_CU = 2;
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }

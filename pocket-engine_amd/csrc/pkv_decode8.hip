@@ -10,7 +10,7 @@
 // (pkv_decode.hip). What changes is the inner loop: an E4M3 page holds half
 // the bytes of a bf16 page, so a wave walks two pages (32 keys, 8 KiB of K
 // and V for its kv head) per step, which keeps the same bytes in flight per
-// wave as the bf16 kernel:
+// wave as the bf16 kernel, and both products run on the matrix cores:
 //   q.k on MFMA: per page S[16 keys][16 columns] in 8 steps of
 //      v_mfma_f32_16x16x32_bf16. Lane (column s = lane % 16, group
 //      r = lane / 16) loads 64 contiguous bytes of key s (dims 16 r + 64 c,
@@ -21,11 +21,13 @@
 //   softmax: per head over the lane's 8 keys and its 4 lane groups (two
 //      shuffles); exp2 domain; kscale / vscale of the unit's 32 keys come
 //      through 256 bytes of LDS (one 4-byte load per lane).
-//   V on VALU: lane (quarter u = lane / 16, chunk c = lane % 16) loads dims
-//      16 c .. 16 c + 15 of keys 8 u .. 8 u + 7 (16 bytes each), converts
-//      them to f32 (v_cvt_pk_f32_fp8) and accumulates 16 dims x 4 heads with
-//      f32 FMAs of weight x vscale (the reference's f32 products); the four
-//      quarters are summed at the end of a piece.
+//   P.V on MFMA: the unit's V bytes are converted to bf16 (exact) into
+//      row-major LDS rows (544 bytes apart), and per page and 16-dim block
+//      O^T[16 dims][16 columns] += V^T P^T as two v_mfma_f32_16x16x16_bf16:
+//      A = V^T through ds_read_b64_tr_b16 (4 x 4 blocks transposed on the
+//      read), B = P^T, which is the score accumulator's own lane layout,
+//      holding weight x vscale as a bf16 high part and a bf16 remainder
+//      (~16 mantissa bits, close to the reference's f32 products).
 // Keys outside the piece get score -inf and weight 0 by select, and their V
 // bytes are zeroed, so a stale slot (NaN bytes or scales) contributes
 // nothing.
@@ -37,11 +39,11 @@ namespace pkv {
 constexpr int DPP_ROW_ROR2 = 0x122;  // lane i <- lane (i + 2) % 16 of its row
 constexpr int UNIT8 = 2 * PAGE;      // keys per step of the E4M3 kernel
 
+constexpr int V8_VSTR = HEAD_DIM + 16;  // u16 per staged V row (544 B: conflict-free transposed reads)
+
 struct WaveLds8 {
-    float p[UNIT8 * 4];  // weight x vscale, [key][head]
-    float sc[64];        // the unit's kscale [key], then vscale [key]
-    float c[4];          // rescale factor per head
-    float ml[8];         // final (max, sum) per head
+    uint16_t v[UNIT8 * V8_VSTR];  // the unit's V rows as bf16, [key][dim]
+    float sc[64];                 // the unit's kscale [key], then vscale [key]
 };
 
 // Sixteen E4M3 bytes to sixteen bf16 (two uint4), exact.
@@ -112,11 +114,14 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     };
 
     float m = -INFINITY, l = 0.f;  // head sig (lanes with sig < 4)
-    float acc[G][16];
+    // O^T[256 dims][16 columns]: lane (sig, rho) holds dims 16 db + 4 rho + i
+    // of column (head) sig in acc[db][i].
+    f32x4 acc[16];
 #pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[g][e] = 0.f;
+    for (int db = 0; db < 16; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // transposed-read address of this lane: key row 4 rho + sig / 4 of a
+    // page, dims 4 (sig % 4) + 16 db
+    const uint16_t* tr = lds.v + (4 * rho + (sig >> 2)) * V8_VSTR + 4 * (sig & 3);
 
     const int u0 = j0 / UNIT8, u1 = (j1 - 1) / UNIT8;
     auto unit = [&](int u, int next_u, auto prefetch) {
@@ -154,58 +159,58 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
         mx = fmaxf(mx, shfl_xor(mx, 32));
         const float mn = fmaxf(m, mx);
         const float cr_me = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first unit (m = -inf)
+        // V rows to LDS as bf16 (exact): row 8 rho + k, dims 16 sig .. + 15;
+        // rows of keys outside [j0, j1) as zeros (a stale slot may hold NaN)
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int row = 8 * rho + k, kp = UNIT8 * u + row;
+            const bool in = kp >= j0 && kp < j1;
+            uint16_t* d = lds.v + row * V8_VSTR + 16 * sig;
+            *reinterpret_cast<uint4*>(d) = in ? e4m3x8_to_bf16x8(vb[k].x, vb[k].y) : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4*>(d + 8) = in ? e4m3x8_to_bf16x8(vb[k].z, vb[k].w) : make_uint4(0, 0, 0, 0);
+        }
+        if constexpr (PREFETCH) load_v(na, nb);
+        // P^T operands: the lane's own weights times vscale, as a bf16 high
+        // part plus a bf16 remainder (two MFMAs: ~16 mantissa bits, where one
+        // bf16 would add 2^-9 relative error per weight to products the
+        // reference keeps in f32); a masked key's weight is 0 by select.
         float psum = 0.f;
+        s16x4 pw_hi[2], pw_lo[2];
 #pragma unroll
         for (int pg = 0; pg < 2; pg++) {
             const float4 vs4 = *reinterpret_cast<const float4*>(&lds.sc[32 + 16 * pg + 4 * rho]);
             const float vs[4] = {vs4.x, vs4.y, vs4.z, vs4.w};
+            float w[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int kk = 16 * pg + 4 * rho + i;
                 const float pr = __builtin_amdgcn_exp2f(sc[4 * pg + i] - mn);  // 0 for a masked key
                 psum += pr;
-                // a masked key's weight is 0 by select: its vscale may be NaN
-                if (sig < G) lds.p[kk * G + sig] = sc[4 * pg + i] == -INFINITY ? 0.f : pr * vs[i];
+                w[i] = sc[4 * pg + i] == -INFINITY ? 0.f : pr * vs[i];
             }
+            const uint32_t h01 = pack2_hw(w[0], w[1]), h23 = pack2_hw(w[2], w[3]);
+            const uint32_t r01 = pack2_hw(w[0] - bf_lo(h01), w[1] - bf_hi(h01));
+            const uint32_t r23 = pack2_hw(w[2] - bf_lo(h23), w[3] - bf_hi(h23));
+            pw_hi[pg] = __builtin_bit_cast(s16x4, make_uint2(h01, h23));
+            pw_lo[pg] = __builtin_bit_cast(s16x4, make_uint2(r01, r23));
         }
         l = l * cr_me + psum;
         m = mn;
-        if (rho == 0 && sig < G) lds.c[sig] = cr_me;
-        wave_sync();
-        const float4 cr = *reinterpret_cast<const float4*>(lds.c);
-        const float cg[4] = {cr.x, cr.y, cr.z, cr.w};
-        if (__any(cr.x != 1.f || cr.y != 1.f || cr.z != 1.f || cr.w != 1.f)) {
+        if (__any(cr_me != 1.f)) {
 #pragma unroll
-            for (int g = 0; g < G; g++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) acc[g][e] *= cg[g];
+            for (int db = 0; db < 16; db++) acc[db] *= cr_me;
         }
-        // V bytes of keys outside [j0, j1) (a partial unit) are zeroed.
-        if (UNIT8 * u < j0 || UNIT8 * u + UNIT8 > j1) {
+        wave_sync();  // V staged
+        typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int kp = UNIT8 * u + 8 * rho + k;
-                if (kp < j0 || kp >= j1) vb[k] = make_uint4(0, 0, 0, 0);
+        for (int pg = 0; pg < 2; pg++)
+#pragma unroll
+            for (int db = 0; db < 16; db++) {
+                const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(tr + pg * PAGE * V8_VSTR + 16 * db));
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pw_hi[pg], acc[db], 0, 0, 0);
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pw_lo[pg], acc[db], 0, 0, 0);
             }
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float4 pk = *reinterpret_cast<const float4*>(&lds.p[(8 * rho + k) * G]);
-            const float pg[4] = {pk.x, pk.y, pk.z, pk.w};
-            const uint32_t w[4] = {vb[k].x, vb[k].y, vb[k].z, vb[k].w};
-#pragma unroll
-            for (int e4 = 0; e4 < 4; e4++) {
-                const f32x2 x01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[e4], false);
-                const f32x2 x23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[e4], true);
-                const float x[4] = {x01.x, x01.y, x23.x, x23.y};
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int g = 0; g < G; g++) acc[g][4 * e4 + i] = fmaf(pg[g], x[i], acc[g][4 * e4 + i]);
-            }
-        }
-        wave_sync();  // lds.p / lds.c / lds.sc are rewritten for the next unit
-        if constexpr (PREFETCH) load_v(na, nb);
+        wave_sync();  // lds.v / lds.sc are rewritten for the next unit
     };
     using NONE = std::integral_constant<int, 0>;
     using PF = std::integral_constant<int, 1>;
@@ -217,34 +222,41 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     }
     for (int u = u0; u < u1; u++) unit(u, u + 1, PF{});
     unit(u1, u1, NONE{});
-    // Totals: a head's sum over its 4 lane groups; values over the 4 quarters.
+    // Totals: a head's sum over its 4 lane groups.
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            acc[g][e] += shfl_xor(acc[g][e], 16);
-            acc[g][e] += shfl_xor(acc[g][e], 32);
-        }
-    if (lane < G) {
-        lds.ml[2 * lane] = m;
-        lds.ml[2 * lane + 1] = l;
-    }
-    wave_sync();
-    if (lane >= 16) return;
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        float a[8], b[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            a[e] = acc[g][e];
-            b[e] = acc[g][8 + e];
-        }
-        epi(g, a, lds.ml[2 * g], lds.ml[2 * g + 1], 2 * sig);
-        epi(g, b, lds.ml[2 * g], lds.ml[2 * g + 1], 2 * sig + 1);
-    }
+    if (sig < G) epi(sig, rho, acc, m, l);
 }
+
+// Writes a piece's result for the lanes of head g of the group (dims
+// 16 db + 4 gq + i in acc[db][i]): the gated output when the piece holds
+// all of the token's keys, else the partial record at index idx.
+struct DecodeEpi8 {
+    const DecodeParams& p;
+    int t, kvh, idx;
+    bool direct;
+    __device__ __forceinline__ void operator()(int g, int gq, const f32x4 (&acc)[16], float m, float l) const {
+        const int h = kvh * 4 + g;
+        if (direct) {
+            const float inv = 1.f / l;
+            const uint16_t* gate = p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + 4 * gq;
+            uint16_t* o = p.out + ((size_t)t * p.Hq + h) * HEAD_DIM + 4 * gq;
+#pragma unroll
+            for (int db = 0; db < 16; db++) {
+                const uint2 graw = *reinterpret_cast<const uint2*>(gate + 16 * db);
+                *reinterpret_cast<uint2*>(o + 16 * db) =
+                    gate4(acc[db][0], acc[db][1], acc[db][2], acc[db][3], inv, graw);
+            }
+        } else {
+            const size_t row = (size_t)idx * p.Hq + h;
+            float* pa = p.part_acc + row * HEAD_DIM + 4 * gq;
+#pragma unroll
+            for (int db = 0; db < 16; db++)
+                *reinterpret_cast<float4*>(pa + 16 * db) = make_float4(acc[db][0], acc[db][1], acc[db][2], acc[db][3]);
+            if (gq == 0) *reinterpret_cast<float2*>(p.part_ms + row * 2) = make_float2(m, l);
+        }
+    }
+};
 
 // Key-range kernel over the E4M3 cache: decode_range_kernel<4, false>'s
 // ranges and records with piece_body8 inside. Grid (n_wg, ceil(Hkv / 4)),
@@ -280,7 +292,7 @@ __global__ void __launch_bounds__(256, 2)
         if (L > 0) {
             const int j0 = max(start, off) - off, j1 = min(end, off + L) - off;
             const int seq = __builtin_amdgcn_readfirstlane(tab ? sh_seq[t] : tok_seq[t]);
-            const DecodeEpi<4> epi{p, t, kvh, t + b, j0 == 0 && j1 == L};
+            const DecodeEpi8 epi{p, t, kvh, t + b, j0 == 0 && j1 == L};
             piece_body8(p, block_table + (size_t)seq * p.max_blocks, sh_w[wave], t, kvh, j0, j1, epi);
             off += L;
         }
