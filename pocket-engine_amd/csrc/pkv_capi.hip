@@ -396,10 +396,15 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
         return launch_status();
     }
     if (phases & 2) {
-        // fewer (token, head) blocks than CUs: 16 waves per block, so a
-        // head's records (up to one per range) load in one round
+        // Waves per (token, head) block: 16 when there are fewer blocks than
+        // CUs (a head's records, up to one per range, load in one round);
+        // one when a token has at most 8 records on average ((T + n_wg) / T:
+        // one wave folds 16 per round and skips the cross-wave combine);
+        // else 4. Any count is correct; this only picks the faster launch.
         if ((int64_t)T * Hq < device_cus())
             hipLaunchKernelGGL(pkv::decode_merge_kernel<16>, dim3(T, Hq), dim3(1024), 0, (hipStream_t)stream, p);
+        else if ((int64_t)T + n_wg <= 8 * (int64_t)T)
+            hipLaunchKernelGGL(pkv::decode_merge_kernel<1>, dim3(T, Hq), dim3(64), 0, (hipStream_t)stream, p);
         else
             hipLaunchKernelGGL(pkv::decode_merge_kernel<4>, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p);
         return launch_status();

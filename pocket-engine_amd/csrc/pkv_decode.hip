@@ -126,9 +126,9 @@ __device__ __forceinline__ uint2 gate4(float a0, float a1, float a2, float a3, f
 // threads: wave w folds records w, w + NW, .. into a running (max, sum,
 // values) with U records in flight per lane (4 dims per lane; U = 16, or 10
 // for NW = 16 within its 128 VGPRs), then the NW waves' results are combined
-// through LDS. Every thread reaches the sync. (NW = 16 folds up to 160
-// records in one round of loads: launches with few (row, head) blocks and
-// many records each.)
+// through LDS (NW = 1: written straight from the wave). Every thread
+// reaches the sync. (NW = 16 folds up to 160 records in one round of loads:
+// launches with few (row, head) blocks and many records each.)
 template <int NW = 4, class MsAt, class AccAt>
 __device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccAt acc_at, const uint16_t* gate,
                                            uint16_t* out) {
@@ -173,6 +173,15 @@ __device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccA
             A2 += au[u].z * f;
             A3 += au[u].w * f;
         }
+    }
+    if constexpr (NW == 1) {
+        // one wave: its own fold is the result (the same arithmetic as the
+        // combine below with a single term)
+        const float f = M == -INFINITY ? 0.f : 1.f;
+        const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
+        *reinterpret_cast<uint2*>(out + d) = gate4(0.f + A0 * f, 0.f + A1 * f, 0.f + A2 * f, 0.f + A3 * f,
+                                                   1.f / (0.f + S * f), graw);
+        return;
     }
     *reinterpret_cast<float4*>(&sh_a[w][d]) = make_float4(A0, A1, A2, A3);
     if (lane == 0) {
@@ -626,6 +635,7 @@ __global__ void __launch_bounds__(64 * NW) decode_merge_kernel(DecodeParams p) {
     if (b0 == b1) return;  // finished in place by its range
     merge_head<NW>(p, t, t + b0, 1, b1 - b0 + 1, blockIdx.y);
 }
+template __global__ void decode_merge_kernel<1>(DecodeParams);
 template __global__ void decode_merge_kernel<4>(DecodeParams);
 template __global__ void decode_merge_kernel<16>(DecodeParams);
 
