@@ -36,8 +36,7 @@
 
 namespace pkv {
 
-constexpr int DPP_ROW_ROR2 = 0x122;  // lane i <- lane (i + 2) % 16 of its row
-constexpr int UNIT8 = 2 * PAGE;      // keys per step of the E4M3 kernel
+constexpr int UNIT8 = 2 * PAGE;  // keys per step of the E4M3 kernel
 
 constexpr int V8_VSTR = HEAD_DIM + 16;  // u16 per staged V row (544 B: conflict-free transposed reads)
 
@@ -46,14 +45,9 @@ struct WaveLds8 {
     float sc[64];                 // the unit's kscale [key], then vscale [key]
 };
 
-// Sixteen E4M3 bytes to sixteen bf16 (two uint4), exact.
-__device__ __forceinline__ void e4m3x16_to_bf16(const uint4& b, uint4& lo, uint4& hi) {
-    lo = e4m3x8_to_bf16x8(b.x, b.y);
-    hi = e4m3x8_to_bf16x8(b.z, b.w);
-}
-
 // One wave: token t, kv head kvh, keys [j0, j1) of its sequence (block
-// table row bt), over the E4M3 cache. Results go to epi as in piece_body.
+// table row bt), over the E4M3 cache. Results go to epi(g, gq, acc, m, l) on
+// the lanes of head g (DecodeEpi8).
 template <class Epi>
 __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __restrict__ bt, WaveLds8& lds, int t,
                                             int kvh, int j0, int j1, Epi epi) {
