@@ -112,7 +112,36 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
     if (blockDim.x != 256 || block_size != PAGE || Hq != G * Hkv || (kscale != nullptr) != F8 ||
         (vscale != nullptr) != F8)
         return;
-    const int t = blockIdx.x, kvh = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
+    const int tid = threadIdx.x;
+    // Work item of this workgroup. The grid is the reference's (token, kv
+    // head, range) and so is each item's result slot, but which workgroup
+    // computes which item is free: with up to 256 tokens the k-th workgroup
+    // in dispatch order (x fastest, then y, then z) takes the k-th item in
+    // order of decreasing context (longest tokens first, each token's
+    // ranges and kv heads together), so the long items do not start last.
+    int t = blockIdx.x, kvh = blockIdx.y, z = blockIdx.z;
+    if (gridDim.x <= 256) {
+        __shared__ int sh_len[256], sh_order[256];
+        const int T = gridDim.x;
+        if (tid < T) sh_len[tid] = pos[tid];
+        __syncthreads();
+        if (tid < T) {
+            const int mine = sh_len[tid];
+            int rank = 0;
+            for (int u = 0; u < T; u++) {
+                const int o = sh_len[u];
+                rank += o > mine || (o == mine && u < tid);
+            }
+            sh_order[rank] = tid;
+        }
+        __syncthreads();
+        const int per = gridDim.y * gridDim.z;
+        const int k = blockIdx.x + T * (blockIdx.y + gridDim.y * blockIdx.z);
+        const int rem = k % per;
+        t = sh_order[k / per];
+        z = rem / gridDim.y;
+        kvh = rem % gridDim.y;
+    }
     const int sq = tok_seq[t];
     if (ref_prompt_row(skip_prompts, cu, sq, outs, spec)) return;
     const int L = pos[t] + 1;

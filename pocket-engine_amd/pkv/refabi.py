@@ -11,7 +11,10 @@ import os
 
 import torch  # noqa: F401  (the HIP runtime this process already uses)
 
-HSACO = os.path.join(os.path.dirname(os.path.abspath(__file__)), "pkv_kernels.hsaco")
+# PKV_KERNELS selects another build of the code object, as POCKET_KERNELS
+# does for the reference engine (src/gpu.rs:451-457).
+HSACO = os.environ.get("PKV_KERNELS") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                      "pkv_kernels.hsaco")
 HEAD_DIM = 256
 SPLIT_MIN_KEYS = 64   # model.rs:26 (ROCm)
 SPLIT_MAX = 64        # model.rs:38
