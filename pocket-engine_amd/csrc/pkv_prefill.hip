@@ -102,12 +102,24 @@ constexpr int PF_IDS_BYTES = (PF_THREADS / 64) * 4 * 4 * 4;
 constexpr size_t prefill_smem_bytes(int nst = PF_NST) { return (size_t)nst * PF_STAGE * 2 + PF_IDS_BYTES; }
 
 // The query tile of this workgroup among the prompt sequences: tile
-// blockIdx.x of the concatenated BQ-query tiles of the prompt sequences
-// (sequences of more than one row that do not verify drafts). Returns false
-// if the grid has more blocks than tiles.
+// total - 1 - blockIdx.x of the concatenated BQ-query tiles of the prompt
+// sequences (sequences of more than one row that do not verify drafts).
+// Returns false if the grid has more blocks than tiles.
 template <int BQ>
 __device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s, int& tb, int& nb) {
+    // Tiles are taken last first: a sequence's later tiles attend more keys,
+    // so the longest work is dispatched first and the short tiles fill the
+    // tail.
     int tile = blockIdx.x;
+    {
+        int total = 0;
+        for (int i = 0; i < p.seqs; i++) {
+            const int n = p.cu[i + 1] - p.cu[i];
+            if (n > 1 && !is_spec(p.outs, p.spec, i)) total += (n + BQ - 1) / BQ;
+        }
+        if (tile >= total) return false;
+        tile = total - 1 - tile;
+    }
     s = -1;
     for (int i = 0; i < p.seqs; i++) {
         const int n = p.cu[i + 1] - p.cu[i];
