@@ -392,8 +392,26 @@ def bench_prefill(args):
     stream = torch.cuda.current_stream()
     evs = HipEvents(args.steps)
 
+    if args.refabi:
+        # the code object's prompt kernel, launched as the reference engine
+        # launches it on gfx950 (fa_shape's attn_groupr_g4_t2_k32, model.rs:
+        # 2438-2493); timed with events recorded around the launch
+        from pkv import refabi
+        from pkv.refabi import F, I, P as Pa
+        rk = refabi.RefKernels()
+        fname, fgrid, fthreads, fsmem = refabi.flash_launch(T, B, Hkv)
+        fargs = [Pa(q), Pa(kc), Pa(vc), Pa(None), Pa(None), Pa(qkv), I(qstride), I(Hq), I(Hkv), Pa(pos_d), Pa(cu_d),
+                 I(B), Pa(bt_d), I(pp + cp), I(BS), Pa(out), F(1 / 16), Pa(None), I(1)]
+
     def step(ev=None):
         pkv.append(k_rows, v_rows, qstride * 2, slot_d, T, Hkv, D * 2, kc, vc, pages * BS)
+        if args.refabi:
+            if ev:
+                evs.record(ev[0], stream.cuda_stream)
+            rk.launch(fname, fgrid, fthreads, fsmem, fargs)
+            if ev:
+                evs.record(ev[1], stream.cuda_stream)
+            return
         if ev:
             pkv.time_next_prefill_kernel(ev[0], ev[1])
         pkv.attn_prefill(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d, cu_d, B, bt_d, pp + cp, BS, out, 1 / 16, None, 1,
@@ -429,13 +447,13 @@ def bench_prefill(args):
         "config": {"workload": "c4: 8 seqs x 2048-token chunk over a shared 16,384-token prefix (append + prefill)",
                    "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS, "flop_per_step": flops,
                    "seed": seed, "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "prefill_kernel", "achieved": round(tflops, 1),
+        "roofline": {"bound": "mfma", "kernel": (f"{fname} (reference ABI, events around the launch)" if args.refabi
+                                                  else "prefill_kernel"), "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "avg_us": round(kern_us, 1), "traffic": None,
-                     "traffic_profiled": {"source": "profiles/prefill_c4_shared_prefix.md (rocprofv3 --pmc, "
-                                                    "copy-calibrated, seed 1)",
-                                          "read_bytes": 1.34e9, "write_bytes": 138e6,
-                                          "note": "MFMA-bound: 0.30 TB/s of HBM"}},
+                     "traffic_profiled": None if args.refabi else {
+                         "source": "profiles/prefill_c4_shared_prefix.md (rocprofv3 --pmc, copy-calibrated, seed 1)",
+                         "read_bytes": 1.34e9, "write_bytes": 138e6, "note": "MFMA-bound: 0.30 TB/s of HBM"}},
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)

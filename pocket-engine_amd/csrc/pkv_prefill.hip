@@ -80,7 +80,10 @@ __device__ __forceinline__ constexpr int pf_key_of_row(int r) { return (r & 7) +
 __device__ __forceinline__ constexpr int pf_row_of_key(int j) { return (j & 7) + 8 * ((j >> 4) & 1) + 16 * ((j >> 3) & 1); }
 // Element offset of row r (0..31) of a K or V tile.
 __device__ __forceinline__ constexpr int pf_krow(int r) { return (r & 15) * PF_KPAIR + (r >> 4) * HEAD_DIM; }
-__device__ __forceinline__ constexpr int pf_vrow(int r) { return (r & 15) * PF_VPAIR + (r >> 4) * HEAD_DIM; }
+template <int VP = PF_VPAIR>
+__device__ __forceinline__ constexpr int pf_vrow(int r) { return (r & 15) * VP + (r >> 4) * HEAD_DIM; }
+// Elements of one K + V stage with V pairs VP elements apart.
+__host__ __device__ constexpr int pf_stage(int vp) { return PF_K_ELEMS + 16 * vp; }
 
 // Query positions per workgroup (BQ) and 32-query blocks per wave (NQB):
 // waves = 4 query heads x BQ / (32 NQB). NQB = 2 feeds every K / V^T
@@ -142,12 +145,12 @@ __device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s
 // THREADS / 32 keys. F8: an E4M3 cache, dequantised while
 // the tiles load as the reference's attn_group8 does (qwen35.cu:1424-1436):
 // K' = bf16(k * kscale), V' = bf16(v * vscale); the rest is unchanged.
-template <int BQ, int NQB, bool F8, bool UPAGE, int NST, bool DMA>
+template <int BQ, int NQB, bool F8, bool UPAGE, int NST, bool DMA, int VP = PF_VPAIR>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb) {
     constexpr int THREADS = pf_threads(BQ, NQB);
     static_assert(PF_BK * HEAD_DIM / 8 % THREADS == 0, "whole 16-byte chunks per thread");
     // Buffer b: K tile at pf_smem + b * STAGE, V tile right after it.
-    constexpr int STAGE = PF_STAGE;
+    constexpr int STAGE = pf_stage(VP);
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31,
               lh = lane >> 5;
     const int kvh = blockIdx.y;
@@ -285,7 +288,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         for (int u = 0; u < NCH; u++) {
             const int r = pf_row_of_key(u * KPU + kl0);
             *reinterpret_cast<uint4*>(sk + pf_krow(r) + c8) = kr[u];
-            *reinterpret_cast<uint4*>(sv + pf_vrow(r) + c8) = vr[u];
+            *reinterpret_cast<uint4*>(sv + pf_vrow<VP>(r) + c8) = vr[u];
         }
     };
     // V^T fragments (A operand of O^T += V^T P^T, dims 32 db + lq, keys
@@ -294,7 +297,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     // element i % 4 of what lane i / 4 + 4 e read, so lane s of the group
     // reads row 16 kk + 8 h + 4 lh + s / 4, dims 32 db + 16 (group & 1) +
     // 4 (s % 4) (row 16 kk + x sits at pf_vrow(x) + 256 kk).
-    const int tr_at = (4 * lh + ((lane & 15) >> 2)) * PF_VPAIR + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int tr_at = (4 * lh + ((lane & 15) >> 2)) * VP + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     const int ntiles = (L + PF_BK - 1) / PF_BK;
     // Tile k0 from stage buf: S^T, online softmax, O^T update.
@@ -371,7 +374,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                         (lds_s16x4*)(vtr + 256 * kk + 32 * db));
                     const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_s16x4*)(vtr + 8 * PF_VPAIR + 256 * kk + 32 * db));
+                        (lds_s16x4*)(vtr + 8 * VP + 256 * kk + 32 * db));
                     const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
                     for (int qb = 0; qb < NQB; qb++)
@@ -390,7 +393,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         // or more on this path) and reads their page ids from its own 4-slot
         // ring, filled 4 tiles ahead by its own DMA, so the loop issues no
         // other vector memory reads.
-        static_assert(!F8 && UPAGE && NST == 3 && THREADS == PF_THREADS, "bf16, 16-key pages, 3 stages");
+        static_assert(!F8 && UPAGE, "bf16, 16-key pages");
         constexpr int NPW = 16 / (THREADS / 64);  // pairs per wave (2 with 8 waves, 4 with 4)
         static_assert(NPW <= 4, "page-id ring slots hold 4 ids");
         int* ring = reinterpret_cast<int*>(pf_smem + NST * STAGE) + wave * 16;
@@ -415,7 +418,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                 pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
                 const size_t slot_at = (((size_t)pg << bs_log2) + (kp & bs_mask)) * row;  // uniform
                 dma16_s(p.kc + slot_at, lane_off, lds_addr(st + pf_krow(r)));
-                dma16_s(p.vc + slot_at, lane_off, lds_addr(st + PF_K_ELEMS + pf_vrow(r)));
+                dma16_s(p.vc + slot_at, lane_off, lds_addr(st + PF_K_ELEMS + pf_vrow<VP>(r)));
             }
         };
         // V rows of keys at or past L (partial last tile) read stale slots:
@@ -427,7 +430,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             for (int j = 0; j < NPW; j++) {
                 const int r = NPW * wave + j + 16 * hi;
                 if (k0 + pf_key_of_row(r) >= L)
-                    *reinterpret_cast<uint4*>(pf_smem + buf * STAGE + PF_K_ELEMS + pf_vrow(r) + 8 * (lane & 31)) =
+                    *reinterpret_cast<uint4*>(pf_smem + buf * STAGE + PF_K_ELEMS + pf_vrow<VP>(r) + 8 * (lane & 31)) =
                         make_uint4(0, 0, 0, 0);
             }
         };
@@ -436,6 +439,30 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             if (t < ntiles) dma_ids(t * PF_BK, t);
         wait_vm<0>();
         dma_tile(0, 0, 0);
+        if constexpr (NST == 2) {
+            // Two stages: iteration i requests tile i + 1 into the stage the
+            // barrier that ended iteration i - 1 freed (and the page ids of
+            // tile i + 4), computes tile i, waits for its own DMA of tile
+            // i + 1, then one barrier publishes it: one tile of lead.
+            wait_vm<0>();
+            zero_tail(0, 0);
+            __syncthreads();
+            int buf = 0;
+            for (int it = 0; it < ntiles; it++) {
+                const int k0 = it * PF_BK;
+                const bool more1 = it + 1 < ntiles, more4 = it + 4 < ntiles;
+                if (more1) dma_tile(k0 + PF_BK, buf ^ 1, (it + 1) & 3);
+                if (more4) dma_ids(k0 + 4 * PF_BK, it & 3);
+                compute(buf, k0);
+                if (more1) {
+                    if (more4) wait_vm<1>();
+                    else wait_vm<0>();
+                    buf ^= 1;
+                    zero_tail(k0 + PF_BK, buf);
+                    __syncthreads();
+                }
+            }
+        } else {
         if (ntiles > 1) {
             dma_tile(PF_BK, 1, 1);
             wait_vm<2 * NPW>();
@@ -460,6 +487,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                 zero_tail(k0 + PF_BK, buf);
                 __syncthreads();
             }
+        }
         }
     } else {
     if constexpr (UPAGE) fetch_ids(0);
@@ -518,7 +546,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     }
 }
 
-template <int BQ, int NQB, bool F8 = false, int NST = PF_NST>
+template <int BQ, int NQB, bool F8 = false, int NST = PF_NST, int VP = PF_VPAIR>
 __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
     int s, tb, nb;
     if (!find_prefill_tile<BQ>(p, s, tb, nb)) return;
@@ -526,13 +554,13 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* p
     // DMA; otherwise through
     // registers, with uniform page ids per chunk when pages hold at least
     // THREADS / 32 keys.
-    constexpr bool DMA = !F8 && NST == 3 && pf_threads(BQ, NQB) == PF_THREADS;
+    constexpr bool DMA = !F8;
     if (DMA && p.bs_log2 >= 4)
-        prefill_tile<BQ, NQB, F8, true, NST, DMA>(p, pf_smem, s, tb, nb);
+        prefill_tile<BQ, NQB, F8, true, NST, DMA, VP>(p, pf_smem, s, tb, nb);
     else if (p.bs_log2 >= __builtin_ctz(pf_threads(BQ, NQB) / 32))
-        prefill_tile<BQ, NQB, F8, true, NST, false>(p, pf_smem, s, tb, nb);
+        prefill_tile<BQ, NQB, F8, true, NST, false, VP>(p, pf_smem, s, tb, nb);
     else
-        prefill_tile<BQ, NQB, F8, false, NST, false>(p, pf_smem, s, tb, nb);
+        prefill_tile<BQ, NQB, F8, false, NST, false, VP>(p, pf_smem, s, tb, nb);
 }
 
 __global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {

@@ -289,15 +289,42 @@ namespace pkv {
 
 // The prompt kernel on a grid of 32-query tiles (BQ = 32: one workgroup per
 // tile; BQ = 64: one per two tiles, the other blocks of the grid exit).
-// Stages in static LDS (the launch's dynamic shared memory is not used, but
-// it is still allocated: up to 67,584 bytes for attn_groupr, so the static
-// part stays at two stages, 70,656 bytes, within the CU's 160 KiB).
+// Tiles load by LDS DMA into two stages (one barrier per tile, one tile of
+// lead) with each wave's page-id ring after them.
+// BQ = 32 (attn_groupr, 4 waves): the stages and rings live in the launch's
+// dynamic shared memory (the engine asks for 67,584 bytes; two stages with
+// V pairs 1,056 bytes apart and 4 rings take 67,328) and nothing is static,
+// so two workgroups fit a CU (2 x 67,584 of its 160 KiB) at up to 256
+// VGPRs: 8 waves per CU. A launch with less dynamic memory (the dispatch
+// packet's group segment size) does nothing, like one with another block
+// size. BQ = 64 (attn_mfma, 8 waves): two stages of the default layout and
+// 8 rings in static LDS (68,608 bytes beside the launch's 37,376 dynamic
+// ones).
+constexpr int REF_VP32 = 528;  // V pair stride of the BQ = 32 stages (elements)
+constexpr uint32_t REF_SMEM32 = 2u * pf_stage(REF_VP32) * 2u + 4u * 64u;  // bytes the BQ = 32 path uses
+
+template <int BQ>
+__device__ __forceinline__ uint16_t* flash_stages() {
+    if constexpr (BQ == 32) {
+        extern __shared__ __align__(16) uint16_t dyn_sm[];
+        return dyn_sm;
+    } else {
+        __shared__ __align__(16) uint16_t sm[2 * PF_STAGE + PF_IDS_BYTES / 2];
+        return sm;
+    }
+}
+
 template <int BQ>
 __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
-    __shared__ __align__(16) uint16_t sm[2 * PF_STAGE];
+    uint16_t* sm = flash_stages<BQ>();
     if ((int)blockDim.x != pf_threads(BQ, 1) || Hq != 4 * Hkv || kscale || vscale || block_size <= 0 ||
         (block_size & (block_size - 1)))
         return;
+    if constexpr (BQ == 32) {
+        // hsa_kernel_dispatch_packet_t::group_segment_size (byte offset 28)
+        const uint32_t group_bytes = reinterpret_cast<const uint32_t*>(__builtin_amdgcn_dispatch_ptr())[7];
+        if (group_bytes < REF_SMEM32) return;
+    }
     PrefillParams p;
     p.q = q;
     p.kc = (const uint16_t*)kcache;
@@ -320,12 +347,12 @@ __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
     p.num_blocks = REF_NO_CLAMP;
     p.kscale = nullptr;
     p.vscale = nullptr;
-    prefill_body<BQ, 1, false, 2>(p, sm);
+    prefill_body<BQ, 1, false, 2, BQ == 32 ? REF_VP32 : PF_VPAIR>(p, sm);
 }
 
 }  // namespace pkv
 
-extern "C" __global__ void __launch_bounds__(256, 1) attn_groupr_g4_t2_k32(PKV_FLASH_ARGS) {
+extern "C" __global__ void __launch_bounds__(256, 2) attn_groupr_g4_t2_k32(PKV_FLASH_ARGS) {
     pkv::flash_ref<32>(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
                        max_blocks, block_size, out, scale, outs, spec);
 }

@@ -126,3 +126,9 @@ def test_reference_prompt_kernels_fit_lds(tmp_path):
         name, _, _, smem = refabi.flash_launch(100, 3, 4, **kw)
         assert name in static, (name, sorted(static))
         assert static[name] + smem <= 160 * 1024, (name, static[name], smem)
+    # attn_groupr keeps its two K / V stages (K pairs 1,040 B, V pairs 1,056 B
+    # apart, 16 pairs each) and 4 page-id rings of 64 B in the engine's
+    # dynamic allocation, with no static LDS: two workgroups per CU
+    name, _, _, smem = refabi.flash_launch(100, 3, 4)
+    assert static[name] == 0 and 2 * smem <= 160 * 1024, (static[name], smem)
+    assert smem >= 2 * (16 * 1040 + 16 * 1056) + 4 * 64, smem
