@@ -370,8 +370,19 @@ def bench_prefill(args):
     pages = pp + B * cp + 8
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    kc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
-    vc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    e4m3 = args.kv == "e4m3"
+    if e4m3:
+        # random E4M3 bytes (NaN codes replaced), scales amax/448-like; the
+        # step is the prefill kernel alone (no bf16 append into this cache)
+        kc = torch.randint(0, 256, (pages * BS, Hkv, D), device=dev, generator=gen, dtype=torch.int32).to(torch.uint8)
+        vc = torch.randint(0, 256, (pages * BS, Hkv, D), device=dev, generator=gen, dtype=torch.int32).to(torch.uint8)
+        for t_ in (kc, vc):
+            t_[(t_ & 0x7F) == 0x7F] = 0x7E
+        kscale = torch.rand(pages * BS, Hkv, device=dev, generator=gen) * 0.004 + 0.001
+        vscale = torch.rand(pages * BS, Hkv, device=dev, generator=gen) * 0.004 + 0.001
+    else:
+        kc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+        vc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
     rng = np.random.default_rng(seed)
     perm = rng.permutation(pages).astype(np.int32)
     bt = np.zeros((B, pp + cp), np.int32)
@@ -399,12 +410,13 @@ def bench_prefill(args):
         from pkv import refabi
         from pkv.refabi import F, I, P as Pa
         rk = refabi.RefKernels()
-        fname, fgrid, fthreads, fsmem = refabi.flash_launch(T, B, Hkv)
-        fargs = [Pa(q), Pa(kc), Pa(vc), Pa(None), Pa(None), Pa(qkv), I(qstride), I(Hq), I(Hkv), Pa(pos_d), Pa(cu_d),
+        fname, fgrid, fthreads, fsmem = refabi.flash_launch(T, B, Hkv, fp8=e4m3)
+        fargs = [Pa(q), Pa(kc), Pa(vc), Pa(kscale if e4m3 else None), Pa(vscale if e4m3 else None), Pa(qkv), I(qstride), I(Hq), I(Hkv), Pa(pos_d), Pa(cu_d),
                  I(B), Pa(bt_d), I(pp + cp), I(BS), Pa(out), F(1 / 16), Pa(None), I(1)]
 
     def step(ev=None):
-        pkv.append(k_rows, v_rows, qstride * 2, slot_d, T, Hkv, D * 2, kc, vc, pages * BS)
+        if not e4m3:
+            pkv.append(k_rows, v_rows, qstride * 2, slot_d, T, Hkv, D * 2, kc, vc, pages * BS)
         if args.refabi:
             if ev:
                 evs.record(ev[0], stream.cuda_stream)
@@ -414,6 +426,10 @@ def bench_prefill(args):
             return
         if ev:
             pkv.time_next_prefill_kernel(ev[0], ev[1])
+        if e4m3:
+            pkv.attn_prefill_e4m3(q, kc, vc, kscale, vscale, qkv, qstride, Hq, Hkv, pos_d, cu_d, B, bt_d, pp + cp, BS,
+                                  out, 1 / 16, None, 1, T, pages)
+            return
         pkv.attn_prefill(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d, cu_d, B, bt_d, pp + cp, BS, out, 1 / 16, None, 1,
                          T, pages)
 
@@ -445,13 +461,14 @@ def bench_prefill(args):
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1)*0.5)",
         "config": {"workload": "c4: 8 seqs x 2048-token chunk over a shared 16,384-token prefix (append + prefill)",
-                   "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS, "flop_per_step": flops,
+                   "kv": args.kv, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS, "flop_per_step": flops,
                    "seed": seed, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": (f"{fname} (reference ABI, events around the launch)" if args.refabi
-                                                  else "prefill_kernel"), "achieved": round(tflops, 1),
+                                                  else "prefill_e4m3_kernel" if e4m3 else "prefill_kernel"),
+                     "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "avg_us": round(kern_us, 1), "traffic": None,
-                     "traffic_profiled": None if args.refabi else {
+                     "traffic_profiled": None if args.refabi or e4m3 else {
                          "source": "profiles/prefill_c4_shared_prefix.md (rocprofv3 --pmc, copy-calibrated, seed 1)",
                          "read_bytes": 1.34e9, "write_bytes": 138e6, "note": "MFMA-bound: 0.30 TB/s of HBM"}},
         "cpu_baseline": None,

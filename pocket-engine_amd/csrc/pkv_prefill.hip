@@ -209,6 +209,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     constexpr int NCH = PF_BK / KPU;
     const int kl0 = tid >> 5, c8 = (tid & 31) * 8;
     uint4 kr[NCH], vr[NCH];
+    // E4M3: the raw bytes and scales stay in registers until the tile is
+    // stored, so the loads keep their lead over the conversion
+    uint2 kw[F8 ? NCH : 1], vw[F8 ? NCH : 1];
+    float ksv[F8 ? NCH : 1], vsv[F8 ? NCH : 1];
     // Block size is a power of two (checked on the host): shifts, no division.
     const int bs_log2 = p.bs_log2, bs_mask = (1 << bs_log2) - 1;
     const int last_pi = (L - 1) >> bs_log2;
@@ -221,15 +225,24 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     // the slot's scale (at `scale_at`), rounded to bf16.
     // `slot` is the key's cache slot, or (fast path) the uniform slot of the
     // KPU-key group with the lane's key offset folded into at / scale_at.
+    auto raw8 = [&](const uint16_t* pool, const float* scales, size_t slot, uint32_t at, uint32_t scale_at, uint2& w,
+                    float& sc) {
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(pool) + slot * row;  // uniform on the fast path
+        w = *reinterpret_cast<const uint2*>(base + at);
+        sc = (scales + slot * p.Hkv)[scale_at];
+    };
+    auto cvt8 = [&](uint2 w, float sc) -> uint4 {
+        const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, true);
+        const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, true);
+        return make_uint4(pack2_hw(a.x * sc, a.y * sc), pack2_hw(b.x * sc, b.y * sc), pack2_hw(c.x * sc, c.y * sc),
+                          pack2_hw(d.x * sc, d.y * sc));
+    };
     auto load8 = [&](const uint16_t* pool, const float* scales, size_t slot, uint32_t at, uint32_t scale_at) -> uint4 {
         if constexpr (F8) {
-            const uint8_t* base = reinterpret_cast<const uint8_t*>(pool) + slot * row;  // uniform on the fast path
-            const uint2 w = *reinterpret_cast<const uint2*>(base + at);
-            const float sc = (scales + slot * p.Hkv)[scale_at];
-            const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, true);
-            const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, true);
-            return make_uint4(pack2_hw(a.x * sc, a.y * sc), pack2_hw(b.x * sc, b.y * sc), pack2_hw(c.x * sc, c.y * sc),
-                              pack2_hw(d.x * sc, d.y * sc));
+            uint2 w;
+            float sc;
+            raw8(pool, scales, slot, at, scale_at, w, sc);
+            return cvt8(w, sc);
         } else {
             // uniform base + 32-bit lane byte offset (the saddr addressing form)
             const uint8_t* base = reinterpret_cast<const uint8_t*>(pool + slot * row);
@@ -256,8 +269,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                 pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
                 const size_t slot = ((size_t)pg << bs_log2) + (kg & bs_mask);  // uniform
                 if constexpr (F8) {
-                    kr[u] = load8(p.kc, p.kscale, slot, lane_at, lane_sc);
-                    vr[u] = load8(p.vc, p.vscale, slot, lane_at, lane_sc);
+                    raw8(p.kc, p.kscale, slot, lane_at, lane_sc, kw[u], ksv[u]);
+                    raw8(p.vc, p.vscale, slot, lane_at, lane_sc, vw[u], vsv[u]);
                 } else {
                     // buffer loads: uniform base in the descriptor, the lane's
                     // 32-bit byte offset in one VGPR shared by K and V
@@ -271,14 +284,26 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             for (int u = 0; u < NCH; u++) {
                 const int kp = k0 + u * KPU + kl0;
                 const size_t slot = (page_id(kp >> bs_log2) << bs_log2) + (kp & bs_mask);
-                kr[u] = load8(p.kc, p.kscale, slot, kvh * HEAD_DIM + c8, kvh);
-                vr[u] = load8(p.vc, p.vscale, slot, kvh * HEAD_DIM + c8, kvh);
+                if constexpr (F8) {
+                    raw8(p.kc, p.kscale, slot, kvh * HEAD_DIM + c8, kvh, kw[u], ksv[u]);
+                    raw8(p.vc, p.vscale, slot, kvh * HEAD_DIM + c8, kvh, vw[u], vsv[u]);
+                } else {
+                    kr[u] = load8(p.kc, p.kscale, slot, kvh * HEAD_DIM + c8, kvh);
+                    vr[u] = load8(p.vc, p.vscale, slot, kvh * HEAD_DIM + c8, kvh);
+                }
             }
         }
     };
     auto store_tile = [&](int buf, int k0) {
         uint16_t* sk = pf_smem + buf * STAGE;
         uint16_t* sv = sk + PF_K_ELEMS;
+        if constexpr (F8) {
+#pragma unroll
+            for (int u = 0; u < NCH; u++) {
+                kr[u] = cvt8(kw[u], ksv[u]);
+                vr[u] = cvt8(vw[u], vsv[u]);
+            }
+        }
         if (k0 + PF_BK > L) {
 #pragma unroll
             for (int u = 0; u < NCH; u++)
