@@ -194,11 +194,15 @@ def main():
     def step_on(i, strm, ev=None):
         s_ = strm.cuda_stream
         if args.refabi:
-            pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=s_)
+            if e4m3:
+                pkv.attn_prep(qkv, qstride, Hq, Hkv, qn, kn, rope_d[i], B, 11, 11, slot_d[i], inv_freq, q, kc, vc,
+                              1e-6, B, pages * BS, kscale=kscale, vscale=vscale, stream=s_)
+            else:
+                pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=s_)
             if ev:
                 kev.record(ev[0], s_)
-            rk.launch("attn_paged_g4", (B, Hkv, Z), 256, 0,
-                      [P_(q), P_(kc), P_(vc), P_(None), P_(None), P_(qkv), I_(qstride), I_(Hq), I_(Hkv),
+            rk.launch("attn_paged8_g4" if e4m3 else "attn_paged_g4", (B, Hkv, Z), 256, 0,
+                      [P_(q), P_(kc), P_(vc), P_(kscale if e4m3 else None), P_(vscale if e4m3 else None), P_(qkv), I_(qstride), I_(Hq), I_(Hkv),
                        P_(pos_d[i]), P_(ts), P_(bt), I_(meta.max_blocks), I_(BS), P_(out), F_(1 / 16), P_(None),
                        P_(None), I_(0), I_(0), P_(cu), I_(0), I_(refabi.SPLIT_MIN_KEYS), P_(part), P_(None), I_(1)],
                       stream=s_)
@@ -291,7 +295,8 @@ def main():
         # key-range kernel: every key's K and V rows (all kv heads) + q; its
         # partials are overhead, not algorithmic.
         kern_bytes = [kk * Hkv * (D + 4 if e4m3 else D * 2) * 2 + B * Hq * D * 2 for kk in keys]
-        kname = ("decode_range8_kernel (E4M3 cache, after attn_prep)" if e4m3 else
+        kname = ("attn_paged8_g4 (reference ABI, E4M3 cache, after attn_prep)" if e4m3 and args.refabi else
+                 "decode_range8_kernel (E4M3 cache, after attn_prep)" if e4m3 else
                  "attn_paged_g4 (reference ABI)" if args.refabi else
                  "decode_range_kernel<4,false> (after attn_prep)" if args.with_prep else
                  "verify_range_kernel" if args.verify_kernel else "decode_range_kernel<4,false>")

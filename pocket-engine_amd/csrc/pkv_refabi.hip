@@ -35,6 +35,7 @@
 // size).
 #include "pkv_copy.hip"
 #include "pkv_decode.hip"
+#include "pkv_decode8.hip"
 #include "pkv_prefill.hip"
 #include "pkv_prep.hip"
 #include "pkv_verify.hip"
@@ -95,7 +96,7 @@ namespace pkv {
 
 // attn_paged_g4 / attn_paged8_g4 on the reference's grid (token t, kv head,
 // range z): the range's pages split over the 4 waves (bf16: the decode wave
-// body; E4M3: the MFMA verify body with one row), combined through LDS.
+// body; E4M3: the E4M3 decode body, two pages per step), combined through LDS.
 template <bool F8>
 __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache, const void* vcache,
                                           const float* kscale, const float* vscale, const uint16_t* qkv, int qstride,
@@ -105,10 +106,18 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
                                           const int* __restrict__ cu, int skip_prompts, int min_chunk, float* part,
                                           const int* __restrict__ outs, int spec) {
     constexpr int G = 4;
+    // bf16: the decode wave body's LDS and a separate record per wave. E4M3:
+    // the E4M3 decode body's LDS per wave, whose V staging rows also hold the
+    // wave's record once its loop is done (72 KB in all: two workgroups per
+    // CU).
     __shared__ WaveLds<G> sh_w[F8 ? 1 : 4];
-    __shared__ __align__(16) uint16_t sh_v[F8 ? 4 : 1][F8 ? VF_LDS : 8];
-    __shared__ float sh_acc[4][G][HEAD_DIM];
+    __shared__ WaveLds8 sh_w8[F8 ? 4 : 1];
+    __shared__ float sh_acc_bf[F8 ? 1 : 4][G][HEAD_DIM];
     __shared__ float sh_ml[4][G][2];
+    auto rec = [&](int w) -> float (*)[HEAD_DIM] {
+        if constexpr (F8) return reinterpret_cast<float (*)[HEAD_DIM]>(sh_w8[w].v);
+        else return sh_acc_bf[w];
+    };
     if (blockDim.x != 256 || block_size != PAGE || Hq != G * Hkv || (kscale != nullptr) != F8 ||
         (vscale != nullptr) != F8)
         return;
@@ -179,7 +188,7 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
 #pragma unroll
         for (int g = 0; g < G; g++) {
 #pragma unroll
-            for (int e = 0; e < 4; e++) sh_acc[wave][g][4 * lane + e] = 0.f;
+            for (int e = 0; e < 4; e++) rec(wave)[g][4 * lane + e] = 0.f;
             if (lane == 0) {
                 sh_ml[wave][g][0] = -INFINITY;
                 sh_ml[wave][g][1] = 0.f;
@@ -190,21 +199,21 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
     if (a < b) {
         const int* bt = block_table + (size_t)sq * max_blocks;
         if constexpr (F8) {
-            auto epi = [&](int r, int g, int gq, const f32x4 (&acc)[16], float m, float l) {
+            auto epi = [&](int g, int gq, const f32x4 (&acc)[16], float m, float l) {
 #pragma unroll
                 for (int db = 0; db < 16; db++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) sh_acc[wave][g][16 * db + 4 * gq + i] = acc[db][i];
+                    for (int i = 0; i < 4; i++) rec(wave)[g][16 * db + 4 * gq + i] = acc[db][i];
                 if (gq == 0) {
                     sh_ml[wave][g][0] = m;
                     sh_ml[wave][g][1] = l;
                 }
             };
-            verify_piece<true>(p, bt, sh_v[wave], t, kvh, a, b, L, 0, 0, 0, epi);
+            piece_body8(p, bt, sh_w8[wave], t, kvh, a, b, epi);
         } else {
             auto epi = [&](int g, const float (&acc)[8], float m, float l, int ch) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) sh_acc[wave][g][8 * ch + e] = acc[e];
+                for (int e = 0; e < 8; e++) rec(wave)[g][8 * ch + e] = acc[e];
                 if (ch == 0) {
                     sh_ml[wave][g][0] = m;
                     sh_ml[wave][g][1] = l;
@@ -225,7 +234,7 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
         for (int w = 0; w < 4; w++) {
             const float f = sh_ml[w][g][0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sh_ml[w][g][0] - M);
             S += sh_ml[w][g][1] * f;
-            A += sh_acc[w][g][d] * f;
+            A += rec(w)[g][d] * f;
         }
         const int h = kvh * G + g;
         if (part) {
@@ -259,7 +268,7 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
 extern "C" __global__ void __launch_bounds__(256) attn_paged_g4(PKV_PAGED_ARGS) { pkv::paged_ref<false>(PKV_PAGED_PASS); }
 
 // The same over an E4M3 cache (kscale / vscale given).
-extern "C" __global__ void __launch_bounds__(256) attn_paged8_g4(PKV_PAGED_ARGS) { pkv::paged_ref<true>(PKV_PAGED_PASS); }
+extern "C" __global__ void __launch_bounds__(256, 2) attn_paged8_g4(PKV_PAGED_ARGS) { pkv::paged_ref<true>(PKV_PAGED_PASS); }
 
 extern "C" __global__ void __launch_bounds__(256)
     attn_merge(const float* __restrict__ part, int Z, int min_chunk, const uint16_t* __restrict__ qkv, int qstride,
