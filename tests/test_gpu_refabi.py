@@ -147,3 +147,23 @@ def test_ref_prefill_matches_oracle(dev, rk, mfma, ctxs, chunks, Hkv, seed):
                                c["seqs"], c["bt"], c["max_blocks"], BS, SCALE, out=init.copy())
     ok, err = close(got, want)
     assert ok, f"max |diff| {err}"
+
+
+def test_ref_prefill_short_dynamic_lds_writes_nothing(dev, rk):
+    """attn_groupr_g4_t2_k32 keeps its stages in the launch's dynamic shared
+    memory: a launch that passes less than they take (here 32 KiB instead of
+    the engine's 67,584 bytes) returns before any work, like a launch with
+    another block size, and leaves the output untouched."""
+    print("case refabi prefill short dynamic LDS", flush=True)
+    c = prefill_case([100], [64], 4, 5, decode_rows=1)
+    T, Hq = c["T"], c["Hq"]
+    name, grid, threads, smem = flash_launch(T, c["seqs"], 4)
+    assert name == "attn_groupr_g4_t2_k32" and smem >= 67328
+    init = np.full((T, Hq, D), 0x3333, np.uint16)
+    out = i16(init, dev)
+    rk.launch(name, grid, threads, 32 * 1024,
+              [P(i16(c["q"], dev)), P(i16(c["kc"], dev)), P(i16(c["vc"], dev)), P(None), P(None),
+               P(i16(c["qkv"], dev)), I(c["qstride"]), I(Hq), I(4), P(i32(c["pos"], dev)), P(i32(c["cu"], dev)),
+               I(c["seqs"]), P(i32(c["bt"], dev)), I(c["max_blocks"]), I(BS), P(out), F(SCALE), P(None), I(1)])
+    torch.cuda.synchronize()
+    assert (out.cpu().numpy().view(np.uint16) == 0x3333).all()
