@@ -519,11 +519,22 @@ def bench_verify(args):
     slot = (bt[seqs[None, :], pos // BS] * BS + pos % BS).astype(np.int32)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    kc = torch.empty(pages * BS, Hkv, D, dtype=torch.bfloat16, device=dev)
-    vc = torch.empty_like(kc)
-    for t in (kc, vc):
-        for i in range(0, t.shape[0], 1 << 18):
-            t[i:i + (1 << 18)] = torch.randn(t[i:i + (1 << 18)].shape, device=dev, generator=gen) * 0.5
+    e4m3 = args.kv == "e4m3"
+    if e4m3:
+        # random E4M3 bytes (NaN codes replaced) and scales; the step is the
+        # attention kernel and merge alone (no bf16 append into this cache)
+        kc = torch.randint(0, 256, (pages * BS, Hkv, D), device=dev, generator=gen, dtype=torch.int32).to(torch.uint8)
+        vc = torch.randint(0, 256, (pages * BS, Hkv, D), device=dev, generator=gen, dtype=torch.int32).to(torch.uint8)
+        for t in (kc, vc):
+            t[(t & 0x7F) == 0x7F] = 0x7E
+        kscale = torch.rand(pages * BS, Hkv, device=dev, generator=gen) * 0.004 + 0.001
+        vscale = torch.rand(pages * BS, Hkv, device=dev, generator=gen) * 0.004 + 0.001
+    else:
+        kc = torch.empty(pages * BS, Hkv, D, dtype=torch.bfloat16, device=dev)
+        vc = torch.empty_like(kc)
+        for t in (kc, vc):
+            for i in range(0, t.shape[0], 1 << 18):
+                t[i:i + (1 << 18)] = torch.randn(t[i:i + (1 << 18)].shape, device=dev, generator=gen) * 0.5
     T = B * n
     q = (torch.randn(T, Hq, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
     qstride = synth.qkv_stride(Hq, Hkv)
@@ -540,10 +551,18 @@ def bench_verify(args):
     v_rows = k_rows + 2 * Hkv * D
     stream = torch.cuda.current_stream()
 
-    def step(i, ev=None, fn=pkv.attn_verify):
-        pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], T, Hkv, D * 2, kc, vc, pages * BS)
+    verify_fn, decode_fn = ((pkv.attn_verify_e4m3, pkv.attn_decode_e4m3) if e4m3 else
+                            (pkv.attn_verify, pkv.attn_decode))
+
+    def step(i, ev=None, fn=verify_fn):
+        if not e4m3:
+            pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], T, Hkv, D * 2, kc, vc, pages * BS)
         if ev:
             pkv.time_next_range_kernel(ev[0], ev[1])
+        if e4m3:
+            fn(q, kc, vc, kscale, vscale, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt_d, mb, BS, out, 1 / 16, cu, 1, outs,
+               1, T, pages, ws)
+            return
         fn(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d[i], ts, bt_d, mb, BS, out, 1 / 16, cu, 1, outs, 1, T, pages, ws)
 
     def timed(fn, k0, K):
@@ -559,17 +578,19 @@ def bench_verify(args):
 
     for i in range(args.warmup):
         step(i)
-    total_ms, kern_ms = timed(pkv.attn_verify, args.warmup, args.steps)
+    total_ms, kern_ms = timed(verify_fn, args.warmup, args.steps)
     ms_step = total_ms / args.steps
     keys = [int((lens[args.warmup + k] + n).sum()) for k in range(args.steps)]  # unique keys per step
-    step_bytes = [kk * Hkv * D * 2 * 2 + 3 * T * Hq * D * 2 + synth.algorithmic_bytes_append(T, Hkv) for kk in keys]
+    key_bytes = Hkv * (D + 4) * 2 if e4m3 else Hkv * D * 2 * 2  # K + V (+ scales) per key
+    step_bytes = [kk * key_bytes + 3 * T * Hq * D * 2 + (0 if e4m3 else synth.algorithmic_bytes_append(T, Hkv))
+                  for kk in keys]
     gbs = sum(step_bytes) / (total_ms * 1e-3) / 1e9
-    kern_bytes = [kk * Hkv * D * 2 * 2 + T * Hq * D * 2 for kk in keys]
+    kern_bytes = [kk * key_bytes + T * Hq * D * 2 for kk in keys]
     kern_gbs = sum(kern_bytes) / (sum(kern_ms) * 1e-3) / 1e9
     kern_avg_us = 1e3 * sum(kern_ms) / len(kern_ms)
     # per-token decode attention on the same steps (each row re-reads its pages)
     Kd = min(args.steps, 20)
-    dec_ms, _ = timed(pkv.attn_decode, args.warmup, Kd)
+    dec_ms, _ = timed(decode_fn, args.warmup, Kd)
     line = {
         "metric": "speculative verify step us + achieved HBM GB/s over unique KV bytes (config 5), 1 MI355X",
         "value": round(gbs, 1),
@@ -587,16 +608,16 @@ def bench_verify(args):
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1)*0.5 K/V/q, U[32768,131072] contexts, seeded accepted counts)",
         "config": {"workload": "c5: 16 seqs x 4 draft rows, append + verify attention + rewind",
-                   "batch": B, "drafts": n, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
+                   "kv": args.kv, "batch": B, "drafts": n, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
                    "pool_pages": pages, "seed": seed, "mean_unique_keys_per_step": round(float(np.mean(keys)), 1),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "verify_range_kernel", "achieved": round(kern_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": "verify_range8_kernel (E4M3 cache, no append)" if e4m3 else
+                     "verify_range_kernel", "achieved": round(kern_gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
                      "avg_us": round(kern_avg_us, 2), "traffic": None,
-                     "traffic_profiled": {"source": "profiles/verify_step_c5_batch16.md (rocprofv3 --pmc, "
-                                                    "copy-calibrated, seed 1)",
-                                          "read_bytes": 5.502e9, "write_bytes": 17.9e6,
-                                          "algorithmic_bytes": 5.48e9, "ratio": 1.007}},
+                     "traffic_profiled": None if e4m3 else {
+                         "source": "profiles/verify_step_c5_batch16.md (rocprofv3 --pmc, copy-calibrated, seed 1)",
+                         "read_bytes": 5.502e9, "write_bytes": 17.9e6, "algorithmic_bytes": 5.48e9, "ratio": 1.007}},
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)

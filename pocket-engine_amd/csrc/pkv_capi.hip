@@ -293,7 +293,7 @@ int pkv_attn_decode_workspace(int T, int Hq, size_t* bytes) {
 
 int pkv_attn_verify_workspace(int T, int Hq, size_t* bytes) {
     if (T < 0 || Hq <= 0 || !bytes) return PKV_ERR_INVALID;
-    *bytes = decode_layout(T, Hq, decode_n_wg(), true).total;
+    *bytes = decode_layout(T, Hq, decode_n_wg() * F8_WG_PER_CU, true).total;
     return PKV_OK;
 }
 
@@ -339,7 +339,7 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
             app->row_stride < (int64_t)Hkv * pkv::HEAD_DIM * 2)
             return PKV_ERR_INVALID;
     }
-    const int n_wg = decode_n_wg() * (f8 && !verify ? F8_WG_PER_CU : 1);
+    const int n_wg = decode_n_wg() * (f8 ? F8_WG_PER_CU : 1);
     const DecodeLayout lay = decode_layout(T, Hq, n_wg, verify);
     if (workspace_bytes < lay.total) return PKV_ERR_INVALID;
     pkv::DecodeParams p;
@@ -373,10 +373,10 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
         hipEvent_t e0 = t_ev_start, e1 = t_ev_stop;
         t_ev_start = t_ev_stop = nullptr;
         if (verify && f8)
-            hipExtLaunchKernelGGL((pkv::verify_range_kernel<true>), dim3(n_wg, groups), dim3(threads), 0,
+            hipExtLaunchKernelGGL(pkv::verify_range8_kernel, dim3(n_wg, groups), dim3(threads), 0,
                                   (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs);
         else if (verify)
-            hipExtLaunchKernelGGL((pkv::verify_range_kernel<false>), dim3(n_wg, groups), dim3(threads), 0,
+            hipExtLaunchKernelGGL(pkv::verify_range_kernel, dim3(n_wg, groups), dim3(threads), 0,
                                   (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs);
         else if (f8)
             hipExtLaunchKernelGGL(pkv::decode_range8_kernel, dim3(n_wg, groups), dim3(threads), 0,

@@ -70,7 +70,7 @@ struct DecodeParams {
     const uint16_t* k_rows;
     const uint16_t* v_rows;
     long row_stride;          // elements
-    // E4M3 cache (verify_range_kernel<true>): f32 scale per (slot, kv head)
+    // E4M3 cache (decode_range8_kernel, verify_range8_kernel): f32 scale per (slot, kv head)
     const float* kscale;
     const float* vscale;
 };

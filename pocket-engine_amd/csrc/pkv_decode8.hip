@@ -45,14 +45,24 @@ struct WaveLds8 {
     float sc[64];                 // the unit's kscale [key], then vscale [key]
 };
 
-// One wave: token t, kv head kvh, keys [j0, j1) of its sequence (block
-// table row bt), over the E4M3 cache. Results go to epi(g, gq, acc, m, l) on
-// the lanes of head g (DecodeEpi8).
-template <class Epi>
+// One wave: rows t .. t + NR - 1 of one sequence (row r attends keys
+// [0, Lr[r]); NR = 1: decode, the piece's bounds alone), kv head kvh, keys
+// [j0, j1) of the sequence (block table row bt), over the E4M3 cache. Column
+// c = 4 r + g of the products is row r, query head kvh * 4 + g. Results go
+// to epi(c, gq, acc, m, l) on the lanes of the columns of attending rows
+// (DecodeEpi8 for decode; m = -inf, l = 0 for a column with no key in the
+// piece).
+template <int NR = 1, class Epi>
 __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __restrict__ bt, WaveLds8& lds, int t,
-                                            int kvh, int j0, int j1, Epi epi) {
+                                            int kvh, int j0, int j1, Epi epi, const int* Lr = nullptr) {
     constexpr int G = 4;
+    static_assert(NR == 1 || NR == 4, "one decode row or a verify segment of up to 4 rows");
     const int lane = threadIdx.x & 63, sig = lane & 15, rho = lane >> 4;
+    const int col_r = sig >> 2;
+    // this lane's column: its row's key bound (decode: the piece's), and
+    // whether the column is a row that attends
+    const int myL = NR == 1 ? j1 : col_r == 0 ? Lr[0] : col_r == 1 ? Lr[1] : col_r == 2 ? Lr[2] : Lr[3];
+    const bool active = col_r < NR && myL > 0;
     const int Hkv = p.Hkv;
     const float sl2 = p.scale * LOG2E;
     const uint8_t* kc = reinterpret_cast<const uint8_t*>(p.kc);
@@ -66,11 +76,12 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     // the page for head sig.
     bf16x8 qf[8];
     {
-        const uint16_t* qrow = p.q + ((size_t)t * p.Hq + kvh * G + (sig & 3)) * HEAD_DIM + 16 * rho;
+        const uint16_t* qrow = p.q + ((size_t)(t + (active ? col_r : 0)) * p.Hq + kvh * G + (sig & 3)) * HEAD_DIM +
+                               16 * rho;
 #pragma unroll
         for (int s = 0; s < 8; s++)
-            qf[s] = as_bf16x8(sig < G ? *reinterpret_cast<const uint4*>(qrow + 64 * (s >> 1) + 8 * (s & 1))
-                                      : make_uint4(0, 0, 0, 0));
+            qf[s] = as_bf16x8(active ? *reinterpret_cast<const uint4*>(qrow + 64 * (s >> 1) + 8 * (s & 1))
+                                     : make_uint4(0, 0, 0, 0));
     }
     const size_t row_bytes = (size_t)Hkv * HEAD_DIM;  // one slot row (all kv heads), bytes
     auto page_id = [&](int pi) -> long {
@@ -145,14 +156,16 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int kpos = UNIT8 * u + 16 * pg + 4 * rho + i;
-                sc[4 * pg + i] = kpos >= j0 && kpos < j1 ? sacc[pg][i] * ks[i] * sl2 : -INFINITY;
+                sc[4 * pg + i] = kpos >= j0 && kpos < j1 && kpos < myL ? sacc[pg][i] * ks[i] * sl2 : -INFINITY;
                 mx = fmaxf(mx, sc[4 * pg + i]);
             }
         }
         mx = fmaxf(mx, shfl_xor(mx, 16));
         mx = fmaxf(mx, shfl_xor(mx, 32));
         const float mn = fmaxf(m, mx);
-        const float cr_me = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first unit (m = -inf)
+        // a column with no key yet subtracts 0 (its weights are all 0)
+        const float mref = mn == -INFINITY ? 0.f : mn;
+        const float cr_me = __builtin_amdgcn_exp2f(m - mref);  // 0 while m = -inf
         // V rows to LDS as bf16 (exact): row 8 rho + k, dims 16 sig .. + 15;
         // rows of keys outside [j0, j1) as zeros (a stale slot may hold NaN)
 #pragma unroll
@@ -177,7 +190,7 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
             float w[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float pr = __builtin_amdgcn_exp2f(sc[4 * pg + i] - mn);  // 0 for a masked key
+                const float pr = __builtin_amdgcn_exp2f(sc[4 * pg + i] - mref);  // 0 for a masked key
                 psum += pr;
                 w[i] = sc[4 * pg + i] == -INFINITY ? 0.f : pr * vs[i];
             }
@@ -219,7 +232,7 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     // Totals: a head's sum over its 4 lane groups.
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
-    if (sig < G) epi(sig, rho, acc, m, l);
+    if (active) epi(sig, rho, acc, m, l);
 }
 
 // Writes a piece's result for the lanes of head g of the group (dims

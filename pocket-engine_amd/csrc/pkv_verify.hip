@@ -32,6 +32,7 @@
 // SIMD, so the kernel stays bandwidth-bound with the compute hidden.
 #pragma once
 #include "pkv_common.h"
+#include "pkv_decode8.hip"
 
 #include <type_traits>
 
@@ -56,28 +57,24 @@ __device__ __forceinline__ int seg_len(int t, int T, const int* __restrict__ pos
 }
 
 // One wave: segment headed by token t (rows t + r, r < 4, attending Lr[r]
-// keys; Lr = 0 for absent rows), kv head kvh, keys [j0, j1).
-// F8: an E4M3 cache (bytes [slot][Hkv][256], f32 kscale / vscale per slot and
-// kv head; reference attn_paged8, qwen35.cu:1146-1309 with F8): K and V bytes
-// are converted to bf16 in registers (exact), each score is multiplied by its
-// key's kscale, and each weight by its key's vscale before P.V (the softmax
-// sum takes the unscaled weights).
+// keys; Lr = 0 for absent rows), kv head kvh, keys [j0, j1), bf16 cache (an
+// E4M3 cache runs piece_body8 with 4 rows, pkv_decode8.hip).
 // The result goes to epi(r, g, gq, acc, m, l) on the lanes of attending rows:
 // row r, query head kvh * 4 + g, dims 16 db + 4 gq + i in acc[db][i]; m in
 // log2 units, l the sum of weights (m = -inf, l = 0 when the piece has no
 // key for the row).
-template <bool F8, class Epi>
+template <class Epi>
 __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* __restrict__ bt, uint16_t* vl, int t,
                                              int kvh, int j0, int j1, int L0, int L1, int L2, int L3, Epi epi) {
     const int lane = threadIdx.x & 63, c16 = lane & 15, gq = lane >> 4;
     const int r_me = c16 >> 2, g_me = c16 & 3;
     const int myL = r_me == 0 ? L0 : r_me == 1 ? L1 : r_me == 2 ? L2 : L3;
     const float sl2 = p.scale * LOG2E;
-    const size_t row_elems = (size_t)p.Hkv * HEAD_DIM;  // slot row: elements (bf16) or bytes (E4M3)
+    const size_t row_elems = (size_t)p.Hkv * HEAD_DIM;  // slot row, elements
 
     // q.k over the 256 dims in 8 steps of 32: step c, lane group gq takes
     // dims dim0(c) .. + 7 (the same for q and k).
-    auto dim0 = [&](int c) { return F8 ? 64 * gq + 16 * (c >> 1) + 8 * (c & 1) : 32 * c + 8 * gq; };
+    auto dim0 = [&](int c) { return 32 * c + 8 * gq; };
     bf16x8 qf[8];
     if (myL > 0) {
         const uint16_t* qrow = p.q + ((size_t)(t + r_me) * p.Hq + kvh * 4 + g_me) * HEAD_DIM;
@@ -92,49 +89,24 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
         return pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
     };
     auto page_base = [&](int pi) -> size_t { return (size_t)page_of(pi) * PAGE * row_elems + (size_t)kvh * HEAD_DIM; };
-    constexpr int NK = F8 ? 4 : 8, NV = F8 ? 4 : 8;  // 16-byte loads per lane per page
-    // One page's loads: K and V rows (E4M3: plus this lane's keys' scales).
+    constexpr int NK = 8, NV = 8;  // 16-byte loads per lane per page
+    // One page's loads: K and V rows.
     struct Buf {
         uint4 kb[NK], vb[NV];
-        float ksc[4], vsc[4];  // E4M3: scales of keys 4 gq + i
     };
     auto load_k = [&](Buf& B, size_t base, int pi) {
-        if constexpr (F8) {
-            const uint8_t* r = reinterpret_cast<const uint8_t*>(p.kc) + base + (size_t)c16 * row_elems + 64 * gq;
+        const uint16_t* r = p.kc + base + (size_t)c16 * row_elems + 8 * gq;
 #pragma unroll
-            for (int c = 0; c < NK; c++) B.kb[c] = load_nt(r + 16 * c);
-            const size_t s0 = ((size_t)page_of(pi) * PAGE + 4 * gq) * p.Hkv + kvh;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                B.ksc[i] = p.kscale[s0 + (size_t)i * p.Hkv];
-                B.vsc[i] = p.vscale[s0 + (size_t)i * p.Hkv];
-            }
-        } else {
-            const uint16_t* r = p.kc + base + (size_t)c16 * row_elems + 8 * gq;
-#pragma unroll
-            for (int c = 0; c < NK; c++) B.kb[c] = load_nt(r + 32 * c);
-        }
+        for (int c = 0; c < NK; c++) B.kb[c] = load_nt(r + 32 * c);
     };
     auto load_v = [&](Buf& B, size_t base) {
-        if constexpr (F8) {
-            // keys 4 k + lane / 16, bytes 16 (lane % 16) .. + 15
-            const uint8_t* r = reinterpret_cast<const uint8_t*>(p.vc) + base + (size_t)(lane >> 4) * row_elems + 16 * c16;
+        const uint16_t* r = p.vc + base + (size_t)(lane >> 5) * row_elems + 8 * (lane & 31);
 #pragma unroll
-            for (int k = 0; k < NV; k++) B.vb[k] = load_nt(r + (size_t)(4 * k) * row_elems);
-        } else {
-            const uint16_t* r = p.vc + base + (size_t)(lane >> 5) * row_elems + 8 * (lane & 31);
-#pragma unroll
-            for (int k = 0; k < NV; k++) B.vb[k] = load_nt(r + (size_t)(2 * k) * row_elems);
-        }
+        for (int k = 0; k < NV; k++) B.vb[k] = load_nt(r + (size_t)(2 * k) * row_elems);
     };
     // A operand of step c: K dims dim0(c) .. + 7 of key c16
     auto k_frag = [&](const Buf& B, int c) -> bf16x8 {
-        if constexpr (F8) {
-            const uint4 w = B.kb[c >> 1];
-            return as_bf16x8((c & 1) ? e4m3x8_to_bf16x8(w.z, w.w) : e4m3x8_to_bf16x8(w.x, w.y));
-        } else {
-            return as_bf16x8(B.kb[c]);
-        }
+        return as_bf16x8(B.kb[c]);
     };
 
     f32x4 acc[16];
@@ -153,32 +125,13 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < 8; c++) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_frag(B, c), qf[c], s, 0, 0, 0);
-        float ks_cur[4], vs_cur[4];
-        if constexpr (F8) {
+        // rows of keys outside [j0, j1) as zeros: their weight is 0, and
+        // a stale slot may hold NaN
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int kp = pi * PAGE + 4 * gq + i;
-                ks_cur[i] = B.ksc[i];
-                vs_cur[i] = (kp >= j0 && kp < j1) ? B.vsc[i] : 0.f;  // a stale scale may be NaN
-            }
-            // V rows to LDS as bf16: row 4 k + lane / 16, dims 16 (lane % 16) .. + 15
-#pragma unroll
-            for (int k = 0; k < NV; k++) {
-                uint16_t* d = vl + (4 * k + (lane >> 4)) * VF_VSTR + 16 * c16;
-                const int kp = pi * PAGE + 4 * k + (lane >> 4);
-                const bool in = kp >= j0 && kp < j1;
-                *reinterpret_cast<uint4*>(d) = in ? e4m3x8_to_bf16x8(B.vb[k].x, B.vb[k].y) : make_uint4(0, 0, 0, 0);
-                *reinterpret_cast<uint4*>(d + 8) = in ? e4m3x8_to_bf16x8(B.vb[k].z, B.vb[k].w) : make_uint4(0, 0, 0, 0);
-            }
-        } else {
-            // rows of keys outside [j0, j1) as zeros: their weight is 0, and
-            // a stale slot may hold NaN
-#pragma unroll
-            for (int k = 0; k < NV; k++) {
-                const int kp = pi * PAGE + 2 * k + (lane >> 5);
-                *reinterpret_cast<uint4*>(st + 2 * k * VF_VSTR) =
-                    (kp >= j0 && kp < j1) ? B.vb[k] : make_uint4(0, 0, 0, 0);
-            }
+        for (int k = 0; k < NV; k++) {
+            const int kp = pi * PAGE + 2 * k + (lane >> 5);
+            *reinterpret_cast<uint4*>(st + 2 * k * VF_VSTR) =
+                (kp >= j0 && kp < j1) ? B.vb[k] : make_uint4(0, 0, 0, 0);
         }
         if constexpr (PREFETCH) {
             const size_t next = page_base(nxt);
@@ -190,8 +143,7 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int kp = k0 + i;
-            const float v = F8 ? s[i] * ks_cur[i] : s[i];
-            sc[i] = (kp >= j0 && kp < j1 && kp < myL) ? v * sl2 : -INFINITY;
+            sc[i] = (kp >= j0 && kp < j1 && kp < myL) ? s[i] * sl2 : -INFINITY;
             mx = fmaxf(mx, sc[i]);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -202,38 +154,21 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
         float pr[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) pr[i] = __builtin_amdgcn_exp2f(sc[i] - mref);
-        uint32_t p01, p23, r01 = 0, r23 = 0;
-        if constexpr (F8) {
-            // The sum takes the weights, P.V the weights times vscale, as a
-            // bf16 high part plus a bf16 remainder (two MFMAs: ~16 mantissa
-            // bits, where one bf16 would add 2^-9 relative error per weight
-            // to values the reference keeps in f32).
-            l = l * corr + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-            const float w0 = pr[0] * vs_cur[0], w1 = pr[1] * vs_cur[1], w2 = pr[2] * vs_cur[2], w3 = pr[3] * vs_cur[3];
-            p01 = pack2_hw(w0, w1);
-            p23 = pack2_hw(w2, w3);
-            r01 = pack2_hw(w0 - bf_lo(p01), w1 - bf_hi(p01));
-            r23 = pack2_hw(w2 - bf_lo(p23), w3 - bf_hi(p23));
-        } else {
-            p01 = pack2_hw(pr[0], pr[1]);
-            p23 = pack2_hw(pr[2], pr[3]);
-            // the denominator sums the same bf16 weights P.V uses
-            l = l * corr + ((bf_lo(p01) + bf_hi(p01)) + (bf_lo(p23) + bf_hi(p23)));
-        }
+        const uint32_t p01 = pack2_hw(pr[0], pr[1]), p23 = pack2_hw(pr[2], pr[3]);
+        // the denominator sums the same bf16 weights P.V uses
+        l = l * corr + ((bf_lo(p01) + bf_hi(p01)) + (bf_lo(p23) + bf_hi(p23)));
         m = mn;
         if (__any(corr != 1.f)) {
 #pragma unroll
             for (int db = 0; db < 16; db++) acc[db] *= corr;
         }
         const s16x4 pb = __builtin_bit_cast(s16x4, make_uint2(p01, p23));
-        const s16x4 pr_lo = __builtin_bit_cast(s16x4, make_uint2(r01, r23));
         wave_sync();  // V staged
 #pragma unroll
         for (int db = 0; db < 16; db++) {
             const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) s16x4*)(tr + 16 * db));
             acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb, acc[db], 0, 0, 0);
-            if constexpr (F8) acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pr_lo, acc[db], 0, 0, 0);
         }
         wave_sync();  // reads done before the next page is staged
     };
@@ -286,7 +221,6 @@ struct VerifyEpi {
 // threads. Same range split as decode_range_kernel with segment lengths in
 // place of token lengths; block 0 writes offs[t] (segment offsets by head
 // token, equal neighbours for other tokens), offs[T] = W, offs[T + 1] = R.
-template <bool F8>
 __global__ void __launch_bounds__(256, 1)
     verify_range_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                         const int* __restrict__ block_table, const int* __restrict__ cu,
@@ -315,8 +249,47 @@ __global__ void __launch_bounds__(256, 1)
             const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
             const int j0 = max(start, off) - off, j1 = min(end, off + Ls) - off;
             const VerifyEpi epi{p, t, kvh, t + b, j0 == 0 && j1 == Ls};
-            verify_piece<F8>(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Lr[0], Lr[1],
+            verify_piece(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Lr[0], Lr[1],
                              Lr[2], Lr[3], epi);
+            off += Ls;
+        }
+        t++;
+    }
+}
+
+// The same over an E4M3 cache with the E4M3 decode body (two pages per
+// step, both products on MFMA, 16 columns = 4 rows x 4 query heads): grid
+// (n_wg, ceil(Hkv / 4)) with two workgroups per CU (at most 256 VGPRs).
+__global__ void __launch_bounds__(256, 2)
+    verify_range8_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
+                         const int* __restrict__ block_table, const int* __restrict__ cu,
+                         const int* __restrict__ outs) {
+    __shared__ int sh_scan[16];
+    __shared__ int sh_t0[2];
+    __shared__ WaveLds8 sh_w8[4];
+    const int T = p.T, tid = threadIdx.x, b = blockIdx.x;
+    int nr, start, end, t0, off0;
+    if (!find_range(
+            p, [&](int t) { return seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr); }, sh_scan,
+            sh_t0, start, end, t0, off0))
+        return;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = blockIdx.y * 4 + wave;
+    int t = t0, off = off0;
+    while (off < end && t < T) {
+        const int Ls = __builtin_amdgcn_readfirstlane(seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr));
+        if (Ls > 0) {
+            nr = __builtin_amdgcn_readfirstlane(nr);
+            int Lr[VF_ROWS];
+#pragma unroll
+            for (int r = 0; r < VF_ROWS; r++)
+                Lr[r] = r < nr ? __builtin_amdgcn_readfirstlane(
+                                     decode_len(t + r, pos, tok_seq, cu, p.skip_prompts, outs, p.spec))
+                               : 0;
+            const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
+            const int j0 = max(start, off) - off, j1 = min(end, off + Ls) - off;
+            const VerifyEpi vepi{p, t, kvh, t + b, j0 == 0 && j1 == Ls};
+            auto epi = [&](int c, int gq, const f32x4 (&acc)[16], float m, float l) { vepi(c >> 2, c & 3, gq, acc, m, l); };
+            piece_body8<VF_ROWS>(p, block_table + (size_t)seq * p.max_blocks, sh_w8[wave], t, kvh, j0, j1, epi, Lr);
             off += Ls;
         }
         t++;
@@ -341,10 +314,5 @@ __global__ void __launch_bounds__(256)
     if (b0 == b1) return;
     merge_head(p, t, (th + b0) * VF_ROWS + r, VF_ROWS, b1 - b0 + 1, blockIdx.y);
 }
-
-template __global__ void verify_range_kernel<false>(DecodeParams, const int*, const int*, const int*, const int*,
-                                                    const int*);
-template __global__ void verify_range_kernel<true>(DecodeParams, const int*, const int*, const int*, const int*,
-                                                   const int*);
 
 }  // namespace pkv
