@@ -221,7 +221,9 @@ struct VerifyEpi {
 // threads. Same range split as decode_range_kernel with segment lengths in
 // place of token lengths; block 0 writes offs[t] (segment offsets by head
 // token, equal neighbours for other tokens), offs[T] = W, offs[T + 1] = R.
-__global__ void __launch_bounds__(256, 1)
+// The bound caps it at 256 VGPRs (210, no spills); it runs one workgroup per
+// CU (two ranges per CU measured slower: 856 against 817 us at C5).
+__global__ void __launch_bounds__(256, 2)
     verify_range_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                         const int* __restrict__ block_table, const int* __restrict__ cu,
                         const int* __restrict__ outs) {
