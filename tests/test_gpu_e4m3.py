@@ -216,7 +216,7 @@ def test_prefill_e4m3_matches_oracle(dev, refabi_kernel, ctxs, chunks, Hkv, seed
 
 
 @pytest.mark.parametrize("lens,Z", [([1, 2, 15, 16, 17], None), ([4097], None), ([513, 8193, 1000, 64], None),
-                                    ([900, 70], 1)])
+                                    ([900, 70], 1), ([40, 3, 100] * 100, None)])
 def test_reference_named_paged8(dev, lens, Z):
     """attn_paged8_g4 (+ attn_merge when split) of the code object, launched
     as model.rs:2366-2437 does for an E4M3 cache, against the oracle."""
