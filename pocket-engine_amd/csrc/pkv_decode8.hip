@@ -15,9 +15,11 @@
 //      v_mfma_f32_16x16x32_bf16. Lane (column s = lane % 16, group
 //      r = lane / 16) loads 64 contiguous bytes of key s (dims 16 r + 64 c,
 //      c = 0..3: 4 loads per page) and converts them to bf16 (exact,
-//      v_cvt_scalef32_pk_bf16_fp8) as the A operand; the B operand is query
-//      head s (columns 4..15 zero) over the same dims. The lane ends with the
-//      scores of keys 4 r .. 4 r + 3 of the page for head s.
+//      v_cvt_scalef32_pk_bf16_fp8) as the A operand; the B operand is
+//      column s over the same dims: query head s for decode (columns 4..15
+//      zero), row s / 4 and head s % 4 for a verify segment
+//      (verify_range8_kernel). The lane ends with the scores of keys
+//      4 r .. 4 r + 3 of the page for column s.
 //   softmax: per head over the lane's 8 keys and its 4 lane groups (two
 //      shuffles); exp2 domain; kscale / vscale of the unit's 32 keys come
 //      through 256 bytes of LDS (one 4-byte load per lane).
@@ -118,9 +120,9 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
         }
     };
 
-    float m = -INFINITY, l = 0.f;  // head sig (lanes with sig < 4)
+    float m = -INFINITY, l = 0.f;  // column sig
     // O^T[256 dims][16 columns]: lane (sig, rho) holds dims 16 db + 4 rho + i
-    // of column (head) sig in acc[db][i].
+    // of column sig in acc[db][i].
     f32x4 acc[16];
 #pragma unroll
     for (int db = 0; db < 16; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -147,7 +149,7 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
         lds.sc[lane] = sc_ld;  // kscale [0, 32), vscale [32, 64) of the unit's keys
         if constexpr (PREFETCH) load_k(na, nb);
         wave_sync();
-        // Lane (sig, rho): keys 16 pg + 4 rho + i of the unit, head sig.
+        // Lane (sig, rho): keys 16 pg + 4 rho + i of the unit, column sig.
         float sc[8], mx = -INFINITY;
 #pragma unroll
         for (int pg = 0; pg < 2; pg++) {
@@ -229,7 +231,7 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     }
     for (int u = u0; u < u1; u++) unit(u, u + 1, PF{});
     unit(u1, u1, NONE{});
-    // Totals: a head's sum over its 4 lane groups.
+    // Totals: a column's sum over its 4 lane groups.
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
     if (active) epi(sig, rho, acc, m, l);
