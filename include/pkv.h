@@ -149,6 +149,30 @@ int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_str
                          int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the device array pkv_attn_decode_step_noalloc uses as its
+ * workspace (one copy per GPU, held until the process ends). */
+#define PKV_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* pkv_attn_decode_step without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference (whose split partials
+ * come from a caller buffer, model.rs:1490-1494). The workspace is a
+ * file-scope device array of PKV_NOALLOC_SCRATCH_BYTES per GPU; the call
+ * allocates nothing (no hipMalloc / hipFree, no allocating library routine).
+ * Same arguments and results as pkv_attn_decode_step otherwise. Returns
+ * PKV_ERR_UNSUPPORTED when the step's workspace exceeds the array:
+ * 256-aligned (T + 2) int32 offsets, then (T + R) * Hq partial rows of 2 + 256
+ * f32 (R = key ranges = CUs x pkv_attn_decode_config's wg_per_cu); at Hq = 16
+ * on a 256-CU device, T <= 759. Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (different streams, or host threads) race; calls in
+ * order on one stream are safe. */
+int pkv_attn_decode_step_noalloc(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map,
+                                 const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride,
+                                 int Hq, int Hkv, const int32_t* pos, const int32_t* tok_seq,
+                                 const int32_t* block_table, int max_blocks, int block_size, void* out, float scale,
+                                 const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T,
+                                 int64_t num_blocks, void* stream);
+
 /* Draft-verify attention: the same results as pkv_attn_decode (every
  * decode row t attends keys 0..pos[t] of its sequence, gated output), for
  * batches whose sequences feed several rows at once — the reference's

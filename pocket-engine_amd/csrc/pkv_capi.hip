@@ -460,3 +460,61 @@ int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_str
 }
 
 }  // extern "C"
+
+// Scratch of pkv_attn_decode_step_noalloc: the decode workspace (key offsets
+// and split partials) in a file-scope device array, so the call allocates
+// nothing. Each device holds its own copy for the life of the process. In
+// host code `scratch` names a host-side stand-in, never the device array:
+// kernels get the address hipGetSymbolAddress returns for the current
+// device, looked up once per device and kept in g_scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[PKV_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {nullptr};
+
+// The current device's scratch address (looked up on the device's first
+// call, with that device current).
+int scratch_ptr(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return status_of(e);
+    if (dev < 0 || dev >= MAX_DEVICES) return PKV_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return status_of(e);
+        if (!p) return PKV_ERR_INVALID;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return PKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pkv_attn_decode_step_noalloc(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map,
+                                 const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride,
+                                 int Hq, int Hkv, const int32_t* pos, const int32_t* tok_seq,
+                                 const int32_t* block_table, int max_blocks, int block_size, void* out, float scale,
+                                 const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T,
+                                 int64_t num_blocks, void* stream) {
+    if (T < 0 || Hq <= 0) return PKV_ERR_INVALID;
+    // The fused step runs the bf16 key-range kernel (decode_n_wg() ranges);
+    // its layout must fit the array. Nothing in it needs clearing: the range
+    // kernel writes every offset and partial the merge reads.
+    if (decode_layout(T, Hq, decode_n_wg()).total > PKV_NOALLOC_SCRATCH_BYTES) return PKV_ERR_UNSUPPORTED;
+    void* workspace = nullptr;
+    const int st = scratch_ptr(&workspace);
+    if (st != PKV_OK) return st;
+    const size_t workspace_bytes = PKV_NOALLOC_SCRATCH_BYTES;
+    const AppendArgs app{k_rows, v_rows, row_stride, slot_map};
+    return attn_decode_phases(4 | 2, &app, nullptr, nullptr, PKV_DECODE_PASS);
+}
+
+}  // extern "C"

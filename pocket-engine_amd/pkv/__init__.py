@@ -84,6 +84,7 @@ _SIGS = {
     "pkv_kv_pad": (_c_int, [_c_int] * 6 + [ctypes.POINTER(ctypes.c_int32)] * 6),
     "pkv_meta_layout": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
 }
+_SIGS["pkv_attn_decode_step_noalloc"] = (_c_int, _SIGS["pkv_attn_decode_step"][1][:-3] + [_c_p])
 _SIGS["pkv_attn_decode_split"] = _SIGS["pkv_attn_decode"]
 _SIGS["pkv_attn_verify"] = _SIGS["pkv_attn_decode"]
 _SIGS["pkv_attn_prefill_e4m3"] = (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p] + _SIGS["pkv_attn_prefill"][1][3:])
@@ -197,6 +198,18 @@ def attn_decode_step(k_rows, v_rows, row_stride, slot_map, q, kcache, vcache, qk
                                      _ptr(block_table), max_blocks, block_size, _ptr(out), scale, _ptr(cu),
                                      int(skip_prompts), _ptr(outs), spec, T, num_blocks, _ptr(workspace),
                                      workspace_bytes, _stream(stream)), "pkv_attn_decode_step")
+
+
+def attn_decode_step_noalloc(k_rows, v_rows, row_stride, slot_map, q, kcache, vcache, qkv, qstride, Hq, Hkv, pos,
+                             tok_seq, block_table, max_blocks, block_size, out, scale, cu, skip_prompts, outs, spec, T,
+                             num_blocks, stream=None):
+    """pkv_attn_decode_step with the library's per-GPU device array as its
+    workspace: allocates nothing; calls overlapping on one GPU race."""
+    _check(_lib.pkv_attn_decode_step_noalloc(_ptr(k_rows), _ptr(v_rows), row_stride, _ptr(slot_map), _ptr(q),
+                                             _ptr(kcache), _ptr(vcache), _ptr(qkv), qstride, Hq, Hkv, _ptr(pos),
+                                             _ptr(tok_seq), _ptr(block_table), max_blocks, block_size, _ptr(out),
+                                             scale, _ptr(cu), int(skip_prompts), _ptr(outs), spec, T, num_blocks,
+                                             _stream(stream)), "pkv_attn_decode_step_noalloc")
 
 
 def attn_decode(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, out,
