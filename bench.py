@@ -78,6 +78,9 @@ def main():
                          "context; c4: chunked prefill of 8 x 2048 tokens over a shared 16,384-token prefix; "
                          "c5: speculative verify of 4 drafts x 16 sequences at 32k..128k context")
     ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--prefix", type=int, default=16384,
+                    help="c4: shared prefix tokens (a multiple of 64 reaches the sequences through the prefix cache; "
+                         "otherwise shared pages with the partial last page copied on write)")
     ap.add_argument("--pages", type=int, default=65536)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--wg-per-cu", type=int, default=None)
@@ -308,8 +311,16 @@ def main():
 
     copy_gbs, read_gbs = hbm_copy_probe(dev)
     cpu = None
-    if not args.no_cpu and args.config == "c3":
-        cpu = cpu_baseline(kc, vc, q, qkv, meta, steps[args.warmup], Hq, Hkv, qstride, dev)
+    st0 = steps[args.warmup]
+    if not args.no_cpu and args.config == "c3" and not e4m3:
+        cpu = cpu_baseline(kc, vc, q, qkv, meta, st0, Hq, Hkv, qstride, dev)
+    elif not args.no_cpu:
+        # c2: its one row; c3 over E4M3: 16 of the 64 rows (every 4th)
+        sample = np.arange(0, B, 4) if B > 1 else np.arange(1)
+        cpu = cpu_baseline_rows(kc, vc, q, qkv, meta.block_table, st0["pos"], st0["tok_seq"], Hq, Hkv, qstride,
+                                meta.max_blocks, sample, "every 4th sequence" if B > 1 else "the one sequence",
+                                kscale=kscale if e4m3 else None, vscale=vscale if e4m3 else None,
+                                append_rows=0 if e4m3 else B)
 
     line = {
         "metric": "paged decode step us + achieved HBM GB/s (% of peak) at batch 64, 1 MI355X",
@@ -327,8 +338,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1)*0.5 K/V/q, U[512,8192] contexts)",
+        "dtype": "e4m3 KV (bf16 q/out, f32 accum)" if e4m3 else "bf16",
+        "data": ("synthetic (random E4M3 bytes and scales, seeded N(0,1)*0.5 q, U[512,8192] contexts)" if e4m3 else
+                 "synthetic (seeded N(0,1)*0.5 K/V/q, U[512,8192] contexts)"),
         "config": {"workload": ("c3: batch-64 paged decode step (append 1 token/seq + paged decode attention)"
                                 if args.config == "c3" else
                                 "c2: single-sequence paged decode step at 4096 context (append + attention)"),
@@ -337,7 +349,7 @@ def main():
                             "reference-ABI code object (append, attn_paged_g4, attn_merge)" if args.refabi else
                             "attn_prep (norm + rotary + append), key ranges, merge" if args.with_prep else
                             "unfused (append, key ranges, merge)" if args.unfused else "fused step (one launch)"),
-                   "batch": B, "ctx": "U[512,8192]", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
+                   "batch": B, "ctx": "4096" if args.config == "c2" else "U[512,8192]", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
                    "pool_pages": pages, "seed": seed, "mean_keys_per_step": round(float(np.mean(keys)), 1),
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(kern_gbs, 1),
@@ -346,7 +358,8 @@ def main():
                      "hbm_copy_probe_gbs": round(copy_gbs, 1), "hbm_read_probe_gbs": round(read_gbs, 1),
                      "frac_of_read_probe": round(kern_gbs / read_gbs, 4),
                      "traffic": None,
-                     "traffic_profiled": None if (e4m3 or args.refabi or args.with_prep or args.unfused) else {
+                     "traffic_profiled_constant": None if (e4m3 or args.refabi or args.with_prep or args.unfused) else {
+                         "note": "quoted from the committed counter runs (seed 1), not measured by this run",
                          "source": "profiles/decode_step_c3_batch64.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, "
                                    "copy-calibrated, seed 1)",
                          "read_bytes": 1131.9e6, "write_bytes": 5.53e6, "algorithmic_bytes": 1113.9e6,
@@ -357,22 +370,33 @@ def main():
 
 
 def bench_prefill(args):
-    """Config 4: 8 sequences share a refcounted 16,384-token cached prefix
-    (the same 1,024 pages in every block table); each appends a 2,048-token
-    chunk (pkv_append) and runs causal paged attention of the chunk over
-    prefix + chunk (pkv_attn_prefill). FLOPs = 4 * 256 * Hq * sum over query
-    rows of keys attended (QK^T and PV, the reference bench-attn formula,
-    src/main.rs:950-952)."""
+    """Config 4: 8 sequences share a refcounted 16,384-token cached prefix,
+    set up through the KV manager (pkv_kv: the seed's whole 64-token units
+    cached, each sequence admitted with a prefix-cache hit so the same 1,024
+    pages sit in every block table at refs 9; --prefix not a multiple of 64
+    shares the seed's pages instead and copies the partial last page on
+    write). Each step appends every sequence's 2,048-token chunk
+    (pkv_append at the manager's slots) and runs causal paged attention of
+    the chunk over prefix + chunk (pkv_attn_prefill). FLOPs = 4 * 256 * Hq *
+    sum over query rows of keys attended (QK^T and PV, the reference
+    bench-attn formula, src/main.rs:950-952). The append is timed on its own
+    against the HBM roofline (bytes in + out)."""
     import numpy as np
     import torch
 
     import pkv
+    from pkv import synth
 
     seed = args.seed if args.seed is not None else int(time.time()) % 100000
     dev = torch.device("cuda:0")
-    Hq, Hkv, D, BS, B, P, N = 16, 4, 256, 16, 8, 16384, 2048
-    pp, cp = P // BS, N // BS
-    pages = pp + B * cp + 8
+    Hq, Hkv, D, BS, B, P, N = 16, 4, 256, 16, 8, args.prefix, 2048
+    per_seq = (P + N + BS - 1) // BS
+    pages = (P + BS - 1) // BS + B * (per_seq - P // BS) + 8
+    kv = pkv.Kv(pages, BS)
+    plan = synth.c4_kv_plan(kv, P, N, B, seed=seed)
+    st, mb = plan["step"], plan["max_blocks"]
+    bt, pos, slot, cu = st["block_table"], st["pos"], st["slot_map"], st["cu"]
+    prefix_refs = kv.refs(plan["seed_blocks"][0])
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     e4m3 = args.kv == "e4m3"
@@ -388,25 +412,22 @@ def bench_prefill(args):
     else:
         kc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
         vc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
-    rng = np.random.default_rng(seed)
-    perm = rng.permutation(pages).astype(np.int32)
-    bt = np.zeros((B, pp + cp), np.int32)
-    for s in range(B):
-        bt[s, :pp] = perm[:pp]
-        bt[s, pp:] = perm[pp + s * cp:pp + (s + 1) * cp]
+    if plan["cow"] and not e4m3:
+        # the copies on write the manager asked for, before any chunk write
+        cs = torch.from_numpy(np.array([c[0] for c in plan["cow"]], np.int32)).to(dev)
+        cd = torch.from_numpy(np.array([c[1] for c in plan["cow"]], np.int32)).to(dev)
+        pkv.page_copy(kc, vc, cs, cd, len(plan["cow"]), BS * Hkv * D * 2, pages)
     T = B * N
-    pos = np.tile(np.arange(P, P + N, dtype=np.int32), B)
-    slot = (bt[np.repeat(np.arange(B), N), pos // BS] * BS + pos % BS).astype(np.int32)
-    cu = (np.arange(B + 1) * N).astype(np.int32)
     q = (torch.randn(T, Hq, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
     qstride = (2 * Hq + 2 * Hkv) * D
     qkv = (torch.randn(T, qstride, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
     out = torch.empty(T, Hq, D, dtype=torch.bfloat16, device=dev)
-    bt_d, pos_d, cu_d, slot_d = (torch.from_numpy(a).to(dev) for a in (bt, pos, cu, slot))
+    bt_d, pos_d, cu_d, slot_d = (torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in (bt, pos, cu, slot))
     k_rows = qkv.data_ptr() + 2 * (2 * Hq * D)
     v_rows = k_rows + 2 * Hkv * D
     stream = torch.cuda.current_stream()
     evs = HipEvents(args.steps)
+    aevs = HipEvents(args.steps)
 
     if args.refabi:
         # the code object's prompt kernel, launched as the reference engine
@@ -417,11 +438,15 @@ def bench_prefill(args):
         rk = refabi.RefKernels()
         fname, fgrid, fthreads, fsmem = refabi.flash_launch(T, B, Hkv, fp8=e4m3)
         fargs = [Pa(q), Pa(kc), Pa(vc), Pa(kscale if e4m3 else None), Pa(vscale if e4m3 else None), Pa(qkv), I(qstride), I(Hq), I(Hkv), Pa(pos_d), Pa(cu_d),
-                 I(B), Pa(bt_d), I(pp + cp), I(BS), Pa(out), F(1 / 16), Pa(None), I(1)]
+                 I(B), Pa(bt_d), I(mb), I(BS), Pa(out), F(1 / 16), Pa(None), I(1)]
 
-    def step(ev=None):
+    def step(ev=None, aev=None):
         if not e4m3:
+            if aev:
+                aevs.record(aev[0], stream.cuda_stream)
             pkv.append(k_rows, v_rows, qstride * 2, slot_d, T, Hkv, D * 2, kc, vc, pages * BS)
+            if aev:
+                aevs.record(aev[1], stream.cuda_stream)
         if args.refabi:
             if ev:
                 evs.record(ev[0], stream.cuda_stream)
@@ -432,10 +457,10 @@ def bench_prefill(args):
         if ev:
             pkv.time_next_prefill_kernel(ev[0], ev[1])
         if e4m3:
-            pkv.attn_prefill_e4m3(q, kc, vc, kscale, vscale, qkv, qstride, Hq, Hkv, pos_d, cu_d, B, bt_d, pp + cp, BS,
+            pkv.attn_prefill_e4m3(q, kc, vc, kscale, vscale, qkv, qstride, Hq, Hkv, pos_d, cu_d, B, bt_d, mb, BS,
                                   out, 1 / 16, None, 1, T, pages)
             return
-        pkv.attn_prefill(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d, cu_d, B, bt_d, pp + cp, BS, out, 1 / 16, None, 1,
+        pkv.attn_prefill(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d, cu_d, B, bt_d, mb, BS, out, 1 / 16, None, 1,
                          T, pages)
 
     for _ in range(args.warmup):
@@ -444,7 +469,7 @@ def bench_prefill(args):
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
     for k in range(args.steps):
-        step(evs.pairs[k])
+        step(evs.pairs[k], aevs.pairs[k])
     t1.record(stream)
     torch.cuda.synchronize()
     ms_step = t0.elapsed_time(t1) / args.steps
@@ -452,6 +477,19 @@ def bench_prefill(args):
     flops = 4.0 * D * Hq * float((pos.astype(np.int64) + 1).sum())
     kern_us = 1e3 * sum(kern_ms) / len(kern_ms)
     tflops = flops / (kern_us * 1e-6) / 1e12
+    append = None
+    if not e4m3:
+        app_ms = aevs.elapsed_ms()
+        app_us = 1e3 * float(np.median(app_ms))
+        app_bytes = synth.algorithmic_bytes_append(T, Hkv)
+        append = {"kernel": "append_kernel (events around the launch)", "bytes": app_bytes,
+                  "median_us": round(app_us, 2), "achieved": round(app_bytes / (app_us * 1e-6) / 1e9, 1),
+                  "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                  "frac": round(app_bytes / (app_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_prefill(kc, vc, q, qkv, bt, pos, cu, B, Hq, Hkv, qstride, mb, flops, e4m3,
+                                   kscale if e4m3 else None, vscale if e4m3 else None)
     line = {
         "metric": "chunked-prefill attention TFLOP/s over paged context (config 4), 1 MI355X",
         "value": round(tflops, 1),
@@ -463,20 +501,26 @@ def bench_prefill(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1)*0.5)",
-        "config": {"workload": "c4: 8 seqs x 2048-token chunk over a shared 16,384-token prefix (append + prefill)",
+        "dtype": "e4m3 KV (bf16 MFMA, f32 accum)" if e4m3 else "bf16",
+        "data": ("synthetic (random E4M3 bytes and scales; q N(0,1)*0.5)" if e4m3 else
+                 "synthetic (seeded N(0,1)*0.5)"),
+        "config": {"workload": (f"c4: 8 seqs x 2048-token chunk over a shared {P}-token prefix through the KV "
+                                f"manager ({'prefix-cache hits' if plan['via_cache'] else 'shared pages, partial page copied on write'}; "
+                                + ("prefill kernel only, no append)" if e4m3 else "append + prefill)")),
                    "kv": args.kv, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS, "flop_per_step": flops,
+                   "prefix": P, "prefix_page_refs": prefix_refs, "cow_copies": len(plan["cow"]),
                    "seed": seed, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": (f"{fname} (reference ABI, events around the launch)" if args.refabi
                                                   else "prefill_e4m3_kernel" if e4m3 else "prefill_kernel"),
                      "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "avg_us": round(kern_us, 1), "traffic": None,
-                     "traffic_profiled": None if args.refabi or e4m3 else {
+                     "traffic_profiled_constant": None if args.refabi or e4m3 else {
+                         "note": "quoted from the committed counter runs (seed 1), not measured by this run",
                          "source": "profiles/prefill_c4_shared_prefix.md (rocprofv3 --pmc, copy-calibrated, seed 1)",
-                         "read_bytes": 1.34e9, "write_bytes": 138e6, "note": "MFMA-bound: 0.30 TB/s of HBM"}},
-        "cpu_baseline": None,
+                         "read_bytes": 1.34e9, "write_bytes": 138e6, "note_hbm": "MFMA-bound: 0.30 TB/s of HBM"}},
+        "append": append,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
@@ -591,6 +635,13 @@ def bench_verify(args):
     # per-token decode attention on the same steps (each row re-reads its pages)
     Kd = min(args.steps, 20)
     dec_ms, _ = timed(decode_fn, args.warmup, Kd)
+    cpu = None
+    if not args.no_cpu:
+        # every row of 4 of the 16 sequences (the 1st, 5th, 9th and 13th)
+        sample = np.concatenate([np.arange(s_ * n, s_ * n + n) for s_ in range(0, B, 4)])
+        cpu = cpu_baseline_rows(kc, vc, q, qkv, bt, pos[args.warmup], seqs.astype(np.int32), Hq, Hkv, qstride, mb,
+                                sample, "every row of sequences 0, 4, 8, 12", kscale=kscale if e4m3 else None,
+                                vscale=vscale if e4m3 else None, append_rows=0 if e4m3 else T)
     line = {
         "metric": "speculative verify step us + achieved HBM GB/s over unique KV bytes (config 5), 1 MI355X",
         "value": round(gbs, 1),
@@ -605,9 +656,12 @@ def bench_verify(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1)*0.5 K/V/q, U[32768,131072] contexts, seeded accepted counts)",
-        "config": {"workload": "c5: 16 seqs x 4 draft rows, append + verify attention + rewind",
+        "dtype": "e4m3 KV (bf16 q/out, f32 accum)" if e4m3 else "bf16",
+        "data": ("synthetic (random E4M3 bytes and scales, q N(0,1)*0.5, U[32768,131072] contexts, seeded accepted "
+                 "counts)" if e4m3 else
+                 "synthetic (seeded N(0,1)*0.5 K/V/q, U[32768,131072] contexts, seeded accepted counts)"),
+        "config": {"workload": ("c5: 16 seqs x 4 draft rows over an E4M3 cache, verify attention + rewind (no append)"
+                                if e4m3 else "c5: 16 seqs x 4 draft rows, append + verify attention + rewind"),
                    "kv": args.kv, "batch": B, "drafts": n, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
                    "pool_pages": pages, "seed": seed, "mean_unique_keys_per_step": round(float(np.mean(keys)), 1),
                    "parallelism": "single GPU"},
@@ -615,10 +669,11 @@ def bench_verify(args):
                      "verify_range_kernel", "achieved": round(kern_gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
                      "avg_us": round(kern_avg_us, 2), "traffic": None,
-                     "traffic_profiled": None if e4m3 else {
+                     "traffic_profiled_constant": None if e4m3 else {
+                         "note": "quoted from the committed counter runs (seed 1), not measured by this run",
                          "source": "profiles/verify_step_c5_batch16.md (rocprofv3 --pmc, copy-calibrated, seed 1)",
                          "read_bytes": 5.502e9, "write_bytes": 17.9e6, "algorithmic_bytes": 5.48e9, "ratio": 1.007}},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
@@ -745,14 +800,193 @@ def cpu_baseline(kc, vc, q, qkv, meta, st, Hq, Hkv, qstride, dev):
             "cpu": _cpu_model()}
 
 
+def _host_pages(tensors, bt, need):
+    """Host copies (numpy) of the pages sequence s uses (bt[s, :need[s]]) from
+    device pools shaped [pages * 16][...], gathered once each, and bt
+    remapped to them."""
+    import numpy as np
+    import torch
+
+    rows = [bt[s, :int(n)] for s, n in enumerate(need)]
+    sub = np.unique(np.concatenate(rows))
+    out = []
+    for t in tensors:
+        idx = torch.from_numpy(sub.astype(np.int64)).to(t.device)
+        x = t.view(-1, 16, *t.shape[1:])[idx].cpu()
+        x = (x.view(torch.int16).numpy().view(np.uint16) if x.dtype == torch.bfloat16 else x.numpy())
+        out.append(np.ascontiguousarray(x.reshape(-1, *t.shape[1:])))
+    where = np.full(int(bt.max()) + 1, -1, np.int64)
+    where[sub] = np.arange(len(sub))
+    bt_h = np.zeros(bt.shape, np.int32)
+    for s, r in enumerate(rows):
+        bt_h[s, :len(r)] = where[r]
+    return out, bt_h
+
+
+def _bits(x):
+    import numpy as np
+    import torch
+    return x.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def _cpu_rates(items, run, weight, budget1=10.0, budget_mt=5.0):
+    """Oracle throughput in work units per second: on 1 thread (items in
+    order, cycling, until budget1 seconds) and on up to 16 threads (items
+    spread over a thread pool, ctypes releasing the GIL, until budget_mt).
+    Returns (rate_1, rate_mt, threads, detail)."""
+    import concurrent.futures
+    nthr = max(1, min(16, os.cpu_count() or 1, len(items)))
+    done, i, t = 0.0, 0, time.perf_counter()
+    while True:
+        run(items[i % len(items)])
+        done += weight(items[i % len(items)])
+        i += 1
+        t1 = time.perf_counter() - t
+        if t1 >= budget1:
+            break
+    rate1 = done / t1
+    detail = f"1 thread: {i} units in {t1:.1f} s"
+    if nthr == 1:
+        return rate1, rate1, 1, detail
+    done_mt, rounds, t = 0.0, 0, time.perf_counter()
+    with concurrent.futures.ThreadPoolExecutor(nthr) as ex:
+        while True:
+            list(ex.map(run, items))
+            done_mt += sum(weight(x) for x in items)
+            rounds += 1
+            tm = time.perf_counter() - t
+            if tm >= budget_mt:
+                break
+    detail += f"; {nthr} threads: {rounds} rounds of {len(items)} units in {tm:.1f} s"
+    return rate1, done_mt / tm, nthr, detail
+
+
+def cpu_baseline_prefill(kc, vc, q, qkv, bt, pos, cu, B, Hq, Hkv, qstride, mb, flops, e4m3, kscale, vscale):
+    """The oracle's chunked prefill (scalar C, f64 softmax) on a bounded
+    sample of config 4: groups of 2 query rows spread over all sequences and
+    positions, timed on 1 thread and on up to 16, scaled to the step's
+    FLOPs; plus the oracle's append of the step's 16,384 K/V rows (timed
+    once, added to both). E4M3 caches are not timed on the host (null)."""
+    import numpy as np
+
+    import oracle
+    if e4m3:
+        return None
+    BS, D = 16, 256
+    need = np.full(B, mb)
+    (kc_h, vc_h), bt_h = _host_pages([kc, vc], bt, need)
+    q_h, qkv_h = _bits(q), _bits(qkv)
+    rng = np.random.default_rng(0)
+    N = int(cu[1] - cu[0])
+    items = []
+    for s in range(B):
+        for j in rng.choice(N // 2, 4, replace=False):
+            rows = np.array([cu[s] + 2 * j, cu[s] + 2 * j + 1])
+            items.append((s, rows))
+
+    def run(it):
+        s, rows = it
+        oracle.attn_prefill(np.ascontiguousarray(q_h[rows]), kc_h, vc_h, np.ascontiguousarray(qkv_h[rows]), qstride,
+                            Hq, Hkv, pos[rows], np.array([0, len(rows)], np.int32), 1,
+                            np.ascontiguousarray(bt_h[s:s + 1]), mb, BS, 1 / 16)
+
+    def weight(it):
+        return 4.0 * D * Hq * float((pos[it[1]].astype(np.int64) + 1).sum())
+
+    rate1, rate_mt, nthr, detail = _cpu_rates(items, run, weight)
+    T = len(pos)
+    kn = np.ascontiguousarray(qkv_h[:, 2 * Hq * D:2 * Hq * D + Hkv * D])
+    vn = np.ascontiguousarray(qkv_h[:, 2 * Hq * D + Hkv * D:2 * Hq * D + 2 * Hkv * D])
+    slot_h = np.zeros(T, np.int32)  # the host pool holds the used pages only: append into its first slots
+    slot_h[:] = np.arange(T) % (kc_h.shape[0])
+    t = time.perf_counter()
+    oracle.append(kn, vn, slot_h, kc_h, vc_h)
+    app_s = time.perf_counter() - t
+    us1 = (flops / rate1 + app_s) * 1e6
+    us_mt = (flops / rate_mt + app_s) * 1e6
+    return {"value": round(us_mt, 1), "unit": "us/step", "cores": nthr, "kind": "port",
+            "sample": f"oracle prefill of {len(items)} groups of 2 query rows (4 per sequence, all 8 sequences) "
+                      f"scaled by FLOPs to the full step ({flops:.3e} FLOP), plus the oracle append of all {T} "
+                      f"K/V rows ({app_s * 1e3:.0f} ms); {detail}",
+            "single_thread_us_per_step": round(us1, 1),
+            "tflops_single_thread": round(rate1 / 1e12, 6), "tflops_threads": round(rate_mt / 1e12, 6),
+            "cpu": _cpu_model()}
+
+
+def cpu_baseline_rows(kc, vc, q, qkv, bt, pos, tok_seq, Hq, Hkv, qstride, mb, sample_rows, what, kscale=None,
+                      vscale=None, append_rows=0):
+    """The oracle's paged decode attention (per row, scalar C) on a bounded
+    sample of the step's rows (sample_rows, each row one work unit weighted
+    by its keys), timed on 1 thread and on up to 16 and scaled by keys to
+    the whole step, plus the oracle append of append_rows K/V rows. E4M3
+    caches (kscale given) run oracle.attn_decode8."""
+    import numpy as np
+    import torch
+
+    import oracle
+    BS, D = 16, 256
+    seqs = np.unique(tok_seq[sample_rows])
+    need = np.zeros(len(seqs), np.int64)
+    for i, s in enumerate(seqs):
+        need[i] = int(pos[sample_rows][tok_seq[sample_rows] == s].max()) // BS + 1
+    tens = [kc, vc] + ([kscale, vscale] if kscale is not None else [])
+    hosts, bt_h = _host_pages(tens, bt[seqs], need)
+    remap = {int(s): i for i, s in enumerate(seqs)}
+    q_h = _bits(q[torch.from_numpy(np.asarray(sample_rows)).to(q.device)])
+    qkv_h = _bits(qkv[torch.from_numpy(np.asarray(sample_rows)).to(q.device)])
+    items = list(range(len(sample_rows)))
+
+    def run(i):
+        r = sample_rows[i]
+        args8 = (hosts[2], hosts[3]) if kscale is not None else ()
+        fn = oracle.attn_decode8 if kscale is not None else oracle.attn_decode
+        fn(np.ascontiguousarray(q_h[i:i + 1]), hosts[0], hosts[1], *args8, np.ascontiguousarray(qkv_h[i:i + 1]),
+           qstride, Hq, Hkv, np.array([pos[r]], np.int32), np.array([remap[int(tok_seq[r])]], np.int32), bt_h, mb,
+           BS, 1 / 16)
+
+    def weight(i):
+        return float(pos[sample_rows[i]] + 1)
+
+    rate1, rate_mt, nthr, detail = _cpu_rates(items, run, weight)
+    keys = float((pos.astype(np.int64) + 1).sum())
+    app_s = 0.0
+    if append_rows and kscale is None:
+        kn = np.ascontiguousarray(qkv_h[:1, 2 * Hq * D:2 * Hq * D + Hkv * D].repeat(append_rows, 0))
+        slot_h = (np.arange(append_rows) % hosts[0].shape[0]).astype(np.int32)
+        t = time.perf_counter()
+        oracle.append(kn, kn, slot_h, hosts[0], hosts[1])
+        app_s = time.perf_counter() - t
+    us1 = (keys / rate1 + app_s) * 1e6
+    us_mt = (keys / rate_mt + app_s) * 1e6
+    return {"value": round(us_mt, 1), "unit": "us/step", "cores": nthr, "kind": "port",
+            "sample": f"oracle {'E4M3 ' if kscale is not None else ''}decode attention of {len(sample_rows)} of the "
+                      f"step's {len(pos)} rows ({what}), scaled by keys to the whole step ({int(keys)} keys)"
+                      + (f", plus the oracle append of {append_rows} K/V rows" if append_rows else "")
+                      + f"; {detail}",
+            "single_thread_us_per_step": round(us1, 1),
+            "cpu": _cpu_model()}
+
+
 def _cpu_model():
+    """The host CPU as /proc/cpuinfo names it (model name, family, model,
+    stepping of the first processor entry) with the logical CPU count and
+    the CPUs this process may run on."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break
+            k, _, v = line.partition(":")
+            fields[k.strip()] = v.strip()
     except OSError:
         pass
-    return "unknown"
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = None
+    return (f"{fields.get('model name', 'unknown')} (family {fields.get('cpu family', '?')}, model "
+            f"{fields.get('model', '?')}, stepping {fields.get('stepping', '?')}; {os.cpu_count()} logical CPUs, "
+            f"{allowed} allowed to this process)")
 
 
 if __name__ == "__main__":

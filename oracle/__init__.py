@@ -50,6 +50,8 @@ _lib.orc_attn_partial.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P, _I, _I, _I, _F
 _lib.orc_merge.argtypes = [_P, _P, _P, _I, _P]
 _lib.orc_attn_prefill.restype = _I
 _lib.orc_attn_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I]
+_lib.orc_attn_prefill_t.restype = _I
+_lib.orc_attn_prefill_t.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I, _I]
 _lib.orc_mtp_slots.argtypes = [_P, _P, _P, _I, _I, _P, _I, _P, _P, _I]
 _lib.orc_mtp_next.argtypes = [_P, _P, _P, _I, _P, _I, _I, _P, _I, _P, _P, _P, _I]
 _lib.orc_attn_prep.argtypes = [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _F, _I, _L, _P, _P, _P]
@@ -60,7 +62,7 @@ _lib.orc_f_to_e4m3.argtypes = [_F]
 _lib.orc_store_e4m3.argtypes = [_P, _P, _P]
 _lib.orc_attn_prep8.argtypes = [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _F, _I, _L, _P, _P, _P, _P, _P]
 _lib.orc_attn_prefill8.restype = _I
-_lib.orc_attn_prefill8.argtypes = [_P, _P, _P, _P, _P, _L, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F]
+_lib.orc_attn_prefill8.argtypes = [_P, _P, _P, _P, _P, _L, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _I]
 _lib.orc_attn_decode8.restype = _I
 _lib.orc_attn_decode8.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _F, _P, _I, _P, _I, _I]
 
@@ -159,14 +161,19 @@ def merge(Ms, Ss, As):
     return o
 
 
+P_TILE = 32  # the reference's prefill key tile (AM_BN, amd/attention.cuh:10)
+
+
 def attn_prefill(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks, block_size, scale,
-                 outs=None, spec=1, out=None):
+                 outs=None, spec=1, out=None, p_tile=P_TILE):
+    """Chunked prefill. p_tile = 32 (default): the reference's tiled softmax
+    with P rounded to bf16 for P.V; p_tile = 0: P in double (textbook)."""
     T = len(pos)
     if out is None:
         out = np.zeros((T, Hq, 256), np.uint16)
     pos, cu, block_table, outs = _i32(pos), _i32(cu), _i32(block_table), _i32(outs)
-    _lib.orc_attn_prefill(_p(q), _p(kcache), _p(vcache), _p(qkv), qstride, Hq, Hkv, _p(pos), _p(cu), seqs,
-                          _p(block_table), max_blocks, block_size, _p(out), scale, _p(outs), spec)
+    _lib.orc_attn_prefill_t(_p(q), _p(kcache), _p(vcache), _p(qkv), qstride, Hq, Hkv, _p(pos), _p(cu), seqs,
+                            _p(block_table), max_blocks, block_size, _p(out), scale, _p(outs), spec, p_tile)
     return out
 
 
@@ -262,7 +269,7 @@ def attn_decode8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, pos
 
 
 def attn_prefill8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,
-                  block_size, scale, out=None):
+                  block_size, scale, out=None, p_tile=P_TILE):
     """Chunked prefill over an E4M3 cache (reference attn_group8)."""
     T = len(pos)
     if out is None:
@@ -272,5 +279,5 @@ def attn_prefill8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, po
     vscale = np.ascontiguousarray(vscale, np.float32)
     num_slots = kcache8.size // (Hkv * 256)
     _lib.orc_attn_prefill8(_p(q), _p(kcache8), _p(vcache8), _p(kscale), _p(vscale), num_slots, _p(qkv), qstride, Hq,
-                           Hkv, _p(pos), _p(cu), seqs, _p(block_table), max_blocks, block_size, _p(out), scale)
+                           Hkv, _p(pos), _p(cu), seqs, _p(block_table), max_blocks, block_size, _p(out), scale, p_tile)
     return out

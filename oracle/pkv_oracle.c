@@ -34,10 +34,14 @@
  *       0 leaves rows unrotated; a rotation keeps each pair's norm; the axis
  *       rule picks height/width positions for exactly the frequencies
  *       d % 3 == 1 / 2 below 3 sec_h / 3 sec_w), v copied bit for bit.
- *   Parity unpinned beyond the stated tolerance: the reference GPU kernels'
- *   exact bf16 rounding of P inside the prefill tiles (amd/attention.cuh:115)
- *   and expf vs exp2f last bits; in attn_prep the f32 order of the squared
- *   sum and the last bits of cosf/sinf (1 bf16 ulp).
+ *   prefill with the reference's P rounding (p_tile = 32): a 3-key closed
+ *       form where a new fractional max in the second tile moves the anchor
+ *       (any other anchoring or rounding point gives other bits), and exact
+ *       equality with the textbook softmax when every p is a power of two.
+ *   Parity unpinned beyond the stated tolerance: expf vs exp2f last bits
+ *   (the reference's fast_exp2 against exp2 in double), f32 against double
+ *   accumulation order; in attn_prep the f32 order of the squared sum and
+ *   the last bits of cosf/sinf (1 bf16 ulp).
  *
  * Arithmetic: softmax and weighted sums in double; the epilogue follows the
  * reference exactly in f32: o = bf16_round(A / S); y = o / (1 + expf(-gate));
@@ -245,12 +249,20 @@ void orc_merge(const double* M, const double* S, const double* A, int n, double*
  * kp <= qp and kp < L, attention.cuh:81-89; with positions contiguous within
  * the chunk that is kp <= pos[t]). The query is rounded to bf16 after scaling
  * by scale * log2(e) as the reference does (amd/attention.cuh:37-44); scores
- * are exp2-domain. The bf16 rounding of P before P.V (attention.cuh:115) is
- * NOT restated: P is kept in double. Gated epilogue as decode. Returns the
- * number of token rows written. ---- */
-int orc_attn_prefill(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, const uint16_t* qkv,
-                     int qstride, int Hq, int Hkv, const int* pos, const int* cu, int seqs, const int* block_table,
-                     int max_blocks, int block_size, uint16_t* out, float scale, const int* outs, int spec) {
+ * are exp2-domain. Gated epilogue as decode.
+ * p_tile = 0 keeps P in double (textbook softmax: the form the torch SDPA
+ * goldens pin). p_tile = 32 restates the reference's tiled online softmax
+ * (attention.cuh:55-121 with AM_BN = 32, attention.cuh:10): keys in tiles
+ * [k0, k0 + 32) from key 0; after each tile the anchor b = running max
+ * (over keys seen so far), p = exp2(s - b); the denominator adds p
+ * unrounded (attention.cuh:101-107), P.V takes p rounded to bf16
+ * (pack4, attention.cuh:115), and earlier sums are rescaled by
+ * exp2(b_old - b) (attention.cuh:108-110). Returns the number of token rows
+ * written. ---- */
+int orc_attn_prefill_t(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, const uint16_t* qkv,
+                       int qstride, int Hq, int Hkv, const int* pos, const int* cu, int seqs, const int* block_table,
+                       int max_blocks, int block_size, uint16_t* out, float scale, const int* outs, int spec,
+                       int p_tile) {
     const double LOG2E = 1.4426950408889634;
     const int G = Hq / Hkv;
     int rows = 0;
@@ -276,11 +288,33 @@ int orc_attn_prefill(const uint16_t* q, const uint16_t* kcache, const uint16_t* 
                 }
                 double S = 0.0;
                 for (int d = 0; d < HEAD_DIM; d++) A[d] = 0.0;
-                for (int j = 0; j < L; j++) {
-                    const double p = exp2(sc[j] - m);
-                    S += p;
-                    const size_t at = ((size_t)orc_slot(bt, j, block_size) * Hkv + kvh) * HEAD_DIM;
-                    for (int d = 0; d < HEAD_DIM; d++) A[d] += p * orc_b2f(vcache[at + d]);
+                if (p_tile > 0) {
+                    /* the reference's tiles: anchor b after each tile, bf16 P in P.V */
+                    double b = -INFINITY;
+                    for (int k0 = 0; k0 < L; k0 += p_tile) {
+                        const int k1 = k0 + p_tile < L ? k0 + p_tile : L;
+                        double bn = b;
+                        for (int j = k0; j < k1; j++)
+                            if (sc[j] > bn) bn = sc[j];
+                        const double c = exp2(b - bn); /* 0 on the first tile (b = -inf) */
+                        S *= c;
+                        for (int d = 0; d < HEAD_DIM; d++) A[d] *= c;
+                        b = bn;
+                        for (int j = k0; j < k1; j++) {
+                            const double p = exp2(sc[j] - b);
+                            S += p;
+                            const double pb = orc_b2f(orc_f2b((float)p));
+                            const size_t at = ((size_t)orc_slot(bt, j, block_size) * Hkv + kvh) * HEAD_DIM;
+                            for (int d = 0; d < HEAD_DIM; d++) A[d] += pb * orc_b2f(vcache[at + d]);
+                        }
+                    }
+                } else {
+                    for (int j = 0; j < L; j++) {
+                        const double p = exp2(sc[j] - m);
+                        S += p;
+                        const size_t at = ((size_t)orc_slot(bt, j, block_size) * Hkv + kvh) * HEAD_DIM;
+                        for (int d = 0; d < HEAD_DIM; d++) A[d] += p * orc_b2f(vcache[at + d]);
+                    }
                 }
                 for (int d = 0; d < HEAD_DIM; d++) {
                     const float gate = orc_b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d]);
@@ -292,6 +326,13 @@ int orc_attn_prefill(const uint16_t* q, const uint16_t* kcache, const uint16_t* 
         }
     }
     return rows;
+}
+
+int orc_attn_prefill(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, const uint16_t* qkv,
+                     int qstride, int Hq, int Hkv, const int* pos, const int* cu, int seqs, const int* block_table,
+                     int max_blocks, int block_size, uint16_t* out, float scale, const int* outs, int spec) {
+    return orc_attn_prefill_t(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,
+                              block_size, out, scale, outs, spec, 0);
 }
 
 /* ---- draft-token (speculative verify) metadata (mtp_next, qwen35.cu:2633-2650):
@@ -502,7 +543,7 @@ int orc_attn_decode8(const uint16_t* q, const uint8_t* kcache8, const uint8_t* v
 int orc_attn_prefill8(const uint16_t* q, const uint8_t* kcache8, const uint8_t* vcache8, const float* kscale,
                       const float* vscale, long num_slots, const uint16_t* qkv, int qstride, int Hq, int Hkv,
                       const int* pos, const int* cu, int seqs, const int* block_table, int max_blocks,
-                      int block_size, uint16_t* out, float scale) {
+                      int block_size, uint16_t* out, float scale, int p_tile) {
     const size_t n = (size_t)num_slots * Hkv;
     uint16_t* kb = (uint16_t*)malloc(n * HEAD_DIM * 2);
     uint16_t* vb = (uint16_t*)malloc(n * HEAD_DIM * 2);
@@ -511,8 +552,8 @@ int orc_attn_prefill8(const uint16_t* q, const uint8_t* kcache8, const uint8_t* 
             kb[r * HEAD_DIM + d] = orc_f2b(orc_e4m3_to_f(kcache8[r * HEAD_DIM + d]) * kscale[r]);
             vb[r * HEAD_DIM + d] = orc_f2b(orc_e4m3_to_f(vcache8[r * HEAD_DIM + d]) * vscale[r]);
         }
-    const int rc = orc_attn_prefill(q, kb, vb, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,
-                                    block_size, out, scale, NULL, 1);
+    const int rc = orc_attn_prefill_t(q, kb, vb, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,
+                                      block_size, out, scale, NULL, 1, p_tile);
     free(kb);
     free(vb);
     return rc;

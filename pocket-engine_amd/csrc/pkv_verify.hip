@@ -20,9 +20,10 @@
 //     bytes at dims 32c + 8 (l / 16) for c = 0..7 (each instruction reads 64
 //     contiguous bytes of 16 key rows; two consecutive ones a full 128-byte
 //     line). B = Q^T with the same dims, held in registers for the piece.
-//   O^T[256 dims][16 cols] += V^T P^T  16 x v_mfma_f32_16x16x16_bf16
-//     B = P^T is the S^T accumulator itself, rounded to bf16 (lane l holds
-//     keys 4 (l / 16) + i of column l % 16 in both layouts). A = V^T comes
+//   O^T[256 dims][16 cols] += V^T P^T  32 x v_mfma_f32_16x16x16_bf16
+//     B = P^T is the S^T accumulator itself (lane l holds keys 4 (l / 16) + i
+//     of column l % 16 in both layouts), as a bf16 high part and a bf16
+//     remainder in two MFMAs (32 per page). A = V^T comes
 //     from the page's V staged row-major in LDS (one fully coalesced 512-byte
 //     row per half-wave load) through ds_read_b64_tr_b16, which transposes
 //     4 x 4 blocks of 16-bit values on the way out of LDS.
@@ -154,21 +155,28 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
         float pr[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) pr[i] = __builtin_amdgcn_exp2f(sc[i] - mref);
-        const uint32_t p01 = pack2_hw(pr[0], pr[1]), p23 = pack2_hw(pr[2], pr[3]);
-        // the denominator sums the same bf16 weights P.V uses
-        l = l * corr + ((bf_lo(p01) + bf_hi(p01)) + (bf_lo(p23) + bf_hi(p23)));
+        // P^T as a bf16 high part plus a bf16 remainder (two MFMAs, ~16
+        // mantissa bits): decode rows keep their weights in f32 (the
+        // reference's attn_paged_g4), which one bf16 per weight would miss by
+        // up to 2^-9 relative; the denominator sums the f32 weights.
+        const uint32_t h01 = pack2_hw(pr[0], pr[1]), h23 = pack2_hw(pr[2], pr[3]);
+        const uint32_t r01 = pack2_hw(pr[0] - bf_lo(h01), pr[1] - bf_hi(h01));
+        const uint32_t r23 = pack2_hw(pr[2] - bf_lo(h23), pr[3] - bf_hi(h23));
+        l = l * corr + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
         m = mn;
         if (__any(corr != 1.f)) {
 #pragma unroll
             for (int db = 0; db < 16; db++) acc[db] *= corr;
         }
-        const s16x4 pb = __builtin_bit_cast(s16x4, make_uint2(p01, p23));
+        const s16x4 pb_hi = __builtin_bit_cast(s16x4, make_uint2(h01, h23));
+        const s16x4 pb_lo = __builtin_bit_cast(s16x4, make_uint2(r01, r23));
         wave_sync();  // V staged
 #pragma unroll
         for (int db = 0; db < 16; db++) {
             const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) s16x4*)(tr + 16 * db));
-            acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb, acc[db], 0, 0, 0);
+            acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb_hi, acc[db], 0, 0, 0);
+            acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb_lo, acc[db], 0, 0, 0);
         }
         wave_sync();  // reads done before the next page is staged
     };

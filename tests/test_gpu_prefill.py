@@ -15,7 +15,7 @@ import torch
 
 import oracle
 import pkv
-from _util import BS, D, bf16_bits, close, decode_case, nan_stale
+from _util import BS, D, bf16_bits, bits, close, decode_case, host_pages, nan_stale, run_threads
 
 pytestmark = pytest.mark.gpu
 SCALE = 1.0 / 16.0
@@ -135,65 +135,103 @@ def test_prefill_leaves_decode_rows_untouched(dev):
     assert ok, err
 
 
-def test_prefill_c4_shared_prefix_sampled_rows(dev):
-    """Config 4: 8 sequences share a 16,384-token cached prefix (the same
-    1,024 pages in every block table) and each feeds a 2,048-token chunk.
-    Sampled rows against the oracle; each chunk's last row against the paged
-    decode kernel on the same cache."""
-    print("case prefill c4", flush=True)
-    Hq, Hkv, B, P, N = 16, 4, 8, 16384, 2048
-    pp, cp = P // BS, N // BS
-    pages = pp + B * cp + 8
+def test_prefill_c4_through_kv_manager(dev):
+    """Config 4 through the KV manager at full size, with a prefix that ends
+    inside a page (16,392 tokens): a seed sequence holds the prefix (written
+    by pkv_append) and caches its whole 64-token units; 8 sequences share
+    its pages (pkv_kv_share), copy the shared partial page on write
+    (pkv_kv_prepare_write + pkv_page_copy) and feed a 2,048-token chunk
+    each (pkv_kv_fill's slots, pkv_append, pkv_attn_prefill). Checks: the
+    copies' bytes (the prefix's 8 slots as the seed wrote them, then the
+    chunk's first rows) and the seed's page left as it was; refcounts (the
+    prefix's whole pages at 9 = the cache entry + 8 sequences once the seed
+    is released, each copy at 1, the seed's partial page freed); 1,024 rows
+    (4 in every 64-row query tile of every sequence) against the oracle's
+    prefill; each chunk's last row against the paged decode kernel."""
+    from pkv import synth
+    print("case prefill c4 through the KV manager, prefix 16392", flush=True)
+    Hq, Hkv, B, P, N = 16, 4, 8, 16392, 2048
+    qstride = (2 * Hq + 2 * Hkv) * D
+    per_seq = (P + N + BS - 1) // BS
+    pages = (P + BS - 1) // BS + B * (per_seq - P // BS) + 16
+    kv = pkv.Kv(pages, BS)
+    plan = synth.c4_kv_plan(kv, P, N, B, seed=11, release_seed=False)
+    st, mb = plan["step"], plan["max_blocks"]
+    assert not plan["via_cache"] and len(plan["cow"]) == B
+    partial = plan["seed_blocks"][-1]
+    assert all(src_ == partial for src_, _ in plan["cow"])
     gen = torch.Generator(device=dev)
     gen.manual_seed(11)
     kc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
     vc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
-    rng = np.random.default_rng(11)
-    perm = rng.permutation(pages).astype(np.int32)
-    shared = perm[:pp]
-    bt = np.zeros((B, pp + cp), np.int32)
-    for s in range(B):
-        bt[s, :pp] = shared
-        bt[s, pp:] = perm[pp + s * cp:pp + (s + 1) * cp]
+    pk = (torch.randn(P, Hkv * D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    pv = (torch.randn(P, Hkv * D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
     T = B * N
-    pos = np.tile(np.arange(P, P + N, dtype=np.int32), B)
-    cu = (np.arange(B + 1) * N).astype(np.int32)
     q = (torch.randn(T, Hq, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
-    qstride = (2 * Hq + 2 * Hkv) * D
     qkv = torch.randn(T, qstride, device=dev, generator=gen).to(torch.bfloat16)
     out = torch.zeros(T, Hq, D, dtype=torch.bfloat16, device=dev)
-    bt_d, pos_d, cu_d = i32(bt, dev), i32(pos, dev), i32(cu, dev)
-    pkv.attn_prefill(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d, cu_d, B, bt_d, pp + cp, BS, out, SCALE, None, 1, T,
-                     pages)
+    pos, slot, cu, bt = st["pos"], st["slot_map"], st["cu"], st["block_table"]
+    pos_d, cu_d, bt_d = i32(pos, dev), i32(cu, dev), i32(bt, dev)
+    k_rows = qkv.data_ptr() + 2 * (2 * Hq * D)
+    v_rows = k_rows + 2 * Hkv * D
+    # device work in stream order: prefix rows, copies on write, the chunk, prefill
+    pkv.append(pk, pv, Hkv * D * 2, i32(plan["prefix_slots"], dev), P, Hkv, D * 2, kc, vc, pages * BS)
+    page_before = (bits(kc.view(pages, BS, Hkv, D)[partial]), bits(vc.view(pages, BS, Hkv, D)[partial]))
+    src = [c_[0] for c_ in plan["cow"]]
+    dst = [c_[1] for c_ in plan["cow"]]
+    pkv.page_copy(kc, vc, i32(src, dev), i32(dst, dev), B, BS * Hkv * D * 2, pages)
+    pkv.append(k_rows, v_rows, qstride * 2, i32(slot, dev), T, Hkv, D * 2, kc, vc, pages * BS)
+    pkv.attn_prefill(q, kc, vc, qkv, qstride, Hq, Hkv, pos_d, cu_d, B, bt_d, mb, BS, out, SCALE, None, 1, T, pages)
     torch.cuda.synchronize()
-    # (1) the last row of every chunk against paged decode attention (the
-    # decode kernel does not round q; within tolerance of each other)
+    # copies on write: bytes and the tables
+    off = P % BS
+    kq = bits(qkv[:, 2 * Hq * D:2 * Hq * D + Hkv * D]).reshape(T, Hkv, D)
+    vq = bits(qkv[:, 2 * Hq * D + Hkv * D:2 * Hq * D + 2 * Hkv * D]).reshape(T, Hkv, D)
+    assert np.array_equal(bits(kc.view(pages, BS, Hkv, D)[partial]), page_before[0]), "seed's page changed"
+    assert np.array_equal(bits(vc.view(pages, BS, Hkv, D)[partial]), page_before[1])
+    for s, d_ in enumerate(dst):
+        assert bt[s, P // BS] == d_ and d_ not in plan["seed_blocks"]
+        for cache, pre, new in ((kc, page_before[0], kq), (vc, page_before[1], vq)):
+            got_page = bits(cache.view(pages, BS, Hkv, D)[d_])
+            assert np.array_equal(got_page[:off], pre[:off]), f"sequence {s}: copied prefix slots differ"
+            assert np.array_equal(got_page[off:], new[cu[s]:cu[s] + BS - off]), f"sequence {s}: chunk slots differ"
+    kv.release(plan["seed_id"])
+    whole = plan["seed_blocks"][:P // BS]
+    assert all(kv.refs(b_) == B + 1 for b_ in whole), "prefix pages: cache entry + 8 sequences"
+    assert kv.refs(partial) == 0 and all(kv.refs(d_) == 1 for d_ in dst)
+    assert all((bt[s, :P // BS] == whole).all() for s in range(B))
+    # (1) the last row of every chunk against paged decode attention
     last = cu[1:] - 1
     dout = torch.zeros(B, Hq, D, dtype=torch.bfloat16, device=dev)
     ws = torch.empty(pkv.attn_decode_workspace(B, Hq), dtype=torch.uint8, device=dev)
     pkv.attn_decode(q[last], kc, vc, qkv[last], qstride, Hq, Hkv, pos_d[last], torch.arange(B, dtype=torch.int32,
-                    device=dev), bt_d, pp + cp, BS, dout, SCALE, i32(np.arange(B + 1), dev), 0, None, 1, B, pages, ws)
+                    device=dev), bt_d, mb, BS, dout, SCALE, i32(np.arange(B + 1), dev), 0, None, 1, B, pages, ws)
     torch.cuda.synchronize()
-    ok, err = close(out[last].cpu().view(torch.int16).numpy().view(np.uint16),
-                    dout.cpu().view(torch.int16).numpy().view(np.uint16))
+    ok, err = close(bits(out[last]), bits(dout), what="c4 last rows, prefill vs decode kernel")
     assert ok, f"prefill last rows vs decode: {err}"
-    # (2) sampled rows against the oracle, as decode rows with q pre-rounded
-    rows = np.concatenate([[0, 1, 63, 64, 2047], rng.integers(0, T, size=7)])
-    seqs = rows // N
-    need = [(pos[r] + BS) // BS for r in rows]
-    sub = np.unique(np.concatenate([bt[s, :n] for s, n in zip(seqs, need)]))
-    idx = torch.from_numpy(sub).to(dev).long()
-    kc_h = kc.view(pages, BS, Hkv, D)[idx].cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1, Hkv, D)
-    vc_h = vc.view(pages, BS, Hkv, D)[idx].cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1, Hkv, D)
-    remap = {int(p_): i for i, p_ in enumerate(sub)}
-    bt_r = np.zeros((len(rows), pp + cp), np.int32)
-    for i, (s, n) in enumerate(zip(seqs, need)):
-        bt_r[i, :n] = [remap[int(p_)] for p_ in bt[s, :n]]
-    qh = q[torch.from_numpy(rows).to(dev)].float().cpu().numpy()
-    q_r = bf16_bits(qh * np.float32(SCALE * LOG2E))
-    qkv_h = qkv[torch.from_numpy(rows).to(dev)].cpu().view(torch.int16).numpy().view(np.uint16)
-    want, _ = oracle.attn_decode(q_r, kc_h, vc_h, qkv_h, qstride, Hq, Hkv, pos[rows],
-                                 np.arange(len(rows), dtype=np.int32), bt_r, pp + cp, BS, LN2)
-    got = out[torch.from_numpy(rows).to(dev)].cpu().view(torch.int16).numpy().view(np.uint16)
-    ok, err = close(got, want)
+    # (2) 4 rows in every 64-row query tile of every sequence against the
+    # oracle's prefill (groups of 8 rows run in parallel on host pages)
+    rng = np.random.default_rng(12)
+    tiles = N // 64
+    picks = np.sort(np.stack([rng.choice(64, 4, replace=False) + 64 * j for j in range(tiles)]).reshape(-1))
+    kc_h, vc_h, bt_h, _ = host_pages(kc, vc, bt, np.full(B, per_seq))
+    q_h, qkv_h = bits(q), bits(qkv)
+    groups = [(s, cu[s] + picks[i:i + 8]) for s in range(B) for i in range(0, len(picks), 8)]
+
+    def one(g):
+        s, rows = g
+        return rows, oracle.attn_prefill(np.ascontiguousarray(q_h[rows]), kc_h, vc_h,
+                                         np.ascontiguousarray(qkv_h[rows]), qstride, Hq, Hkv, pos[rows],
+                                         np.array([0, len(rows)], np.int32), 1, np.ascontiguousarray(bt_h[s:s + 1]),
+                                         mb, BS, SCALE)
+
+    rows_all = np.concatenate([g[1] for g in groups])
+    want = np.zeros((len(rows_all), Hq, D), np.uint16)
+    at = 0
+    for rows, o in run_threads(one, groups):
+        want[at:at + len(rows)] = o
+        at += len(rows)
+    got = bits(out)[rows_all]
+    assert len(rows_all) == 1024
+    ok, err = close(got, want, what="c4 through the KV manager, 1024 rows (4 per tile, all 8 x 32 tiles)")
     assert ok, f"sampled rows vs oracle: {err}"

@@ -6,15 +6,15 @@ Tolerance (north star): bf16 outputs within max-abs 2e-3 and relative 1e-2,
 |got - want| <= 2e-3 + 1e-2 * |want|. The verify kernel rounds the softmax
 weights to bf16 before P.V (the oracle keeps them in double), which the
 tolerance covers. Config 5 at full size (16 sequences of 32k..128k keys, 4
-rows each) is checked against the decode kernel on the same cache and, for
-one sequence, against the oracle on that sequence's pages."""
+rows each) is checked against the decode kernel on the same cache and, on
+every row, against the oracle."""
 import numpy as np
 import pytest
 import torch
 
 import oracle
 import pkv
-from _util import BS, D, bf16_bits, close, nan_stale
+from _util import BS, D, bf16_bits, close, host_pages, nan_stale, oracle_decode_rows
 
 pytestmark = pytest.mark.gpu
 SCALE = 1.0 / 16.0
@@ -172,14 +172,9 @@ def test_verify_c5_full_size(dev):
     bits = lambda x: x.cpu().view(torch.int16).numpy().view(np.uint16)
     ok, err = close(bits(vout), bits(dout))
     assert ok, f"verify vs decode: {err}"
-    # the shortest sequence against the oracle, on a copy of its own pages
-    s = int(np.argmin(L0))
-    idx = torch.from_numpy(bt[s, :need[s]]).to(dev).long()
-    kc_h = bits(kc.view(pages, BS, Hkv, D)[idx]).reshape(-1, Hkv, D)
-    vc_h = bits(vc.view(pages, BS, Hkv, D)[idx]).reshape(-1, Hkv, D)
-    rows = torch.arange(s * n, s * n + n, device=dev)
-    want, _ = oracle.attn_decode(bits(q[rows]), kc_h, vc_h, bits(qkv[rows]), qstride, Hq, Hkv, pos[s * n:s * n + n],
-                                 np.zeros(n, np.int32), np.arange(need[s], dtype=np.int32)[None, :], int(need[s]), BS,
-                                 SCALE)
-    ok, err = close(bits(vout[rows]), want)
-    assert ok, f"verify vs oracle (sequence {s}, L0 {L0[s]}): {err}"
+    # every row (16 sequences x 4 drafts x 16 heads) against the oracle
+    kc_h, vc_h, bt_h, _ = host_pages(kc, vc, bt, need)
+    want = oracle_decode_rows(bits(q), kc_h, vc_h, bits(qkv), qstride, Hq, Hkv, pos, ts, bt_h, mb, SCALE)
+    del kc_h, vc_h
+    ok, err = close(bits(vout), want, what="c5 full, all 64 x 16 rows")
+    assert ok, f"verify vs oracle: {err}"

@@ -211,3 +211,36 @@ def test_meta_layout_regions_follow_the_reference_order():
         assert lay["words"] == at
     with pytest.raises(RuntimeError):
         pkv.meta_layout(0, 1, 1, 1)
+
+
+@pytest.mark.parametrize("prefix", [16384, 16392])
+def test_c4_plan_through_the_manager(prefix):
+    """Config 4's tables as bench.py and the GPU test build them: a whole-unit
+    prefix reaches the 8 sequences through the prefix cache (admission
+    hits it), a prefix ending inside a page through sharing plus one
+    copy-on-write per sequence; either way the prefix's whole pages end at
+    refs 9 (entry + 8 sequences) once the seed is released."""
+    from pkv import synth
+    B, N = 8, 2048
+    per_seq = (prefix + N + 15) // 16
+    kv = pkv.Kv((prefix + 15) // 16 + B * (per_seq - prefix // 16) + 16, 16)
+    plan = synth.c4_kv_plan(kv, prefix, N, B, seed=5)
+    st, seed_blocks = plan["step"], plan["seed_blocks"]
+    whole = seed_blocks[:prefix // 16]
+    assert plan["via_cache"] == (prefix % 64 == 0)
+    assert len(plan["cow"]) == (0 if prefix % 16 == 0 else B)
+    assert all(kv.refs(b) == B + 1 for b in whole)
+    assert list(st["cu"][:B + 1]) == [i * N for i in range(B + 1)]
+    for s in range(B):
+        assert (st["block_table"][s, :len(whole)] == whole).all()
+        rows = slice(s * N, (s + 1) * N)
+        assert (st["pos"][rows] == np.arange(prefix, prefix + N)).all()
+        p = st["pos"][rows]
+        assert (st["slot_map"][rows] == st["block_table"][s, p // 16] * 16 + p % 16).all()
+    for src, dst in plan["cow"]:
+        assert src == seed_blocks[-1] and kv.refs(dst) == 1
+    if plan["cow"]:
+        assert kv.refs(seed_blocks[-1]) == 0
+    # every table page outside the prefix is the sequence's own
+    own = st["block_table"][:, len(whole):]
+    assert len(np.unique(own)) == own.size

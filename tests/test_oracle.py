@@ -195,7 +195,7 @@ def test_prefill_oracle_matches_causal_sdpa():
     pos = np.arange(ctx, ctx + n, dtype=np.int32)
     cu = np.array([0, n], np.int32)
     out = oracle.attn_prefill(q, c["kc"], c["vc"], qkv, c["qstride"], Hq, Hkv, pos, cu, 1, c["bt"], c["max_blocks"],
-                              BS, 0.0625)
+                              BS, 0.0625, p_tile=0)
     slots = c["bt"][0][np.arange(L) // BS] * BS + np.arange(L) % BS
     K = torch.from_numpy(oracle.b2f(c["kc"][slots]).astype(np.float64)).permute(1, 0, 2).repeat_interleave(4, 0)
     V = torch.from_numpy(oracle.b2f(c["vc"][slots]).astype(np.float64)).permute(1, 0, 2).repeat_interleave(4, 0)
@@ -208,6 +208,79 @@ def test_prefill_oracle_matches_causal_sdpa():
     assert np.abs(got - oracle.b2f(want)).max() <= 2 ** -9  # one bf16 rounding apart at most
     # the causal bound matters: the first row differs from attending all keys
     assert not np.allclose(o[:, 0], o[:, -1])
+
+
+def _prefill_scores_case(scores, n_keys, seed=0):
+    """One sequence of n_keys keys whose scores (exp2 domain) for its last
+    two query rows are `scores` (dict key -> bf16-exact score, others 0):
+    q = e_0 scaled by ln 2 (so q' = bf16(q * scale * log2 e) = e_0), K rows
+    zero except dim 0 = score, V random; gates large (sigmoid = 1 in f32)."""
+    Hq, Hkv = 4, 1
+    rng = np.random.default_rng(seed)
+    pages = (n_keys + BS - 1) // BS
+    kc = np.zeros((pages * BS, Hkv, D), np.uint16)
+    for j, sc in scores.items():
+        kc[j, 0, 0] = bf16_bits(np.array([sc], np.float32))[0]
+    vc = bf16_bits(rng.standard_normal((pages * BS, Hkv, D)) * 0.5)
+    q = np.zeros((2, Hq, D), np.uint16)
+    q[:, :, 0] = bf16_bits(np.float32(1.0))
+    qstride = (2 * Hq + 2 * Hkv) * D
+    qkv = np.zeros((2, qstride), np.uint16)
+    for h in range(Hq):
+        qkv[:, h * 2 * D + D:h * 2 * D + 2 * D] = bf16_bits(np.float32(30.0))
+    pos = np.array([n_keys - 2, n_keys - 1], np.int32)
+    bt = np.arange(pages, dtype=np.int32)[None, :]
+    return dict(q=q, kc=kc, vc=vc, qkv=qkv, qstride=qstride, pos=pos, cu=np.array([0, 2], np.int32), bt=bt,
+                pages=pages, Hq=Hq, Hkv=Hkv)
+
+
+def test_prefill_oracle_reference_tiles_round_p_against_the_running_max():
+    """The reference's prefill softmax (amd/attention.cuh:55-121, AM_BN = 32):
+    per 32-key tile the anchor is the running max, P.V takes bf16(p) and the
+    denominator the unrounded p. Three keys: scores 0 and r = bf16(-0.3) in
+    the first tile, 0.5 at key 32 (a new max in the second tile). Closed
+    form: A = (v0 + bf16(2^r) v1) 2^-0.5 + v32, S = (1 + 2^r) 2^-0.5 + 1.
+    Anchoring every p on the final max instead, rounding the denominator
+    too, or not rounding at all all give other bits; with p_tile = 0 the
+    result is the textbook softmax."""
+    r = float(oracle.b2f(bf16_bits(np.float32(-0.3))))
+    n = 34  # keys 0..33 for the last row (key 33 score 0, like key 0)
+    c = _prefill_scores_case({1: r, 32: 0.5}, n)
+    args = (c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], c["Hq"], c["Hkv"], c["pos"], c["cu"], 1, c["bt"],
+            c["pages"], BS, float(np.log(2.0)))
+    got = oracle.attn_prefill(*args, p_tile=32)
+    exact = oracle.attn_prefill(*args, p_tile=0)
+    v = oracle.b2f(c["vc"][:, 0]).astype(np.float64)
+    sc = np.zeros(n)
+    sc[1], sc[32] = r, 0.5
+    # row 1 (position 33): tile 1 = keys 0..31 (anchor 0), tile 2 = keys 32, 33 (anchor 0.5)
+    p1 = 2.0 ** (sc[:32] - 0.0)
+    p2 = 2.0 ** (sc[32:34] - 0.5)
+    rb = lambda x: oracle.b2f(bf16_bits(np.asarray(x, np.float32))).astype(np.float64)
+    A = (rb(p1) @ v[:32]) * 2 ** -0.5 + rb(p2) @ v[32:34]
+    S = p1.sum() * 2 ** -0.5 + p2.sum()
+    want = bf16_bits(oracle.b2f(bf16_bits((A / S).astype(np.float32))))
+    for h in range(c["Hq"]):
+        assert np.abs(oracle.b2f(got[1, h]) - oracle.b2f(want)).max() == 0
+    # a final-max anchor rounds other values: the tiled result is not that
+    p_fin = 2.0 ** (sc - 0.5)
+    alt = bf16_bits(((rb(p_fin) @ v[:n]) / p_fin.sum()).astype(np.float32))
+    assert not np.array_equal(got[1, 0], alt)
+    # and differs from the textbook softmax by P rounding only
+    assert not np.array_equal(got[1], exact[1])
+    assert np.abs(oracle.b2f(got) - oracle.b2f(exact)).max() <= 2e-2
+
+
+def test_prefill_oracle_tiles_equal_textbook_when_p_is_exact():
+    """Scores whose differences are integers make every p a power of two
+    (exact in bf16, exact under any anchor): the tiled softmax with rounding
+    must then equal the textbook one bit for bit, across 5 tiles with the
+    max moving up in tiles 2 and 4 (the rescale of earlier sums)."""
+    scores = {3: -2.0, 40: 1.0, 77: -1.0, 100: 3.0, 140: -4.0}
+    c = _prefill_scores_case(scores, 150, seed=3)
+    args = (c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], c["Hq"], c["Hkv"], c["pos"], c["cu"], 1, c["bt"],
+            c["pages"], BS, float(np.log(2.0)))
+    assert np.array_equal(oracle.attn_prefill(*args, p_tile=32), oracle.attn_prefill(*args, p_tile=0))
 
 
 def test_mtp_slots_closed_form():
