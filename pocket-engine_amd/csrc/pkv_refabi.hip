@@ -369,12 +369,20 @@ extern "C" __global__ void __launch_bounds__(256, 2) attn_groupr_g4_t2_k32(PKV_F
 // The E4M3 prompt kernel a gfx950 device selects for an E4M3 cache
 // (fa_shape(4, 95, true): attn_group8_g4_t2_k16, 256 threads, grid of
 // 32-query tiles, 101,376 bytes of dynamic shared memory, which holds this
-// kernel's two 34.5 KiB stages: the 2-stage loop).
+// kernel's two 34,048-byte stages: the 2-stage loop; a launch with fewer than
+// 68,096 bytes returns before any work).
+namespace pkv {
+constexpr uint32_t REF_SMEM8 = 2u * PF_STAGE * 2u;  // bytes attn_group8's two stages use
+}  // namespace pkv
+
 extern "C" __global__ void __launch_bounds__(256, 1) attn_group8_g4_t2_k16(PKV_FLASH_ARGS) {
     extern __shared__ __align__(16) uint16_t g8_smem[];
     if ((int)blockDim.x != pkv::pf_threads(32, 1) || Hq != 4 * Hkv || !kscale || !vscale || block_size <= 0 ||
         (block_size & (block_size - 1)))
         return;
+    // A launch whose dynamic shared memory (the dispatch packet's group
+    // segment size, byte offset 28) cannot hold the two stages does nothing.
+    if (reinterpret_cast<const uint32_t*>(__builtin_amdgcn_dispatch_ptr())[7] < pkv::REF_SMEM8) return;
     pkv::PrefillParams p;
     p.q = q;
     p.kc = (const uint16_t*)kcache;

@@ -324,3 +324,54 @@ def test_prefill_e4m3_stale_slots_are_nan(dev, refabi_kernel):
                                 c["bt"], c["max_blocks"], BS, SCALE)
     ok, err = close(got, want)
     assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("Hkv,min_range", [(1, 16), (2, 16), (8, 32), (4, 1 << 20)])
+def test_verify_e4m3_four_row_segments(dev, Hkv, min_range):
+    """pkv_attn_verify_e4m3 with full 4-row segments (the NR = 4 columns of
+    the E4M3 wave body) at Hkv 1 and 2 (fewer waves per block) and 8 (two
+    kv-head groups), contexts long enough to cross several key ranges (small
+    min_range), plus ragged 1..3-row tails; every row against the oracle."""
+    print(f"case verify e4m3 4-row segments Hkv={Hkv} min_range={min_range}", flush=True)
+    pkv.attn_decode_config(1, min_range)
+    try:
+        c = verify_case([(700, 4), (1500, 4), (33, 3), (2100, 8), (5, 1), (400, 6)], Hkv, 30 + Hkv)
+        rng = np.random.default_rng(31 + Hkv)
+        k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+        ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+        vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+        outs = np.zeros(6, np.int32)
+        got = run_decode8(c, k8, v8, ks, vs, dev, skip=1, outs=outs, entry="verify")
+        want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], 4 * Hkv, Hkv, c["pos"],
+                                   c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"], skip_prompts=1,
+                                   outs=outs)
+        ok, err = close(got, want, what=f"verify e4m3 Hkv {Hkv}")
+        assert ok, err
+    finally:
+        pkv.attn_decode_config(1, 32)
+
+
+def test_ref_group8_short_dynamic_lds_writes_nothing(dev):
+    """attn_group8_g4_t2_k16 keeps its two stages in the launch's dynamic
+    shared memory: a launch with less than they take (32 KiB instead of the
+    engine's 101,376 bytes; the stages need 68,096) returns before any work
+    and leaves the output untouched."""
+    print("case refabi group8 short dynamic LDS", flush=True)
+    from test_gpu_prefill import prefill_case
+    from pkv.refabi import F, I, P, RefKernels, flash_launch
+    c = prefill_case([100], [64], 4, 5, decode_rows=1)
+    rng = np.random.default_rng(5)
+    k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+    ks = (rng.random(c["kc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+    T, Hq = c["T"], c["Hq"]
+    name, grid, threads, smem = flash_launch(T, c["seqs"], 4, fp8=True)
+    assert name == "attn_group8_g4_t2_k16" and smem >= 68096
+    init = np.full((T, Hq, D), 0x3333, np.uint16)
+    out = t_(init, dev)
+    RefKernels().launch(name, grid, threads, 32 * 1024,
+                        [P(t_(c["q"], dev)), P(t_(k8, dev)), P(t_(v8, dev)), P(t_(ks, dev)), P(t_(ks, dev)),
+                         P(t_(c["qkv"], dev)), I(c["qstride"]), I(Hq), I(4), P(t_(c["pos"], dev)),
+                         P(t_(c["cu"], dev)), I(c["seqs"]), P(t_(c["bt"], dev)), I(c["max_blocks"]), I(BS), P(out),
+                         F(SCALE), P(None), I(1)])
+    torch.cuda.synchronize()
+    assert (out.cpu().numpy().view(np.uint16) == 0x3333).all()
