@@ -89,7 +89,8 @@ def main():
                     help="report the eager step only (default: the K steps are also captured into one HIP graph and "
                          "replayed, as the reference engine replays its decode step, and value is the replayed step)")
     ap.add_argument("--calibrate-copy", action="store_true",
-                    help="only run a plain 2 GiB device copy (x3), to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
+                    help="only run kernels of known traffic (2 GiB copy, read-only sum, fill; x3 each), to scale rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--verify-kernel", action="store_true",
                     help="c2/c3 unfused through the verify kernels (pkv_attn_verify) instead of decode")
     ap.add_argument("--refabi", action="store_true",
@@ -113,12 +114,19 @@ def main():
     import torch
 
     if args.calibrate_copy:
+        # Kernels of known traffic for scaling rocprofv3 FETCH_SIZE /
+        # WRITE_SIZE: a device copy (reads 2 GiB, writes 2 GiB), an integer
+        # sum (reads 2 GiB, writes 8 bytes) and a fill (writes 2 GiB), 3 each.
         src = torch.ones(1 << 30, dtype=torch.int16, device="cuda:0")
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)  # reads 2 GiB, writes 2 GiB
+            dst.copy_(src)
+        for _ in range(3):
+            src.view(torch.int64).sum()
+        for _ in range(3):
+            dst.fill_(7)
         torch.cuda.synchronize()
-        print(json.dumps({"calibrate_copy_bytes": 2 << 30, "copies": 3}))
+        print(json.dumps({"calibrate_bytes": 2 << 30, "copies": 3, "sums": 3, "fills": 3}))
         return
 
     import pkv
