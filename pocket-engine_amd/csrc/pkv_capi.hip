@@ -102,6 +102,15 @@ int pkv_append(const void* k_rows, const void* v_rows, int64_t row_stride, const
     const int64_t row_bytes = (int64_t)Hkv * head_bytes;
     if (row_bytes > (1 << 24) || row_stride < row_bytes || T > (1 << 30)) return PKV_ERR_INVALID;
     const int vec = vec_mode(k_rows, v_rows, kcache, vcache, row_stride, (int)row_bytes);
+    if (vec == 2 && (row_bytes == 2048 || row_bytes == 4096 || row_bytes == 8192)) {
+        // whole-row moves, APP_TOK tokens per block
+        const dim3 grid((T + pkv::APP_TOK - 1) / pkv::APP_TOK);
+        auto k = row_bytes == 2048 ? pkv::append_rows_kernel<1>
+                 : row_bytes == 4096 ? pkv::append_rows_kernel<2> : pkv::append_rows_kernel<4>;
+        hipLaunchKernelGGL(k, grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t*)k_rows, (const uint8_t*)v_rows,
+                           (long)row_stride, slot_map, T, (uint8_t*)kcache, (uint8_t*)vcache, (long)num_slots);
+        return launch_status();
+    }
     hipLaunchKernelGGL(pkv::append_kernel, dim3(T, 2), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)k_rows,
                        (const uint8_t*)v_rows, (long)row_stride, slot_map, (int)row_bytes, (uint8_t*)kcache,
                        (uint8_t*)vcache, (long)num_slots, vec);

@@ -43,6 +43,47 @@ __global__ void __launch_bounds__(256) append_kernel(const uint8_t* __restrict__
         copy_row<uint8_t>(dst, src, row_bytes, threadIdx.x, blockDim.x);
 }
 
+// The same for rows of 256 * CPT / 2 16-byte chunks (2, 4 or 8 KiB: Hkv 4,
+// 8 or 16 at head_dim 256 in bf16), 16-byte aligned: a block of 256 threads
+// takes APP_TOK tokens, thread i moving chunk i (then i + 256, ...) of the
+// token's K row followed by its V row, and issues all of its loads (read-once
+// source rows: nontemporal) before its stores, so each thread keeps
+// APP_TOK * CPT 16-byte moves in flight.
+constexpr int APP_TOK = 4;
+template <int CPT>
+__global__ void __launch_bounds__(256) append_rows_kernel(const uint8_t* __restrict__ ksrc,
+                                                          const uint8_t* __restrict__ vsrc, long stride,
+                                                          const int* __restrict__ slot_map, int T,
+                                                          uint8_t* __restrict__ kc, uint8_t* __restrict__ vc,
+                                                          long num_slots) {
+    constexpr int N = 128 * CPT;  // 16-byte chunks per row
+    const int t0 = blockIdx.x * APP_TOK, tid = threadIdx.x;
+    uint4 buf[APP_TOK][CPT];
+    long slot[APP_TOK];
+#pragma unroll
+    for (int u = 0; u < APP_TOK; u++) {
+        const int t = t0 + u;
+        slot[u] = t < T ? slot_map[t] : -1;
+        if (slot[u] < 0 || slot[u] >= num_slots) continue;
+#pragma unroll
+        for (int c = 0; c < CPT; c++) {
+            const int i = c * 256 + tid;  // < 2 N
+            const uint8_t* src = (i < N ? ksrc : vsrc) + (size_t)t * stride + 16 * (i < N ? i : i - N);
+            buf[u][c] = load_nt(src);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < APP_TOK; u++) {
+        if (slot[u] < 0 || slot[u] >= num_slots) continue;
+#pragma unroll
+        for (int c = 0; c < CPT; c++) {
+            const int i = c * 256 + tid;
+            uint8_t* dst = (i < N ? kc : vc) + (size_t)slot[u] * (16 * N) + 16 * (i < N ? i : i - N);
+            *reinterpret_cast<uint4*>(dst) = buf[u][c];
+        }
+    }
+}
+
 // Gather one sequence's first L slot rows into dense [L][row] buffers:
 // dense[j] = cache[bt[j / bs] * bs + j % bs]. Four rows per block of 256.
 // Page ids outside [0, num_blocks) are clamped into the pool (garbage in,

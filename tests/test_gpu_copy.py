@@ -59,17 +59,22 @@ def test_c1_plumbing_append_gather_f32(dev):
         assert np.array_equal(ko.cpu().numpy(), data[s][0]) and np.array_equal(vo.cpu().numpy(), data[s][1])
 
 
-@pytest.mark.parametrize("T", [1, 64, 513])
-def test_append_bf16_from_qkv_rows_with_padding(dev, T):
+@pytest.mark.parametrize("T,Hkv", [(1, 4), (64, 4), (513, 4), (7, 8), (130, 16), (3, 2)])
+def test_append_bf16_from_qkv_rows_with_padding(dev, T, Hkv):
     """Append K/V straight out of qkv projection rows (stride (2Hq + 2Hkv)
-    * 256 elements), with padding rows (slot -1) and ragged T."""
-    print(f"case append bf16 T={T}", flush=True)
+    * 256 elements), with padding rows (slot -1), slots past the pool and
+    ragged T (token counts that do not fill the whole-row kernel's blocks of
+    4); rows of 2, 4 and 8 KiB take the whole-row kernel, 1 KiB the generic
+    one."""
+    print(f"case append bf16 T={T} Hkv={Hkv}", flush=True)
     rng = np.random.default_rng(T)
-    Hq, Hkv, pages = 16, 4, 128
+    Hq, pages = 4 * Hkv, 128
     qstride = (2 * Hq + 2 * Hkv) * D
     qkv = bf16_bits(rng.standard_normal((T, qstride)))
     slots = rng.permutation(pages * BS)[:T].astype(np.int32)
     slots[rng.random(T) < 0.1] = -1
+    if T > 2:
+        slots[1] = pages * BS + 5  # past the pool: skipped like padding
     kc_h = bf16_bits(rng.standard_normal((pages * BS, Hkv, D)))
     vc_h = bf16_bits(rng.standard_normal((pages * BS, Hkv, D)))
     kc_d, vc_d = to_dev(as_i16(kc_h), dev), to_dev(as_i16(vc_h), dev)
@@ -79,7 +84,8 @@ def test_append_bf16_from_qkv_rows_with_padding(dev, T):
                kc_d, vc_d, pages * BS)
     k_rows = np.ascontiguousarray(qkv[:, k_off:k_off + Hkv * D])
     v_rows = np.ascontiguousarray(qkv[:, v_off:v_off + Hkv * D])
-    oracle.append(k_rows, v_rows, slots, kc_h, vc_h)
+    # the C-ABI skips slots outside the pool; the oracle takes them as padding
+    oracle.append(k_rows, v_rows, np.where(slots < pages * BS, slots, -1), kc_h, vc_h)
     torch.cuda.synchronize()
     assert np.array_equal(kc_d.cpu().numpy().view(np.uint16), kc_h)
     assert np.array_equal(vc_d.cpu().numpy().view(np.uint16), vc_h)
