@@ -104,6 +104,39 @@ constexpr int PF_NST = 3;
 constexpr int PF_IDS_BYTES = (PF_THREADS / 64) * 4 * 4 * 4;
 constexpr size_t prefill_smem_bytes(int nst = PF_NST) { return (size_t)nst * PF_STAGE * 2 + PF_IDS_BYTES; }
 
+// NP LDS DMA pairs from one uniform base: pair j reads 16 bytes per lane at
+// base + off[j] into LDS at m0 + j * lds_step (+ 16 x lane). The m0 writes
+// (and the one wait state each needs) stay in one asm block.
+template <int NP>
+__device__ __forceinline__ void dma_pairs(const void* base, const uint32_t (&off)[NP], uint32_t m0,
+                                          uint32_t lds_step) {
+    static_assert(NP == 2 || NP == 4, "2 or 4 pairs");
+    if constexpr (NP == 2) {
+        asm volatile(
+            "s_mov_b32 m0, %3\n\ts_nop 0\n\t"
+            "global_load_lds_dwordx4 %1, %0\n\t"
+            "s_add_u32 m0, m0, %4\n\ts_nop 0\n\t"
+            "global_load_lds_dwordx4 %2, %0"
+            :
+            : "s"(base), "v"(off[0]), "v"(off[1]), "s"(__builtin_amdgcn_readfirstlane(m0)), "s"(lds_step)
+            : "memory", "scc");
+    } else {
+        asm volatile(
+            "s_mov_b32 m0, %5\n\ts_nop 0\n\t"
+            "global_load_lds_dwordx4 %1, %0\n\t"
+            "s_add_u32 m0, m0, %6\n\ts_nop 0\n\t"
+            "global_load_lds_dwordx4 %2, %0\n\t"
+            "s_add_u32 m0, m0, %6\n\ts_nop 0\n\t"
+            "global_load_lds_dwordx4 %3, %0\n\t"
+            "s_add_u32 m0, m0, %6\n\ts_nop 0\n\t"
+            "global_load_lds_dwordx4 %4, %0"
+            :
+            : "s"(base), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]),
+              "s"(__builtin_amdgcn_readfirstlane(m0)), "s"(lds_step)
+            : "memory", "scc");
+    }
+}
+
 // The query tile of this workgroup among the prompt sequences: tile
 // total - 1 - blockIdx.x of the concatenated BQ-query tiles of the prompt
 // sequences (sequences of more than one row that do not verify drafts).
@@ -423,28 +456,28 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         static_assert(NPW <= 4, "page-id ring slots hold 4 ids");
         int* ring = reinterpret_cast<int*>(pf_smem + NST * STAGE) + wave * 16;
         const int hi = lane >> 5;
-        // lane byte offset inside a pair's page: key + 8 for the upper half
+        // Wave w's pairs are rows NPW w .. NPW w + NPW - 1: keys kb + j and
+        // kb + j + 8 (j < NPW) of one 16-key half, i.e. one page per tile
+        // (pages hold 16 keys or more here): one page id per tile, one
+        // uniform base, lane offsets fixed for the loop.
+        const int kb = pf_key_of_row(NPW * wave);
+        const uint32_t row2 = (uint32_t)row * 2;
         const uint32_t lane_off = (uint32_t)(hi * 8 * row + kvh * HEAD_DIM + 8 * (lane & 31)) * 2;
+        uint32_t offs[NPW];
+#pragma unroll
+        for (int j = 0; j < NPW; j++) offs[j] = lane_off + j * row2;
+        const uint32_t lds_k = lds_addr(pf_smem) + (uint32_t)(pf_krow(NPW * wave)) * 2;
+        const uint32_t lds_v = lds_addr(pf_smem) + (uint32_t)(PF_K_ELEMS + pf_vrow<VP>(NPW * wave)) * 2;
         auto dma_ids = [&](int k0, int slot) __attribute__((always_inline)) {
-            if (lane < NPW) {
-                const int j = pf_key_of_row(NPW * wave + lane);
-                dma4(bt + min((k0 + j) >> bs_log2, last_pi), lds_addr(ring + 4 * slot));
-            }
+            if (lane == 0) dma4(bt + min((k0 + kb) >> bs_log2, last_pi), lds_addr(ring + 4 * slot));
         };
         auto dma_tile = [&](int k0, int buf, int slot) __attribute__((always_inline)) {
-            const int4 idv = *reinterpret_cast<const int4*>(ring + 4 * slot);
-            const int id[4] = {__builtin_amdgcn_readfirstlane(idv.x), __builtin_amdgcn_readfirstlane(idv.y),
-                               __builtin_amdgcn_readfirstlane(idv.z), __builtin_amdgcn_readfirstlane(idv.w)};
-            uint16_t* st = pf_smem + buf * STAGE;
-#pragma unroll
-            for (int j = 0; j < NPW; j++) {
-                const int r = NPW * wave + j, kp = k0 + pf_key_of_row(r);
-                long pg = id[j];
-                pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
-                const size_t slot_at = (((size_t)pg << bs_log2) + (kp & bs_mask)) * row;  // uniform
-                dma16_s(p.kc + slot_at, lane_off, lds_addr(st + pf_krow(r)));
-                dma16_s(p.vc + slot_at, lane_off, lds_addr(st + PF_K_ELEMS + pf_vrow<VP>(r)));
-            }
+            long pg = __builtin_amdgcn_readfirstlane(ring[4 * slot]);
+            pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
+            const size_t at = (((size_t)pg << bs_log2) + ((k0 + kb) & bs_mask)) * row2;  // uniform
+            const uint32_t so = (uint32_t)(buf * STAGE) * 2;
+            dma_pairs<NPW>(reinterpret_cast<const char*>(p.kc) + at, offs, lds_k + so, PF_KPAIR * 2);
+            dma_pairs<NPW>(reinterpret_cast<const char*>(p.vc) + at, offs, lds_v + so, VP * 2);
         };
         // V rows of keys at or past L (partial last tile) read stale slots:
         // the wave zeroes its own rows once its DMA has landed (P is 0 there,
