@@ -339,8 +339,7 @@ __device__ __forceinline__ void piece_body(const DecodeParams& p, const int* __r
         const float sc = (kpos >= j0 && kpos < j1) ? v[0] * sl2 : -INFINITY;
         float mx = fmaxf(sc, dpp<DPP_ROW_ROR4>(sc));
         mx = fmaxf(mx, dpp<DPP_ROW_ROR8>(mx));
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
+        mx = max_xor32(max_xor16(mx));
         const float mn = fmaxf(m, mx);
         const float corr = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first page (m = -inf)
         const float pr = __builtin_amdgcn_exp2f(sc - mn);
@@ -409,12 +408,11 @@ __device__ __forceinline__ void piece_body(const DecodeParams& p, const int* __r
     // Totals: the sum over the head's 16 lanes, the two halves' values.
     l += dpp<DPP_ROW_ROR4>(l);
     l += dpp<DPP_ROW_ROR8>(l);
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    l = add_xor32(add_xor16(l));
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int e = 0; e < 8; e++) acc[g][e] += shfl_xor(acc[g][e], 32);
+        for (int e = 0; e < 8; e++) acc[g][e] = add_xor32(acc[g][e]);
     if (lane < G) {
         lds.ml[2 * lane] = m;
         lds.ml[2 * lane + 1] = l;

@@ -162,8 +162,7 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
                 mx = fmaxf(mx, sc[4 * pg + i]);
             }
         }
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
+        mx = max_xor32(max_xor16(mx));
         const float mn = fmaxf(m, mx);
         // a column with no key yet subtracts 0 (its weights are all 0)
         const float mref = mn == -INFINITY ? 0.f : mn;
@@ -232,8 +231,7 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     for (int u = u0; u < u1; u++) unit(u, u + 1, PF{});
     unit(u1, u1, NONE{});
     // Totals: a column's sum over its 4 lane groups.
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    l = add_xor32(add_xor16(l));
     if (active) epi(sig, rho, acc, m, l);
 }
 

@@ -393,7 +393,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                 float mx = m[qb];
 #pragma unroll
                 for (int r = 0; r < 16; r++) mx = fmaxf(mx, st[qb][r]);
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                mx = max_xor32(mx);
                 // A query with no key yet keeps -inf; it subtracts 0 so exp2 gives 0.
                 const float bse = mx == -INFINITY ? 0.f : mx;
                 const float corr = __builtin_amdgcn_exp2f(m[qb] - bse);
@@ -403,7 +403,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                     st[qb][r] = __builtin_amdgcn_exp2f(st[qb][r] - bse);
                     sum += st[qb][r];
                 }
-                sum += __shfl_xor(sum, 32, 64);
+                sum = add_xor32(sum);
                 l[qb] = l[qb] * corr + sum;
                 m[qb] = mx;
                 // Rescale only when some query's max moved (rare after the first tiles).

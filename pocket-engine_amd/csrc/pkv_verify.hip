@@ -147,8 +147,7 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
             sc[i] = (kp >= j0 && kp < j1 && kp < myL) ? s[i] * sl2 : -INFINITY;
             mx = fmaxf(mx, sc[i]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = max_xor32(max_xor16(mx));
         const float mn = fmaxf(m, mx);
         const float mref = mn == -INFINITY ? 0.f : mn;  // a column with no key yet keeps zeros
         const float corr = __builtin_amdgcn_exp2f(m - mref);
@@ -189,8 +188,7 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
     for (int pi = pg0; pi < pg1; pi++) page(A, pi, pi + 1, PF{});
     page(A, pg1, 0, NOPF{});
 
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = add_xor32(add_xor16(l));
     if (myL == 0) return;
     epi(r_me, g_me, gq, acc, m, l);
 }
