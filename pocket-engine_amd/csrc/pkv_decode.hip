@@ -77,8 +77,6 @@ struct DecodeParams {
 
 constexpr int PAGE = 16;
 
-__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
-
 // Exclusive prefix sum over the block; returns the block total in `total`.
 __device__ __forceinline__ int block_scan(int v, int* sh, int& total) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
