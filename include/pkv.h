@@ -85,7 +85,8 @@ int pkv_mtp_next(const int32_t* rows, const int32_t* pos, const int32_t* rope, i
                  int32_t* dpos, int32_t* dslot, int32_t* drope, int S, void* stream);
 
 /* ---------------------------------------------------------------------------
- * Device: paged decode attention (bf16, head_dim 256, block_size 16, G = 4)
+ * Device: paged decode attention (bf16, head_dim 256, block_size 16,
+ * G = Hq / Hkv in {1, 2, 4, 6, 8})
  * ------------------------------------------------------------------------- */
 
 /* Workspace bytes pkv_attn_decode needs for T tokens and Hq query heads on
@@ -106,8 +107,10 @@ int pkv_attn_decode_workspace(int T, int Hq, size_t* bytes);
  * The key-range split is the library's own (the reference's part/min_chunk
  * pair is replaced by `workspace`, of pkv_attn_decode_workspace bytes).
  * num_blocks bounds page ids (ids outside the pool are clamped, never read
- * out of bounds). Returns PKV_ERR_UNSUPPORTED unless Hq = 4 Hkv and
- * block_size = 16. */
+ * out of bounds). G = Hq / Hkv is one of the reference's groups 1, 2, 4, 6, 8
+ * (qwen35.cu:1330-1334); for G other than 4 the call runs the verify kernels
+ * (one row per segment) and `cu` is required. Returns PKV_ERR_UNSUPPORTED for
+ * another G or block_size != 16. */
 int pkv_attn_decode(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
                     int Hkv, const int32_t* pos, const int32_t* tok_seq, const int32_t* block_table, int max_blocks,
                     int block_size, void* out, float scale, const int32_t* cu, int skip_prompts,
@@ -140,7 +143,9 @@ int pkv_attn_decode_merge(const void* q, const void* kcache, const void* vcache,
  * are consecutive rows cu[s] .. cu[s+1]-1 at consecutive positions and
  * slot_map[t] is the slot of pos[t]. Keys at positions the step itself feeds
  * are read from k_rows/v_rows; the step's rows are written to the pools.
- * `cu` is required. row_stride is in bytes (a multiple of 16). No
+ * `cu` is required; G = Hq / Hkv = 4 only (PKV_ERR_UNSUPPORTED otherwise;
+ * other groups run pkv_append then pkv_attn_decode). row_stride is in bytes
+ * (a multiple of 16). No
  * reference counterpart as one call: it saves the append launch. */
 int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map,
                          const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
@@ -182,6 +187,8 @@ int pkv_attn_decode_step_noalloc(const void* k_rows, const void* v_rows, int64_t
  * consecutive rows of a sequence share one pass over its pages. `cu` is
  * required and each sequence's rows must be consecutive (cu[s] ..
  * cu[s+1]-1, as Scheduler::fill writes them, src/sched.rs:1105-1115).
+ * Segments hold 4 rows for G <= 4 and 2 rows for G = 6 or 8 (the 16 MFMA
+ * columns are rows x query heads).
  * Workspace: pkv_attn_verify_workspace bytes. Shapes as pkv_attn_decode. */
 int pkv_attn_verify_workspace(int T, int Hq, size_t* bytes);
 int pkv_attn_verify(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,

@@ -296,7 +296,10 @@ int pkv_attn_decode_config(int wg_per_cu, int min_range) {
 
 int pkv_attn_decode_workspace(int T, int Hq, size_t* bytes) {
     if (T < 0 || Hq <= 0 || !bytes) return PKV_ERR_INVALID;
-    *bytes = decode_layout(T, Hq, decode_n_wg() * F8_WG_PER_CU).total;
+    // Groups other than 4 query heads per kv head run the verify kernels'
+    // records, so the size covers both layouts.
+    *bytes = std::max(decode_layout(T, Hq, decode_n_wg() * F8_WG_PER_CU).total,
+                      decode_layout(T, Hq, decode_n_wg() * F8_WG_PER_CU, true).total);
     return PKV_OK;
 }
 
@@ -317,6 +320,15 @@ struct AppendArgs {
     const int32_t* slot_map;
 };
 
+// Query heads per kv head the decode, verify and E4M3 kernels serve (the
+// reference instantiates attn_paged_g<G> for the same groups,
+// qwen35.cu:1326-1334).
+bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 6 || G == 8; }
+template <class K>
+K by_group(int G, K g1, K g2, K g4, K g6, K g8) {
+    return G == 1 ? g1 : G == 2 ? g2 : G == 4 ? g4 : G == 6 ? g6 : g8;
+}
+
 // phase bit 1: key-range kernel; bit 2: merge kernel; bit 4: the key-range
 // kernel with the step's append fused in (needs `app`); bit 8: the verify
 // kernels (rows grouped by sequence, 4 per page pass) instead of per-token
@@ -327,15 +339,22 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
                        const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
                        void* workspace, size_t workspace_bytes, void* stream) {
     if (T < 0 || Hq <= 0 || Hkv <= 0 || max_blocks <= 0 || num_blocks <= 0 || spec < 1) return PKV_ERR_INVALID;
-    if (Hq != 4 * Hkv || block_size != 16 || (Hkv > 4 && Hkv % 4 != 0)) return PKV_ERR_UNSUPPORTED;
+    const int G = Hkv > 0 && Hq % Hkv == 0 ? Hq / Hkv : 0;
+    if (!supported_group(G) || block_size != 16 || (Hkv > 4 && Hkv % 4 != 0)) return PKV_ERR_UNSUPPORTED;
+    // The fused step's kernel is the G = 4 decode body.
+    if ((phases & 4) && G != 4) return PKV_ERR_UNSUPPORTED;
     if (num_blocks > (int64_t)INT32_MAX / 16) return PKV_ERR_INVALID;
     if (T == 0) return PKV_OK;
     if (!q || !kcache || !vcache || !qkv || !pos || !tok_seq || !block_table || !out || !workspace)
         return PKV_ERR_INVALID;
+    const bool f8 = kscale != nullptr;
+    // bf16 decode for G != 4 runs the verify kernels (each row of a
+    // sequence's consecutive rows attends its own keys, the same results as
+    // one token at a time), which read cu.
+    if (G != 4 && !f8 && (phases & 3)) phases |= 8;
     if ((skip_prompts || (phases & 8)) && !cu) return PKV_ERR_INVALID;
     const bool verify = phases & 8;
     if (verify && (phases & 4)) return PKV_ERR_INVALID;
-    const bool f8 = kscale != nullptr;
     if (f8 && ((phases & 4) || !vscale || !aligned(kscale, 4) || !aligned(vscale, 4))) return PKV_ERR_INVALID;
     if (qstride < 2 * Hq * pkv::HEAD_DIM || qstride % 8 != 0) return PKV_ERR_INVALID;
     if (!aligned(q, 16) || !aligned(kcache, 16) || !aligned(vcache, 16) || !aligned(qkv, 16) || !aligned(out, 16) ||
@@ -381,15 +400,26 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
     if (phases & 5) {
         hipEvent_t e0 = t_ev_start, e1 = t_ev_stop;
         t_ev_start = t_ev_stop = nullptr;
-        if (verify && f8)
-            hipExtLaunchKernelGGL(pkv::verify_range8_kernel, dim3(n_wg, groups), dim3(threads), 0,
-                                  (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs);
-        else if (verify)
-            hipExtLaunchKernelGGL(pkv::verify_range_kernel, dim3(n_wg, groups), dim3(threads), 0,
-                                  (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs);
-        else if (f8)
-            hipExtLaunchKernelGGL(pkv::decode_range8_kernel, dim3(n_wg, groups), dim3(threads), 0,
-                                  (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs);
+        using RangeKernel = void (*)(pkv::DecodeParams, const int*, const int*, const int*, const int*, const int*);
+        const RangeKernel rk = verify && f8 ? by_group<RangeKernel>(G, pkv::verify_range8_kernel<1>,
+                                                                    pkv::verify_range8_kernel<2>,
+                                                                    pkv::verify_range8_kernel<4>,
+                                                                    pkv::verify_range8_kernel<6>,
+                                                                    pkv::verify_range8_kernel<8>)
+                               : verify ? by_group<RangeKernel>(G, pkv::verify_range_kernel<1>,
+                                                                pkv::verify_range_kernel<2>,
+                                                                pkv::verify_range_kernel<4>,
+                                                                pkv::verify_range_kernel<6>,
+                                                                pkv::verify_range_kernel<8>)
+                               : f8 ? by_group<RangeKernel>(G, pkv::decode_range8_kernel<1>,
+                                                            pkv::decode_range8_kernel<2>,
+                                                            pkv::decode_range8_kernel<4>,
+                                                            pkv::decode_range8_kernel<6>,
+                                                            pkv::decode_range8_kernel<8>)
+                                    : nullptr;
+        if (rk)
+            hipExtLaunchKernelGGL(rk, dim3(n_wg, groups), dim3(threads), 0, (hipStream_t)stream, e0, e1, 0, p, pos,
+                                  tok_seq, block_table, cu, outs);
         else if (phases & 4)
             hipExtLaunchKernelGGL((pkv::decode_range_kernel<4, true>), dim3(n_wg, groups), dim3(threads), 0,
                                   (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs, slot_map);
@@ -400,8 +430,12 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
         if (st != PKV_OK) return st;
     }
     if ((phases & 2) && verify) {
-        hipLaunchKernelGGL(pkv::verify_merge_kernel, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p, pos,
-                           tok_seq, cu, outs);
+        if (pkv::vf_rows(G) == 4)
+            hipLaunchKernelGGL(pkv::verify_merge_kernel<4>, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p, pos,
+                               tok_seq, cu, outs);
+        else
+            hipLaunchKernelGGL(pkv::verify_merge_kernel<2>, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p, pos,
+                               tok_seq, cu, outs);
         return launch_status();
     }
     if (phases & 2) {

@@ -49,21 +49,20 @@ struct WaveLds8 {
 
 // One wave: rows t .. t + NR - 1 of one sequence (row r attends keys
 // [0, Lr[r]); NR = 1: decode, the piece's bounds alone), kv head kvh, keys
-// [j0, j1) of the sequence (block table row bt), over the E4M3 cache. Column
-// c = 4 r + g of the products is row r, query head kvh * 4 + g. Results go
-// to epi(c, gq, acc, m, l) on the lanes of the columns of attending rows
-// (DecodeEpi8 for decode; m = -inf, l = 0 for a column with no key in the
-// piece).
-template <int NR = 1, class Epi>
+// [j0, j1) of the sequence (block table row bt), over the E4M3 cache, for a
+// group of G query heads per kv head (NR * G <= 16). Column c = G r + g of
+// the products is row r, query head kvh * G + g. Results go to epi(c, gq,
+// acc, m, l) on the lanes of the columns of attending rows (DecodeEpi8 for
+// decode; m = -inf, l = 0 for a column with no key in the piece).
+template <int NR = 1, int G = 4, class Epi>
 __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __restrict__ bt, WaveLds8& lds, int t,
                                             int kvh, int j0, int j1, Epi epi, const int* Lr = nullptr) {
-    constexpr int G = 4;
-    static_assert(NR == 1 || NR == 4, "one decode row or a verify segment of up to 4 rows");
+    static_assert(NR >= 1 && NR <= 4 && NR * G <= 16, "up to 16 columns of up to 4 rows");
     const int lane = threadIdx.x & 63, sig = lane & 15, rho = lane >> 4;
-    const int col_r = sig >> 2;
+    const int col_r = sig / G, col_g = sig % G;
     // this lane's column: its row's key bound (decode: the piece's), and
     // whether the column is a row that attends
-    const int myL = NR == 1 ? j1 : col_r == 0 ? Lr[0] : col_r == 1 ? Lr[1] : col_r == 2 ? Lr[2] : Lr[3];
+    const int myL = NR == 1 ? j1 : col_r == 0 ? Lr[0] : col_r == 1 ? Lr[1] : col_r == 2 ? Lr[2] : col_r == 3 ? Lr[3] : 0;
     const bool active = col_r < NR && myL > 0;
     const int Hkv = p.Hkv;
     const float sl2 = p.scale * LOG2E;
@@ -78,8 +77,8 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     // the page for head sig.
     bf16x8 qf[8];
     {
-        const uint16_t* qrow = p.q + ((size_t)(t + (active ? col_r : 0)) * p.Hq + kvh * G + (sig & 3)) * HEAD_DIM +
-                               16 * rho;
+        const uint16_t* qrow = p.q + ((size_t)(t + (active ? col_r : 0)) * p.Hq + kvh * G + (active ? col_g : 0)) *
+                                         HEAD_DIM + 16 * rho;
 #pragma unroll
         for (int s = 0; s < 8; s++)
             qf[s] = as_bf16x8(active ? *reinterpret_cast<const uint4*>(qrow + 64 * (s >> 1) + 8 * (s & 1))
@@ -238,12 +237,13 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
 // Writes a piece's result for the lanes of head g of the group (dims
 // 16 db + 4 gq + i in acc[db][i]): the gated output when the piece holds
 // all of the token's keys, else the partial record at index idx.
+template <int G = 4>
 struct DecodeEpi8 {
     const DecodeParams& p;
     int t, kvh, idx;
     bool direct;
     __device__ __forceinline__ void operator()(int g, int gq, const f32x4 (&acc)[16], float m, float l) const {
-        const int h = kvh * 4 + g;
+        const int h = kvh * G + g;
         if (direct) {
             const float inv = 1.f / l;
             const uint16_t* gate = p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + 4 * gq;
@@ -266,8 +266,10 @@ struct DecodeEpi8 {
 };
 
 // Key-range kernel over the E4M3 cache: decode_range_kernel<4, false>'s
-// ranges and records with piece_body8 inside. Grid (n_wg, ceil(Hkv / 4)),
-// 64 * min(Hkv, 4) threads; two workgroups per CU (at most 256 VGPRs).
+// ranges and records with piece_body8 inside (G query heads per kv head).
+// Grid (n_wg, ceil(Hkv / 4)), 64 * min(Hkv, 4) threads; two workgroups per
+// CU (at most 256 VGPRs).
+template <int G>
 __global__ void __launch_bounds__(256, 2)
     decode_range8_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                          const int* __restrict__ block_table, const int* __restrict__ cu,
@@ -299,8 +301,8 @@ __global__ void __launch_bounds__(256, 2)
         if (L > 0) {
             const int j0 = max(start, off) - off, j1 = min(end, off + L) - off;
             const int seq = __builtin_amdgcn_readfirstlane(tab ? sh_seq[t] : tok_seq[t]);
-            const DecodeEpi8 epi{p, t, kvh, t + b, j0 == 0 && j1 == L};
-            piece_body8(p, block_table + (size_t)seq * p.max_blocks, sh_w[wave], t, kvh, j0, j1, epi);
+            const DecodeEpi8<G> epi{p, t, kvh, t + b, j0 == 0 && j1 == L};
+            piece_body8<1, G>(p, block_table + (size_t)seq * p.max_blocks, sh_w[wave], t, kvh, j0, j1, epi);
             off += L;
         }
         t++;

@@ -39,37 +39,44 @@
 
 namespace pkv {
 
-constexpr int VF_ROWS = 4;                // query rows per segment
+constexpr int VF_ROWS = 4;                // most query rows per segment (partial records per index)
+// Rows per segment for G query heads per kv head: the 16 MFMA columns hold
+// rows x heads, so 4 rows up to G = 4 and 2 rows for G = 6 or 8.
+__host__ __device__ constexpr int vf_rows(int G) { return G <= 4 ? 4 : 2; }
 constexpr int VF_VSTR = HEAD_DIM + 16;    // u16 per staged V row (544 B: conflict-free transposed reads)
 constexpr int VF_LDS = PAGE * VF_VSTR;    // u16 per wave
 
-// Keys of the segment headed by token t; 0 when t does not head a segment
-// (it is not at offset 4i of its sequence) or none of its rows attends.
+// Keys of the segment headed by token t (segments of NR rows, NR a power of
+// two); 0 when t does not head a segment (it is not at offset NR i of its
+// sequence) or none of its rows attends.
+template <int NR>
 __device__ __forceinline__ int seg_len(int t, int T, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                                        const int* __restrict__ cu, int skip, const int* __restrict__ outs, int spec,
                                        int& nrows) {
     const int s = tok_seq[t];
     nrows = 0;
-    if ((t - cu[s]) & (VF_ROWS - 1)) return 0;
-    nrows = min(VF_ROWS, min(cu[s + 1], T) - t);
+    if ((t - cu[s]) & (NR - 1)) return 0;
+    nrows = min(NR, min(cu[s + 1], T) - t);
     int L = 0;
     for (int r = 0; r < nrows; r++) L = max(L, decode_len(t + r, pos, tok_seq, cu, skip, outs, spec));
     return L;
 }
 
-// One wave: segment headed by token t (rows t + r, r < 4, attending Lr[r]
-// keys; Lr = 0 for absent rows), kv head kvh, keys [j0, j1), bf16 cache (an
-// E4M3 cache runs piece_body8 with 4 rows, pkv_decode8.hip).
+// One wave: segment headed by token t (rows t + r, r < vf_rows(G),
+// attending Lr[r] keys; Lr = 0 for absent rows), kv head kvh with G query
+// heads, keys [j0, j1), bf16 cache (an E4M3 cache runs piece_body8,
+// pkv_decode8.hip). MFMA column c is row c / G, head c % G.
 // The result goes to epi(r, g, gq, acc, m, l) on the lanes of attending rows:
-// row r, query head kvh * 4 + g, dims 16 db + 4 gq + i in acc[db][i]; m in
+// row r, query head kvh * G + g, dims 16 db + 4 gq + i in acc[db][i]; m in
 // log2 units, l the sum of weights (m = -inf, l = 0 when the piece has no
 // key for the row).
-template <class Epi>
+template <int G, class Epi>
 __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* __restrict__ bt, uint16_t* vl, int t,
-                                             int kvh, int j0, int j1, int L0, int L1, int L2, int L3, Epi epi) {
+                                             int kvh, int j0, int j1, const int (&Lr)[VF_ROWS], Epi epi) {
+    constexpr int NR = vf_rows(G);
     const int lane = threadIdx.x & 63, c16 = lane & 15, gq = lane >> 4;
-    const int r_me = c16 >> 2, g_me = c16 & 3;
-    const int myL = r_me == 0 ? L0 : r_me == 1 ? L1 : r_me == 2 ? L2 : L3;
+    const int r_me = c16 / G, g_me = c16 % G;
+    const int myL = r_me >= NR ? 0 : r_me == 0 ? Lr[0] : r_me == 1 ? Lr[1] : r_me == 2 ? Lr[2] : Lr[3];
     const float sl2 = p.scale * LOG2E;
     const size_t row_elems = (size_t)p.Hkv * HEAD_DIM;  // slot row, elements
 
@@ -78,7 +85,7 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
     auto dim0 = [&](int c) { return 32 * c + 8 * gq; };
     bf16x8 qf[8];
     if (myL > 0) {
-        const uint16_t* qrow = p.q + ((size_t)(t + r_me) * p.Hq + kvh * 4 + g_me) * HEAD_DIM;
+        const uint16_t* qrow = p.q + ((size_t)(t + r_me) * p.Hq + kvh * G + g_me) * HEAD_DIM;
 #pragma unroll
         for (int c = 0; c < 8; c++) qf[c] = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + dim0(c)));
     } else {
@@ -195,13 +202,14 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
 
 // Writes a verify piece's result for the lanes of (row r, head g): the gated
 // output when the piece holds all of the segment's keys, else the partial
-// record at index idx.
+// record at index idx (VF_ROWS records per index).
+template <int G>
 struct VerifyEpi {
     const DecodeParams& p;
     int t, kvh, idx;
     bool direct;
     __device__ __forceinline__ void operator()(int r, int g, int gq, const f32x4 (&acc)[16], float m, float l) const {
-        const int h = kvh * 4 + g, row_t = t + r;
+        const int h = kvh * G + g, row_t = t + r;
         if (direct) {
             const float inv = 1.f / l;
             const uint16_t* gate = p.qkv + (size_t)row_t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + 4 * gq;
@@ -223,29 +231,33 @@ struct VerifyEpi {
     }
 };
 
-// Key-range kernel over segments; grid (n_wg, ceil(Hkv / 4)), 64 * min(Hkv, 4)
-// threads. Same range split as decode_range_kernel with segment lengths in
-// place of token lengths; block 0 writes offs[t] (segment offsets by head
-// token, equal neighbours for other tokens), offs[T] = W, offs[T + 1] = R.
-// The bound caps it at 256 VGPRs (210, no spills); it runs one workgroup per
-// CU (two ranges per CU measured slower: 856 against 817 us at C5).
+// Key-range kernel over segments of vf_rows(G) rows; grid (n_wg,
+// ceil(Hkv / 4)), 64 * min(Hkv, 4) threads. Same range split as
+// decode_range_kernel with segment lengths in place of token lengths; block 0
+// writes offs[t] (segment offsets by head token, equal neighbours for other
+// tokens), offs[T] = W, offs[T + 1] = R. The bound caps it at 256 VGPRs (no
+// spills); it runs one workgroup per CU (two ranges per CU measured slower:
+// 856 against 817 us at C5).
+template <int G>
 __global__ void __launch_bounds__(256, 2)
     verify_range_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                         const int* __restrict__ block_table, const int* __restrict__ cu,
                         const int* __restrict__ outs) {
+    constexpr int NR = vf_rows(G);
     __shared__ int sh_scan[16];
     __shared__ int sh_t0[2];
     __shared__ __align__(16) uint16_t sh_v[4][VF_LDS];
     const int T = p.T, nthr = blockDim.x, tid = threadIdx.x, b = blockIdx.x;
     int nr, start, end, t0, off0;
     if (!find_range(
-            p, [&](int t) { return seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr); }, sh_scan,
+            p, [&](int t) { return seg_len<NR>(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr); }, sh_scan,
             sh_t0, start, end, t0, off0))
         return;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = blockIdx.y * 4 + wave;
     int t = t0, off = off0;
     while (off < end && t < T) {
-        const int Ls = __builtin_amdgcn_readfirstlane(seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr));
+        const int Ls =
+            __builtin_amdgcn_readfirstlane(seg_len<NR>(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr));
         if (Ls > 0) {
             nr = __builtin_amdgcn_readfirstlane(nr);
             int Lr[VF_ROWS];
@@ -256,9 +268,8 @@ __global__ void __launch_bounds__(256, 2)
                                : 0;
             const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
             const int j0 = max(start, off) - off, j1 = min(end, off + Ls) - off;
-            const VerifyEpi epi{p, t, kvh, t + b, j0 == 0 && j1 == Ls};
-            verify_piece(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Lr[0], Lr[1],
-                             Lr[2], Lr[3], epi);
+            const VerifyEpi<G> epi{p, t, kvh, t + b, j0 == 0 && j1 == Ls};
+            verify_piece<G>(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Lr, epi);
             off += Ls;
         }
         t++;
@@ -266,25 +277,28 @@ __global__ void __launch_bounds__(256, 2)
 }
 
 // The same over an E4M3 cache with the E4M3 decode body (two pages per
-// step, both products on MFMA, 16 columns = 4 rows x 4 query heads): grid
+// step, both products on MFMA, 16 columns = rows x query heads): grid
 // (n_wg, ceil(Hkv / 4)) with two workgroups per CU (at most 256 VGPRs).
+template <int G>
 __global__ void __launch_bounds__(256, 2)
     verify_range8_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                          const int* __restrict__ block_table, const int* __restrict__ cu,
                          const int* __restrict__ outs) {
+    constexpr int NR = vf_rows(G);
     __shared__ int sh_scan[16];
     __shared__ int sh_t0[2];
     __shared__ WaveLds8 sh_w8[4];
     const int T = p.T, tid = threadIdx.x, b = blockIdx.x;
     int nr, start, end, t0, off0;
     if (!find_range(
-            p, [&](int t) { return seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr); }, sh_scan,
+            p, [&](int t) { return seg_len<NR>(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr); }, sh_scan,
             sh_t0, start, end, t0, off0))
         return;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = blockIdx.y * 4 + wave;
     int t = t0, off = off0;
     while (off < end && t < T) {
-        const int Ls = __builtin_amdgcn_readfirstlane(seg_len(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr));
+        const int Ls =
+            __builtin_amdgcn_readfirstlane(seg_len<NR>(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr));
         if (Ls > 0) {
             nr = __builtin_amdgcn_readfirstlane(nr);
             int Lr[VF_ROWS];
@@ -295,9 +309,11 @@ __global__ void __launch_bounds__(256, 2)
                                : 0;
             const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
             const int j0 = max(start, off) - off, j1 = min(end, off + Ls) - off;
-            const VerifyEpi vepi{p, t, kvh, t + b, j0 == 0 && j1 == Ls};
-            auto epi = [&](int c, int gq, const f32x4 (&acc)[16], float m, float l) { vepi(c >> 2, c & 3, gq, acc, m, l); };
-            piece_body8<VF_ROWS>(p, block_table + (size_t)seq * p.max_blocks, sh_w8[wave], t, kvh, j0, j1, epi, Lr);
+            const VerifyEpi<G> vepi{p, t, kvh, t + b, j0 == 0 && j1 == Ls};
+            auto epi = [&](int c, int gq, const f32x4 (&acc)[16], float m, float l) {
+                vepi(c / G, c % G, gq, acc, m, l);
+            };
+            piece_body8<NR, G>(p, block_table + (size_t)seq * p.max_blocks, sh_w8[wave], t, kvh, j0, j1, epi, Lr);
             off += Ls;
         }
         t++;
@@ -305,15 +321,16 @@ __global__ void __launch_bounds__(256, 2)
 }
 
 // Merges the split segments: one block per (row, query head); row t's
-// segment is headed by the row at offset 4 * floor((t - cu[s]) / 4) of its
-// sequence.
+// segment (NR rows) is headed by the row at offset NR * floor((t - cu[s]) /
+// NR) of its sequence.
+template <int NR>
 __global__ void __launch_bounds__(256)
     verify_merge_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                         const int* __restrict__ cu, const int* __restrict__ outs) {
     const int t = blockIdx.x, T = p.T;
     if (decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec) <= 0) return;
     const int c0 = cu[tok_seq[t]];
-    const int r = (t - c0) & (VF_ROWS - 1), th = t - r;
+    const int r = (t - c0) & (NR - 1), th = t - r;
     if (th < 0) return;
     const int o0 = p.offs[th], o1 = p.offs[th + 1];
     if (o1 <= o0) return;

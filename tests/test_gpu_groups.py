@@ -1,0 +1,105 @@
+"""GPU parity for the query-head groups other than 4 (G = Hq / Hkv in 1, 2,
+6, 8: the reference instantiates attn_paged_g<G> / attn_paged8_g<G> for
+these, src/kernels/qwen35.cu:1326-1334, and loads the one of the model's
+ratio, src/model.rs:1054). bf16 and E4M3 caches, per-token decode and
+grouped verify rows, against the oracle, which takes any G.
+
+Tolerance (north star): bf16 outputs within max-abs 2e-3 and relative 1e-2,
+|got - want| <= 2e-3 + 1e-2 * |want|."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import pkv
+from _util import BS, D, close, decode_case, nan_stale
+from test_gpu_decode import run_gpu, run_oracle
+from test_gpu_e4m3 import e4m3_cache, run_decode8
+from test_gpu_verify import run_oracle as run_oracle_v, run_verify, verify_case
+
+pytestmark = pytest.mark.gpu
+SCALE = 1.0 / 16.0
+
+# (G, Hkv): the reference's 27B shape is 24 query heads over 4 kv heads.
+GROUPS = [(1, 4), (2, 2), (6, 4), (6, 1), (8, 2), (8, 8)]
+
+
+@pytest.fixture(autouse=True)
+def default_config():
+    pkv.attn_decode_config(1, 32)
+    yield
+    pkv.attn_decode_config(1, 32)
+
+
+@pytest.mark.parametrize("G,Hkv", GROUPS)
+@pytest.mark.parametrize("lens,seed,min_range", [
+    ([1, 2, 15, 16, 17, 33], 0, 32),        # page edges, one key
+    ([513, 4097, 1000, 64], 1, 32),         # split over ranges
+    ([700, 2000], 2, 1 << 20),              # whole tokens per range
+])
+def test_decode_groups_match_oracle(dev, G, Hkv, lens, seed, min_range):
+    print(f"case decode G={G} Hkv={Hkv} lens={lens} min_range={min_range}", flush=True)
+    pkv.attn_decode_config(1, min_range)
+    c = decode_case(lens, G * Hkv, Hkv, seed)
+    ok, err = close(run_gpu(c, dev), run_oracle(c, cu=c["cu"]))
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("G,Hkv", GROUPS)
+def test_verify_groups_match_oracle(dev, G, Hkv):
+    """Rows of a sequence share a pass: 4 rows per segment for G <= 4, 2
+    for G = 6 and 8; ragged row counts, one skipped prompt."""
+    print(f"case verify G={G} Hkv={Hkv}", flush=True)
+    c = verify_case([(300, 4), (0, 9), (40, 3), (90, 1), (2000, 5), (12, 2)], Hkv, 20 + G, G=G)
+    outs = np.array([0, -1, 0, 0, 0, 0], np.int32)
+    init = np.full((c["T"], c["Hq"], D), 0x5555, np.uint16)
+    got = run_verify(c, dev, skip=1, outs=outs, out_init=init)
+    assert (got[4:13] == 0x5555).all()
+    want = run_oracle_v(c, skip_prompts=1, outs=outs, spec=1, out=init.copy())
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("G,Hkv", [(6, 4), (8, 2)])
+def test_groups_stale_slots_are_nan(dev, G, Hkv):
+    print(f"case decode G={G} NaN stale slots", flush=True)
+    lens = [1, 17, 130, 2049]
+    c = nan_stale(decode_case(lens, G * Hkv, Hkv, 40 + G), lens)
+    ok, err = close(run_gpu(c, dev), run_oracle(c, cu=c["cu"]))
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("entry", ["decode", "verify"])
+@pytest.mark.parametrize("G,Hkv", GROUPS)
+def test_e4m3_groups_match_oracle(dev, entry, G, Hkv):
+    print(f"case {entry} e4m3 G={G} Hkv={Hkv}", flush=True)
+    if entry == "verify":
+        c = verify_case([(300, 4), (40, 3), (90, 1), (2000, 5), (12, 2)], Hkv, 60 + G, G=G)
+    else:
+        c = decode_case([1, 16, 17, 513, 4097, 64], G * Hkv, Hkv, 60 + G)
+    rng = np.random.default_rng(70 + G)
+    k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+    ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+    vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+    got = run_decode8(c, k8, v8, ks, vs, dev, entry=entry)
+    want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], c["Hq"], Hkv, c["pos"], c["tok_seq"],
+                               c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
+
+
+def test_fused_step_rejects_other_groups(dev):
+    """The fused append + decode step serves G = 4 only; other groups get
+    PKV_ERR_UNSUPPORTED before any launch."""
+    c = decode_case([40, 50], 24, 4, 3)
+    T = 2
+    q = torch.zeros(T, 24, D, dtype=torch.int16, device=dev)
+    kc = torch.zeros(c["pages"] * BS, 4, D, dtype=torch.int16, device=dev)
+    rows = torch.zeros(T, 4 * D, dtype=torch.int16, device=dev)
+    qkv = torch.zeros(T, c["qstride"], dtype=torch.int16, device=dev)
+    i = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+    ws = torch.empty(pkv.attn_decode_workspace(T, 24), dtype=torch.uint8, device=dev)
+    with pytest.raises(pkv.PkvError, match="unsupported"):
+        pkv.attn_decode_step(rows, rows, 4 * D * 2, i([0, 16]), q, kc, kc, qkv, c["qstride"], 24, 4, i(c["pos"]),
+                             i(c["tok_seq"]), i(c["bt"]), c["max_blocks"], BS, q, SCALE, i(c["cu"]), 0, None, 1, T,
+                             c["pages"], ws)

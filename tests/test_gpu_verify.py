@@ -35,11 +35,12 @@ def default_config():
     pkv.attn_decode_config(1, 32)
 
 
-def verify_case(groups, Hkv, seed):
+def verify_case(groups, Hkv, seed, G=4):
     """groups: (L0, n) per sequence: n rows at positions L0 .. L0 + n - 1,
-    every key already cached; pages from a seeded permutation."""
+    every key already cached; pages from a seeded permutation; G query
+    heads per kv head."""
     rng = np.random.default_rng(seed)
-    Hq = 4 * Hkv
+    Hq = G * Hkv
     need = [(L0 + n + BS - 1) // BS for L0, n in groups]
     mb = max(need)
     pages = sum(need) + 3
