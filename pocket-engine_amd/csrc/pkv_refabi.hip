@@ -8,8 +8,9 @@
 // kernel bodies:
 //
 //   attn_prep       (qwen35.cu:1076-1082)  grid (T, Hq + 2 Hkv), 128 threads
-//   attn_paged_g4   (qwen35.cu:1313-1334)  grid (T, Hkv, Z), 256 threads
-//   attn_paged8_g4  the same over an E4M3 cache (kscale / vscale)
+//   attn_paged_g<G> (qwen35.cu:1313-1334)  grid (T, Hkv, Z), 256 threads
+//                   (G = 1, 2, 4) or 128 (G = 6, 8)
+//   attn_paged8_g<G> the same over an E4M3 cache (kscale / vscale)
 //   attn_merge      (qwen35.cu:2245-2249)  grid (T, Hq), 256 threads
 //   attn_groupr_g4_t2_k32 (qwen35.cu:1600-1616) grid (ceil(T/32) + seqs, Hkv),
 //                   256 threads: the prompt kernel a gfx950 device (compute
@@ -24,13 +25,15 @@
 // range z of nz = split_parts(L, Z, min_chunk) covers keys [z c, z c + c),
 // c = ceil(L / nz), and leaves a record [M (natural log), S, A[256]] at
 // part[((s * spec + t - cu[s]) * Hq + h) * Z + z]; attn_merge combines the nz
-// records. Inside a block the 4 waves take a quarter of the range's pages each
-// (this build's decode wave body: dot2 + DPP reduce-scatter, online softmax,
-// one page in flight) and combine through LDS.
+// records. Inside a block the waves take an equal share of the range's pages
+// each (G = 4: this build's decode wave body, dot2 + DPP reduce-scatter,
+// online softmax, one page in flight; other groups: the verify body with one
+// row) and combine through LDS.
 //
 // Bounds of this ABI: FP8
 // output copies (fmode != 0) are not produced; block_size 16 for decode, a
-// power of two for prompts; G = Hq / Hkv = 4. A launch outside these bounds
+// power of two for prompts; G = Hq / Hkv = 4 for prompts, 1, 2, 4, 6 or 8 for
+// decode. A launch outside these bounds
 // writes nothing. Page ids are not clamped (the reference ABI passes no pool
 // size).
 #include "pkv_copy.hip"
@@ -94,10 +97,12 @@ extern "C" __global__ void __launch_bounds__(128)
 
 namespace pkv {
 
-// attn_paged_g4 / attn_paged8_g4 on the reference's grid (token t, kv head,
-// range z): the range's pages split over the 4 waves (bf16: the decode wave
-// body; E4M3: the E4M3 decode body, two pages per step), combined through LDS.
-template <bool F8>
+// attn_paged_g<G> / attn_paged8_g<G> on the reference's grid (token t, kv
+// head, range z) and block (256 threads for G <= 4, 128 for G = 6 and 8,
+// model.rs:2374): the range's pages split over the NW waves (bf16: the decode
+// wave body for G = 4, the verify body with one row for other groups; E4M3:
+// the E4M3 decode body, two pages per step), combined through LDS.
+template <int G, bool F8>
 __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache, const void* vcache,
                                           const float* kscale, const float* vscale, const uint16_t* qkv, int qstride,
                                           int Hq, int Hkv, const int* __restrict__ pos,
@@ -105,20 +110,24 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
                                           int max_blocks, int block_size, uint16_t* out, float scale,
                                           const int* __restrict__ cu, int skip_prompts, int min_chunk, float* part,
                                           const int* __restrict__ outs, int spec) {
-    constexpr int G = 4;
-    // bf16: the decode wave body's LDS and a separate record per wave. E4M3:
-    // the E4M3 decode body's LDS per wave, whose V staging rows also hold the
-    // wave's record once its loop is done (72 KB in all: two workgroups per
-    // CU).
-    __shared__ WaveLds<G> sh_w[F8 ? 1 : 4];
-    __shared__ WaveLds8 sh_w8[F8 ? 4 : 1];
-    __shared__ float sh_acc_bf[F8 ? 1 : 4][G][HEAD_DIM];
-    __shared__ float sh_ml[4][G][2];
+    constexpr int NW = G >= 6 ? 2 : 4;  // waves
+    constexpr bool BODY4 = !F8 && G == 4;
+    constexpr bool BODYV = !F8 && G != 4;
+    static_assert(G * HEAD_DIM * 4 <= (int)sizeof(WaveLds8::v), "E4M3 record fits the V staging rows");
+    // bf16: the decode wave body's LDS (or the verify body's V staging) and a
+    // separate record per wave. E4M3: the E4M3 decode body's LDS per wave,
+    // whose V staging rows also hold the wave's record once its loop is done
+    // (72 KB in all at G = 4: two workgroups per CU).
+    __shared__ WaveLds<4> sh_w[BODY4 ? NW : 1];
+    __shared__ __align__(16) uint16_t sh_v[BODYV ? NW : 1][BODYV ? VF_LDS : 8];
+    __shared__ WaveLds8 sh_w8[F8 ? NW : 1];
+    __shared__ float sh_acc_bf[F8 ? 1 : NW][G][HEAD_DIM];
+    __shared__ float sh_ml[NW][G][2];
     auto rec = [&](int w) -> float (*)[HEAD_DIM] {
         if constexpr (F8) return reinterpret_cast<float (*)[HEAD_DIM]>(sh_w8[w].v);
         else return sh_acc_bf[w];
     };
-    if (blockDim.x != 256 || block_size != PAGE || Hq != G * Hkv || (kscale != nullptr) != F8 ||
+    if (blockDim.x != 64 * NW || block_size != PAGE || Hq != G * Hkv || (kscale != nullptr) != F8 ||
         (vscale != nullptr) != F8)
         return;
     const int tid = threadIdx.x;
@@ -132,16 +141,16 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
     if (gridDim.x <= 256) {
         __shared__ int sh_len[256], sh_order[256];
         const int T = gridDim.x;
-        if (tid < T) sh_len[tid] = pos[tid];
+        for (int u = tid; u < T; u += 64 * NW) sh_len[u] = pos[u];
         __syncthreads();
-        if (tid < T) {
-            const int mine = sh_len[tid];
+        for (int me = tid; me < T; me += 64 * NW) {
+            const int mine = sh_len[me];
             int rank = 0;
             for (int u = 0; u < T; u++) {
                 const int o = sh_len[u];
-                rank += o > mine || (o == mine && u < tid);
+                rank += o > mine || (o == mine && u < me);
             }
-            sh_order[rank] = tid;
+            sh_order[rank] = me;
         }
         __syncthreads();
         const int per = gridDim.y * gridDim.z;
@@ -177,7 +186,7 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int a = j1, b = j1;
     if (j0 < j1) {
-        const int pg0 = j0 / PAGE, np = (j1 - 1) / PAGE - pg0 + 1, per = (np + 3) / 4;
+        const int pg0 = j0 / PAGE, np = (j1 - 1) / PAGE - pg0 + 1, per = (np + NW - 1) / NW;
         a = max(j0, (pg0 + wave * per) * PAGE);
         b = min(j1, (pg0 + (wave + 1) * per) * PAGE);
     }
@@ -209,7 +218,20 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
                     sh_ml[wave][g][1] = l;
                 }
             };
-            piece_body8(p, bt, sh_w8[wave], t, kvh, a, b, epi);
+            piece_body8<1, G>(p, bt, sh_w8[wave], t, kvh, a, b, epi);
+        } else if constexpr (BODYV) {
+            auto epi = [&](int, int g, int gq, const f32x4 (&acc)[16], float m, float l) {
+#pragma unroll
+                for (int db = 0; db < 16; db++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) rec(wave)[g][16 * db + 4 * gq + i] = acc[db][i];
+                if (gq == 0) {
+                    sh_ml[wave][g][0] = m;
+                    sh_ml[wave][g][1] = l;
+                }
+            };
+            const int Lr[VF_ROWS] = {L, 0, 0, 0};
+            verify_piece<G>(p, bt, sh_v[wave], t, kvh, a, b, Lr, epi);
         } else {
             auto epi = [&](int g, const float (&acc)[8], float m, float l, int ch) {
 #pragma unroll
@@ -219,19 +241,19 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
                     sh_ml[wave][g][1] = l;
                 }
             };
-            piece_body<G, false>(p, bt, sh_w[wave], t, kvh, a, b, L, INT_MAX, 0, epi);
+            piece_body<4, false>(p, bt, sh_w[wave], t, kvh, a, b, L, INT_MAX, 0, epi);
         }
     }
     __syncthreads();
-    // Combine the waves: thread d owns dimension d of every head.
-    const int d = tid;
-    for (int g = 0; g < G; g++) {
+    // Combine the waves: thread d owns dimensions d, d + 64 NW, .. of every head.
+    for (int gd = tid; gd < G * HEAD_DIM; gd += 64 * NW) {
+        const int g = gd / HEAD_DIM, d = gd % HEAD_DIM;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; w++) M = fmaxf(M, sh_ml[w][g][0]);
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sh_ml[w][g][0]);
         float S = 0.f, A = 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
+        for (int w = 0; w < NW; w++) {
             const float f = sh_ml[w][g][0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sh_ml[w][g][0] - M);
             S += sh_ml[w][g][1] * f;
             A += rec(w)[g][d] * f;
@@ -265,10 +287,21 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
     q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, \
         out, scale, cu, skip_prompts, min_chunk, part, outs, spec
 
-extern "C" __global__ void __launch_bounds__(256) attn_paged_g4(PKV_PAGED_ARGS) { pkv::paged_ref<false>(PKV_PAGED_PASS); }
-
-// The same over an E4M3 cache (kscale / vscale given).
-extern "C" __global__ void __launch_bounds__(256, 2) attn_paged8_g4(PKV_PAGED_ARGS) { pkv::paged_ref<true>(PKV_PAGED_PASS); }
+// attn_paged_g<G> over a bf16 cache and attn_paged8_g<G> over an E4M3 cache
+// (kscale / vscale given), for the groups the reference instantiates
+// (qwen35.cu:1330-1334).
+#define PKV_PAGED_KERNELS(G, THREADS)                                                                            \
+    extern "C" __global__ void __launch_bounds__(THREADS) attn_paged_g##G(PKV_PAGED_ARGS) {                      \
+        pkv::paged_ref<G, false>(PKV_PAGED_PASS);                                                                \
+    }                                                                                                            \
+    extern "C" __global__ void __launch_bounds__(THREADS, 2) attn_paged8_g##G(PKV_PAGED_ARGS) {                  \
+        pkv::paged_ref<G, true>(PKV_PAGED_PASS);                                                                 \
+    }
+PKV_PAGED_KERNELS(1, 256)
+PKV_PAGED_KERNELS(2, 256)
+PKV_PAGED_KERNELS(4, 256)
+PKV_PAGED_KERNELS(6, 128)
+PKV_PAGED_KERNELS(8, 128)
 
 extern "C" __global__ void __launch_bounds__(256)
     attn_merge(const float* __restrict__ part, int Z, int min_chunk, const uint16_t* __restrict__ qkv, int qstride,

@@ -35,19 +35,27 @@ def i32(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
 
 
-def ref_decode(rk, c, dev, Z=None, spec=1, skip=0, outs=None, out_init=None, keep_part=False):
-    """attn_paged_g4 (+ attn_merge when split) as model.rs:2366-2437 launches them."""
+def ref_decode(rk, c, dev, Z=None, spec=1, skip=0, outs=None, out_init=None, keep_part=False, f8=None):
+    """attn_paged_g<G> (+ attn_merge when split) as model.rs:2366-2437 launches
+    them: the kernel of the model's G = Hq / Hkv, 128 threads for G >= 6, else
+    256. f8 = (k8, v8, kscale, vscale) launches attn_paged8_g<G> over an E4M3
+    cache."""
     T, Hq, Hkv = len(c["pos"]), c["Hq"], c["Hkv"]
+    G = Hq // Hkv
     sms = torch.cuda.get_device_properties(0).multi_processor_count
     ranges = split_ranges(T, Hkv, sms) if Z is None else Z
     seqs = len(c["cu"]) - 1
     part = (torch.full((seqs * spec * ranges * Hq * (D + 2),), float("nan"), device=dev) if ranges > 1 else None)
-    q, kc, vc, qkv = (i16(c[k], dev) for k in ("q", "kc", "vc", "qkv"))
+    q, qkv = i16(c["q"], dev), i16(c["qkv"], dev)
+    if f8 is None:
+        kc, vc, ks, vs = i16(c["kc"], dev), i16(c["vc"], dev), None, None
+    else:
+        kc, vc, ks, vs = (torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in f8)
     pos, ts, bt, cu = i32(c["pos"], dev), i32(c["tok_seq"], dev), i32(c["bt"], dev), i32(c["cu"], dev)
     outs_d = None if outs is None else i32(outs, dev)
     out = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev) if out_init is None else i16(out_init, dev)
-    rk.launch("attn_paged_g4", (T, Hkv, ranges), 256, 0,
-              [P(q), P(kc), P(vc), P(None), P(None), P(qkv), I(c["qstride"]), I(Hq), I(Hkv), P(pos), P(ts), P(bt),
+    rk.launch(f"attn_paged{'8' if f8 is not None else ''}_g{G}", (T, Hkv, ranges), 128 if G >= 6 else 256, 0,
+              [P(q), P(kc), P(vc), P(ks), P(vs), P(qkv), I(c["qstride"]), I(Hq), I(Hkv), P(pos), P(ts), P(bt),
                I(c["max_blocks"]), I(BS), P(out), F(SCALE), P(None), P(None), I(0), I(0), P(cu), I(skip),
                I(SPLIT_MIN_KEYS), P(part), P(outs_d), I(spec)])
     if part is not None:
@@ -80,6 +88,55 @@ def test_ref_decode_matches_oracle(dev, rk, lens, Hkv, seed, Z):
     c = decode_case(lens, 4 * Hkv, Hkv, seed)
     ok, err = close(ref_decode(rk, c, dev, Z=Z), oracle_decode(c))
     assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("G,Hkv", [(1, 4), (2, 2), (6, 4), (6, 1), (8, 2), (8, 8)])
+@pytest.mark.parametrize("lens,seed,Z", [
+    ([1, 2, 15, 16, 17, 33], 0, None),
+    ([513, 4097, 1000, 64], 1, None),
+    ([900, 70, 4000], 2, 1),
+    ([40, 3, 100] * 100, 3, None),             # 300 tokens: more than a block's threads to order
+])
+def test_ref_decode_groups_match_oracle(dev, rk, G, Hkv, lens, seed, Z):
+    """attn_paged_g1/g2/g6/g8: the reference loads attn_paged_g<Hq / Hkv>
+    (model.rs:1053-1054)."""
+    print(f"case refabi decode G={G} Hkv={Hkv} lens={lens[:6]} Z={Z}", flush=True)
+    c = decode_case(lens, G * Hkv, Hkv, seed)
+    ok, err = close(ref_decode(rk, c, dev, Z=Z), oracle_decode(c))
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("G,Hkv", [(1, 4), (2, 2), (4, 4), (6, 4), (8, 2)])
+def test_ref_paged8_groups_match_oracle(dev, rk, G, Hkv):
+    print(f"case refabi paged8 G={G} Hkv={Hkv}", flush=True)
+    from test_gpu_e4m3 import e4m3_cache
+    c = decode_case([1, 17, 513, 4097, 64, 900], G * Hkv, Hkv, 30 + G)
+    rng = np.random.default_rng(31 + G)
+    k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+    ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+    vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+    got = ref_decode(rk, c, dev, f8=(k8, v8, ks, vs))
+    want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], c["Hq"], Hkv, c["pos"], c["tok_seq"],
+                               c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
+
+
+def test_ref_paged_wrong_block_writes_nothing(dev, rk):
+    """attn_paged_g6 launched with 64 threads (not the engine's 128) returns
+    before any work. (A block above the kernel's 128-thread bound is refused
+    by the runtime at launch.)"""
+    print("case refabi paged g6 wrong block", flush=True)
+    c = decode_case([100, 40], 24, 4, 9)
+    init = np.full((2, 24, D), 0x3333, np.uint16)
+    out = i16(init, dev)
+    rk.launch("attn_paged_g6", (2, 4, 1), 64, 0,
+              [P(i16(c["q"], dev)), P(i16(c["kc"], dev)), P(i16(c["vc"], dev)), P(None), P(None),
+               P(i16(c["qkv"], dev)), I(c["qstride"]), I(24), I(4), P(i32(c["pos"], dev)), P(i32(c["tok_seq"], dev)),
+               P(i32(c["bt"], dev)), I(c["max_blocks"]), I(BS), P(out), F(SCALE), P(None), P(None), I(0), I(0),
+               P(i32(c["cu"], dev)), I(0), I(SPLIT_MIN_KEYS), P(None), P(None), I(1)])
+    torch.cuda.synchronize()
+    assert (out.cpu().numpy().view(np.uint16) == 0x3333).all()
 
 
 def test_ref_spec_rows_and_prompt_skip(dev, rk):
