@@ -101,6 +101,9 @@ def main():
     ap.add_argument("--with-prep", action="store_true",
                     help="c2/c3: the step's append is pkv_attn_prep (q/k RMSNorm + rotary + K/V slot writes, the "
                          "reference's attn_prep) on the raw qkv rows, followed by the key ranges and the merge")
+    ap.add_argument("--q-heads", type=int, default=16,
+                    help="c2/c3 query heads over the 4 kv heads (16: the configs' G = 4; 24: the reference's 27B "
+                         "shape, G = 6, run unfused: append, then decode attention)")
     ap.add_argument("--unfused", action="store_true",
                     help="append, key ranges and merge as three launches instead of the fused step")
     args = ap.parse_args()
@@ -141,7 +144,10 @@ def main():
         pkv.attn_decode_config(args.wg_per_cu or 1, args.min_range or 32)
     seed = args.seed if args.seed is not None else int(time.time()) % 100000
     dev = torch.device("cuda:0")
-    Hq, Hkv, D, BS = 16, 4, 256, 16
+    Hq, Hkv, D, BS = args.q_heads, 4, 256, 16
+    G = Hq // Hkv
+    if G != 4:
+        args.unfused = True  # the fused step serves G = 4
     B, pages = args.batch, args.pages
     S = args.warmup + args.steps
     if args.config == "c2":
@@ -212,7 +218,7 @@ def main():
                 pkv.append(k_rows, v_rows, qstride * 2, slot_d[i], B, Hkv, D * 2, kc, vc, pages * BS, stream=s_)
             if ev:
                 kev.record(ev[0], s_)
-            rk.launch("attn_paged8_g4" if e4m3 else "attn_paged_g4", (B, Hkv, Z), 256, 0,
+            rk.launch(f"attn_paged8_g{G}" if e4m3 else f"attn_paged_g{G}", (B, Hkv, Z), 128 if G >= 6 else 256, 0,
                       [P_(q), P_(kc), P_(vc), P_(kscale if e4m3 else None), P_(vscale if e4m3 else None), P_(qkv), I_(qstride), I_(Hq), I_(Hkv),
                        P_(pos_d[i]), P_(ts), P_(bt), I_(meta.max_blocks), I_(BS), P_(out), F_(1 / 16), P_(None),
                        P_(None), I_(0), I_(0), P_(cu), I_(0), I_(refabi.SPLIT_MIN_KEYS), P_(part), P_(None), I_(1)],
@@ -306,11 +312,12 @@ def main():
         # key-range kernel: every key's K and V rows (all kv heads) + q; its
         # partials are overhead, not algorithmic.
         kern_bytes = [kk * Hkv * (D + 4 if e4m3 else D * 2) * 2 + B * Hq * D * 2 for kk in keys]
-        kname = ("attn_paged8_g4 (reference ABI, E4M3 cache, after attn_prep)" if e4m3 and args.refabi else
-                 "decode_range8_kernel (E4M3 cache, after attn_prep)" if e4m3 else
-                 "attn_paged_g4 (reference ABI)" if args.refabi else
+        kname = (f"attn_paged8_g{G} (reference ABI, E4M3 cache, after attn_prep)" if e4m3 and args.refabi else
+                 f"decode_range8_kernel<{G}> (E4M3 cache, after attn_prep)" if e4m3 else
+                 f"attn_paged_g{G} (reference ABI)" if args.refabi else
+                 f"verify_range_kernel<{G}> (one row per segment)" if G != 4 else
                  "decode_range_kernel<4,false> (after attn_prep)" if args.with_prep else
-                 "verify_range_kernel" if args.verify_kernel else "decode_range_kernel<4,false>")
+                 "verify_range_kernel<4>" if args.verify_kernel else "decode_range_kernel<4,false>")
     else:
         kern_bytes = step_bytes  # the fused kernel does the whole step
         kname = "decode_range_kernel<4,true> (fused append + attention + merge)"
@@ -354,7 +361,7 @@ def main():
                                 "c2: single-sequence paged decode step at 4096 context (append + attention)"),
                    "kv": args.kv,
                    "path": ("attn_prep (E4M3 store), key ranges over the E4M3 cache, merge" if e4m3 else
-                            "reference-ABI code object (append, attn_paged_g4, attn_merge)" if args.refabi else
+                            f"reference-ABI code object (append, attn_paged_g{G}, attn_merge)" if args.refabi else
                             "attn_prep (norm + rotary + append), key ranges, merge" if args.with_prep else
                             "unfused (append, key ranges, merge)" if args.unfused else "fused step (one launch)"),
                    "batch": B, "ctx": "4096" if args.config == "c2" else "U[512,8192]", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,

@@ -12,8 +12,19 @@
 #include <hip/hip_ext.h>
 
 #include <mutex>
+#include <set>
 
 namespace {
+
+// Query heads per kv head the attention kernels serve (the
+// reference instantiates attn_paged_g<G> for the same groups,
+// qwen35.cu:1326-1334).
+bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 6 || G == 8; }
+template <class K>
+K by_group(int G, K g1, K g2, K g4, K g6, K g8) {
+    return G == 1 ? g1 : G == 2 ? g2 : G == 4 ? g4 : G == 6 ? g6 : g8;
+}
+
 
 int status_of(hipError_t e) { return e == hipSuccess ? PKV_OK : (int)e; }
 
@@ -202,7 +213,8 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     if (T < 0 || seqs < 0 || Hq <= 0 || Hkv <= 0 || max_blocks <= 0 || block_size <= 0 || num_blocks <= 0 ||
         spec < 1)
         return PKV_ERR_INVALID;
-    if (Hq != 4 * Hkv || (block_size & (block_size - 1)) != 0) return PKV_ERR_UNSUPPORTED;
+    const int G = Hq % Hkv == 0 ? Hq / Hkv : 0;
+    if (!supported_group(G) || (block_size & (block_size - 1)) != 0) return PKV_ERR_UNSUPPORTED;
     if (T == 0 || seqs == 0) return PKV_OK;
     if (!q || !kcache || !vcache || !qkv || !pos || !cu || !block_table || !out) return PKV_ERR_INVALID;
     if (qstride < 2 * Hq * pkv::HEAD_DIM || qstride % 8 != 0) return PKV_ERR_INVALID;
@@ -210,14 +222,27 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
         return PKV_ERR_INVALID;
     const bool f8 = kscale != nullptr;
     if (f8 && (!vscale || !aligned(kscale, 4) || !aligned(vscale, 4))) return PKV_ERR_INVALID;
-    static bool attr_set = false;  // per process: the kernels' LDS above the 64 KiB default
-    const size_t smem = pkv::prefill_smem_bytes();
-    if (!attr_set) {
-        for (const void* k : {(const void*)pkv::prefill_kernel, (const void*)pkv::prefill_e4m3_kernel}) {
-            const int st = status_of(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    using PrefillKernel = void (*)(pkv::PrefillParams);
+    const PrefillKernel kern =
+        f8 ? by_group<PrefillKernel>(G, pkv::prefill_e4m3_kernel<1>, pkv::prefill_e4m3_kernel<2>,
+                                     pkv::prefill_e4m3_kernel<4>, pkv::prefill_e4m3_kernel<6>,
+                                     pkv::prefill_e4m3_kernel<8>)
+           : by_group<PrefillKernel>(G, pkv::prefill_kernel<1>, pkv::prefill_kernel<2>, pkv::prefill_kernel<4>,
+                                     pkv::prefill_kernel<6>, pkv::prefill_kernel<8>);
+    const int bq = pkv::pf_lib_bq(G);
+    const int threads = 64 * G * bq / 32 / (G == 4 ? pkv::PF_NQB : 1);
+    const size_t smem = pkv::prefill_smem_bytes(pkv::PF_NST, threads);
+    // per process: the kernels' LDS above the 64 KiB default, once per kernel
+    static std::mutex attr_mu;
+    static std::set<const void*> attr_set;
+    {
+        std::lock_guard<std::mutex> lk(attr_mu);
+        if (!attr_set.count((const void*)kern)) {
+            const int st = status_of(
+                hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
             if (st != PKV_OK) return st;
+            attr_set.insert((const void*)kern);
         }
-        attr_set = true;
     }
     pkv::PrefillParams p;
     p.q = (const uint16_t*)q;
@@ -244,9 +269,8 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     hipEvent_t e0 = t_pf_start, e1 = t_pf_stop;
     t_pf_start = t_pf_stop = nullptr;
     // Upper bound on query tiles: each prompt sequence rounds up once.
-    const int tiles = (T + pkv::PF_BQ - 1) / pkv::PF_BQ + seqs;
-    hipExtLaunchKernelGGL(f8 ? pkv::prefill_e4m3_kernel : pkv::prefill_kernel, dim3(tiles, Hkv),
-                          dim3(pkv::PF_THREADS), smem, (hipStream_t)stream, e0, e1, 0, p);
+    const int tiles = (T + bq - 1) / bq + seqs;
+    hipExtLaunchKernelGGL(kern, dim3(tiles, Hkv), dim3(threads), smem, (hipStream_t)stream, e0, e1, 0, p);
     return launch_status();
 }
 
@@ -319,15 +343,6 @@ struct AppendArgs {
     int64_t row_stride;  // bytes
     const int32_t* slot_map;
 };
-
-// Query heads per kv head the decode, verify and E4M3 kernels serve (the
-// reference instantiates attn_paged_g<G> for the same groups,
-// qwen35.cu:1326-1334).
-bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 6 || G == 8; }
-template <class K>
-K by_group(int G, K g1, K g2, K g4, K g6, K g8) {
-    return G == 1 ? g1 : G == 2 ? g2 : G == 4 ? g4 : G == 6 ? g6 : g8;
-}
 
 // phase bit 1: key-range kernel; bit 2: merge kernel; bit 4: the key-range
 // kernel with the step's append fused in (needs `app`); bit 8: the verify

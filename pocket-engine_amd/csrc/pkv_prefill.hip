@@ -7,10 +7,11 @@
 // P is rounded to bf16 for the P.V product, and the output is gated
 // bf16(rbf(O / l) * sigmoid(gate)).
 //
-// Tiling (this build's own). A workgroup takes 64 consecutive query
-// positions of one sequence and one kv head (32 for launches on a grid of
-// 32-query tiles): a wave per (query head of the group, block of 32
-// queries), 8 waves. Keys stream in tiles of 32 (two pages) staged in LDS
+// Tiling (this build's own). A workgroup takes BQ consecutive query
+// positions of one sequence and one kv head with its G query heads; its
+// BQ x G (query, head) columns go 32 to a wave: a wave per (query head,
+// block of 32 queries) when BQ >= 32 (G = 4: 64 queries, 8 waves), or per
+// (2 heads, 16 queries) on grids of 16-query tiles. Keys stream in tiles of 32 (two pages) staged in LDS
 // once for all waves (GQA sharing), K and V both row-major [key][d]. Per
 // tile a wave computes
 //   S^T[32 keys][32 queries] = K Q^T     16 x v_mfma_f32_32x32x16_bf16
@@ -85,24 +86,38 @@ __device__ __forceinline__ constexpr int pf_vrow(int r) { return (r & 15) * VP +
 // Elements of one K + V stage with V pairs VP elements apart.
 __host__ __device__ constexpr int pf_stage(int vp) { return PF_K_ELEMS + 16 * vp; }
 
-// Query positions per workgroup (BQ) and 32-query blocks per wave (NQB):
-// waves = 4 query heads x BQ / (32 NQB). NQB = 2 feeds every K / V^T
-// fragment read from LDS into two MFMAs (half the LDS traffic per MFMA) at
-// the cost of 128 q + 256 accumulator registers per wave (one wave per SIMD).
+// Query positions per workgroup (BQ), query heads per kv head (G) and
+// 32-query blocks per wave (NQB): waves = G x BQ / (32 NQB). NQB = 2 feeds
+// every K / V^T fragment read from LDS into two MFMAs (half the LDS traffic
+// per MFMA) at the cost of 128 q + 256 accumulator registers per wave (one
+// wave per SIMD).
 #ifndef PKV_PF_NQB
 #define PKV_PF_NQB 1
 #endif
 constexpr int PF_BQ = 64;
 constexpr int PF_NQB = PKV_PF_NQB;
-constexpr int pf_threads(int bq, int nqb) { return 64 * 4 * (bq / 32) / nqb; }
+constexpr int pf_threads(int bq, int nqb, int G = 4) { return 64 * G * bq / 32 / nqb; }
 constexpr int PF_THREADS = pf_threads(PF_BQ, PF_NQB);
+// The library's query positions per workgroup for G heads per kv head: 6 or
+// 8 waves of 32 columns (G = 6: 6 waves, 32 queries).
+constexpr int pf_lib_bq(int G) { return G >= 6 ? 32 : 256 / G; }
+constexpr int pow2_floor(int x) { return x >= 1024 ? 1024 : x >= 512 ? 512 : x >= 256 ? 256 : x >= 128 ? 128 : 64; }
+// Threads that load and store tiles through registers: a power of two
+// (whole 16-byte chunks each); any others only compute.
+constexpr int pf_load_threads(int threads) { return pow2_floor(threads); }
+// Waves that issue the DMA path's tile loads (pairs per wave 16 / that: 2,
+// 4 or 8).
+constexpr int pf_dma_waves(int threads) { return pow2_floor(threads) / 64 > 8 ? 8 : pow2_floor(threads) / 64; }
 constexpr int PF_STAGE = PF_K_ELEMS + PF_V_ELEMS;
 // LDS stages of K / V tiles: 3 (one barrier per tile) unless the launch's
 // shared memory only holds 2 (two barriers per tile).
 constexpr int PF_NST = 3;
-// The DMA path's page-id ring after the stages: per wave 4 slots x 4 ids.
-constexpr int PF_IDS_BYTES = (PF_THREADS / 64) * 4 * 4 * 4;
-constexpr size_t prefill_smem_bytes(int nst = PF_NST) { return (size_t)nst * PF_STAGE * 2 + PF_IDS_BYTES; }
+// The DMA path's page-id ring after the stages: per DMA wave 4 slots x 4 ids.
+constexpr int pf_ids_bytes(int threads) { return pf_dma_waves(threads) * 4 * 4 * 4; }
+constexpr int PF_IDS_BYTES = pf_ids_bytes(PF_THREADS);
+constexpr size_t prefill_smem_bytes(int nst = PF_NST, int threads = PF_THREADS) {
+    return (size_t)nst * PF_STAGE * 2 + pf_ids_bytes(threads);
+}
 
 // NP LDS DMA pairs from one uniform base: pair j reads 16 bytes per lane at
 // base + off[j] into LDS at m0 + j * lds_step (+ 16 x lane). The m0 writes
@@ -110,8 +125,12 @@ constexpr size_t prefill_smem_bytes(int nst = PF_NST) { return (size_t)nst * PF_
 template <int NP>
 __device__ __forceinline__ void dma_pairs(const void* base, const uint32_t (&off)[NP], uint32_t m0,
                                           uint32_t lds_step) {
-    static_assert(NP == 2 || NP == 4, "2 or 4 pairs");
-    if constexpr (NP == 2) {
+    static_assert(NP == 2 || NP == 4 || NP == 8, "2, 4 or 8 pairs");
+    if constexpr (NP == 8) {
+        const uint32_t lo[4] = {off[0], off[1], off[2], off[3]}, hi[4] = {off[4], off[5], off[6], off[7]};
+        dma_pairs<4>(base, lo, m0, lds_step);
+        dma_pairs<4>(base, hi, m0 + 4 * lds_step, lds_step);
+    } else if constexpr (NP == 2) {
         asm volatile(
             "s_mov_b32 m0, %3\n\ts_nop 0\n\t"
             "global_load_lds_dwordx4 %1, %0\n\t"
@@ -178,16 +197,29 @@ __device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s
 // THREADS / 32 keys. F8: an E4M3 cache, dequantised while
 // the tiles load as the reference's attn_group8 does (qwen35.cu:1424-1436):
 // K' = bf16(k * kscale), V' = bf16(v * vscale); the rest is unchanged.
-template <int BQ, int NQB, bool F8, bool UPAGE, int NST, bool DMA, int VP = PF_VPAIR>
+template <int G, int BQ, int NQB, bool F8, bool UPAGE, int NST, bool DMA, int VP = PF_VPAIR>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb) {
-    constexpr int THREADS = pf_threads(BQ, NQB);
-    static_assert(PF_BK * HEAD_DIM / 8 % THREADS == 0, "whole 16-byte chunks per thread");
+    constexpr int THREADS = pf_threads(BQ, NQB, G);
+    // BQ = 16: a wave's 32 columns are 2 heads x 16 queries
+    constexpr bool PAIRED = BQ < 32;
+    static_assert(!PAIRED || (BQ == 16 && NQB == 1 && G % 2 == 0), "16-query tiles pair heads");
+    static_assert(PAIRED || BQ % (32 * NQB) == 0, "whole 32-query blocks");
+    // Tiles load through the first LDT threads (a power of two).
+    constexpr int LDT = pf_load_threads(THREADS);
+    static_assert(PF_BK * HEAD_DIM / 8 % LDT == 0, "whole 16-byte chunks per thread");
     // Buffer b: K tile at pf_smem + b * STAGE, V tile right after it.
     constexpr int STAGE = pf_stage(VP);
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31,
               lh = lane >> 5;
+    const bool loader = LDT == THREADS || tid < LDT;  // wave-uniform
     const int kvh = blockIdx.y;
-    const int G = 4, h = kvh * G + (wave & 3), qb0 = (wave >> 2) * NQB;  // the wave's first query block
+    // This lane's query head, and the wave's first query block (BQ >= 32).
+    const int h = kvh * G + (PAIRED ? 2 * wave + (lq >> 4) : wave % G);
+    const int qb0 = PAIRED ? 0 : (wave / G) * NQB;
+    // Query (index in the tile) of this lane's column in block qb, and the
+    // first query of the block.
+    auto qcol = [&](int qb) { return PAIRED ? (lq & 15) : (qb0 + qb) * 32 + lq; };
+    auto qfirst = [&](int qb) { return PAIRED ? 0 : (qb0 + qb) * 32; };
     const int qp0 = p.pos[tb];
     const int L = qp0 + nb;  // keys this tile needs: 0 .. L - 1
     const int* bt = p.block_table + (size_t)s * p.max_blocks;
@@ -200,7 +232,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         const float f = p.scale * LOG2E;
 #pragma unroll
         for (int qb = 0; qb < NQB; qb++) {
-            const int myq = (qb0 + qb) * 32 + lq;
+            const int myq = qcol(qb);
             const bool ok = myq < nb;
             const uint16_t* qrow = p.q + ((size_t)(tb + (ok ? myq : 0)) * p.Hq + h) * HEAD_DIM;
 #pragma unroll
@@ -226,8 +258,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         m[qb] = -INFINITY;
         l[qb] = 0.f;
     }
-    const int qpw = qp0 + qb0 * 32;                        // the wave's first query position
-    const int last = qp0 + min(nb, (qb0 + NQB) * 32) - 1;  // and its last
+    // the wave's last query position
+    const int last = qp0 + min(nb, PAIRED ? BQ : (qb0 + NQB) * 32) - 1;
 
     // Tile loads: 32 keys x 256 dims of K and of V, both row-major in LDS,
     // NCH 16-byte chunks of each per thread: chunk u is key KPU u + kl0 of
@@ -238,7 +270,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     // address (page index clamped to the sequence's last key); keys at or
     // past L are zeroed when the tile is stored to LDS, so no load result is
     // overwritten while in flight.
-    constexpr int KPU = THREADS / 32;
+    constexpr int KPU = LDT / 32;
     constexpr int NCH = PF_BK / KPU;
     const int kl0 = tid >> 5, c8 = (tid & 31) * 8;
     uint4 kr[NCH], vr[NCH];
@@ -382,7 +414,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             uint4 pb[NQB][2];
 #pragma unroll
             for (int qb = 0; qb < NQB; qb++) {
-                const int qb_first = qpw + qb * 32, qp = qb_first + lq;
+                const int qb_first = qp0 + qfirst(qb), qp = qp0 + qcol(qb);
                 if (k0 + PF_BK - 1 > qb_first || k0 + PF_BK > L) {
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
@@ -452,9 +484,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         // ring, filled 4 tiles ahead by its own DMA, so the loop issues no
         // other vector memory reads.
         static_assert(!F8 && UPAGE, "bf16, 16-key pages");
-        constexpr int NPW = 16 / (THREADS / 64);  // pairs per wave (2 with 8 waves, 4 with 4)
-        static_assert(NPW <= 4, "page-id ring slots hold 4 ids");
-        int* ring = reinterpret_cast<int*>(pf_smem + NST * STAGE) + wave * 16;
+        // The first NDW waves issue the DMA (the others only compute; their
+        // waits below find nothing outstanding).
+        constexpr int NDW = pf_dma_waves(THREADS);
+        constexpr int NPW = 16 / NDW;  // pairs per DMA wave (2 with 8 waves, 4 with 4, 8 with 2)
+        const bool dmaw = NDW * 64 == THREADS || wave < NDW;  // wave-uniform
+        int* ring = reinterpret_cast<int*>(pf_smem + NST * STAGE) + (dmaw ? wave : 0) * 16;
         const int hi = lane >> 5;
         // Wave w's pairs are rows NPW w .. NPW w + NPW - 1: keys kb + j and
         // kb + j + 8 (j < NPW) of one 16-key half, i.e. one page per tile
@@ -469,9 +504,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         const uint32_t lds_k = lds_addr(pf_smem) + (uint32_t)(pf_krow(NPW * wave)) * 2;
         const uint32_t lds_v = lds_addr(pf_smem) + (uint32_t)(PF_K_ELEMS + pf_vrow<VP>(NPW * wave)) * 2;
         auto dma_ids = [&](int k0, int slot) __attribute__((always_inline)) {
-            if (lane == 0) dma4(bt + min((k0 + kb) >> bs_log2, last_pi), lds_addr(ring + 4 * slot));
+            if (dmaw && lane == 0) dma4(bt + min((k0 + kb) >> bs_log2, last_pi), lds_addr(ring + 4 * slot));
         };
         auto dma_tile = [&](int k0, int buf, int slot) __attribute__((always_inline)) {
+            if (!dmaw) return;
             long pg = __builtin_amdgcn_readfirstlane(ring[4 * slot]);
             pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
             const size_t at = (((size_t)pg << bs_log2) + ((k0 + kb) & bs_mask)) * row2;  // uniform
@@ -483,7 +519,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         // the wave zeroes its own rows once its DMA has landed (P is 0 there,
         // but 0 x a stale NaN would not be).
         auto zero_tail = [&](int k0, int buf) __attribute__((always_inline)) {
-            if (k0 + PF_BK <= L) return;
+            if (!dmaw || k0 + PF_BK <= L) return;
 #pragma unroll
             for (int j = 0; j < NPW; j++) {
                 const int r = NPW * wave + j + 16 * hi;
@@ -548,25 +584,30 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         }
         }
     } else {
-    if constexpr (UPAGE) fetch_ids(0);
+    // Only the first LDT threads load and store tiles.
+    if (UPAGE && loader) fetch_ids(0);
     // NST 3: iteration i stores tile i + 1 (loaded during iteration i - 1)
     // into the stage tile i - 2 used, requests tile i + 2, computes tile i,
     // then one barrier. NST 2: iteration i requests tile i + 1, computes
     // tile i, and stores between two barriers.
-    load_tile(0);
-    store_tile(0, 0);
-    if (NST == 3 && ntiles > 1) load_tile(PF_BK);
+    if (loader) {
+        load_tile(0);
+        store_tile(0, 0);
+        if (NST == 3 && ntiles > 1) load_tile(PF_BK);
+    }
     __syncthreads();
     int buf = 0;
     for (int it = 0; it < ntiles; it++) {
         const int k0 = it * PF_BK;
-        if constexpr (NST == 3) {
-            if (it + 1 < ntiles) {
-                store_tile(buf == 2 ? 0 : buf + 1, k0 + PF_BK);
-                if (it + 2 < ntiles) load_tile(k0 + 2 * PF_BK);
+        if (loader) {
+            if constexpr (NST == 3) {
+                if (it + 1 < ntiles) {
+                    store_tile(buf == 2 ? 0 : buf + 1, k0 + PF_BK);
+                    if (it + 2 < ntiles) load_tile(k0 + 2 * PF_BK);
+                }
+            } else {
+                if (it + 1 < ntiles) load_tile(k0 + PF_BK);
             }
-        } else {
-            if (it + 1 < ntiles) load_tile(k0 + PF_BK);
         }
         compute(buf, k0);
         if constexpr (NST == 3) {
@@ -574,7 +615,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             buf = buf == 2 ? 0 : buf + 1;
         } else if (it + 1 < ntiles) {
             __syncthreads();  // everyone is done with the buffer two tiles back
-            store_tile(buf ^ 1, k0 + PF_BK);
+            if (loader) store_tile(buf ^ 1, k0 + PF_BK);
             __syncthreads();
             buf ^= 1;
         }
@@ -582,7 +623,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     }
 #pragma unroll
     for (int qb = 0; qb < NQB; qb++) {
-        const int myq = (qb0 + qb) * 32 + lq;
+        const int myq = qcol(qb);
         if (myq >= nb) continue;
         const float inv = l[qb] > 0.f ? 1.f / l[qb] : 0.f;
         const size_t t = (size_t)tb + myq;
@@ -604,32 +645,37 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     }
 }
 
-template <int BQ, int NQB, bool F8 = false, int NST = PF_NST, int VP = PF_VPAIR>
+template <int G, int BQ, int NQB, bool F8 = false, int NST = PF_NST, int VP = PF_VPAIR>
 __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
     int s, tb, nb;
     if (!find_prefill_tile<BQ>(p, s, tb, nb)) return;
-    // bf16 with 3 stages, 8 waves and pages of 16 keys or more: tiles by LDS
-    // DMA; otherwise through
-    // registers, with uniform page ids per chunk when pages hold at least
-    // THREADS / 32 keys.
+    // bf16 with pages of 16 keys or more: tiles by LDS DMA; otherwise
+    // through registers, with uniform page ids per chunk when pages hold at
+    // least (loading threads) / 32 keys.
     constexpr bool DMA = !F8;
     if (DMA && p.bs_log2 >= 4)
-        prefill_tile<BQ, NQB, F8, true, NST, DMA, VP>(p, pf_smem, s, tb, nb);
-    else if (p.bs_log2 >= __builtin_ctz(pf_threads(BQ, NQB) / 32))
-        prefill_tile<BQ, NQB, F8, true, NST, false, VP>(p, pf_smem, s, tb, nb);
+        prefill_tile<G, BQ, NQB, F8, true, NST, DMA, VP>(p, pf_smem, s, tb, nb);
+    else if (p.bs_log2 >= __builtin_ctz(pf_load_threads(pf_threads(BQ, NQB, G)) / 32))
+        prefill_tile<G, BQ, NQB, F8, true, NST, false, VP>(p, pf_smem, s, tb, nb);
     else
-        prefill_tile<BQ, NQB, F8, false, NST, false, VP>(p, pf_smem, s, tb, nb);
+        prefill_tile<G, BQ, NQB, F8, false, NST, false, VP>(p, pf_smem, s, tb, nb);
 }
 
-__global__ void __launch_bounds__(PF_THREADS, 1) prefill_kernel(PrefillParams p) {
+// The library's prompt kernels for G query heads per kv head: pf_lib_bq(G)
+// queries per workgroup, one workgroup per CU.
+template <int G>
+__global__ void __launch_bounds__(pf_threads(pf_lib_bq(G), G == 4 ? PF_NQB : 1, G), 1)
+    prefill_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
-    prefill_body<PF_BQ, PF_NQB>(p, pf_smem);
+    prefill_body<G, pf_lib_bq(G), G == 4 ? PF_NQB : 1>(p, pf_smem);
 }
 
 // The same over an E4M3 cache (p.kscale / p.vscale set).
-__global__ void __launch_bounds__(PF_THREADS, 1) prefill_e4m3_kernel(PrefillParams p) {
+template <int G>
+__global__ void __launch_bounds__(pf_threads(pf_lib_bq(G), G == 4 ? PF_NQB : 1, G), 1)
+    prefill_e4m3_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
-    prefill_body<PF_BQ, PF_NQB, true>(p, pf_smem);
+    prefill_body<G, pf_lib_bq(G), G == 4 ? PF_NQB : 1, true>(p, pf_smem);
 }
 
 }  // namespace pkv

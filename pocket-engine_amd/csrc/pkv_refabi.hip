@@ -20,6 +20,11 @@
 //   attn_group8_g4_t2_k16 (qwen35.cu:1593-1608) the same grid, 256 threads,
 //                   over an E4M3 cache (kscale / vscale): gfx950's choice
 //                   for an E4M3 cache
+//   the other groups' prompt kernels gfx950 selects (fa_shape), on grids of
+//   16 x NT-query tiles with 32 x G x NT threads (qwen35.cu:1593-1616):
+//   attn_groupr_g6_t1_k32 (192), attn_group_g1_t8_k16, attn_group_g2_t4_k16,
+//   attn_group_g8_t1_k16 (256), and over an E4M3 cache
+//   attn_group8_g{1,2,6,8}_t{8,4,1,1}_k16
 //
 // Split decode follows the reference's contract so its buffer sizing holds:
 // range z of nz = split_parts(L, Z, min_chunk) covers keys [z c, z c + c),
@@ -32,8 +37,8 @@
 //
 // Bounds of this ABI: FP8
 // output copies (fmode != 0) are not produced; block_size 16 for decode, a
-// power of two for prompts; G = Hq / Hkv = 4 for prompts, 1, 2, 4, 6 or 8 for
-// decode. A launch outside these bounds
+// power of two for prompts; G = Hq / Hkv of the kernel's name (1, 2, 4, 6
+// or 8). A launch outside these bounds
 // writes nothing. Page ids are not clamped (the reference ABI passes no pool
 // size).
 #include "pkv_copy.hip"
@@ -329,44 +334,40 @@ extern "C" __global__ void __launch_bounds__(256)
 
 namespace pkv {
 
-// The prompt kernel on a grid of 32-query tiles (BQ = 32: one workgroup per
-// tile; BQ = 64: one per two tiles, the other blocks of the grid exit).
-// Tiles load by LDS DMA into two stages (one barrier per tile, one tile of
-// lead) with each wave's page-id ring after them.
-// BQ = 32 (attn_groupr, 4 waves): the stages and rings live in the launch's
+// The prompt kernels on the engine's grid of BQ-query tiles (attn_mfma:
+// one workgroup per two 32-query tiles, the other blocks of the grid exit).
+// Tiles load by LDS DMA (bf16) or through registers (E4M3) into two stages
+// (one tile of lead) with the DMA waves' page-id rings after them.
+// attn_groupr (4 or 3 waves): the stages and rings live in the launch's
 // dynamic shared memory (the engine asks for 67,584 bytes; two stages with
-// V pairs 1,056 bytes apart and 4 rings take 67,328) and nothing is static,
-// so two workgroups fit a CU (2 x 67,584 of its 160 KiB) at up to 256
-// VGPRs: 8 waves per CU. A launch with less dynamic memory (the dispatch
-// packet's group segment size) does nothing, like one with another block
-// size. BQ = 64 (attn_mfma, 8 waves): two stages of the default layout and
-// 8 rings in static LDS (68,608 bytes beside the launch's 37,376 dynamic
-// ones).
-constexpr int REF_VP32 = 528;  // V pair stride of the BQ = 32 stages (elements)
-constexpr uint32_t REF_SMEM32 = 2u * pf_stage(REF_VP32) * 2u + 4u * 64u;  // bytes the BQ = 32 path uses
+// V pairs 1,056 bytes apart and the rings take 67,328 at G = 4, 67,200 at
+// G = 6) and nothing is static, so two workgroups fit a CU at up to 256
+// VGPRs. attn_mfma (8 waves): two stages of the default layout and 8 rings
+// in static LDS (68,608 bytes beside the launch's 37,376 dynamic ones).
+constexpr int REF_VP32 = 528;  // V pair stride of the attn_groupr stages (elements)
 
-template <int BQ>
-__device__ __forceinline__ uint16_t* flash_stages() {
-    if constexpr (BQ == 32) {
-        extern __shared__ __align__(16) uint16_t dyn_sm[];
-        return dyn_sm;
-    } else {
-        __shared__ __align__(16) uint16_t sm[2 * PF_STAGE + PF_IDS_BYTES / 2];
-        return sm;
-    }
-}
-
-template <int BQ>
+// G heads per kv head, BQ queries per workgroup (16 x the name's tiles),
+// F8: E4M3 cache, VP: V pair stride of the two stages, DYN: stages in the
+// launch's dynamic shared memory (checked against the dispatch packet's
+// group segment size, byte offset 28: a launch with too little does
+// nothing), else in static LDS.
+template <int G, int BQ, bool F8, int VP, bool DYN>
 __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
-    uint16_t* sm = flash_stages<BQ>();
-    if ((int)blockDim.x != pf_threads(BQ, 1) || Hq != 4 * Hkv || kscale || vscale || block_size <= 0 ||
-        (block_size & (block_size - 1)))
-        return;
-    if constexpr (BQ == 32) {
-        // hsa_kernel_dispatch_packet_t::group_segment_size (byte offset 28)
+    constexpr int THREADS = pf_threads(BQ, 1, G);
+    uint16_t* sm;
+    if constexpr (DYN) {
+        extern __shared__ __align__(16) uint16_t dyn_sm[];
+        sm = dyn_sm;
+        constexpr uint32_t need = 2u * pf_stage(VP) * 2u + (F8 ? 0u : (uint32_t)pf_ids_bytes(THREADS));
         const uint32_t group_bytes = reinterpret_cast<const uint32_t*>(__builtin_amdgcn_dispatch_ptr())[7];
-        if (group_bytes < REF_SMEM32) return;
+        if (group_bytes < need) return;
+    } else {
+        __shared__ __align__(16) uint16_t st_sm[2 * pf_stage(VP) + pf_ids_bytes(THREADS) / 2];
+        sm = st_sm;
     }
+    if ((int)blockDim.x != THREADS || Hq != G * Hkv || (kscale != nullptr) != F8 || (vscale != nullptr) != F8 ||
+        block_size <= 0 || (block_size & (block_size - 1)))
+        return;
     PrefillParams p;
     p.q = q;
     p.kc = (const uint16_t*)kcache;
@@ -387,63 +388,49 @@ __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
     p.outs = outs;
     p.spec = spec;
     p.num_blocks = REF_NO_CLAMP;
-    p.kscale = nullptr;
-    p.vscale = nullptr;
-    prefill_body<BQ, 1, false, 2, BQ == 32 ? REF_VP32 : PF_VPAIR>(p, sm);
-}
-
-}  // namespace pkv
-
-extern "C" __global__ void __launch_bounds__(256, 2) attn_groupr_g4_t2_k32(PKV_FLASH_ARGS) {
-    pkv::flash_ref<32>(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
-                       max_blocks, block_size, out, scale, outs, spec);
-}
-
-// The E4M3 prompt kernel a gfx950 device selects for an E4M3 cache
-// (fa_shape(4, 95, true): attn_group8_g4_t2_k16, 256 threads, grid of
-// 32-query tiles, 101,376 bytes of dynamic shared memory, which holds this
-// kernel's two 34,048-byte stages: the 2-stage loop; a launch with fewer than
-// 68,096 bytes returns before any work).
-namespace pkv {
-constexpr uint32_t REF_SMEM8 = 2u * PF_STAGE * 2u;  // bytes attn_group8's two stages use
-}  // namespace pkv
-
-extern "C" __global__ void __launch_bounds__(256, 1) attn_group8_g4_t2_k16(PKV_FLASH_ARGS) {
-    extern __shared__ __align__(16) uint16_t g8_smem[];
-    if ((int)blockDim.x != pkv::pf_threads(32, 1) || Hq != 4 * Hkv || !kscale || !vscale || block_size <= 0 ||
-        (block_size & (block_size - 1)))
-        return;
-    // A launch whose dynamic shared memory (the dispatch packet's group
-    // segment size, byte offset 28) cannot hold the two stages does nothing.
-    if (reinterpret_cast<const uint32_t*>(__builtin_amdgcn_dispatch_ptr())[7] < pkv::REF_SMEM8) return;
-    pkv::PrefillParams p;
-    p.q = q;
-    p.kc = (const uint16_t*)kcache;
-    p.vc = (const uint16_t*)vcache;
-    p.qkv = qkv;
-    p.qstride = qstride;
-    p.Hq = Hq;
-    p.Hkv = Hkv;
-    p.pos = pos;
-    p.cu = cu;
-    p.seqs = seqs;
-    p.block_table = block_table;
-    p.max_blocks = max_blocks;
-    p.block_size = block_size;
-    p.bs_log2 = __builtin_ctz((unsigned)block_size);
-    p.out = out;
-    p.scale = scale;
-    p.outs = outs;
-    p.spec = spec;
-    p.num_blocks = pkv::REF_NO_CLAMP;
     p.kscale = kscale;
     p.vscale = vscale;
-    pkv::prefill_body<32, 1, true, 2>(p, g8_smem);
+    prefill_body<G, BQ, 1, F8, 2, VP>(p, sm);
 }
 
+}  // namespace pkv
+
+#define PKV_FLASH_PASS                                                                                           \
+    q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks, block_size, \
+        out, scale, outs, spec
+
+// bf16 cache, queries in registers (what gfx950 selects for G = 4 and 6):
+// stages with V pairs REF_VP32 apart fit the engine's 67,584 bytes, two
+// workgroups per CU.
+extern "C" __global__ void __launch_bounds__(256, 2) attn_groupr_g4_t2_k32(PKV_FLASH_ARGS) {
+    pkv::flash_ref<4, 32, false, pkv::REF_VP32, true>(PKV_FLASH_PASS);
+}
+extern "C" __global__ void __launch_bounds__(192, 2) attn_groupr_g6_t1_k32(PKV_FLASH_ARGS) {
+    pkv::flash_ref<6, 16, false, pkv::REF_VP32, true>(PKV_FLASH_PASS);
+}
+
+// bf16 cache, G = 1, 2, 8 (fa_shape's 16-key default: 128 queries x 1
+// head, 64 x 2, 16 x 8 per workgroup, 256 threads, 101,376 bytes of dynamic
+// shared memory from the engine), and every group over an E4M3 cache
+// (attn_group8_*; 84,480 bytes for G = 6, 101,376 otherwise). Two stages of
+// the default layout; one workgroup per CU.
+#define PKV_FLASH_K16(NAME, G, BQ, F8)                                                                           \
+    extern "C" __global__ void __launch_bounds__(pkv::pf_threads(BQ, 1, G), 1) NAME(PKV_FLASH_ARGS) {            \
+        pkv::flash_ref<G, BQ, F8, pkv::PF_VPAIR, true>(PKV_FLASH_PASS);                                          \
+    }
+PKV_FLASH_K16(attn_group_g1_t8_k16, 1, 128, false)
+PKV_FLASH_K16(attn_group_g2_t4_k16, 2, 64, false)
+PKV_FLASH_K16(attn_group_g8_t1_k16, 8, 16, false)
+PKV_FLASH_K16(attn_group8_g1_t8_k16, 1, 128, true)
+PKV_FLASH_K16(attn_group8_g2_t4_k16, 2, 64, true)
+PKV_FLASH_K16(attn_group8_g4_t2_k16, 4, 32, true)
+PKV_FLASH_K16(attn_group8_g6_t1_k16, 6, 16, true)
+PKV_FLASH_K16(attn_group8_g8_t1_k16, 8, 16, true)
+
+// gfx942's name for G = 4 (attn_mfma_g4_t2, 512 threads): 64 queries per
+// workgroup, stages in static LDS beside the launch's 37,376 dynamic bytes.
 extern "C" __global__ void __launch_bounds__(512, 1) attn_mfma_g4_t2(PKV_FLASH_ARGS) {
-    pkv::flash_ref<64>(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
-                       max_blocks, block_size, out, scale, outs, spec);
+    pkv::flash_ref<4, 64, false, pkv::PF_VPAIR, false>(PKV_FLASH_PASS);
 }
 
 // The draft passes' slot mapping under the reference's name and signature

@@ -26,22 +26,24 @@ def split_ranges(t, hkv, sms):
 
 
 def flash_launch(t, s, hkv, g=4, mfma=False, fp8=False):
-    """(name, grid, threads, dynamic smem) of the prompt kernel: fa_shape for
-    a bf16 cache on gfx950 (compute capability 9.5: attn_groupr_g4_t2_k32) or
-    gfx942 (attn_mfma_g4_t2), or for an E4M3 cache on either
-    (attn_group8_g4_t2_k16), model.rs:58-79, 112-141, 2455-2463."""
-    tiles, keys = 2, 32
-    if fp8:
-        keys = 16
-        name, threads = f"attn_group8_g{g}_t{tiles}_k{keys}", 32 * g * tiles
-        smem = (g * 16 * tiles + 4 * keys) * (HEAD_DIM + 8) * 2
-    elif mfma:
+    """(name, grid, threads, dynamic smem) of the prompt kernel as fa_shape
+    picks it (model.rs:58-79, 112-141, 2455-2463) for a gfx950 device
+    (compute capability 9.5): a bf16 cache takes attn_groupr_g4_t2_k32 or
+    attn_groupr_g6_t1_k32 (queries in registers, 32-key tiles), other groups
+    and every E4M3 cache the 16-key default attn_group[8]_g<G>_t<NT>_k16 with
+    NT = 1 for G = 6, else 8 / G; mfma: gfx942's attn_mfma_g<G>_t2."""
+    if mfma and not fp8:
+        tiles, keys = 2, 32
         name, threads = f"attn_mfma_g{g}_t{tiles}", 64 * g * tiles
         smem = (keys * (HEAD_DIM + 8) + HEAD_DIM * (keys + 8)) * 2
-    else:
+    elif not fp8 and g in (4, 6):
+        tiles, keys = (2 if g == 4 else 1), 32
         name, threads = f"attn_groupr_g{g}_t{tiles}_k{keys}", 32 * g * tiles
-        q, kv = g * 16 * tiles, 4 * keys
-        smem = max(q, kv) * (HEAD_DIM + 8) * 2
+        smem = max(g * 16 * tiles, 4 * keys) * (HEAD_DIM + 8) * 2
+    else:
+        tiles, keys = (1 if g == 6 else 8 // g), 16
+        name, threads = f"attn_group{'8' if fp8 else ''}_g{g}_t{tiles}_k{keys}", 32 * g * tiles
+        smem = (g * 16 * tiles + 4 * keys) * (HEAD_DIM + 8) * 2
     return name, (-(-t // (16 * tiles)) + s, hkv, 1), threads, smem
 
 

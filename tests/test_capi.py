@@ -105,6 +105,13 @@ def test_reference_launch_shapes():
     assert (name, grid, threads, smem) == ("attn_mfma_g4_t2", (7, 4, 1), 512, 37376)
     name, grid, threads, smem = refabi.flash_launch(100, 3, 4, fp8=True)
     assert (name, grid, threads, smem) == ("attn_group8_g4_t2_k16", (7, 4, 1), 256, 101376)
+    # other groups (fa_shape arm (_, 6, false) and the 16-key default)
+    assert refabi.flash_launch(100, 3, 4, g=6) == ("attn_groupr_g6_t1_k32", (10, 4, 1), 192, 67584)
+    assert refabi.flash_launch(100, 3, 4, g=6, fp8=True) == ("attn_group8_g6_t1_k16", (10, 4, 1), 192, 84480)
+    assert refabi.flash_launch(100, 3, 4, g=6, mfma=True) == ("attn_mfma_g6_t2", (7, 4, 1), 768, 37376)
+    assert refabi.flash_launch(100, 3, 8, g=1) == ("attn_group_g1_t8_k16", (4, 8, 1), 256, 101376)
+    assert refabi.flash_launch(100, 3, 8, g=2, fp8=True) == ("attn_group8_g2_t4_k16", (5, 8, 1), 256, 101376)
+    assert refabi.flash_launch(100, 3, 2, g=8) == ("attn_group_g8_t1_k16", (10, 2, 1), 256, 101376)
 
 
 def test_reference_prompt_kernels_fit_lds(tmp_path):
@@ -126,7 +133,8 @@ def test_reference_prompt_kernels_fit_lds(tmp_path):
         lds = re.search(r"\.group_segment_fixed_size:\s+(\d+)", item)
         if name and lds:
             static[name.group(1)] = int(lds.group(1))
-    for kw in ({}, {"mfma": True}, {"fp8": True}):
+    for kw in ({}, {"mfma": True}, {"fp8": True}, {"g": 6}, {"g": 6, "fp8": True}, {"g": 1}, {"g": 2}, {"g": 8},
+               {"g": 1, "fp8": True}, {"g": 2, "fp8": True}, {"g": 8, "fp8": True}):
         name, _, _, smem = refabi.flash_launch(100, 3, 4, **kw)
         assert name in static, (name, sorted(static))
         assert static[name] + smem <= 160 * 1024, (name, static[name], smem)

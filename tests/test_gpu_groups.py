@@ -103,3 +103,74 @@ def test_fused_step_rejects_other_groups(dev):
         pkv.attn_decode_step(rows, rows, 4 * D * 2, i([0, 16]), q, kc, kc, qkv, c["qstride"], 24, 4, i(c["pos"]),
                              i(c["tok_seq"]), i(c["bt"]), c["max_blocks"], BS, q, SCALE, i(c["cu"]), 0, None, 1, T,
                              c["pages"], ws)
+
+
+PREFILL_CASES = [
+    ([0], [37], 0),                     # no prefix, partial query tile
+    ([100, 16], [64, 130], 1),          # tiles crossing a tile edge after a prefix
+    ([1000, 33, 0], [70, 200, 65], 2),  # three prompts, a decode row first
+]
+
+
+def _prefill(c, dev, entry, f8=None):
+    """entry: "lib" (pkv_attn_prefill[_e4m3]) or "ref" (the code object's
+    kernel for this group, launched as the engine's fa_shape picks it)."""
+    from pkv.refabi import F, I, P, RefKernels, flash_launch
+    T, Hq, Hkv = c["T"], c["Hq"], c["Hkv"]
+    init = np.full((T, Hq, D), 0x3333, np.uint16)
+    out = torch.from_numpy(init.view(np.int16).copy()).to(dev)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16) if a.dtype == np.uint16
+                                   else np.ascontiguousarray(a)).to(dev)
+    kc, vc = (t(c["kc"]), t(c["vc"])) if f8 is None else (t(f8[0]), t(f8[1]))
+    ks, vs = (None, None) if f8 is None else (t(f8[2]), t(f8[3]))
+    q, qkv, pos, cu, bt = t(c["q"]), t(c["qkv"]), t(c["pos"]), t(c["cu"]), t(c["bt"])
+    if entry == "ref":
+        name, grid, threads, smem = flash_launch(T, c["seqs"], Hkv, g=Hq // Hkv, fp8=f8 is not None)
+        print(f"  kernel {name} grid {grid} threads {threads} smem {smem}", flush=True)
+        RefKernels().launch(name, grid, threads, smem,
+                            [P(q), P(kc), P(vc), P(ks), P(vs), P(qkv), I(c["qstride"]), I(Hq), I(Hkv), P(pos), P(cu),
+                             I(c["seqs"]), P(bt), I(c["max_blocks"]), I(BS), P(out), F(SCALE), P(None), I(1)])
+    elif f8 is None:
+        pkv.attn_prefill(q, kc, vc, qkv, c["qstride"], Hq, Hkv, pos, cu, c["seqs"], bt, c["max_blocks"], BS, out,
+                         SCALE, None, 1, T, c["pages"])
+    else:
+        pkv.attn_prefill_e4m3(q, kc, vc, ks, vs, qkv, c["qstride"], Hq, Hkv, pos, cu, c["seqs"], bt, c["max_blocks"],
+                              BS, out, SCALE, None, 1, T, c["pages"])
+    torch.cuda.synchronize()
+    return out.cpu().numpy().view(np.uint16), init
+
+
+@pytest.mark.parametrize("entry", ["lib", "ref"])
+@pytest.mark.parametrize("G,Hkv", [(1, 4), (2, 2), (6, 4), (6, 1), (8, 2)])
+@pytest.mark.parametrize("ctxs,chunks,seed", PREFILL_CASES)
+def test_prefill_groups_match_oracle(dev, entry, G, Hkv, ctxs, chunks, seed):
+    """Prompt attention for G = 1, 2, 6, 8: the library's kernels and the
+    code object's attn_groupr_g6_t1_k32 / attn_group_g{1,2,8}_t*_k16."""
+    print(f"case prefill {entry} G={G} Hkv={Hkv} ctx={ctxs} chunk={chunks}", flush=True)
+    from test_gpu_prefill import prefill_case
+    c = prefill_case(ctxs, chunks, Hkv, seed, decode_rows=1, G=G)
+    got, init = _prefill(c, dev, entry)
+    assert (got[0] == 0x3333).all()  # the decode row is left to decode attention
+    want = oracle.attn_prefill(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], c["Hq"], Hkv, c["pos"], c["cu"],
+                               c["seqs"], c["bt"], c["max_blocks"], BS, SCALE, out=init.copy())
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("entry", ["lib", "ref"])
+@pytest.mark.parametrize("G,Hkv", [(1, 4), (2, 2), (6, 4), (8, 2)])
+@pytest.mark.parametrize("ctxs,chunks,seed", PREFILL_CASES[1:])
+def test_prefill_e4m3_groups_match_oracle(dev, entry, G, Hkv, ctxs, chunks, seed):
+    print(f"case prefill e4m3 {entry} G={G} Hkv={Hkv} ctx={ctxs} chunk={chunks}", flush=True)
+    from test_gpu_prefill import prefill_case
+    c = prefill_case(ctxs, chunks, Hkv, seed, decode_rows=1, G=G)
+    rng = np.random.default_rng(seed + 90 + G)
+    k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+    ks = (rng.random(c["kc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+    vs = (rng.random(c["vc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+    got, init = _prefill(c, dev, entry, f8=(k8, v8, ks, vs))
+    assert (got[0] == 0x3333).all()
+    want = oracle.attn_prefill8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], c["Hq"], Hkv, c["pos"], c["cu"],
+                                c["seqs"], c["bt"], c["max_blocks"], BS, SCALE, out=init.copy())
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"

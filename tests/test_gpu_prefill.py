@@ -31,11 +31,11 @@ def i32(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
 
 
-def prefill_case(ctxs, chunks, Hkv, seed, decode_rows=0):
+def prefill_case(ctxs, chunks, Hkv, seed, decode_rows=0, G=4):
     """Sequences with ctx cached tokens feeding a chunk of n tokens (all
     already in the cache, as after pkv_append); optional extra one-token
-    decode sequences first."""
-    Hq = 4 * Hkv
+    decode sequences first; G query heads per kv head."""
+    Hq = G * Hkv
     lens = [c + n for c, n in zip(ctxs, chunks)]
     dec = [40 + 13 * i for i in range(decode_rows)]
     c = decode_case(dec + lens, Hq, Hkv, seed)
