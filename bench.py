@@ -102,8 +102,8 @@ def main():
                     help="c2/c3: the step's append is pkv_attn_prep (q/k RMSNorm + rotary + K/V slot writes, the "
                          "reference's attn_prep) on the raw qkv rows, followed by the key ranges and the merge")
     ap.add_argument("--q-heads", type=int, default=16,
-                    help="c2/c3 query heads over the 4 kv heads (16: the configs' G = 4; 24: the reference's 27B "
-                         "shape, G = 6, run unfused: append, then decode attention)")
+                    help="query heads over the 4 kv heads (16: the configs' G = 4; 24: the reference's 27B shape, "
+                         "G = 6; c2/c3 then run unfused: append, then decode attention)")
     ap.add_argument("--unfused", action="store_true",
                     help="append, key ranges and merge as three launches instead of the fused step")
     args = ap.parse_args()
@@ -404,7 +404,7 @@ def bench_prefill(args):
 
     seed = args.seed if args.seed is not None else int(time.time()) % 100000
     dev = torch.device("cuda:0")
-    Hq, Hkv, D, BS, B, P, N = 16, 4, 256, 16, 8, args.prefix, 2048
+    Hq, Hkv, D, BS, B, P, N = args.q_heads, 4, 256, 16, 8, args.prefix, 2048
     per_seq = (P + N + BS - 1) // BS
     pages = (P + BS - 1) // BS + B * (per_seq - P // BS) + 8
     kv = pkv.Kv(pages, BS)
@@ -451,7 +451,7 @@ def bench_prefill(args):
         from pkv import refabi
         from pkv.refabi import F, I, P as Pa
         rk = refabi.RefKernels()
-        fname, fgrid, fthreads, fsmem = refabi.flash_launch(T, B, Hkv, fp8=e4m3)
+        fname, fgrid, fthreads, fsmem = refabi.flash_launch(T, B, Hkv, g=Hq // Hkv, fp8=e4m3)
         fargs = [Pa(q), Pa(kc), Pa(vc), Pa(kscale if e4m3 else None), Pa(vscale if e4m3 else None), Pa(qkv), I(qstride), I(Hq), I(Hkv), Pa(pos_d), Pa(cu_d),
                  I(B), Pa(bt_d), I(mb), I(BS), Pa(out), F(1 / 16), Pa(None), I(1)]
 
@@ -526,7 +526,7 @@ def bench_prefill(args):
                    "prefix": P, "prefix_page_refs": prefix_refs, "cow_copies": len(plan["cow"]),
                    "seed": seed, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": (f"{fname} (reference ABI, events around the launch)" if args.refabi
-                                                  else "prefill_e4m3_kernel" if e4m3 else "prefill_kernel"),
+                                                  else f"prefill_e4m3_kernel<{Hq // Hkv}>" if e4m3 else f"prefill_kernel<{Hq // Hkv}>"),
                      "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "avg_us": round(kern_us, 1), "traffic": None,

@@ -230,7 +230,7 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
            : by_group<PrefillKernel>(G, pkv::prefill_kernel<1>, pkv::prefill_kernel<2>, pkv::prefill_kernel<4>,
                                      pkv::prefill_kernel<6>, pkv::prefill_kernel<8>);
     const int bq = pkv::pf_lib_bq(G);
-    const int threads = 64 * G * bq / 32 / (G == 4 ? pkv::PF_NQB : 1);
+    const int threads = pkv::pf_lib_threads(G);
     const size_t smem = pkv::prefill_smem_bytes(pkv::PF_NST, threads);
     // per process: the kernels' LDS above the 64 KiB default, once per kernel
     static std::mutex attr_mu;

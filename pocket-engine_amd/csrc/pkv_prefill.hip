@@ -98,9 +98,6 @@ constexpr int PF_BQ = 64;
 constexpr int PF_NQB = PKV_PF_NQB;
 constexpr int pf_threads(int bq, int nqb, int G = 4) { return 64 * G * bq / 32 / nqb; }
 constexpr int PF_THREADS = pf_threads(PF_BQ, PF_NQB);
-// The library's query positions per workgroup for G heads per kv head: 6 or
-// 8 waves of 32 columns (G = 6: 6 waves, 32 queries).
-constexpr int pf_lib_bq(int G) { return G >= 6 ? 32 : 256 / G; }
 constexpr int pow2_floor(int x) { return x >= 1024 ? 1024 : x >= 512 ? 512 : x >= 256 ? 256 : x >= 128 ? 128 : 64; }
 // Threads that load and store tiles through registers: a power of two
 // (whole 16-byte chunks each); any others only compute.
@@ -115,6 +112,13 @@ constexpr int PF_NST = 3;
 // The DMA path's page-id ring after the stages: per DMA wave 4 slots x 4 ids.
 constexpr int pf_ids_bytes(int threads) { return pf_dma_waves(threads) * 4 * 4 * 4; }
 constexpr int PF_IDS_BYTES = pf_ids_bytes(PF_THREADS);
+// The library's query positions per workgroup for G heads per kv head: 6 or
+// 8 waves of 32 columns (G = 6: 6 waves, 32 queries), one workgroup per CU
+// with 3 stages. (Over an E4M3 cache, G = 6 in 3 waves of 16 queries x 2
+// heads with two workgroups per CU spills 584 bytes per lane at 256 VGPRs.)
+constexpr int pf_lib_bq(int G) { return G >= 6 ? 32 : 256 / G; }
+constexpr int pf_lib_nqb(int G) { return G == 4 ? PF_NQB : 1; }
+constexpr int pf_lib_threads(int G) { return pf_threads(pf_lib_bq(G), pf_lib_nqb(G), G); }
 constexpr size_t prefill_smem_bytes(int nst = PF_NST, int threads = PF_THREADS) {
     return (size_t)nst * PF_STAGE * 2 + pf_ids_bytes(threads);
 }
@@ -362,23 +366,23 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     auto store_tile = [&](int buf, int k0) {
         uint16_t* sk = pf_smem + buf * STAGE;
         uint16_t* sv = sk + PF_K_ELEMS;
-        if constexpr (F8) {
-#pragma unroll
-            for (int u = 0; u < NCH; u++) {
-                kr[u] = cvt8(kw[u], ksv[u]);
-                vr[u] = cvt8(vw[u], vsv[u]);
-            }
-        }
-        if (k0 + PF_BK > L) {
-#pragma unroll
-            for (int u = 0; u < NCH; u++)
-                if (k0 + u * KPU + kl0 >= L) kr[u] = vr[u] = make_uint4(0, 0, 0, 0);
-        }
+        const bool tail = k0 + PF_BK > L;
+        // one chunk at a time (E4M3: converted just before its store, so
+        // only one chunk's bf16 values are live)
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
+            uint4 kx, vx;
+            if constexpr (F8) {
+                kx = cvt8(kw[u], ksv[u]);
+                vx = cvt8(vw[u], vsv[u]);
+            } else {
+                kx = kr[u];
+                vx = vr[u];
+            }
+            if (tail && k0 + u * KPU + kl0 >= L) kx = vx = make_uint4(0, 0, 0, 0);
             const int r = pf_row_of_key(u * KPU + kl0);
-            *reinterpret_cast<uint4*>(sk + pf_krow(r) + c8) = kr[u];
-            *reinterpret_cast<uint4*>(sv + pf_vrow<VP>(r) + c8) = vr[u];
+            *reinterpret_cast<uint4*>(sk + pf_krow(r) + c8) = kx;
+            *reinterpret_cast<uint4*>(sv + pf_vrow<VP>(r) + c8) = vx;
         }
     };
     // V^T fragments (A operand of O^T += V^T P^T, dims 32 db + lq, keys
@@ -661,21 +665,18 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* p
         prefill_tile<G, BQ, NQB, F8, false, NST, false, VP>(p, pf_smem, s, tb, nb);
 }
 
-// The library's prompt kernels for G query heads per kv head: pf_lib_bq(G)
-// queries per workgroup, one workgroup per CU.
+// The library's prompt kernels for G query heads per kv head (shapes above).
 template <int G>
-__global__ void __launch_bounds__(pf_threads(pf_lib_bq(G), G == 4 ? PF_NQB : 1, G), 1)
-    prefill_kernel(PrefillParams p) {
+__global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
-    prefill_body<G, pf_lib_bq(G), G == 4 ? PF_NQB : 1>(p, pf_smem);
+    prefill_body<G, pf_lib_bq(G), pf_lib_nqb(G)>(p, pf_smem);
 }
 
 // The same over an E4M3 cache (p.kscale / p.vscale set).
 template <int G>
-__global__ void __launch_bounds__(pf_threads(pf_lib_bq(G), G == 4 ? PF_NQB : 1, G), 1)
-    prefill_e4m3_kernel(PrefillParams p) {
+__global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_e4m3_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
-    prefill_body<G, pf_lib_bq(G), G == 4 ? PF_NQB : 1, true>(p, pf_smem);
+    prefill_body<G, pf_lib_bq(G), pf_lib_nqb(G), true>(p, pf_smem);
 }
 
 }  // namespace pkv
