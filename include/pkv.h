@@ -251,8 +251,9 @@ int pkv_attn_decode_config(int wg_per_cu, int min_range);
  * rounded to bf16, exp2 softmax, P rounded to bf16 for P.V, output
  * bf16(bf16(O / l) * sigmoid(gate)). Other rows are left untouched. The
  * chunk's own K/V must already be in the cache (pkv_append first). T is the
- * number of token rows. bf16, head_dim 256, G = Hq / Hkv = 4, block size a
- * power of two. kscale/vscale (E4M3 cache) are not part of this path. */
+ * number of token rows. bf16, head_dim 256, G = Hq / Hkv in {1, 2, 4, 6, 8}
+ * (PKV_ERR_UNSUPPORTED otherwise), block size a power of two. kscale/vscale
+ * (E4M3 cache) are not part of this path. */
 int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
                      int Hkv, const int32_t* pos, const int32_t* cu, int seqs, const int32_t* block_table,
                      int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec, int T,

@@ -60,7 +60,7 @@ def check(c, qout, kc, vc, kc0, vc0):
         assert worst <= 1 and exact >= 0.99, f"{name}: max ulp {worst}, exact {exact:.4f}"
 
 
-@pytest.mark.parametrize("T,Hq,Hkv,seed", [(37, 16, 4, 0), (64, 8, 2, 1), (1, 4, 1, 2)])
+@pytest.mark.parametrize("T,Hq,Hkv,seed", [(37, 16, 4, 0), (64, 8, 2, 1), (1, 4, 1, 2), (20, 24, 4, 3), (9, 32, 4, 4), (5, 2, 2, 5)])
 def test_prep_matches_oracle(dev, T, Hq, Hkv, seed):
     print(f"case prep T={T} Hq={Hq} Hkv={Hkv}", flush=True)
     c = case(T, Hq, Hkv, seed, pool=128)
