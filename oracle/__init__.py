@@ -60,6 +60,12 @@ _lib.orc_e4m3_to_f.argtypes = [ctypes.c_uint8]
 _lib.orc_f_to_e4m3.restype = ctypes.c_uint8
 _lib.orc_f_to_e4m3.argtypes = [_F]
 _lib.orc_store_e4m3.argtypes = [_P, _P, _P]
+_lib.orc_mx_index.restype = ctypes.c_size_t
+_lib.orc_mx_index.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+_lib.orc_mx_exp.restype = ctypes.c_int
+_lib.orc_mx_exp.argtypes = [_F]
+_lib.orc_fp8_rows.argtypes = [_P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, _P]
+_lib.orc_gate_rows.argtypes = [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]
 _lib.orc_attn_prep8.argtypes = [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _F, _I, _L, _P, _P, _P, _P, _P]
 _lib.orc_attn_prefill8.restype = _I
 _lib.orc_attn_prefill8.argtypes = [_P, _P, _P, _P, _P, _L, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _I]
@@ -281,3 +287,37 @@ def attn_prefill8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, po
     _lib.orc_attn_prefill8(_p(q), _p(kcache8), _p(vcache8), _p(kscale), _p(vscale), num_slots, _p(qkv), qstride, Hq,
                            Hkv, _p(pos), _p(cu), seqs, _p(block_table), max_blocks, block_size, _p(out), scale, p_tile)
     return out
+
+
+def mx_index(r, kb, KB):
+    """Byte offset of the Mx32 scale of (row r, 32-column block kb)."""
+    return _lib.orc_mx_index(r, kb, KB)
+
+
+def mx_exp(amax):
+    return _lib.orc_mx_exp(float(amax))
+
+
+def fp8_rows(y, mode, rows=None):
+    """f32 rows y [T][K] -> (E4M3 bytes [T][K], scales): mode 1 f32
+    [K / 128][rows], mode 2 uint8 Mx32 bytes (tiled, ceil(T / 128) row tiles)."""
+    y = np.ascontiguousarray(y, np.float32)
+    T, K = y.shape
+    rows = T if rows is None else rows
+    q = np.zeros((T, K), np.uint8)
+    if mode == 1:
+        s = np.zeros((K // 128, rows), np.float32)
+    else:
+        s = np.zeros(((T + 127) // 128) * ((K // 32 + 3) // 4) * 512, np.uint8)
+    _lib.orc_fp8_rows(_p(y), T, K, mode, rows, _p(q), _p(s))
+    return q, s
+
+
+def gate_rows(raw, qkv, qstride, Hq):
+    """Gated f32 outputs y = rbf(o) / (1 + expf(-gate)) of raw attention
+    outputs [T][Hq][256] (the values an FP8 copy quantises)."""
+    raw = np.ascontiguousarray(raw, np.float32)
+    T = raw.shape[0]
+    y = np.zeros_like(raw)
+    _lib.orc_gate_rows(_p(raw), _p(np.ascontiguousarray(qkv)), qstride, T, Hq, _p(y))
+    return y

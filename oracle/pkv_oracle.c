@@ -18,6 +18,10 @@
  *     round-to-nearest-even E4M3 (OCP "E4M3FN": bias 7, max 448, NaN 0x7F /
  *     0xFF, no infinities) bytes (store_e4m3, qwen35.cu:1055-1065), and
  *     decode attention over it (attn_paged8_g*, qwen35.cu:1146-1309 with F8)
+ *   - FP8 activation copies of the gated outputs (Fp8Out / quant8,
+ *     src/kernels/fp8.cuh:29-85, written at qwen35.cu:1297-1307, 2269-2279):
+ *     mode 1 Block128 f32 scales, mode 2 Mx32 E8M0 exponents in the MXFP8
+ *     tiled layout
  *
  * Pinning (what each function is checked against, in tests/test_oracle.py):
  *   append/gather/page_copy: closed forms, gather(append(x)) == x under
@@ -38,6 +42,13 @@
  *       form where a new fractional max in the second tile moves the anchor
  *       (any other anchoring or rounding point gives other bits), and exact
  *       equality with the textbook softmax when every p is a power of two.
+ *   FP8 copies: the Mx32 exponent is the smallest e with amax / 2^e <= 448
+ *       (checked by brute force over a range of amax, powers of two included);
+ *       the tiled index is a bijection onto [0, tiles x 512) and puts rows
+ *       r, r + 32, r + 64, r + 96 of a 128-row tile 4 bytes apart inside the
+ *       same 16 bytes (cuBLASLt's 128 x 4 block-scale tile); bytes dequantise
+ *       to within half an E4M3 step of v, and values on the E4M3 grid times a
+ *       power-of-two scale come back exactly.
  *   Parity unpinned beyond the stated tolerance: expf vs exp2f last bits
  *   (the reference's fast_exp2 against exp2 in double), f32 against double
  *   accumulation order; in attn_prep the f32 order of the squared sum and
@@ -455,6 +466,59 @@ void orc_store_e4m3(const float* v, uint8_t* dst, float* scale) {
     const float inv = 1.f / sc;
     for (int d = 0; d < HEAD_DIM; d++) dst[d] = orc_f_to_e4m3(v[d] * inv);
     *scale = sc;
+}
+
+/* ---- FP8 activation copies (reference Fp8Out / quant8, fp8.cuh:29-85) ---- */
+/* Byte offset of the Mx32 scale of (row r, 32-column block kb), KB blocks per
+ * row (fp8.cuh:29-33). */
+size_t orc_mx_index(int r, int kb, int KB) {
+    const size_t kt = (size_t)(KB + 3) / 4;
+    return ((size_t)(r / 128) * kt + (size_t)(kb / 4)) * 512 + (size_t)(r % 32) * 16 + (size_t)((r % 128) / 32) * 4 +
+           (size_t)(kb % 4);
+}
+/* Smallest e with amax / 2^e <= 448, clamped to [-127, 127]; -127 for
+ * amax <= 0 (fp8.cuh:35-42). */
+int orc_mx_exp(float amax) {
+    if (!(amax > 0.f)) return -127;
+    int ex;
+    const float m = frexpf(amax / 448.f, &ex);
+    if (m == 0.5f) ex -= 1;
+    return ex < -127 ? -127 : ex > 127 ? 127 : ex;
+}
+/* Rows [T][K] of f32 values y to E4M3 bytes q [T][K] and scales s: mode 1
+ * f32 amax / 448 (1 if zero) per 128 columns at s[(e / 128) * rows + t];
+ * mode 2 the byte 127 + orc_mx_exp(amax) per 32 columns at orc_mx_index.
+ * bytes = e4m3(v * (1 / scale)) (fp8.cuh:61-85). */
+void orc_fp8_rows(const float* y, int T, int K, int mode, int rows, uint8_t* q, void* s) {
+    const int gw = mode == 1 ? 128 : 32;
+    for (int t = 0; t < T; t++)
+        for (int e = 0; e < K; e += gw) {
+            const float* v = y + (size_t)t * K + e;
+            float a = 0.f;
+            for (int i = 0; i < gw; i++) a = fmaxf(a, fabsf(v[i]));
+            float inv;
+            if (mode == 1) {
+                const float sc = a > 0.f ? a / 448.f : 1.f;
+                inv = 1.f / sc;
+                ((float*)s)[(size_t)(e / 128) * rows + t] = sc;
+            } else {
+                const int ex = orc_mx_exp(a);
+                inv = ldexpf(1.f, -ex);
+                ((uint8_t*)s)[orc_mx_index(t, e / 32, K / 32)] = (uint8_t)(127 + ex);
+            }
+            for (int i = 0; i < gw; i++) q[(size_t)t * K + e + i] = orc_f_to_e4m3(v[i] * inv);
+        }
+}
+/* The gated f32 outputs y = rbf(o) / (1 + expf(-gate)) of raw attention
+ * outputs o [T][Hq][256] (qwen35.cu:1290-1292, 2270-2272), gate from qkv. */
+void orc_gate_rows(const float* raw, const uint16_t* qkv, int qstride, int T, int Hq, float* y) {
+    for (int t = 0; t < T; t++)
+        for (int h = 0; h < Hq; h++)
+            for (int d = 0; d < HEAD_DIM; d++) {
+                const size_t i = ((size_t)t * Hq + h) * HEAD_DIM + d;
+                const float gate = orc_b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d]);
+                y[i] = rbf(raw[i]) / (1.f + expf(-gate));
+            }
 }
 
 /* attn_prep with an E4M3 cache: as orc_attn_prep, but k (normed, rotated,

@@ -155,6 +155,57 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// FP8 activation copies of the gated attention outputs (the reference's
+// Fp8Out / quant8, src/kernels/fp8.cuh:29-85): row t of K values as E4M3
+// bytes at q[t * K + e] with mode 1 (Block128) one f32 scale amax / 448 (1
+// for an all-zero group) per 128 columns at s[(e / 128) * rows + t], or
+// mode 2 (Mx32) one E8M0 exponent 127 + x per 32 columns (the smallest x
+// with amax / 2^x <= 448) at the MXFP8 tiled index mx_index; bytes =
+// e4m3(v * (1 / scale)), round to nearest even.
+struct Fp8Out {
+    uint8_t* q;
+    void* s;
+    int mode;  // 0 none, 1 Block128, 2 Mx32
+    int rows;  // row capacity (Block128 scale stride)
+};
+// Byte offset of the Mx32 scale of (row r, 32-column block kb) among KB
+// blocks per row: tiles of 128 rows x 4 blocks (512 bytes), inside a tile
+// row r % 32 at 16 r, (r % 128) / 32 at 4 x that, kb % 4 at 1 x that.
+__device__ __forceinline__ size_t mx_index(int r, int kb, int KB) {
+    const int kt = (KB + 3) / 4;
+    return ((size_t)(r / 128) * kt + kb / 4) * 512 + (r % 32) * 16 + ((r % 128) / 32) * 4 + (kb % 4);
+}
+__device__ __forceinline__ int mx_exp(float amax) {
+    if (!(amax > 0.f)) return -127;
+    int ex;
+    const float m = frexpf(amax / 448.f, &ex);  // amax / 448 = m 2^ex, m in [0.5, 1)
+    if (m == 0.5f) ex -= 1;                     // a power of two needs no rounding up
+    return max(-127, min(127, ex));
+}
+// Four consecutive columns e .. e + 3 of row t per lane, the 64 lanes of the
+// wave in column order (a 128-column group spans 32 lanes, a 32-column
+// group 8); every lane calls.
+__device__ __forceinline__ void fp8_quant4(float y0, float y1, float y2, float y3, int t, int e, int K,
+                                           const Fp8Out& o) {
+    float a = fmaxf(fmaxf(fabsf(y0), fabsf(y1)), fmaxf(fabsf(y2), fabsf(y3)));
+    a = fmaxf(a, __shfl_xor(a, 1));
+    a = fmaxf(a, __shfl_xor(a, 2));
+    a = fmaxf(a, __shfl_xor(a, 4));
+    float inv;
+    if (o.mode == 1) {
+        a = fmaxf(a, __shfl_xor(a, 8));
+        a = fmaxf(a, __shfl_xor(a, 16));
+        const float sc = a > 0.f ? a / 448.f : 1.f;
+        inv = 1.f / sc;
+        if (e % 128 == 0) reinterpret_cast<float*>(o.s)[(size_t)(e / 128) * o.rows + t] = sc;
+    } else {
+        const int ex = mx_exp(a);
+        inv = ldexpf(1.f, -ex);
+        if (e % 32 == 0) reinterpret_cast<uint8_t*>(o.s)[mx_index(t, e / 32, K / 32)] = (uint8_t)(127 + ex);
+    }
+    *reinterpret_cast<uint32_t*>(o.q + (size_t)t * K + e) = f32x4_to_e4m3x4(y0 * inv, y1 * inv, y2 * inv, y3 * inv);
+}
+
 // Speculative rows verify drafts: outs[s * spec] >= 0 (reference qwen35.cu:94-100).
 __device__ __forceinline__ bool is_spec(const int* outs, int spec, int s) {
     return outs && outs[(size_t)s * spec] >= 0;

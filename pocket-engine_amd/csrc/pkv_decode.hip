@@ -108,11 +108,18 @@ struct WaveLds {
 
 // Gated output of 4 dims: y = bf16(rbf(a * inv) * sigmoid(gate)) (reference
 // qwen35.cu:1290-1293).
-__device__ __forceinline__ uint2 gate4(float a0, float a1, float a2, float a3, float inv, uint2 graw) {
+__device__ __forceinline__ uint2 gate4(float a0, float a1, float a2, float a3, float inv, uint2 graw,
+                                       float* y = nullptr) {
     const float y0 = rbf(a0 * inv) / (1.f + __expf(-bf_lo(graw.x)));
     const float y1 = rbf(a1 * inv) / (1.f + __expf(-bf_hi(graw.x)));
     const float y2 = rbf(a2 * inv) / (1.f + __expf(-bf_lo(graw.y)));
     const float y3 = rbf(a3 * inv) / (1.f + __expf(-bf_hi(graw.y)));
+    if (y) {
+        y[0] = y0;
+        y[1] = y1;
+        y[2] = y2;
+        y[3] = y3;
+    }
     return make_uint2(pack2(y0, y1), pack2(y2, y3));
 }
 
@@ -127,9 +134,12 @@ __device__ __forceinline__ uint2 gate4(float a0, float a1, float a2, float a3, f
 // through LDS (NW = 1: written straight from the wave). Every thread
 // reaches the sync. (NW = 16 folds up to 160 records in one round of loads:
 // launches with few (row, head) blocks and many records each.)
+// With fo (mode != 0) the gated f32 outputs are also written as an FP8
+// copy: row t, columns col .. col + 255 of a K-wide row.
 template <int NW = 4, class MsAt, class AccAt>
 __device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccAt acc_at, const uint16_t* gate,
-                                           uint16_t* out) {
+                                           uint16_t* out, const Fp8Out* fo = nullptr, int t = 0, int col = 0,
+                                           int K = 0) {
     constexpr int U = NW >= 16 ? 10 : 16;
     __shared__ __align__(16) float sh_a[NW][HEAD_DIM + 4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, d = 4 * lane;
@@ -177,8 +187,10 @@ __device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccA
         // combine below with a single term)
         const float f = M == -INFINITY ? 0.f : 1.f;
         const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
+        float y[4];
         *reinterpret_cast<uint2*>(out + d) = gate4(0.f + A0 * f, 0.f + A1 * f, 0.f + A2 * f, 0.f + A3 * f,
-                                                   1.f / (0.f + S * f), graw);
+                                                   1.f / (0.f + S * f), graw, y);
+        if (fo && fo->mode) fp8_quant4(y[0], y[1], y[2], y[3], t, col + d, K, *fo);
         return;
     }
     *reinterpret_cast<float4*>(&sh_a[w][d]) = make_float4(A0, A1, A2, A3);
@@ -205,7 +217,9 @@ __device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccA
             s += sh_a[k][HEAD_DIM + 1] * f;
         }
         const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
-        *reinterpret_cast<uint2*>(out + d) = gate4(a.x, a.y, a.z, a.w, 1.f / s, graw);
+        float y[4];
+        *reinterpret_cast<uint2*>(out + d) = gate4(a.x, a.y, a.z, a.w, 1.f / s, graw, y);
+        if (fo && fo->mode) fp8_quant4(y[0], y[1], y[2], y[3], t, col + d, K, *fo);
     }
 }
 

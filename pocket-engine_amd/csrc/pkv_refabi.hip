@@ -35,8 +35,11 @@
 // online softmax, one page in flight; other groups: the verify body with one
 // row) and combine through LDS.
 //
-// Bounds of this ABI: FP8
-// output copies (fmode != 0) are not produced; block_size 16 for decode, a
+// FP8 output copies (fq / fs / fmode / frows, the reference's Fp8Out) are
+// written by attn_paged_g<G> when it does not split (part null) and by
+// attn_merge, as the reference writes them (qwen35.cu:1297-1307, 2269-2279).
+//
+// Bounds of this ABI: block_size 16 for decode, a
 // power of two for prompts; G = Hq / Hkv of the kernel's name (1, 2, 4, 6
 // or 8). A launch outside these bounds
 // writes nothing. Page ids are not clamped (the reference ABI passes no pool
@@ -113,8 +116,8 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
                                           int Hq, int Hkv, const int* __restrict__ pos,
                                           const int* __restrict__ tok_seq, const int* __restrict__ block_table,
                                           int max_blocks, int block_size, uint16_t* out, float scale,
-                                          const int* __restrict__ cu, int skip_prompts, int min_chunk, float* part,
-                                          const int* __restrict__ outs, int spec) {
+                                          const Fp8Out fo, const int* __restrict__ cu, int skip_prompts,
+                                          int min_chunk, float* part, const int* __restrict__ outs, int spec) {
     constexpr int NW = G >= 6 ? 2 : 4;  // waves
     constexpr bool BODY4 = !F8 && G == 4;
     constexpr bool BODYV = !F8 && G != 4;
@@ -125,8 +128,8 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
     // (72 KB in all at G = 4: two workgroups per CU).
     __shared__ WaveLds<4> sh_w[BODY4 ? NW : 1];
     __shared__ __align__(16) uint16_t sh_v[BODYV ? NW : 1][BODYV ? VF_LDS : 8];
-    __shared__ WaveLds8 sh_w8[F8 ? NW : 1];
-    __shared__ float sh_acc_bf[F8 ? 1 : NW][G][HEAD_DIM];
+    __shared__ __align__(16) WaveLds8 sh_w8[F8 ? NW : 1];
+    __shared__ __align__(16) float sh_acc_bf[F8 ? 1 : NW][G][HEAD_DIM];
     __shared__ float sh_ml[NW][G][2];
     auto rec = [&](int w) -> float (*)[HEAD_DIM] {
         if constexpr (F8) return reinterpret_cast<float (*)[HEAD_DIM]>(sh_w8[w].v);
@@ -274,7 +277,21 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
             pp[2 + d] = A;
         } else {
             const float gate = b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d]);
-            out[((size_t)t * Hq + h) * HEAD_DIM + d] = (uint16_t)f2b_bits(rbf(A / S) / (1.f + __expf(-gate)));
+            const float y = rbf(A / S) / (1.f + __expf(-gate));
+            out[((size_t)t * Hq + h) * HEAD_DIM + d] = (uint16_t)f2b_bits(y);
+            // element (g, d) of wave 0's record is read above by this
+            // thread only: it now holds the f32 output for the FP8 copy
+            if (fo.mode) rec(0)[g][d] = y;
+        }
+    }
+    if (fo.mode && !part) {
+        // each head's 256 gated outputs as FP8, one wave per head, 4 columns
+        // per lane (the reference's attn_body epilogue, qwen35.cu:1297-1307)
+        __syncthreads();
+        const int lane = tid & 63;
+        for (int g = wave; g < G; g += NW) {
+            const float4 y = *reinterpret_cast<const float4*>(&rec(0)[g][4 * lane]);
+            fp8_quant4(y.x, y.y, y.z, y.w, t, (kvh * G + g) * HEAD_DIM + 4 * lane, Hq * HEAD_DIM, fo);
         }
     }
 }
@@ -290,7 +307,7 @@ __device__ __forceinline__ void paged_ref(const uint16_t* q, const void* kcache,
         int min_chunk, float *part, const int *__restrict__ outs, int spec
 #define PKV_PAGED_PASS                                                                                           \
     q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, \
-        out, scale, cu, skip_prompts, min_chunk, part, outs, spec
+        out, scale, pkv::Fp8Out{fq, fs, fmode, frows}, cu, skip_prompts, min_chunk, part, outs, spec
 
 // attn_paged_g<G> over a bf16 cache and attn_paged8_g<G> over an E4M3 cache
 // (kscale / vscale given), for the groups the reference instantiates
@@ -319,10 +336,12 @@ extern "C" __global__ void __launch_bounds__(256)
     if (pkv::ref_prompt_row(skip_prompts, cu, sq, outs, spec)) return;
     const int nz = pkv::ref_split_parts(pos[t] + 1, Z, min_chunk);
     const float* pp = part + (((size_t)sq * spec + (t - cu[sq])) * Hq + h) * Z * (HEAD_DIM + 2);
+    const pkv::Fp8Out fo{fq, fs, fmode, frows};
     pkv::merge_rows(
         nz, pkv::LOG2E, [&](int i) { return pp + (size_t)i * (HEAD_DIM + 2); },
         [&](int i) { return pp + (size_t)i * (HEAD_DIM + 2) + 2; },
-        qkv + (size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM, out + ((size_t)t * Hq + h) * HEAD_DIM);
+        qkv + (size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM, out + ((size_t)t * Hq + h) * HEAD_DIM,
+        &fo, t, h * HEAD_DIM, Hq * HEAD_DIM);
 }
 
 #define PKV_FLASH_ARGS                                                                                            \

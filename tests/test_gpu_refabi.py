@@ -35,7 +35,7 @@ def i32(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
 
 
-def ref_decode(rk, c, dev, Z=None, spec=1, skip=0, outs=None, out_init=None, keep_part=False, f8=None):
+def ref_decode(rk, c, dev, Z=None, spec=1, skip=0, outs=None, out_init=None, keep_part=False, f8=None, fp8out=None):
     """attn_paged_g<G> (+ attn_merge when split) as model.rs:2366-2437 launches
     them: the kernel of the model's G = Hq / Hkv, 128 threads for G >= 6, else
     256. f8 = (k8, v8, kscale, vscale) launches attn_paged8_g<G> over an E4M3
@@ -54,16 +54,27 @@ def ref_decode(rk, c, dev, Z=None, spec=1, skip=0, outs=None, out_init=None, kee
     pos, ts, bt, cu = i32(c["pos"], dev), i32(c["tok_seq"], dev), i32(c["bt"], dev), i32(c["cu"], dev)
     outs_d = None if outs is None else i32(outs, dev)
     out = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev) if out_init is None else i16(out_init, dev)
+    # fp8out = (mode, frows): the FP8 activation copy buffers (fq [T][Hq 256]
+    # bytes; fs: mode 1 f32 [Hq 256 / 128][frows], mode 2 the Mx32 tiles)
+    fmode, frows = (0, 0) if fp8out is None else fp8out
+    fq = fs = None
+    if fmode:
+        K = Hq * D
+        fq = torch.full((T, K), 0x7F, dtype=torch.uint8, device=dev)
+        fs = (torch.full((K // 128, frows), float("nan"), device=dev) if fmode == 1 else
+              torch.full((((frows + 127) // 128) * ((K // 32 + 3) // 4) * 512,), 0xEE, dtype=torch.uint8, device=dev))
     rk.launch(f"attn_paged{'8' if f8 is not None else ''}_g{G}", (T, Hkv, ranges), 128 if G >= 6 else 256, 0,
               [P(q), P(kc), P(vc), P(ks), P(vs), P(qkv), I(c["qstride"]), I(Hq), I(Hkv), P(pos), P(ts), P(bt),
-               I(c["max_blocks"]), I(BS), P(out), F(SCALE), P(None), P(None), I(0), I(0), P(cu), I(skip),
+               I(c["max_blocks"]), I(BS), P(out), F(SCALE), P(fq), P(fs), I(fmode), I(frows), P(cu), I(skip),
                I(SPLIT_MIN_KEYS), P(part), P(outs_d), I(spec)])
     if part is not None:
         rk.launch("attn_merge", (T, Hq, 1), 256, 0,
                   [P(part), I(ranges), I(SPLIT_MIN_KEYS), P(qkv), I(c["qstride"]), I(Hq), P(pos), P(ts), P(cu),
-                   I(skip), P(out), P(None), P(None), I(0), I(0), P(outs_d), I(spec)])
+                   I(skip), P(out), P(fq), P(fs), I(fmode), I(frows), P(outs_d), I(spec)])
     torch.cuda.synchronize()
     got = out.cpu().numpy().view(np.uint16)
+    if fmode:
+        return got, fq.cpu().numpy(), fs.cpu().numpy()
     if keep_part:
         return got, (None if part is None else part.cpu().numpy()), ranges
     return got
@@ -137,6 +148,54 @@ def test_ref_paged_wrong_block_writes_nothing(dev, rk):
                P(i32(c["cu"], dev)), I(0), I(SPLIT_MIN_KEYS), P(None), P(None), I(1)])
     torch.cuda.synchronize()
     assert (out.cpu().numpy().view(np.uint16) == 0x3333).all()
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("G,Hkv,Z", [(4, 4, 1), (4, 4, None), (6, 4, 1), (6, 4, None), (8, 2, 1)])
+def test_ref_fp8_output_copies(dev, rk, mode, G, Hkv, Z):
+    """fq / fs / fmode / frows (the reference's Fp8Out, fp8.cuh:50-85): the
+    gated f32 outputs as E4M3 bytes with Block128 f32 scales (mode 1) or
+    Mx32 E8M0 exponents in the 128 x 4 tiles (mode 2), written by
+    attn_paged_g<G> unsplit (Z = 1) or by attn_merge after a split. Against
+    the oracle's quantisation of its own gated outputs: every element
+    dequantises to within one E4M3 step of the oracle's f32 output (the two
+    f32 outputs differ by the attention tolerance), bytes and scales agree
+    almost everywhere, and nothing outside the rows' bytes and scales is
+    written."""
+    print(f"case refabi fp8 copies mode={mode} G={G} Hkv={Hkv} Z={Z}", flush=True)
+    lens = [1, 17, 700, 4097, 130, 2000]
+    c = decode_case(lens, G * Hkv, Hkv, 50 + mode + G)
+    T, Hq, K = len(lens), G * Hkv, G * Hkv * D
+    frows = 200  # the engine's row capacity, above T
+    got, fq, fs = ref_decode(rk, c, dev, Z=Z, fp8out=(mode, frows))
+    want_bits, raw = oracle.attn_decode(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], Hq, Hkv, c["pos"],
+                                        c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
+    ok, err = close(got, want_bits)
+    assert ok, err
+    y = oracle.gate_rows(raw, c["qkv"], c["qstride"], Hq).reshape(T, K)
+    wq, ws = oracle.fp8_rows(y, mode, rows=frows)
+    gw = 128 if mode == 1 else 32
+    # per-element scales of the kernel's and the oracle's copies
+    if mode == 1:
+        sg, sw = fs[:, :T].T, ws[:, :T].T                            # [T][K / 128]
+        assert np.isnan(fs[:, T:]).all()                             # rows past T untouched
+    else:
+        idx = np.array([[oracle.mx_index(t, kb, K // 32) for kb in range(K // 32)] for t in range(T)])
+        sg, sw = 2.0 ** (fs[idx].astype(np.float64) - 127), 2.0 ** (ws[idx].astype(np.float64) - 127)
+        mask = np.ones(fs.shape, bool)
+        mask[idx.reshape(-1)] = False
+        assert (fs[mask] == 0xEE).all()                              # other tile bytes untouched
+    deq = oracle.e4m3_to_f(fq).astype(np.float64) * np.repeat(sg, gw, axis=1)
+    step = np.repeat(sw, gw, axis=1) * 2.0 ** -9 + np.abs(y) * 2.0 ** -4
+    bf_ulp = np.abs(y) * 2.0 ** -8
+    assert (np.abs(deq - y) <= step + bf_ulp + 2e-3 + 1e-2 * np.abs(y)).all()
+    assert (fq == wq).mean() > 0.99, (fq == wq).mean()
+    # scales: f32 amax / 448 (mode 1) follows the f32 outputs' last bits (the
+    # kernel's exp against the oracle's expf), so within 1e-5 for most
+    # groups; E8M0 exponents (mode 2) agree almost everywhere
+    rel = np.abs(sg / sw - 1)
+    assert (rel <= 1e-2).all()
+    assert ((rel <= 1e-5).mean() > 0.95) if mode == 1 else ((sg == sw).mean() > 0.99), (rel <= 1e-5).mean()
 
 
 def test_ref_spec_rows_and_prompt_skip(dev, rk):

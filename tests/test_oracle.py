@@ -482,3 +482,69 @@ def test_prefill8_is_prefill_of_the_dequantised_cache():
     want = oracle.attn_prefill(q, kb, vb, qkv, c["qstride"], 8, 2, pos, cu, 2, c["bt"], c["max_blocks"], 16, 1 / 16)
     assert np.array_equal(got, want)
     assert not (got == 0).all()
+
+
+def test_mx_exp_is_the_smallest_exponent_fitting_448():
+    """orc_mx_exp(a) is the smallest e with a / 2^e <= 448 (brute force over
+    random amax, powers of two and 448 2^k exactly, where the frexp mantissa
+    is 0.5), -127 for zero."""
+    rng = np.random.default_rng(3)
+    vals = list(np.float32(rng.random(2000) * 10.0 ** rng.integers(-6, 6, 2000)))
+    vals += [np.float32(448 * 2.0 ** k) for k in range(-20, 20)] + [np.float32(2.0 ** k) for k in range(-20, 20)]
+    vals += [np.nextafter(np.float32(448 * 2.0 ** k), np.float32(np.inf)) for k in range(-5, 5)]
+    for a in vals:
+        e = oracle.mx_exp(a)
+        want = next(x for x in range(-127, 128) if np.float64(a) / 2.0 ** x <= 448)
+        assert e == want, (a, e, want)
+    assert oracle.mx_exp(0.0) == -127
+
+
+def test_mx_index_is_the_128x4_tile_layout():
+    """The Mx32 scale index is a bijection of (row, block) onto the tiles'
+    bytes; inside a 128-row x 4-block tile of 512 bytes the 4 blocks of a row
+    are adjacent and rows r, r + 32, r + 64, r + 96 share one 16-byte line
+    (cuBLASLt's block-scale tile), tiles row-major over the column tiles."""
+    T, KB = 300, 10
+    kt = (KB + 3) // 4
+    seen = set()
+    for r in range(T):
+        for kb in range(KB):
+            i = oracle.mx_index(r, kb, KB)
+            tile, within = divmod(i, 512)
+            assert tile == (r // 128) * kt + kb // 4
+            line, byte = divmod(within, 16)
+            assert line == r % 32 and byte // 4 == (r % 128) // 32 and byte % 4 == kb % 4
+            seen.add(i)
+    assert len(seen) == T * KB
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_fp8_rows_round_trip(mode):
+    """Bytes dequantise to within half an E4M3 step of v (relative 2^-4 for
+    normals, absolute 2^-10 scale for subnormals); a row of E4M3 grid values
+    with amax 448 comes back exactly (scale 1 / exponent 127 + 0), and a zero
+    group gets scale 1 / exponent byte 0."""
+    rng = np.random.default_rng(mode)
+    T, K = 130, 512
+    y = (rng.standard_normal((T, K)) * 10.0 ** rng.integers(-3, 3, (T, 1))).astype(np.float32)
+    y[5, 128:256] = 0.0
+    grid = oracle.e4m3_to_f(np.arange(0, 0x7F, dtype=np.uint8))
+    y[7] = np.resize(grid, K) * np.where(np.arange(K) % 2, 1, -1)
+    y[7, ::32] = 448.0
+    q, s = oracle.fp8_rows(y, mode)
+    gw = 128 if mode == 1 else 32
+    for t in range(T):
+        for e in range(0, K, gw):
+            if mode == 1:
+                sc = s[e // 128, t]
+            else:
+                sc = 2.0 ** (int(s[oracle.mx_index(t, e // 32, K // 32)]) - 127)
+            v = y[t, e:e + gw].astype(np.float64)
+            back = oracle.e4m3_to_f(q[t, e:e + gw]).astype(np.float64) * sc
+            step = np.maximum(np.abs(v) * 2.0 ** -4, sc * 2.0 ** -10)
+            assert (np.abs(back - v) <= step * 1.0001).all(), (t, e)
+            if t == 5 and e == 128:
+                assert (q[t, e:e + gw] == 0).all() and (sc == 1.0 if mode == 1 else
+                                                        s[oracle.mx_index(t, 4, 16)] == 0)
+            if t == 7:
+                assert sc == 1.0 and (back == v).all(), (t, e)
