@@ -64,6 +64,17 @@ int pkv_append(const void* k_rows, const void* v_rows, int64_t row_stride, const
 int pkv_gather(const void* kcache, const void* vcache, const int32_t* bt_row, int L, int block_size, int Hkv,
                int head_bytes, int64_t num_blocks, void* k_out, void* v_out, void* stream);
 
+/* Single-query attention over dense f32 K/V rows, for checks of gathered
+ * sequences (the reference's CPU plumbing configuration: gather to
+ * [len][Hkv][D] f32, attention of the last token's query, compared in
+ * fp64). For s < S: rows off[s] .. off[s] + len[s] - 1 of k / v ([rows][Hkv]
+ * [D] f32, device), query q[s] ([Hq][D] f32), out[s][h] ([Hq][D] f32) =
+ * softmax_j(scale * q[s][h] . k_j) . v_j with kv head h / (Hq / Hkv), ungated.
+ * D <= 256. No reference kernel (the reference checks this case on the
+ * CPU). off / len are device arrays. */
+int pkv_attn_dense_f32(const float* q, const float* k, const float* v, const int32_t* off, const int32_t* len,
+                       int S, int Hq, int Hkv, int D, float scale, float* out, void* stream);
+
 /* Page copy (copy-on-write): for i < n, page dst[i] := page src[i] in both
  * pools; page_bytes = block_size * Hkv * head_bytes (a multiple of 16).
  * src/dst are device arrays. Destinations must be distinct and not sources.

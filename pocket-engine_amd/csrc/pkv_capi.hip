@@ -142,6 +142,16 @@ int pkv_gather(const void* kcache, const void* vcache, const int32_t* bt_row, in
     return launch_status();
 }
 
+int pkv_attn_dense_f32(const float* q, const float* k, const float* v, const int32_t* off, const int32_t* len,
+                       int S, int Hq, int Hkv, int D, float scale, float* out, void* stream) {
+    if (S < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D <= 0 || D > 256) return PKV_ERR_INVALID;
+    if (S == 0) return PKV_OK;
+    if (!q || !k || !v || !off || !len || !out) return PKV_ERR_INVALID;
+    hipLaunchKernelGGL(pkv::attn_dense_f32_kernel, dim3(S, Hq), dim3(256), 0, (hipStream_t)stream, q, k, v, off, len,
+                       Hq, Hkv, D, scale, out);
+    return launch_status();
+}
+
 int pkv_page_copy(void* kcache, void* vcache, const int32_t* src, const int32_t* dst, int n, int64_t page_bytes,
                   int64_t num_blocks, void* stream) {
     if (n < 0 || page_bytes <= 0 || page_bytes % 16 != 0 || num_blocks <= 0) return PKV_ERR_INVALID;

@@ -160,3 +160,72 @@ __global__ void __launch_bounds__(256) mtp_next_kernel(const int* __restrict__ r
 }
 
 }  // namespace pkv
+
+namespace pkv {
+
+// Single-query attention over dense f32 rows (the check path of the
+// reference's CPU plumbing configuration: a sequence gathered to
+// [L][Hkv][D], its last token's query): block (s, h) computes
+// out[s][h][d] = sum_j e^(x_j - max) v_j[d] / sum_j e^(x_j - max),
+// x_j = scale * q[s][h] . k_j over the sequence's rows off[s] .. off[s] +
+// len[s] - 1, kv head h / (Hq / Hkv). Keys in chunks of 256 (a thread per
+// key for the scores, a thread per dim for the weighted sum), with the
+// running max and sum rescaled per chunk; f32 throughout.
+__global__ void __launch_bounds__(256) attn_dense_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                             const float* __restrict__ v,
+                                                             const int* __restrict__ off,
+                                                             const int* __restrict__ len, int Hq, int Hkv, int D,
+                                                             float scale, float* __restrict__ out) {
+    __shared__ float sq[256];
+    __shared__ float sp[256];
+    __shared__ float red[4];
+    const int s = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int kvh = h / (Hq / Hkv), L = len[s];
+    const float* qrow = q + ((size_t)s * Hq + h) * D;
+    if (tid < D) sq[tid] = qrow[tid];
+    __syncthreads();
+    float m = -INFINITY, l = 0.f, acc = 0.f;  // acc: dim tid
+    auto block_max = [&](float x) {
+        for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+        if (lane == 0) red[w] = x;
+        __syncthreads();
+        x = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        __syncthreads();
+        return x;
+    };
+    auto block_sum = [&](float x) {
+        for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+        if (lane == 0) red[w] = x;
+        __syncthreads();
+        x = (red[0] + red[1]) + (red[2] + red[3]);
+        __syncthreads();
+        return x;
+    };
+    for (int j0 = 0; j0 < L; j0 += 256) {
+        const int j = j0 + tid;
+        float x = -INFINITY;
+        if (j < L) {
+            const float* krow = k + ((size_t)(off[s] + j) * Hkv + kvh) * D;
+            float d0 = 0.f;
+            for (int d = 0; d < D; d++) d0 = fmaf(sq[d], krow[d], d0);
+            x = scale * d0;
+        }
+        const float mn = fmaxf(m, block_max(x));
+        const float p = j < L ? expf(x - mn) : 0.f;
+        const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+        sp[tid] = p;
+        l = l * corr + block_sum(p);  // block_sum's barriers also publish sp
+        m = mn;
+        if (tid < D) {
+            float a = acc * corr;
+            const int n = min(256, L - j0);
+            const float* vcol = v + ((size_t)(off[s] + j0) * Hkv + kvh) * D + tid;
+            for (int i = 0; i < n; i++) a = fmaf(sp[i], vcol[(size_t)i * Hkv * D], a);
+            acc = a;
+        }
+        __syncthreads();  // sp is rewritten by the next chunk
+    }
+    if (tid < D) out[((size_t)s * Hq + h) * D + tid] = L > 0 ? acc / l : 0.f;
+}
+
+}  // namespace pkv

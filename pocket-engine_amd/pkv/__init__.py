@@ -37,6 +37,8 @@ _SIGS = {
     "pkv_append": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_i64, _c_p]),
     "pkv_gather": (_c_int, [_c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_p, _c_p, _c_p]),
     "pkv_page_copy": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_i64, _c_i64, _c_p]),
+    "pkv_attn_dense_f32": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_f, _c_p,
+                                    _c_p]),
     "pkv_mtp_next": (_c_int, [_c_p, _c_p, _c_p, _c_int, _c_p, _c_int, _c_int, _c_p, _c_int, _c_p, _c_p, _c_p, _c_int,
                               _c_p]),
     "pkv_attn_decode_workspace": (_c_int, [_c_int, _c_int, ctypes.POINTER(_c_sz)]),
@@ -143,6 +145,12 @@ def append(k_rows, v_rows, row_stride, slot_map, T, Hkv, head_bytes, kcache, vca
 def gather(kcache, vcache, bt_row, L, block_size, Hkv, head_bytes, num_blocks, k_out, v_out, stream=None):
     _check(_lib.pkv_gather(_ptr(kcache), _ptr(vcache), _ptr(bt_row), L, block_size, Hkv, head_bytes, num_blocks,
                            _ptr(k_out), _ptr(v_out), _stream(stream)), "pkv_gather")
+
+
+def attn_dense_f32(q, k, v, off, lens, S, Hq, Hkv, D, scale, out, stream=None):
+    """Single-query attention over dense f32 rows (see include/pkv.h)."""
+    _check(_lib.pkv_attn_dense_f32(_ptr(q), _ptr(k), _ptr(v), _ptr(off), _ptr(lens), S, Hq, Hkv, D, scale, _ptr(out),
+                                   _stream(stream)), "pkv_attn_dense_f32")
 
 
 def page_copy(kcache, vcache, src, dst, n, page_bytes, num_blocks, stream=None):

@@ -88,8 +88,12 @@ def test_reference_abi_code_object_exports_the_reference_kernel_names(tmp_path):
                     "--targets=hipv4-amdgcn-amd-amdhsa--gfx950"], check=True)
     syms = subprocess.run([readelf, "--syms", "--wide", str(co)], check=True, capture_output=True, text=True).stdout
     kernels = {line.split()[-1] for line in syms.splitlines() if " FUNC " in line and "GLOBAL" in line}
-    for name in ("attn_prep", "attn_paged_g4", "attn_merge", "attn_groupr_g4_t2_k32", "attn_mfma_g4_t2",
-                 "attn_group8_g4_t2_k16", "attn_paged8_g4", "mtp_next"):
+    names = ["attn_prep", "attn_merge", "attn_groupr_g4_t2_k32", "attn_mfma_g4_t2", "mtp_next"]
+    # decode for every group the reference instantiates (qwen35.cu:1330-1334)
+    names += [f"attn_paged{e}_g{g}" for e in ("", "8") for g in (1, 2, 4, 6, 8)]
+    # the prompt kernel gfx950's fa_shape picks for each group and cache type
+    names += [refabi.flash_launch(100, 3, 4, g=g, fp8=f8)[0] for g in (1, 2, 4, 6, 8) for f8 in (False, True)]
+    for name in names:
         assert name in kernels, (name, sorted(kernels)[:20])
 
 

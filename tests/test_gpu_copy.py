@@ -22,7 +22,10 @@ def as_i16(a):
 def test_c1_plumbing_append_gather_f32(dev):
     """Config 1: Hkv 2, head_dim 64, f32, page 16; 4 sequences of U[1, 200]
     tokens; tables from a seeded permutation of a 64-page pool; append all,
-    gather back bit-exact."""
+    gather back bit-exact, then single-query attention of each sequence's
+    last token over its gathered rows on the GPU (pkv_attn_dense_f32)
+    against the oracle's fp64 attention over the paged cache: within 1e-5
+    absolute + 1e-5 relative (f32 scores, exp and sums against fp64)."""
     print("case c1 f32 append/gather", flush=True)
     rng = np.random.default_rng(11)
     Hkv, Dh, pages = 2, 64, 64
@@ -50,6 +53,7 @@ def test_c1_plumbing_append_gather_f32(dev):
         data.append((k, v))
     torch.cuda.synchronize()
     assert np.array_equal(kc_d.cpu().numpy(), kc_h) and np.array_equal(vc_d.cpu().numpy(), vc_h)
+    dense = []
     for s, L in enumerate(lens):
         ko = torch.empty(L, Hkv, Dh, dtype=torch.float32, device=dev)
         vo = torch.empty_like(ko)
@@ -57,6 +61,21 @@ def test_c1_plumbing_append_gather_f32(dev):
         pkv.gather(kc_d, vc_d, btd, int(L), BS, Hkv, Dh * 4, pages, ko, vo)
         torch.cuda.synchronize()
         assert np.array_equal(ko.cpu().numpy(), data[s][0]) and np.array_equal(vo.cpu().numpy(), data[s][1])
+        dense.append((ko, vo))
+    k_all = torch.cat([d[0] for d in dense]).contiguous()
+    v_all = torch.cat([d[1] for d in dense]).contiguous()
+    off = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    for Hq in (2, 8):
+        q = rng.standard_normal((4, Hq, Dh)).astype(np.float32)
+        out = torch.full((4, Hq, Dh), float("nan"), device=dev)
+        pkv.attn_dense_f32(to_dev(q, dev), k_all, v_all, to_dev(off, dev), to_dev(lens.astype(np.int32), dev), 4, Hq,
+                           Hkv, Dh, 0.125, out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        for s, L in enumerate(lens):
+            want = oracle.attn_single(q[s], kc_h, vc_h, Dh, Hq, Hkv, bt[s], int(L), BS, 0.125)
+            err = np.abs(got[s] - want)
+            assert (err <= 1e-5 + 1e-5 * np.abs(want)).all(), (Hq, s, float(err.max()))
 
 
 @pytest.mark.parametrize("T,Hkv", [(1, 4), (64, 4), (513, 4), (7, 8), (130, 16), (3, 2)])
