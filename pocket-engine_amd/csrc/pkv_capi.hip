@@ -455,12 +455,14 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
         if (st != PKV_OK) return st;
     }
     if ((phases & 2) && verify) {
-        if (pkv::vf_rows(G) == 4)
-            hipLaunchKernelGGL(pkv::verify_merge_kernel<4>, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p, pos,
-                               tok_seq, cu, outs);
-        else
-            hipLaunchKernelGGL(pkv::verify_merge_kernel<2>, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p, pos,
-                               tok_seq, cu, outs);
+        // waves per (row, head) block chosen as for decode_merge_kernel below
+        using MergeKernel = void (*)(pkv::DecodeParams, const int*, const int*, const int*, const int*);
+        const int nw = (int64_t)T * Hq < device_cus() ? 16 : (int64_t)T + n_wg <= 8 * (int64_t)T ? 1 : 4;
+        const bool r4 = pkv::vf_rows(G) == 4;
+        const MergeKernel mk = nw == 16 ? (r4 ? pkv::verify_merge_kernel<4, 16> : pkv::verify_merge_kernel<2, 16>)
+                               : nw == 1 ? (r4 ? pkv::verify_merge_kernel<4, 1> : pkv::verify_merge_kernel<2, 1>)
+                                         : (r4 ? pkv::verify_merge_kernel<4, 4> : pkv::verify_merge_kernel<2, 4>);
+        hipLaunchKernelGGL(mk, dim3(T, Hq), dim3(64 * nw), 0, (hipStream_t)stream, p, pos, tok_seq, cu, outs);
         return launch_status();
     }
     if (phases & 2) {

@@ -320,11 +320,11 @@ __global__ void __launch_bounds__(256, 2)
     }
 }
 
-// Merges the split segments: one block per (row, query head); row t's
-// segment (NR rows) is headed by the row at offset NR * floor((t - cu[s]) /
-// NR) of its sequence.
-template <int NR>
-__global__ void __launch_bounds__(256)
+// Merges the split segments: one block of 64 NW threads per (row, query
+// head) (NW as decode_merge_kernel's); row t's segment (NR rows) is headed
+// by the row at offset NR * floor((t - cu[s]) / NR) of its sequence.
+template <int NR, int NW = 4>
+__global__ void __launch_bounds__(64 * NW)
     verify_merge_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                         const int* __restrict__ cu, const int* __restrict__ outs) {
     const int t = blockIdx.x, T = p.T;
@@ -337,7 +337,7 @@ __global__ void __launch_bounds__(256)
     const int R = p.offs[T + 1];
     const int b0 = o0 / R, b1 = (o1 - 1) / R;
     if (b0 == b1) return;
-    merge_head(p, t, (th + b0) * VF_ROWS + r, VF_ROWS, b1 - b0 + 1, blockIdx.y);
+    merge_head<NW>(p, t, (th + b0) * VF_ROWS + r, VF_ROWS, b1 - b0 + 1, blockIdx.y);
 }
 
 }  // namespace pkv
