@@ -680,8 +680,8 @@ def bench_verify(args):
                    "kv": args.kv, "batch": B, "drafts": n, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
                    "pool_pages": pages, "seed": seed, "mean_unique_keys_per_step": round(float(np.mean(keys)), 1),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "verify_range8_kernel (E4M3 cache, no append)" if e4m3 else
-                     "verify_range_kernel", "achieved": round(kern_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": "verify_range8_kernel<4> (E4M3 cache, no append)" if e4m3 else
+                     "verify_range_kernel<4>", "achieved": round(kern_gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
                      "avg_us": round(kern_avg_us, 2), "traffic": None,
                      "traffic_profiled_constant": None if e4m3 else {
