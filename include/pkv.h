@@ -242,6 +242,22 @@ int pkv_time_next_range_kernel(void* start_event, void* stop_event);
 /* The same for the next pkv_attn_prefill kernel of this thread. */
 int pkv_time_next_prefill_kernel(void* start_event, void* stop_event);
 
+/* FP8 output copies for this thread's next decode / verify call (the
+ * reference's fq / fs / fmode / frows arguments of attn_paged_g<G> and
+ * attn_merge, written for its --fp8 output projection: Fp8Out / quant8,
+ * src/kernels/fp8.cuh:29-85, qwen35.cu:1297-1307, 2269-2279). With fmode 1
+ * (Block128) or 2 (Mx32) the next pkv_attn_decode, _merge, _step, _verify,
+ * _decode_e4m3, _verify_e4m3 or _step_noalloc call also writes every row's
+ * gated f32 outputs as E4M3 bytes fq[t][Hq * 256] with scales fs: mode 1 one
+ * f32 amax / 448 per 128 columns at fs[(col / 128) * frows + t], mode 2 one
+ * E8M0 byte per 32 columns in the 128-row x 4-block tiles of MXFP8. Rows the
+ * call skips get none. frows (the engine's row capacity) must be >= T. The
+ * request is cleared by the call that runs the merge (a _split call keeps
+ * it for its _merge); fmode 0 clears it. While it is set, every row is
+ * finished by the merge kernel (the key-range kernel leaves a partial record
+ * for every piece), which costs a little time. */
+int pkv_attn_fp8_next(void* fq, void* fs, int fmode, int frows);
+
 /* Tuning: key-range workgroups per CU (default 1) and fewest keys per range
  * (default 32). Process-wide; takes effect for later calls (workspace sizes
  * follow). */

@@ -70,7 +70,7 @@ _lib.orc_attn_prep8.argtypes = [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, 
 _lib.orc_attn_prefill8.restype = _I
 _lib.orc_attn_prefill8.argtypes = [_P, _P, _P, _P, _P, _L, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _I]
 _lib.orc_attn_decode8.restype = _I
-_lib.orc_attn_decode8.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _F, _P, _I, _P, _I, _I]
+_lib.orc_attn_decode8.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _F, _P, _I, _P, _I, _I, _P]
 
 
 def _p(a):
@@ -260,18 +260,20 @@ def attn_prep8(qkv, qstride, Hq, Hkv, q_norm, k_norm, rope, rope_stride, sec_h, 
 
 
 def attn_decode8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks,
-                 block_size, scale, cu=None, skip_prompts=0, outs=None, spec=1, out=None):
-    """Decode attention over an E4M3 cache (reference attn_paged8 semantics)."""
+                 block_size, scale, cu=None, skip_prompts=0, outs=None, spec=1, out=None, return_raw=False):
+    """Decode attention over an E4M3 cache (reference attn_paged8 semantics).
+    Returns out, or (out, o_raw f32 ungated) with return_raw."""
     T = len(pos)
     if out is None:
         out = np.zeros((T, Hq, 256), np.uint16)
+    raw = np.zeros((T, Hq, 256), np.float32)
     cu, outs, pos, tok_seq, block_table = _i32(cu), _i32(outs), _i32(pos), _i32(tok_seq), _i32(block_table)
     kscale = np.ascontiguousarray(kscale, np.float32)
     vscale = np.ascontiguousarray(vscale, np.float32)
     _lib.orc_attn_decode8(_p(q), _p(kcache8), _p(vcache8), _p(kscale), _p(vscale), _p(qkv), qstride, Hq, Hkv,
                           _p(pos), _p(tok_seq), _p(block_table), max_blocks, block_size, _p(out), scale, _p(cu),
-                          skip_prompts, _p(outs), spec, T)
-    return out
+                          skip_prompts, _p(outs), spec, T, _p(raw))
+    return (out, raw) if return_raw else out
 
 
 def attn_prefill8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,

@@ -557,7 +557,8 @@ void orc_attn_prep8(const uint16_t* qkv, int qstride, int Hq, int Hkv, const flo
 int orc_attn_decode8(const uint16_t* q, const uint8_t* kcache8, const uint8_t* vcache8, const float* kscale,
                      const float* vscale, const uint16_t* qkv, int qstride, int Hq, int Hkv, const int* pos,
                      const int* tok_seq, const int* block_table, int max_blocks, int block_size, uint16_t* out,
-                     float scale, const int* cu, int skip_prompts, const int* outs, int spec, int T) {
+                     float scale, const int* cu, int skip_prompts, const int* outs, int spec, int T,
+                     float* o_raw) {
     const int G = Hq / Hkv;
     double* s = NULL;
     size_t cap = 0;
@@ -593,6 +594,7 @@ int orc_attn_decode8(const uint16_t* q, const uint8_t* kcache8, const uint8_t* v
             for (int e = 0; e < HEAD_DIM; e++) {
                 const float gate = orc_b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + e]);
                 out[((size_t)t * Hq + h) * HEAD_DIM + e] = gated(A[e] / S, gate);
+                if (o_raw) o_raw[((size_t)t * Hq + h) * HEAD_DIM + e] = (float)(A[e] / S);
             }
         }
     }

@@ -62,6 +62,9 @@ int g_min_range = 32;
 // end (hipExtLaunchKernelGGL), then forgets.
 thread_local hipEvent_t t_ev_start = nullptr, t_ev_stop = nullptr;
 thread_local hipEvent_t t_pf_start = nullptr, t_pf_stop = nullptr;  // same for the prefill kernel
+// FP8 output copies requested for this thread's next decode / verify call
+// (pkv_attn_fp8_next); cleared by the call that runs the merge.
+thread_local pkv::Fp8Out t_fp8 = {nullptr, nullptr, 0, 0};
 
 int decode_n_wg() { return device_cus() * g_wg_per_cu; }
 // The E4M3 decode kernel runs two workgroups per CU (252 VGPRs and 72.8 KB
@@ -314,6 +317,13 @@ int pkv_time_next_range_kernel(void* start_event, void* stop_event) {
     return PKV_OK;
 }
 
+int pkv_attn_fp8_next(void* fq, void* fs, int fmode, int frows) {
+    if (fmode < 0 || fmode > 2) return PKV_ERR_INVALID;
+    if (fmode && (!fq || !fs || frows <= 0)) return PKV_ERR_INVALID;
+    t_fp8 = {(uint8_t*)fq, fs, fmode, fmode ? frows : 0};
+    return PKV_OK;
+}
+
 int pkv_time_next_prefill_kernel(void* start_event, void* stop_event) {
     t_pf_start = (hipEvent_t)start_event;
     t_pf_stop = (hipEvent_t)stop_event;
@@ -395,7 +405,11 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
     const int n_wg = decode_n_wg() * (f8 ? F8_WG_PER_CU : 1);
     const DecodeLayout lay = decode_layout(T, Hq, n_wg, verify);
     if (workspace_bytes < lay.total) return PKV_ERR_INVALID;
+    const pkv::Fp8Out fo = t_fp8;
+    if (fo.mode && T > fo.rows) return PKV_ERR_INVALID;
+    if (phases & 6) t_fp8 = {nullptr, nullptr, 0, 0};  // consumed by the call that merges
     pkv::DecodeParams p;
+    p.fo = fo;
     p.q = (const uint16_t*)q;
     p.kc = (uint16_t*)kcache;
     p.vc = (uint16_t*)vcache;

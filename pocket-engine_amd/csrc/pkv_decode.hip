@@ -73,6 +73,9 @@ struct DecodeParams {
     // E4M3 cache (decode_range8_kernel, verify_range8_kernel): f32 scale per (slot, kv head)
     const float* kscale;
     const float* vscale;
+    // FP8 copies of the gated outputs (mode != 0): every piece leaves a
+    // partial record and the merge finishes every row, writing them
+    Fp8Out fo;
 };
 
 constexpr int PAGE = 16;
@@ -227,11 +230,13 @@ __device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccA
 // (base + i * stride) * Hq + h of part_ms / part_acc.
 template <int NW = 4>
 __device__ __forceinline__ void merge_head(const DecodeParams& p, int t, int base, int stride, int n, int h) {
+    const Fp8Out* fo = p.fo.mode ? &p.fo : nullptr;
     const size_t r0 = (size_t)base * p.Hq + h, step = (size_t)stride * p.Hq;
     merge_rows<NW>(
         n, 1.f, [&](int i) { return p.part_ms + (r0 + i * step) * 2; },
         [&](int i) { return p.part_acc + (r0 + i * step) * HEAD_DIM; },
-        p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM, p.out + ((size_t)t * p.Hq + h) * HEAD_DIM);
+        p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM, p.out + ((size_t)t * p.Hq + h) * HEAD_DIM,
+        fo, t, h * HEAD_DIM, p.Hq * HEAD_DIM);
 }
 
 // One wave: token t, kv head kvh, keys [j0, j1) of its sequence. With FRESH,
@@ -466,7 +471,7 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* _
                                              int t, int seq, int row0, int P0, int kvh, int j0, int j1, int L,
                                              int idx) {
     const int* __restrict__ bt = block_table + (size_t)seq * p.max_blocks;
-    const DecodeEpi<G> epi{p, t, kvh, idx, j0 == 0 && j1 == L};
+    const DecodeEpi<G> epi{p, t, kvh, idx, j0 == 0 && j1 == L && !p.fo.mode};
     if constexpr (FUSED)
         piece_body<G, true>(p, bt, lds, t, kvh, j0, j1, L, P0, row0, epi);
     else
@@ -642,7 +647,7 @@ __global__ void __launch_bounds__(64 * NW) decode_merge_kernel(DecodeParams p) {
     if (o1 <= o0) return;
     const int R = p.offs[T + 1];
     const int b0 = o0 / R, b1 = (o1 - 1) / R;
-    if (b0 == b1) return;  // finished in place by its range
+    if (b0 == b1 && !p.fo.mode) return;  // finished in place by its range
     merge_head<NW>(p, t, t + b0, 1, b1 - b0 + 1, blockIdx.y);
 }
 template __global__ void decode_merge_kernel<1>(DecodeParams);

@@ -301,7 +301,7 @@ __global__ void __launch_bounds__(256, 2)
         if (L > 0) {
             const int j0 = max(start, off) - off, j1 = min(end, off + L) - off;
             const int seq = __builtin_amdgcn_readfirstlane(tab ? sh_seq[t] : tok_seq[t]);
-            const DecodeEpi8<G> epi{p, t, kvh, t + b, j0 == 0 && j1 == L};
+            const DecodeEpi8<G> epi{p, t, kvh, t + b, j0 == 0 && j1 == L && !p.fo.mode};
             piece_body8<1, G>(p, block_table + (size_t)seq * p.max_blocks, sh_w[wave], t, kvh, j0, j1, epi);
             off += L;
         }

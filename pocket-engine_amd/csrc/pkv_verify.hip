@@ -268,7 +268,7 @@ __global__ void __launch_bounds__(256, 2)
                                : 0;
             const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
             const int j0 = max(start, off) - off, j1 = min(end, off + Ls) - off;
-            const VerifyEpi<G> epi{p, t, kvh, t + b, j0 == 0 && j1 == Ls};
+            const VerifyEpi<G> epi{p, t, kvh, t + b, j0 == 0 && j1 == Ls && !p.fo.mode};
             verify_piece<G>(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Lr, epi);
             off += Ls;
         }
@@ -309,7 +309,7 @@ __global__ void __launch_bounds__(256, 2)
                                : 0;
             const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
             const int j0 = max(start, off) - off, j1 = min(end, off + Ls) - off;
-            const VerifyEpi<G> vepi{p, t, kvh, t + b, j0 == 0 && j1 == Ls};
+            const VerifyEpi<G> vepi{p, t, kvh, t + b, j0 == 0 && j1 == Ls && !p.fo.mode};
             auto epi = [&](int c, int gq, const f32x4 (&acc)[16], float m, float l) {
                 vepi(c / G, c % G, gq, acc, m, l);
             };
@@ -336,7 +336,7 @@ __global__ void __launch_bounds__(64 * NW)
     if (o1 <= o0) return;
     const int R = p.offs[T + 1];
     const int b0 = o0 / R, b1 = (o1 - 1) / R;
-    if (b0 == b1) return;
+    if (b0 == b1 && !p.fo.mode) return;
     merge_head<NW>(p, t, (th + b0) * VF_ROWS + r, VF_ROWS, b1 - b0 + 1, blockIdx.y);
 }
 

@@ -37,6 +37,7 @@ _SIGS = {
     "pkv_append": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_i64, _c_p]),
     "pkv_gather": (_c_int, [_c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_p, _c_p, _c_p]),
     "pkv_page_copy": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_i64, _c_i64, _c_p]),
+    "pkv_attn_fp8_next": (_c_int, [_c_p, _c_p, _c_int, _c_int]),
     "pkv_attn_dense_f32": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_f, _c_p,
                                     _c_p]),
     "pkv_mtp_next": (_c_int, [_c_p, _c_p, _c_p, _c_int, _c_p, _c_int, _c_int, _c_p, _c_int, _c_p, _c_p, _c_p, _c_int,
@@ -145,6 +146,11 @@ def append(k_rows, v_rows, row_stride, slot_map, T, Hkv, head_bytes, kcache, vca
 def gather(kcache, vcache, bt_row, L, block_size, Hkv, head_bytes, num_blocks, k_out, v_out, stream=None):
     _check(_lib.pkv_gather(_ptr(kcache), _ptr(vcache), _ptr(bt_row), L, block_size, Hkv, head_bytes, num_blocks,
                            _ptr(k_out), _ptr(v_out), _stream(stream)), "pkv_gather")
+
+
+def attn_fp8_next(fq, fs, fmode, frows):
+    """FP8 output copies for this thread's next decode / verify call (see include/pkv.h)."""
+    _check(_lib.pkv_attn_fp8_next(_ptr(fq), _ptr(fs), fmode, frows), "pkv_attn_fp8_next")
 
 
 def attn_dense_f32(q, k, v, off, lens, S, Hq, Hkv, D, scale, out, stream=None):

@@ -203,3 +203,45 @@ def bits(x):
     """A bf16 / int16 device tensor as host uint16 bits."""
     import torch
     return x.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def fp8_buffers(T, K, mode, frows, dev):
+    """fq / fs for FP8 output copies, filled with sentinels (0x7F bytes, NaN
+    scales, 0xEE exponent bytes) so untouched entries are visible."""
+    import torch
+    fq = torch.full((T, K), 0x7F, dtype=torch.uint8, device=dev)
+    fs = (torch.full((K // 128, frows), float("nan"), device=dev) if mode == 1 else
+          torch.full((((frows + 127) // 128) * ((K // 32 + 3) // 4) * 512,), 0xEE, dtype=torch.uint8, device=dev))
+    return fq, fs
+
+
+def check_fp8_copies(fq, fs, y, mode, frows, rows=None):
+    """FP8 copies (fq [T][K] E4M3 bytes, fs scales) of f32 outputs y [T][K]
+    against the oracle's quantisation of y (oracle.fp8_rows): every element
+    dequantises to within one E4M3 step of y (plus the attention tolerance,
+    since y is the oracle's own output), > 99 % of bytes identical, scales
+    within 1e-2 (f32 Block128 scales within 1e-5 for > 95 % of groups, Mx32
+    exponents identical for > 99 %), and rows outside `rows` untouched."""
+    import oracle
+    T, K = y.shape
+    rows = np.arange(T) if rows is None else np.asarray(rows)
+    wq, ws = oracle.fp8_rows(y, mode, rows=frows)
+    gw = 128 if mode == 1 else 32
+    if mode == 1:
+        sg, sw = fs[:, :T].T.astype(np.float64), ws[:, :T].T.astype(np.float64)
+        untouched = np.isnan(fs[:, [t for t in range(frows) if t not in set(rows.tolist())]])
+        assert untouched.all()
+    else:
+        idx = np.array([[oracle.mx_index(t, kb, K // 32) for kb in range(K // 32)] for t in range(T)])
+        sg, sw = 2.0 ** (fs[idx].astype(np.float64) - 127), 2.0 ** (ws[idx].astype(np.float64) - 127)
+        mask = np.ones(fs.shape, bool)
+        mask[idx[rows].reshape(-1)] = False
+        assert (fs[mask] == 0xEE).all()
+    sg, sw, fq, wq, y = sg[rows], sw[rows], fq[rows], wq[rows], y[rows]
+    deq = oracle.e4m3_to_f(fq).astype(np.float64) * np.repeat(sg, gw, axis=1)
+    step = np.repeat(sw, gw, axis=1) * 2.0 ** -9 + np.abs(y) * 2.0 ** -4
+    assert (np.abs(deq - y) <= step + np.abs(y) * 2.0 ** -8 + 2e-3 + 1e-2 * np.abs(y)).all()
+    assert (fq == wq).mean() > 0.99, (fq == wq).mean()
+    rel = np.abs(sg / sw - 1)
+    assert (rel <= 1e-2).all()
+    assert ((rel <= 1e-5).mean() > 0.95) if mode == 1 else ((sg == sw).mean() > 0.99)
