@@ -97,6 +97,20 @@ def test_reference_abi_code_object_exports_the_reference_kernel_names(tmp_path):
         assert name in kernels, (name, sorted(kernels)[:20])
 
 
+def test_fp8_next_validates_and_clears():
+    """pkv_attn_fp8_next: mode 0 / 1 / 2 only; a copy request needs both
+    buffers and a row capacity; mode 0 clears (host only, nothing launched)."""
+    L = pkv._lib
+    assert L.pkv_attn_fp8_next(None, None, 3, 10) == pkv.ERR_INVALID
+    assert L.pkv_attn_fp8_next(16, None, 1, 10) == pkv.ERR_INVALID
+    assert L.pkv_attn_fp8_next(16, 16, 2, 0) == pkv.ERR_INVALID
+    assert L.pkv_attn_fp8_next(16, 16, 1, 10) == pkv.OK
+    # a decode call with T > frows is refused before any launch
+    assert L.pkv_attn_decode(16, 16, 16, 16, 10240, 16, 4, 16, 16, 16, 4, 16, 16, 0.1, 16, 0, None, 1, 11, 10, 256,
+                             1 << 30, None) == pkv.ERR_INVALID
+    assert L.pkv_attn_fp8_next(None, None, 0, 0) == pkv.OK
+
+
 def test_reference_launch_shapes():
     """The restated host formulas the code object is launched with."""
     from pkv import refabi
