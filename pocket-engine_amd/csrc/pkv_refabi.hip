@@ -366,18 +366,18 @@ namespace pkv {
 constexpr int REF_VP32 = 528;  // V pair stride of the attn_groupr stages (elements)
 
 // G heads per kv head, BQ queries per workgroup (16 x the name's tiles),
-// F8: E4M3 cache, VP: V pair stride of the two stages, DYN: stages in the
+// F8: E4M3 cache, VP: V pair stride of the NST stages, DYN: stages in the
 // launch's dynamic shared memory (checked against the dispatch packet's
 // group segment size, byte offset 28: a launch with too little does
 // nothing), else in static LDS.
-template <int G, int BQ, bool F8, int VP, bool DYN>
+template <int G, int BQ, bool F8, int VP, bool DYN, int NST = 2>
 __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
     constexpr int THREADS = pf_threads(BQ, 1, G);
     uint16_t* sm;
     if constexpr (DYN) {
         extern __shared__ __align__(16) uint16_t dyn_sm[];
         sm = dyn_sm;
-        constexpr uint32_t need = 2u * pf_stage(VP) * 2u + (F8 ? 0u : (uint32_t)pf_ids_bytes(THREADS));
+        constexpr uint32_t need = (uint32_t)NST * pf_stage(VP) * 2u + (F8 ? 0u : (uint32_t)pf_ids_bytes(THREADS));
         const uint32_t group_bytes = reinterpret_cast<const uint32_t*>(__builtin_amdgcn_dispatch_ptr())[7];
         if (group_bytes < need) return;
     } else {
@@ -409,7 +409,7 @@ __device__ __forceinline__ void flash_ref(PKV_FLASH_ARGS) {
     p.num_blocks = REF_NO_CLAMP;
     p.kscale = kscale;
     p.vscale = vscale;
-    prefill_body<G, BQ, 1, F8, 2, VP>(p, sm);
+    prefill_body<G, BQ, 1, F8, NST, VP>(p, sm);
 }
 
 }  // namespace pkv
@@ -433,18 +433,21 @@ extern "C" __global__ void __launch_bounds__(192, 2) attn_groupr_g6_t1_k32(PKV_F
 // shared memory from the engine), and every group over an E4M3 cache
 // (attn_group8_*; 84,480 bytes for G = 6, 101,376 otherwise). Two stages of
 // the default layout; one workgroup per CU.
-#define PKV_FLASH_K16(NAME, G, BQ, F8)                                                                           \
+#define PKV_FLASH_K16(NAME, G, BQ, F8, NST, VP)                                                                  \
     extern "C" __global__ void __launch_bounds__(pkv::pf_threads(BQ, 1, G), 1) NAME(PKV_FLASH_ARGS) {            \
-        pkv::flash_ref<G, BQ, F8, pkv::PF_VPAIR, true>(PKV_FLASH_PASS);                                          \
+        pkv::flash_ref<G, BQ, F8, VP, true, NST>(PKV_FLASH_PASS);                                                \
     }
-PKV_FLASH_K16(attn_group_g1_t8_k16, 1, 128, false)
-PKV_FLASH_K16(attn_group_g2_t4_k16, 2, 64, false)
-PKV_FLASH_K16(attn_group_g8_t1_k16, 8, 16, false)
-PKV_FLASH_K16(attn_group8_g1_t8_k16, 1, 128, true)
-PKV_FLASH_K16(attn_group8_g2_t4_k16, 2, 64, true)
-PKV_FLASH_K16(attn_group8_g4_t2_k16, 4, 32, true)
-PKV_FLASH_K16(attn_group8_g6_t1_k16, 6, 16, true)
-PKV_FLASH_K16(attn_group8_g8_t1_k16, 8, 16, true)
+// 101,376 bytes hold three stages with V pairs 1,056 bytes apart (100,608
+// bytes, plus 256 of page-id rings for bf16): tiles requested two ahead;
+// G = 6's 84,480 hold two stages.
+PKV_FLASH_K16(attn_group_g1_t8_k16, 1, 128, false, 3, pkv::REF_VP32)
+PKV_FLASH_K16(attn_group_g2_t4_k16, 2, 64, false, 3, pkv::REF_VP32)
+PKV_FLASH_K16(attn_group_g8_t1_k16, 8, 16, false, 3, pkv::REF_VP32)
+PKV_FLASH_K16(attn_group8_g1_t8_k16, 1, 128, true, 3, pkv::REF_VP32)
+PKV_FLASH_K16(attn_group8_g2_t4_k16, 2, 64, true, 3, pkv::REF_VP32)
+PKV_FLASH_K16(attn_group8_g4_t2_k16, 4, 32, true, 3, pkv::REF_VP32)
+PKV_FLASH_K16(attn_group8_g6_t1_k16, 6, 16, true, 2, pkv::PF_VPAIR)
+PKV_FLASH_K16(attn_group8_g8_t1_k16, 8, 16, true, 3, pkv::REF_VP32)
 
 // gfx942's name for G = 4 (attn_mfma_g4_t2, 512 threads): 64 queries per
 // workgroup, stages in static LDS beside the launch's 37,376 dynamic bytes.
