@@ -113,8 +113,9 @@ int pkv_attn_decode_workspace(int T, int Hq, size_t* bytes);
  * q[t][h] * scale over keys 0..pos[t] of sequence tok_seq[t] through
  * block_table[tok_seq[t] * max_blocks ..], then
  * out[t][h] = bf16(bf16(A / S) * sigmoid(gate)), gate = qkv[t * qstride +
- * h * 512 + 256 ..]. Same pointer meanings as the reference; kscale/vscale/
- * fq/fs/fmode/frows (E4M3 cache, FP8 outputs) are not part of this path.
+ * h * 512 + 256 ..]. Same pointer meanings as the reference; kscale/vscale
+ * (E4M3 cache) are pkv_attn_decode_e4m3's, fq/fs/fmode/frows (FP8 output
+ * copies) come from pkv_attn_fp8_next.
  * The key-range split is the library's own (the reference's part/min_chunk
  * pair is replaced by `workspace`, of pkv_attn_decode_workspace bytes).
  * num_blocks bounds page ids (ids outside the pool are clamped, never read
@@ -195,7 +196,8 @@ int pkv_attn_decode_step_noalloc(const void* k_rows, const void* v_rows, int64_t
  * speculative rows (is_spec, src/kernels/qwen35.cu:94-100), which its
  * attn_paged_g<G> serves one token per block, each re-reading the
  * sequence's pages (launched at src/model.rs:2366-2437). Here up to 4
- * consecutive rows of a sequence share one pass over its pages. `cu` is
+ * (G <= 4) or 2 (G = 6, 8) consecutive rows of a sequence share one pass
+ * over its pages. `cu` is
  * required and each sequence's rows must be consecutive (cu[s] ..
  * cu[s+1]-1, as Scheduler::fill writes them, src/sched.rs:1105-1115).
  * Segments hold 4 rows for G <= 4 and 2 rows for G = 6 or 8 (the 16 MFMA
@@ -215,8 +217,8 @@ int pkv_attn_verify(const void* q, const void* kcache, const void* vcache, const
  * bytes [blocks * 16][Hkv][256] and kscale / vscale one f32 per [slot][kv
  * head] (written by pkv_attn_prep with scales): s_j = (q * scale) . k_j *
  * kscale_j, out = bf16(bf16(sum_j p_j vscale_j v_j / sum_j p_j) *
- * sigmoid(gate)). Rows as pkv_attn_decode (`cu` only with skip_prompts);
- * workspace: pkv_attn_decode_workspace bytes. */
+ * sigmoid(gate)). Rows and groups as pkv_attn_decode (`cu` only with
+ * skip_prompts, for every G); workspace: pkv_attn_decode_workspace bytes. */
 int pkv_attn_decode_e4m3(const void* q, const void* kcache, const void* vcache, const float* kscale,
                          const float* vscale, const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos,
                          const int32_t* tok_seq, const int32_t* block_table, int max_blocks, int block_size,
