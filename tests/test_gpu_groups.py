@@ -174,3 +174,68 @@ def test_prefill_e4m3_groups_match_oracle(dev, entry, G, Hkv, ctxs, chunks, seed
                                 c["seqs"], c["bt"], c["max_blocks"], BS, SCALE, out=init.copy())
     ok, err = close(got, want)
     assert ok, f"max |diff| {err}"
+
+
+def paged_prompt_case(ctxs, chunks, Hkv, G, bs, seed):
+    """Prompt sequences (ctx cached tokens + a chunk, all in the cache) over
+    pages of `bs` keys from a seeded permutation."""
+    rng = np.random.default_rng(seed)
+    Hq = G * Hkv
+    lens = [c + n for c, n in zip(ctxs, chunks)]
+    mb = max((L + bs - 1) // bs for L in lens)
+    pages = len(lens) * mb + 3
+    perm = rng.permutation(pages).astype(np.int32)
+    bt = np.zeros((len(lens), mb), np.int32)
+    at = 0
+    for s, L in enumerate(lens):
+        n = (L + bs - 1) // bs
+        bt[s, :n] = perm[at:at + n]
+        at += n
+    pos, cu = [], [0]
+    for ctx, n in zip(ctxs, chunks):
+        pos.extend(range(ctx, ctx + n))
+        cu.append(cu[-1] + n)
+    T = len(pos)
+    qstride = (2 * Hq + 2 * Hkv) * D
+    from _util import bf16_bits
+    return dict(q=bf16_bits(rng.standard_normal((T, Hq, D)) * 0.5),
+                kc=bf16_bits(rng.standard_normal((pages * bs, Hkv, D)) * 0.5),
+                vc=bf16_bits(rng.standard_normal((pages * bs, Hkv, D)) * 0.5),
+                qkv=bf16_bits(rng.standard_normal((T, qstride))), qstride=qstride, bt=bt, max_blocks=mb, pages=pages,
+                pos=np.array(pos, np.int32), cu=np.array(cu, np.int32), seqs=len(lens), T=T, Hq=Hq, Hkv=Hkv)
+
+
+@pytest.mark.parametrize("e4m3", [False, True])
+@pytest.mark.parametrize("G,Hkv", [(4, 4), (6, 4), (1, 4), (8, 2)])
+@pytest.mark.parametrize("bs", [4, 8, 32, 64])
+def test_prefill_block_sizes_match_oracle(dev, e4m3, G, Hkv, bs):
+    """Pages of 4 / 8 / 32 / 64 keys (any power of two; the reference engine
+    uses 16): below 16 keys the tiles load through registers with a page id
+    per key (pages smaller than the loading threads' key groups) or per key
+    group, at 32 and 64 by LDS DMA (bf16) — for every group shape."""
+    print(f"case prefill bs={bs} G={G} Hkv={Hkv} e4m3={e4m3}", flush=True)
+    c = paged_prompt_case([100, 0, 37], [70, 33, 130], Hkv, G, bs, 200 + bs + G)
+    T, Hq = c["T"], c["Hq"]
+    init = np.full((T, Hq, D), 0x3333, np.uint16)
+    out = torch.from_numpy(init.view(np.int16).copy()).to(dev)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16) if a.dtype == np.uint16
+                                   else np.ascontiguousarray(a)).to(dev)
+    pos, cu, bt = t(c["pos"]), t(c["cu"]), t(c["bt"])
+    if e4m3:
+        rng = np.random.default_rng(bs + G)
+        k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+        ks = (rng.random(c["kc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+        vs = (rng.random(c["vc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+        pkv.attn_prefill_e4m3(t(c["q"]), t(k8), t(v8), t(ks), t(vs), t(c["qkv"]), c["qstride"], Hq, Hkv, pos, cu,
+                              c["seqs"], bt, c["max_blocks"], bs, out, SCALE, None, 1, T, c["pages"])
+        want = oracle.attn_prefill8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["cu"],
+                                    c["seqs"], c["bt"], c["max_blocks"], bs, SCALE, out=init.copy())
+    else:
+        pkv.attn_prefill(t(c["q"]), t(c["kc"]), t(c["vc"]), t(c["qkv"]), c["qstride"], Hq, Hkv, pos, cu, c["seqs"],
+                         bt, c["max_blocks"], bs, out, SCALE, None, 1, T, c["pages"])
+        want = oracle.attn_prefill(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["cu"],
+                                   c["seqs"], c["bt"], c["max_blocks"], bs, SCALE, out=init.copy())
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
