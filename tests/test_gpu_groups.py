@@ -13,7 +13,7 @@ import torch
 import oracle
 import pkv
 from _util import BS, D, close, decode_case, nan_stale
-from test_gpu_decode import run_gpu, run_oracle
+from test_gpu_decode import dev_i16, dev_i32, run_gpu, run_oracle
 from test_gpu_e4m3 import e4m3_cache, run_decode8
 from test_gpu_verify import run_oracle as run_oracle_v, run_verify, verify_case
 
@@ -239,3 +239,56 @@ def test_prefill_block_sizes_match_oracle(dev, e4m3, G, Hkv, bs):
     got = out.cpu().numpy().view(np.uint16)
     ok, err = close(got, want)
     assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("fmode", [0, 1, 2])
+def test_groups_graph_replay_matches_eager(dev, fmode):
+    """The G = 6 decode route (range kernels + merge, optionally with FP8
+    output copies) captured into a HIP graph and replayed 4 times, with eager
+    launches and synchronizations in between, reproduces the eager outputs
+    and copies bit for bit each time."""
+    print(f"case decode G=6 graph replay fmode={fmode}", flush=True)
+    from _util import fp8_buffers
+    c = decode_case([513, 4097, 1000, 64, 17], 24, 4, 70 + fmode)
+    T, Hq = len(c["pos"]), c["Hq"]
+    q, kc, vc, qkv = (dev_i16(c[k], dev) for k in ("q", "kc", "vc", "qkv"))
+    pos, ts, bt, cu = (dev_i32(c[k], dev) for k in ("pos", "tok_seq", "bt", "cu"))
+    out = torch.zeros(T, Hq, D, dtype=torch.int16, device=dev)
+    ws = torch.empty(pkv.attn_decode_workspace(T, Hq), dtype=torch.uint8, device=dev)
+    fq, fs = fp8_buffers(T, Hq * D, fmode or 1, T, dev)
+    fq0, fs0 = fq.clone(), fs.clone()  # sentinels; Mx32 scales pad to 128 rows
+
+    def launch():
+        if fmode:
+            pkv.attn_fp8_next(fq, fs, fmode, T)
+        pkv.attn_decode(q, kc, vc, qkv, c["qstride"], Hq, c["Hkv"], pos, ts, bt, c["max_blocks"], BS, out, SCALE,
+                        cu, 0, None, 1, T, c["pages"], ws)
+
+    def snap():
+        torch.cuda.synchronize()
+        return out.cpu().numpy().copy(), fq.cpu().numpy().copy(), fs.cpu().numpy().copy()
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        launch()  # eager reference, outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    e_out, e_fq, e_fs = snap()
+    ok, err = close(e_out.view(np.uint16), run_oracle(c, cu=c["cu"]))
+    assert ok, f"eager max |diff| {err}"
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch()
+    for r in range(4):
+        if r % 2:
+            launch()  # eager work between replays
+            torch.cuda.synchronize()
+        out.fill_(0)
+        fq.copy_(fq0)
+        fs.copy_(fs0)
+        g.replay()
+        g_out, g_fq, g_fs = snap()
+        assert np.array_equal(g_out, e_out), f"replay {r} out"
+        if fmode:
+            assert np.array_equal(g_fq, e_fq), f"replay {r} fq"
+            assert np.array_equal(g_fs.view(np.uint8), e_fs.view(np.uint8)), f"replay {r} fs"
