@@ -292,3 +292,32 @@ def test_groups_graph_replay_matches_eager(dev, fmode):
         if fmode:
             assert np.array_equal(g_fq, e_fq), f"replay {r} fq"
             assert np.array_equal(g_fs.view(np.uint8), e_fs.view(np.uint8)), f"replay {r} fs"
+
+
+@pytest.mark.parametrize("G,Hkv", [(4, 4), (6, 4), (8, 2)])
+def test_groups_more_rows_than_a_block(dev, G, Hkv):
+    """More rows than a workgroup has threads (the range search's two-pass
+    scan and per-row metadata read from memory): 90 sequences of 1..7 draft
+    rows (over 256 rows, segments of every fill) through pkv_attn_verify, and
+    300 single rows through pkv_attn_decode (G != 4 runs the verify kernels),
+    and the verify rows over an E4M3 cache, all against the oracle."""
+    rng = np.random.default_rng(80 + G)
+    groups = [(int(rng.integers(0, 400)), int(rng.integers(1, 8))) for _ in range(90)]
+    print(f"case verify G={G} Hkv={Hkv} rows={sum(n for _, n in groups)}", flush=True)
+    c = verify_case(groups, Hkv, 81 + G, G=G)
+    assert c["T"] > 256
+    ok, err = close(run_verify(c, dev), run_oracle_v(c))
+    assert ok, f"verify max |diff| {err}"
+    lens = [int(x) for x in rng.integers(1, 300, 300)]
+    print(f"case decode G={G} Hkv={Hkv} tokens=300", flush=True)
+    d = decode_case(lens, G * Hkv, Hkv, 82 + G)
+    ok, err = close(run_gpu(d, dev), run_oracle(d, cu=d["cu"]))
+    assert ok, f"decode max |diff| {err}"
+    # the same verify rows over an E4M3 cache
+    k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+    ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+    vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
+    want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], c["Hq"], Hkv, c["pos"], c["tok_seq"],
+                               c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
+    ok, err = close(run_decode8(c, k8, v8, ks, vs, dev, entry="verify"), want)
+    assert ok, f"verify e4m3 max |diff| {err}"
