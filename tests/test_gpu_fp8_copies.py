@@ -57,12 +57,40 @@ def run(c, dev, entry, fp8=None, f8cache=None, outs=None, skip=0):
         v_rows = k_rows + Hkv * D * 2
         pkv.attn_decode_step(k_rows, v_rows, 2 * Hkv * D * 2, t_(slot, dev), q, kc, vc, qkv, c["qstride"], Hq, Hkv,
                              pos, ts, bt, c["max_blocks"], BS, out, SCALE, cu, skip, outs_d, 1, T, c["pages"], ws)
+    elif entry == "split":
+        # pkv_attn_decode_split, then pkv_attn_decode_merge (a copy request
+        # set before the split is kept for the merge)
+        kc, vc = t_(c["kc"], dev), t_(c["vc"], dev)
+        for phase in ("split", "merge"):
+            pkv.attn_decode(q, kc, vc, qkv, c["qstride"], Hq, Hkv, pos, ts, bt, c["max_blocks"], BS, out, SCALE, cu,
+                            skip, outs_d, 1, T, c["pages"], ws, phase=phase)
     else:
         fn = pkv.attn_decode if entry == "decode" else pkv.attn_verify
         fn(q, t_(c["kc"], dev), t_(c["vc"], dev), qkv, c["qstride"], Hq, Hkv, pos, ts, bt, c["max_blocks"], BS, out,
            SCALE, cu, skip, outs_d, 1, T, c["pages"], ws)
     torch.cuda.synchronize()
     return out.cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("G", [4, 6])
+def test_split_then_merge_matches_decode(dev, mode, G):
+    """pkv_attn_decode_split followed by pkv_attn_decode_merge gives the bytes
+    of one pkv_attn_decode call (G = 4: decode ranges; G = 6: the verify
+    route), FP8 copies included."""
+    print(f"case split + merge G={G} fp8 mode={mode}", flush=True)
+    c = decode_case([1, 17, 700, 4097, 130, 2000], G * 4, 4, 90 + G)
+    T, K = len(c["pos"]), G * 4 * D
+    bufs = [fp8_buffers(T, K, mode, FROWS, dev) if mode else (None, None) for _ in range(2)]
+    one = run(c, dev, "decode", fp8=(bufs[0][0], bufs[0][1], mode) if mode else None)
+    two = run(c, dev, "split", fp8=(bufs[1][0], bufs[1][1], mode) if mode else None)
+    assert np.array_equal(one, two)
+    if mode:
+        assert torch.equal(bufs[0][0], bufs[1][0]) and torch.equal(bufs[0][1].view(torch.uint8),
+                                                                    bufs[1][1].view(torch.uint8))
+    ok, err = close(one, oracle.attn_decode(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], c["Hq"], 4, c["pos"],
+                                            c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])[0])
+    assert ok, f"max |diff| {err}"
 
 
 @pytest.mark.parametrize("mode", [1, 2])
