@@ -379,7 +379,10 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
     // The fused step's kernel is the G = 4 decode body.
     if ((phases & 4) && G != 4) return PKV_ERR_UNSUPPORTED;
     if (num_blocks > (int64_t)INT32_MAX / 16) return PKV_ERR_INVALID;
-    if (T == 0) return PKV_OK;
+    if (T == 0) {
+        if (phases & 6) t_fp8 = {nullptr, nullptr, 0, 0};  // a call that merges consumes the request
+        return PKV_OK;
+    }
     if (!q || !kcache || !vcache || !qkv || !pos || !tok_seq || !block_table || !out || !workspace)
         return PKV_ERR_INVALID;
     const bool f8 = kscale != nullptr;
