@@ -67,6 +67,83 @@ class HipEvents:
             self.hip.hipEventDestroy(b)
 
 
+def measure_traffic(args, seed, algorithmic_bytes, want=None):
+    """HBM bytes per launch of the workload's dominant kernel, measured: the
+    same workload (same seed, 1 warm-up + 3 steps) runs twice in a child
+    process under rocprofv3 --pmc, once per counter (FETCH_SIZE, WRITE_SIZE;
+    KiB per dispatch), and each counter is scaled by what it reads for the
+    2 GiB device copies the child also runs (2 GiB read, 2 GiB written). The
+    dominant kernel is this library's kernel with the largest FETCH_SIZE
+    among those whose name holds `want` (any, if None); algorithmic_bytes is
+    its per-launch figure over the child's steps 0 .. 3. Returns (bytes per
+    launch or None, detail dict)."""
+    import csv
+    import glob
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    import numpy as np
+
+    if args.no_traffic or args.traffic_child:
+        return None, None
+    prof = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3" if os.path.exists("/opt/rocm/bin/rocprofv3")
+                                          else None)
+    if prof is None:
+        return None, {"error": "rocprofv3 not found"}
+    child = [sys.executable, "-u", os.path.abspath(__file__), "--traffic-child", "--no-traffic", "--no-cpu",
+             "--no-graph", "--steps", "3", "--warmup", "1", "--seed", str(seed), "--config", args.config,
+             "--kv", args.kv, "--q-heads", str(args.q_heads), "--batch", str(args.batch), "--pages", str(args.pages),
+             "--prefix", str(args.prefix)]
+    for flag in ("unfused", "with_prep", "refabi", "verify_kernel"):
+        if getattr(args, flag):
+            child.append("--" + flag.replace("_", "-"))
+    if args.wg_per_cu or args.min_range:
+        child += ["--wg-per-cu", str(args.wg_per_cu or 1), "--min-range", str(args.min_range or 32)]
+    per_kib, name = {}, None
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = tempfile.mkdtemp(prefix="pkv_traffic_", dir="/tmp")
+        cmd = [prof, "--pmc", ctr, "--output-format", "csv", "-d", out, "-o", "run", "--"] + child
+        proc = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.DEVNULL,
+                                stderr=subprocess.DEVNULL, start_new_session=True)
+        try:
+            proc.wait(timeout=300)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)  # the process group this call started
+            proc.wait()
+            return None, {"error": f"rocprofv3 --pmc {ctr} run timed out"}
+        files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+        if proc.returncode != 0 or not files:
+            return None, {"error": f"rocprofv3 --pmc {ctr} run failed (exit {proc.returncode})"}
+        rows = [r for f in files for r in csv.DictReader(open(f)) if r["Counter_Name"] == ctr]
+        shutil.rmtree(out, ignore_errors=True)
+        copies = sorted((float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]),
+                        reverse=True)[:3]
+        mine = {}
+        for r in rows:
+            k = r["Kernel_Name"]
+            if ("pkv::" in k or k.startswith("attn_")) and (want is None or want in k):
+                mine.setdefault(k, []).append(float(r["Counter_Value"]))
+        if not copies or not mine:
+            return None, {"error": f"no copy or library dispatches in the {ctr} run"}
+        if name is None:  # the dominant kernel: largest median FETCH_SIZE
+            name = max(mine, key=lambda k: float(np.median(mine[k])))
+        if name not in mine:
+            return None, {"error": f"{name} missing from the {ctr} run"}
+        factor = (2 << 30) / (float(np.median(copies)) * 1024)
+        per_kib[ctr] = (float(np.median(mine[name])), factor)
+    rd = per_kib["FETCH_SIZE"][0] * 1024 * per_kib["FETCH_SIZE"][1]
+    wr = per_kib["WRITE_SIZE"][0] * 1024 * per_kib["WRITE_SIZE"][1]
+    return rd + wr, {
+        "kernel": name.split("(")[0].replace("void ", ""), "read_bytes": round(rd), "write_bytes": round(wr),
+        "read_factor": round(per_kib["FETCH_SIZE"][1], 4), "write_factor": round(per_kib["WRITE_SIZE"][1], 4),
+        "algorithmic_bytes": round(algorithmic_bytes), "ratio": round((rd + wr) / algorithmic_bytes, 4),
+        "source": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over the same workload (same seed, 4 launches) in "
+                  "child processes of this run; median per dispatch, scaled by the counter of 2 GiB device copies "
+                  "in the same runs"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +181,10 @@ def main():
     ap.add_argument("--q-heads", type=int, default=16,
                     help="query heads over the 4 kv heads (16: the configs' G = 4; 24: the reference's 27B shape, "
                          "G = 6; c2/c3 then run unfused: append, then decode attention)")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the HBM traffic measurement (two short child runs of the same workload under "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by 2 GiB device copies in the same runs)")
+    ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--unfused", action="store_true",
                     help="append, key ranges and merge as three launches instead of the fused step")
     args = ap.parse_args()
@@ -131,6 +212,16 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_bytes": 2 << 30, "copies": 3, "sums": 3, "fills": 3}))
         return
+
+    if args.traffic_child:
+        # calibration for the parent's counter runs: 2 GiB device copies
+        # (2 GiB read + 2 GiB written each)
+        src = torch.ones(1 << 30, dtype=torch.int16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     import pkv
     from pkv import synth
@@ -325,6 +416,14 @@ def main():
     kern_gbs = sum(kern_bytes) / (sum(kern_ms) * 1e-3) / 1e9
 
     copy_gbs, read_gbs = hbm_copy_probe(dev)
+    # algorithmic bytes of the dominant kernel over the child's steps 0 .. 3
+    # (the same formulas as kern_bytes)
+    keys0 = [meta.keys(k) for k in range(4)]
+    if args.unfused or args.refabi:
+        alg0 = [kk * Hkv * (D + 4 if e4m3 else D * 2) * 2 + B * Hq * D * 2 for kk in keys0]
+    else:
+        alg0 = [synth.algorithmic_bytes_decode(kk, B, Hq, Hkv) + synth.algorithmic_bytes_append(B, Hkv) for kk in keys0]
+    traffic, traffic_detail = measure_traffic(args, seed, float(np.mean(alg0)))
     cpu = None
     st0 = steps[args.warmup]
     if not args.no_cpu and args.config == "c3" and not e4m3:
@@ -372,13 +471,8 @@ def main():
                      "avg_us": round(kern_avg_us, 2), "median_us": round(1e3 * float(np.median(kern_ms)), 2),
                      "hbm_copy_probe_gbs": round(copy_gbs, 1), "hbm_read_probe_gbs": round(read_gbs, 1),
                      "frac_of_read_probe": round(kern_gbs / read_gbs, 4),
-                     "traffic": None,
-                     "traffic_profiled_constant": None if (e4m3 or args.refabi or args.with_prep or args.unfused) else {
-                         "note": "quoted from the committed counter runs (seed 1), not measured by this run",
-                         "source": "profiles/decode_step_c3_batch64.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, "
-                                   "copy-calibrated, seed 1)",
-                         "read_bytes": 1131.9e6, "write_bytes": 5.53e6, "algorithmic_bytes": 1113.9e6,
-                         "ratio": 1.021}},
+                     "traffic": None if traffic is None else round(traffic),
+                     "traffic_detail": traffic_detail},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -501,6 +595,12 @@ def bench_prefill(args):
                   "median_us": round(app_us, 2), "achieved": round(app_bytes / (app_us * 1e-6) / 1e9, 1),
                   "peak": PEAK_HBM_GBS, "unit": "GB/s",
                   "frac": round(app_bytes / (app_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    # algorithmic bytes of one prefill launch: every key of the prefix and
+    # the chunks once (K and V, all kv heads; E4M3 bytes + scales), q, the
+    # gate rows and the outputs
+    key_bytes = Hkv * (D + 4) * 2 if e4m3 else Hkv * D * 2 * 2
+    alg = (P + B * N) * key_bytes + 3 * T * Hq * D * 2
+    traffic, traffic_detail = measure_traffic(args, seed, alg, want=fname if args.refabi else "prefill")
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_prefill(kc, vc, q, qkv, bt, pos, cu, B, Hq, Hkv, qstride, mb, flops, e4m3,
@@ -529,11 +629,8 @@ def bench_prefill(args):
                                                   else f"prefill_e4m3_kernel<{Hq // Hkv}>" if e4m3 else f"prefill_kernel<{Hq // Hkv}>"),
                      "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "avg_us": round(kern_us, 1), "traffic": None,
-                     "traffic_profiled_constant": None if args.refabi or e4m3 else {
-                         "note": "quoted from the committed counter runs (seed 1), not measured by this run",
-                         "source": "profiles/prefill_c4_shared_prefix.md (rocprofv3 --pmc, copy-calibrated, seed 1)",
-                         "read_bytes": 1.34e9, "write_bytes": 138e6, "note_hbm": "MFMA-bound: 0.30 TB/s of HBM"}},
+                     "avg_us": round(kern_us, 1), "traffic": None if traffic is None else round(traffic),
+                     "traffic_detail": traffic_detail},
         "append": append,
         "cpu_baseline": cpu,
     }
@@ -650,6 +747,9 @@ def bench_verify(args):
     # per-token decode attention on the same steps (each row re-reads its pages)
     Kd = min(args.steps, 20)
     dec_ms, _ = timed(decode_fn, args.warmup, Kd)
+    # the verify kernel's algorithmic bytes over the child's steps 0 .. 3
+    alg0 = float(np.mean([int((lens[k] + n).sum()) * key_bytes + T * Hq * D * 2 for k in range(4)]))
+    traffic, traffic_detail = measure_traffic(args, seed, alg0, want="verify_range")
     cpu = None
     if not args.no_cpu:
         # every row of 4 of the 16 sequences (the 1st, 5th, 9th and 13th)
@@ -683,11 +783,8 @@ def bench_verify(args):
         "roofline": {"bound": "hbm", "kernel": "verify_range8_kernel<4> (E4M3 cache, no append)" if e4m3 else
                      "verify_range_kernel<4>", "achieved": round(kern_gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
-                     "avg_us": round(kern_avg_us, 2), "traffic": None,
-                     "traffic_profiled_constant": None if e4m3 else {
-                         "note": "quoted from the committed counter runs (seed 1), not measured by this run",
-                         "source": "profiles/verify_step_c5_batch16.md (rocprofv3 --pmc, copy-calibrated, seed 1)",
-                         "read_bytes": 5.502e9, "write_bytes": 17.9e6, "algorithmic_bytes": 5.48e9, "ratio": 1.007}},
+                     "avg_us": round(kern_avg_us, 2), "traffic": None if traffic is None else round(traffic),
+                     "traffic_detail": traffic_detail},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
