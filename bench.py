@@ -116,7 +116,10 @@ def measure_traffic(args, seed, algorithmic_bytes, want=None):
         files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
         if proc.returncode != 0 or not files:
             return None, {"error": f"rocprofv3 --pmc {ctr} run failed (exit {proc.returncode})"}
-        rows = [r for f in files for r in csv.DictReader(open(f)) if r["Counter_Name"] == ctr]
+        rows = []
+        for f in files:
+            with open(f, newline="") as fh:
+                rows += [r for r in csv.DictReader(fh) if r["Counter_Name"] == ctr]
         shutil.rmtree(out, ignore_errors=True)
         copies = sorted((float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]),
                         reverse=True)[:3]
