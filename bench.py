@@ -14,9 +14,14 @@ in GB/s (algorithmic bytes / measured step time); us_per_step and the
 fraction of the 8 TB/s peak ride along. `roofline` is for the dominant kernel
 (the key-range decode kernel), timed with HIP events on the launch stream.
 `cpu_baseline` times the oracle (a scalar C restatement) on the host.
-`roofline.traffic` stays null (a run does not read hardware counters);
-`roofline.traffic_profiled` quotes the committed rocprofv3 FETCH_SIZE /
-WRITE_SIZE runs of the same workload (seed 1, copy-calibrated).
+`roofline.traffic` is the dominant kernel's HBM bytes per launch, from two
+short child runs of the same workload under rocprofv3 --pmc (FETCH_SIZE,
+WRITE_SIZE), copy-calibrated (--no-traffic skips them).
+
+Other workloads: --config c2 (one sequence at 4096 context), c4 (chunked
+prefill over a shared prefix, TFLOP/s), c5 (speculative verify at 32k-128k
+context), attn (the reference's bench-attn: one prompt of --tokens tokens
+after --context cached keys, the prompt kernel alone).
 """
 import argparse
 import json
@@ -95,7 +100,8 @@ def measure_traffic(args, seed, algorithmic_bytes, want=None):
     child = [sys.executable, "-u", os.path.abspath(__file__), "--traffic-child", "--no-traffic", "--no-cpu",
              "--no-graph", "--steps", "3", "--warmup", "1", "--seed", str(seed), "--config", args.config,
              "--kv", args.kv, "--q-heads", str(args.q_heads), "--batch", str(args.batch), "--pages", str(args.pages),
-             "--prefix", str(args.prefix)]
+             "--prefix", str(args.prefix), "--tokens", str(args.tokens), "--context", str(args.context),
+             "--seqs", str(args.seqs)]
     for flag in ("unfused", "with_prep", "refabi", "verify_kernel"):
         if getattr(args, flag):
             child.append("--" + flag.replace("_", "-"))
@@ -153,11 +159,14 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--seed", type=int, default=None, help="length-mix seed (default: fresh per run)")
-    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5"],
+    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5", "attn"],
                     help="c3 (default, the metric): batch-64 decode step; c2: single-sequence decode at 4096 "
                          "context; c4: chunked prefill of 8 x 2048 tokens over a shared 16,384-token prefix; "
                          "c5: speculative verify of 4 drafts x 16 sequences at 32k..128k context")
     ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--tokens", type=int, default=4096, help="attn: prompt tokens per sequence")
+    ap.add_argument("--context", type=int, default=0, help="attn: cached keys before the prompt")
+    ap.add_argument("--seqs", type=int, default=1, help="attn: sequences")
     ap.add_argument("--prefix", type=int, default=16384,
                     help="c4: shared prefix tokens (a multiple of 64 reaches the sequences through the prefix cache; "
                          "otherwise shared pages with the partial last page copied on write)")
@@ -233,6 +242,8 @@ def main():
         return bench_prefill(args)
     if args.config == "c5":
         return bench_verify(args)
+    if args.config == "attn":
+        return bench_attn(args)
 
     if args.wg_per_cu or args.min_range:
         pkv.attn_decode_config(args.wg_per_cu or 1, args.min_range or 32)
@@ -788,6 +799,175 @@ def bench_verify(args):
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
                      "avg_us": round(kern_avg_us, 2), "traffic": None if traffic is None else round(traffic),
                      "traffic_detail": traffic_detail},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_attn(args):
+    """The reference's bench-attn (src/main.rs:721-955), restated: --seqs
+    sequences of --tokens prompt tokens after --context cached keys, 4 kv
+    heads, G = --q-heads / 4, head_dim 256, inputs from bench-attn's hash
+    (x = ((h % 2001) / 1000 - 1) * scale, h = (i ^ seed * 0x9e3779b9) *
+    2654435761 mod 2^64, main.rs:738-746), each sequence's pages in reverse
+    order (main.rs:755-763). Times the prompt kernel alone over 20 launches
+    by wall clock after one warm-up, as bench-attn does (main.rs:938-955),
+    for this library's pkv_attn_prefill and for the code object's kernel on
+    the engine's grid (fa_shape's choice on gfx950); FLOPs 4 x 256 x Hq x
+    attended keys. bench-attn --check's comparison with the decode kernel
+    (main.rs:843-938) runs on sampled rows."""
+    import numpy as np
+    import torch
+
+    import pkv
+    from pkv import refabi
+    from pkv.refabi import F, I, P as Pa
+
+    dev = torch.device("cuda:0")
+    D, BS, hkv = 256, 16, 4
+    G = args.q_heads // hkv
+    hq, seqs, tokens, context = G * hkv, args.seqs, args.tokens, args.context
+    qstride = (2 * hq + 2 * hkv) * D
+    t = seqs * tokens
+    mb = (context + tokens + BS - 1) // BS
+    slots = seqs * mb * BS
+    two64 = (1 << 64) % 2001
+
+    def rnd(n, seed, scale):
+        # bench-attn's hash in unsigned 64-bit arithmetic (int64 wraps alike;
+        # the remainder is corrected for the sign), in chunks on the device
+        out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        mul = torch.tensor(2654435761, dtype=torch.int64, device=dev)
+        sd = (seed * 0x9E3779B9) & ((1 << 63) - 1)
+        for a in range(0, n, 1 << 26):
+            i = torch.arange(a, min(n, a + (1 << 26)), dtype=torch.int64, device=dev)
+            h = torch.bitwise_xor(i, sd) * mul
+            r = torch.remainder(h, 2001)
+            r = torch.remainder(r + (h < 0).to(torch.int64) * two64, 2001)
+            out[a:a + len(i)] = ((r.to(torch.float32) / 1000.0 - 1.0) * scale).to(torch.bfloat16)
+        return out
+
+    q = rnd(t * hq * D, 1, 1.0).view(t, hq, D)
+    proj = rnd(t * qstride, 2, 1.0).view(t, qstride)
+    kc = rnd(slots * hkv * D, 3, 1.0).view(slots, hkv, D)
+    vc = rnd(slots * hkv * D, 4, 1.0).view(slots, hkv, D)
+    bt = np.array([[s * mb + mb - 1 - b for b in range(mb)] for s in range(seqs)], np.int32)
+    pos = np.array([context + i % tokens for i in range(t)], np.int32)
+    cu = np.arange(seqs + 1, dtype=np.int32) * tokens
+    bt_d, pos_d, cu_d = (torch.from_numpy(a).to(dev) for a in (bt, pos, cu))
+    out = torch.zeros(t, hq, D, dtype=torch.bfloat16, device=dev)
+    out_ref = torch.zeros_like(out)
+    scale = 1.0 / 16.0
+    flops = 4.0 * D * hq * seqs * float(sum(context + i + 1 for i in range(tokens)))
+
+    def lib():
+        pkv.attn_prefill(q, kc, vc, proj, qstride, hq, hkv, pos_d, cu_d, seqs, bt_d, mb, BS, out, scale, None, 1, t,
+                         seqs * mb)
+
+    rk = refabi.RefKernels()
+    fname, fgrid, fthreads, fsmem = refabi.flash_launch(t, seqs, hkv, g=G)
+    fargs = [Pa(q), Pa(kc), Pa(vc), Pa(None), Pa(None), Pa(proj), I(qstride), I(hq), I(hkv), Pa(pos_d), Pa(cu_d),
+             I(seqs), Pa(bt_d), I(mb), I(BS), Pa(out_ref), F(scale), Pa(None), I(1)]
+
+    def ref():
+        rk.launch(fname, fgrid, fthreads, fsmem, fargs)
+
+    def wall_us(fn, n=20):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e6
+
+    lib_us = min(wall_us(lib) for _ in range(3))
+    ref_us = min(wall_us(ref) for _ in range(3))
+    # the library kernel's own duration (events at its start and end)
+    kev = HipEvents(20)
+    for k in range(20):
+        pkv.time_next_prefill_kernel(*kev.pairs[k])
+        lib()
+    torch.cuda.synchronize()
+    kern_us = 1e3 * float(np.median(kev.elapsed_ms()))
+
+    # --check: decode attention of sampled rows (every 64th token of each
+    # sequence and its last) against the prompt kernels' rows
+    rows = np.array(sorted({s * tokens + j for s in range(seqs) for j in list(range(0, tokens, 64)) + [tokens - 1]}),
+                    np.int64)
+    rows_d = torch.from_numpy(rows).to(dev)
+    dq, dproj = q[rows_d].contiguous(), proj[rows_d].contiguous()
+    dseq = (rows // tokens).astype(np.int32)
+    dcu = np.searchsorted(dseq, np.arange(seqs + 1), side="left").astype(np.int32)
+    dout = torch.zeros(len(rows), hq, D, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(max(pkv.attn_decode_workspace(len(rows), hq), pkv.attn_verify_workspace(len(rows), hq)),
+                     dtype=torch.uint8, device=dev)
+    pkv.attn_decode(dq, kc, vc, dproj, qstride, hq, hkv, torch.from_numpy(pos[rows]).to(dev),
+                    torch.from_numpy(dseq).to(dev), bt_d, mb, BS, dout, scale, torch.from_numpy(dcu).to(dev), 0, None,
+                    1, len(rows), seqs * mb, ws)
+    torch.cuda.synchronize()
+    check = {}
+    for what, o in (("library", out), ("code object", out_ref)):
+        got, want = o[rows_d].float(), dout.float()
+        err = (got - want).abs()
+        check[what] = {"max_abs": round(float(err.max()), 6),
+                       "within_tolerance": bool((err <= 2e-3 + 1e-2 * want.abs()).all())}
+
+    # CPU baseline: the oracle's prompt attention on 8 groups of 2 rows spread
+    # over the prompt, scaled by FLOPs to the whole launch
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        (kc_h, vc_h), bt_h = _host_pages([kc, vc], bt, np.full(seqs, mb))
+        q_h, proj_h = _bits(q), _bits(proj)
+        items = [(s, np.array([s * tokens + j, s * tokens + j + 1]))
+                 for s in range(seqs) for j in np.linspace(0, tokens - 2, 8).astype(int)]
+
+        def run(it):
+            s, r = it
+            oracle.attn_prefill(np.ascontiguousarray(q_h[r]), kc_h, vc_h, np.ascontiguousarray(proj_h[r]), qstride,
+                                hq, hkv, pos[r], np.array([0, 2], np.int32), 1, np.ascontiguousarray(bt_h[s:s + 1]),
+                                mb, BS, scale)
+
+        rate1, rate_mt, nthr, detail = _cpu_rates(items, run, lambda it: 4.0 * D * hq * float(
+            (pos[it[1]].astype(np.int64) + 1).sum()))
+        cpu = {"value": round(flops / rate_mt * 1e6, 1), "unit": "us", "cores": nthr, "kind": "port",
+               "sample": f"oracle prompt attention of {len(items)} groups of 2 rows spread over the prompt, scaled "
+                         f"by FLOPs to the launch ({flops:.3e} FLOP); {detail}",
+               "single_thread_us": round(flops / rate1 * 1e6, 1), "cpu": _cpu_model()}
+
+    alg = seqs * (context + tokens) * hkv * D * 2 * 2 + 3 * t * hq * D * 2
+    traffic, traffic_detail = measure_traffic(args, 0, alg, want="prefill")
+    published = {(4, 4096, 0, 1): 1160.0}  # BASELINE.md: bench-attn prefill g4 4096 tokens, RTX 5090
+    base = published.get((G, tokens, context, seqs))
+    tf = flops / (kern_us * 1e-6) / 1e12
+    line = {
+        "metric": f"bench-attn prefill us (group {G}, {tokens} tokens after {context}, {seqs} seq), 1 MI355X",
+        "value": round(lib_us, 1),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": 20,
+        "warmup": 1,
+        "ms_per_step": round(lib_us * 1e-3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None if base is None else round(lib_us / base, 4),
+        "baseline_us": base,
+        "baseline_note": None if base is None else "RTX 5090 (scripts/perf/nvidia-geforce-rtx-5090.json:2)",
+        "tflops_wall": round(flops / (lib_us * 1e-6) / 1e12, 1),
+        "code_object": {"kernel": fname, "grid": list(fgrid), "threads": fthreads, "smem": fsmem,
+                        "us": round(ref_us, 1), "tflops": round(flops / (ref_us * 1e-6) / 1e12, 1),
+                        "vs_baseline": None if base is None else round(ref_us / base, 4)},
+        "dtype": "bf16",
+        "data": "synthetic (bench-attn's hash inputs, reversed block table)",
+        "config": {"workload": "bench-attn: prompt attention alone", "q_heads": hq, "kv_heads": hkv,
+                   "head_dim": D, "page": BS, "seqs": seqs, "tokens": tokens, "context": context,
+                   "flop_per_launch": flops, "parallelism": "single GPU"},
+        "check": {"rows": len(rows), "against": "pkv_attn_decode of the same rows", **check},
+        "roofline": {"bound": "mfma", "kernel": f"prefill_kernel<{G}> (events at its start and end)",
+                     "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4), "median_us": round(kern_us, 1),
+                     "traffic": None if traffic is None else round(traffic), "traffic_detail": traffic_detail},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
