@@ -242,19 +242,31 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
                                      pkv::prefill_e4m3_kernel<8>)
            : by_group<PrefillKernel>(G, pkv::prefill_kernel<1>, pkv::prefill_kernel<2>, pkv::prefill_kernel<4>,
                                      pkv::prefill_kernel<6>, pkv::prefill_kernel<8>);
-    const int bq = pkv::pf_lib_bq(G);
-    const int threads = pkv::pf_lib_threads(G);
-    const size_t smem = pkv::prefill_smem_bytes(pkv::PF_NST, threads);
+    int bq = pkv::pf_lib_bq(G);
+    int threads = pkv::pf_lib_threads(G);
+    size_t smem = pkv::prefill_smem_bytes(pkv::PF_NST, threads);
+    // Upper bound on query tiles: each prompt sequence rounds up once.
+    int tiles = (T + bq - 1) / bq + seqs;
+    // G = 6 / 8 with few query tiles (one prompt of a few thousand tokens):
+    // 16-query tiles, two workgroups per CU, balance the causal tiles better.
+    PrefillKernel kern_run = kern;
+    if (!f8 && G >= 6 && block_size >= 16 && (int64_t)tiles * Hkv < 4 * (int64_t)device_cus()) {
+        kern_run = G == 6 ? pkv::prefill_fine_kernel<6> : pkv::prefill_fine_kernel<8>;
+        bq = 16;
+        threads = pkv::pf_fine_threads(G);
+        smem = pkv::pf_fine_smem_bytes(G);
+        tiles = (T + bq - 1) / bq + seqs;
+    }
     // per process: the kernels' LDS above the 64 KiB default, once per kernel
     static std::mutex attr_mu;
     static std::set<const void*> attr_set;
     {
         std::lock_guard<std::mutex> lk(attr_mu);
-        if (!attr_set.count((const void*)kern)) {
+        if (!attr_set.count((const void*)kern_run)) {
             const int st = status_of(
-                hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+                hipFuncSetAttribute((const void*)kern_run, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
             if (st != PKV_OK) return st;
-            attr_set.insert((const void*)kern);
+            attr_set.insert((const void*)kern_run);
         }
     }
     pkv::PrefillParams p;
@@ -281,9 +293,7 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     p.vscale = vscale;
     hipEvent_t e0 = t_pf_start, e1 = t_pf_stop;
     t_pf_start = t_pf_stop = nullptr;
-    // Upper bound on query tiles: each prompt sequence rounds up once.
-    const int tiles = (T + bq - 1) / bq + seqs;
-    hipExtLaunchKernelGGL(kern, dim3(tiles, Hkv), dim3(threads), smem, (hipStream_t)stream, e0, e1, 0, p);
+    hipExtLaunchKernelGGL(kern_run, dim3(tiles, Hkv), dim3(threads), smem, (hipStream_t)stream, e0, e1, 0, p);
     return launch_status();
 }
 

@@ -122,6 +122,16 @@ constexpr int pf_lib_threads(int G) { return pf_threads(pf_lib_bq(G), pf_lib_nqb
 constexpr size_t prefill_smem_bytes(int nst = PF_NST, int threads = PF_THREADS) {
     return (size_t)nst * PF_STAGE * 2 + pf_ids_bytes(threads);
 }
+// V pairs 1,056 bytes apart (528 elements): two stages then take 67,072
+// bytes, so two workgroups share a CU (the code object's attn_groupr
+// kernels, and the library's fine-tile kernel below).
+constexpr int PF_VPAIR_TIGHT = 528;
+// The fine-tile prompt kernel (G = 6 or 8): 16-query tiles, a wave per 2
+// heads x 16 queries, two stages with tight V pairs.
+constexpr int pf_fine_threads(int G) { return pf_threads(16, 1, G); }
+constexpr size_t pf_fine_smem_bytes(int G) {
+    return (size_t)2 * pf_stage(PF_VPAIR_TIGHT) * 2 + pf_ids_bytes(pf_fine_threads(G));
+}
 
 // NP LDS DMA pairs from one uniform base: pair j reads 16 bytes per lane at
 // base + off[j] into LDS at m0 + j * lds_step (+ 16 x lane). The m0 writes
@@ -670,6 +680,17 @@ template <int G>
 __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
     prefill_body<G, pf_lib_bq(G), pf_lib_nqb(G)>(p, pf_smem);
+}
+
+// G = 6 or 8 with few query tiles (the library kernel's grid would not fill
+// two rounds of CUs, e.g. one prompt of a few thousand tokens): 16-query
+// tiles, two workgroups per CU, so twice the workgroups balance the causal
+// tiles over the CUs (one 4,096-token prompt at G = 6: 380 against 418 us).
+template <int G>
+__global__ void __launch_bounds__(pf_fine_threads(G), 2) prefill_fine_kernel(PrefillParams p) {
+    static_assert(G == 6 || G == 8, "two heads per wave");
+    extern __shared__ __align__(16) uint16_t pf_smem[];
+    prefill_body<G, 16, 1, false, 2, PF_VPAIR_TIGHT>(p, pf_smem);
 }
 
 // The same over an E4M3 cache (p.kscale / p.vscale set).

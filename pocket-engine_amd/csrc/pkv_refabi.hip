@@ -363,7 +363,7 @@ namespace pkv {
 // G = 6) and nothing is static, so two workgroups fit a CU at up to 256
 // VGPRs. attn_mfma (8 waves): two stages of the default layout and 8 rings
 // in static LDS (68,608 bytes beside the launch's 37,376 dynamic ones).
-constexpr int REF_VP32 = 528;  // V pair stride of the attn_groupr stages (elements)
+constexpr int REF_VP32 = PF_VPAIR_TIGHT;  // V pair stride of the attn_groupr stages (elements)
 
 // G heads per kv head, BQ queries per workgroup (16 x the name's tiles),
 // F8: E4M3 cache, VP: V pair stride of the NST stages, DYN: stages in the

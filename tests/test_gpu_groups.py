@@ -321,3 +321,28 @@ def test_groups_more_rows_than_a_block(dev, G, Hkv):
                                c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
     ok, err = close(run_decode8(c, k8, v8, ks, vs, dev, entry="verify"), want)
     assert ok, f"verify e4m3 max |diff| {err}"
+
+
+@pytest.mark.parametrize("G", [6, 8])
+def test_prefill_many_tiles_sampled_rows(dev, G):
+    """G = 6 / 8 prompts with enough query tiles for the library's
+    32-query kernel (9 prompts of 1,000 tokens: 291 tiles x 4 kv heads, at
+    least 4 x CUs; smaller grids take the 16-query kernel, which the cases
+    above cover), all rows computed, 2-row groups at 24 places checked
+    against the oracle."""
+    print(f"case prefill many tiles G={G}", flush=True)
+    from test_gpu_prefill import prefill_case
+    c = prefill_case([0] * 9, [1000] * 9, 4, 170 + G, G=G)
+    assert (c["T"] // 32 + c["seqs"]) * 4 >= 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    got, _ = _prefill(c, dev, "lib")
+    rng = np.random.default_rng(171 + G)
+    for _ in range(24):
+        s = int(rng.integers(0, 9))
+        j = int(rng.integers(0, 999))
+        rows = np.array([c["cu"][s] + j, c["cu"][s] + j + 1])
+        want = oracle.attn_prefill(np.ascontiguousarray(c["q"][rows]), c["kc"], c["vc"],
+                                   np.ascontiguousarray(c["qkv"][rows]), c["qstride"], c["Hq"], 4, c["pos"][rows],
+                                   np.array([0, 2], np.int32), 1, np.ascontiguousarray(c["bt"][s:s + 1]),
+                                   c["max_blocks"], BS, SCALE)
+        ok, err = close(got[rows], want)
+        assert ok, f"seq {s} rows {rows}: max |diff| {err}"
