@@ -114,7 +114,7 @@ def measure_traffic(args, seed, algorithmic_bytes, want=None):
         proc = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.DEVNULL,
                                 stderr=subprocess.DEVNULL, start_new_session=True)
         try:
-            proc.wait(timeout=300)
+            proc.wait(timeout=120)
         except subprocess.TimeoutExpired:
             os.killpg(proc.pid, signal.SIGKILL)  # the process group this call started
             proc.wait()
