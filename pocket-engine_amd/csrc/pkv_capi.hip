@@ -247,12 +247,18 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     size_t smem = pkv::prefill_smem_bytes(pkv::PF_NST, threads);
     // Upper bound on query tiles: each prompt sequence rounds up once.
     int tiles = (T + bq - 1) / bq + seqs;
-    // G = 6 / 8 with few query tiles (one prompt of a few thousand tokens):
-    // 16-query tiles, two workgroups per CU, balance the causal tiles better.
+    // Few query tiles (one prompt, or one sequence's chunk, of a few
+    // thousand tokens): the fine-tile kernel, half the queries per
+    // workgroup and two workgroups per CU, fills and balances the CUs.
+    // (G <= 4: when the 8-wave workgroups would not cover the CUs once;
+    // G = 6 / 8, whose workgroups hold 6 / 8 waves of fewer queries: below
+    // four rounds.)
     PrefillKernel kern_run = kern;
-    if (!f8 && G >= 6 && block_size >= 16 && (int64_t)tiles * Hkv < 4 * (int64_t)device_cus()) {
-        kern_run = G == 6 ? pkv::prefill_fine_kernel<6> : pkv::prefill_fine_kernel<8>;
-        bq = 16;
+    if (!f8 && block_size >= 16 && (int64_t)tiles * Hkv < (G >= 6 ? 4 : 1) * (int64_t)device_cus()) {
+        kern_run = by_group<PrefillKernel>(G, pkv::prefill_fine_kernel<1>, pkv::prefill_fine_kernel<2>,
+                                           pkv::prefill_fine_kernel<4>, pkv::prefill_fine_kernel<6>,
+                                           pkv::prefill_fine_kernel<8>);
+        bq = pkv::pf_fine_bq(G);
         threads = pkv::pf_fine_threads(G);
         smem = pkv::pf_fine_smem_bytes(G);
         tiles = (T + bq - 1) / bq + seqs;

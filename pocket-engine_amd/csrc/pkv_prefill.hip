@@ -126,9 +126,11 @@ constexpr size_t prefill_smem_bytes(int nst = PF_NST, int threads = PF_THREADS) 
 // bytes, so two workgroups share a CU (the code object's attn_groupr
 // kernels, and the library's fine-tile kernel below).
 constexpr int PF_VPAIR_TIGHT = 528;
-// The fine-tile prompt kernel (G = 6 or 8): 16-query tiles, a wave per 2
-// heads x 16 queries, two stages with tight V pairs.
-constexpr int pf_fine_threads(int G) { return pf_threads(16, 1, G); }
+// The fine-tile prompt kernel: 128 / G queries per workgroup for G <= 4
+// (4 waves of one head x 32 queries), 16 for G = 6 or 8 (a wave per 2
+// heads x 16 queries), two stages with tight V pairs: two workgroups per CU.
+constexpr int pf_fine_bq(int G) { return G >= 6 ? 16 : 128 / G; }
+constexpr int pf_fine_threads(int G) { return pf_threads(pf_fine_bq(G), 1, G); }
 constexpr size_t pf_fine_smem_bytes(int G) {
     return (size_t)2 * pf_stage(PF_VPAIR_TIGHT) * 2 + pf_ids_bytes(pf_fine_threads(G));
 }
@@ -682,15 +684,16 @@ __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_kernel(PrefillPa
     prefill_body<G, pf_lib_bq(G), pf_lib_nqb(G)>(p, pf_smem);
 }
 
-// G = 6 or 8 with few query tiles (the library kernel's grid would not fill
-// two rounds of CUs, e.g. one prompt of a few thousand tokens): 16-query
-// tiles, two workgroups per CU, so twice the workgroups balance the causal
-// tiles over the CUs (one 4,096-token prompt at G = 6: 380 against 418 us).
+// Few query tiles (the library kernel's grid would not fill four rounds of
+// CUs: one prompt, or one sequence's chunk, of a few thousand tokens): half
+// the queries per workgroup and two workgroups per CU, so more workgroups
+// share out the causal tiles and fill the CUs (a 2,048-token chunk after
+// 6,144 keys: 362 against 406 us at G = 4; a 4,096-token prompt at G = 6:
+// 383 against 405 us).
 template <int G>
 __global__ void __launch_bounds__(pf_fine_threads(G), 2) prefill_fine_kernel(PrefillParams p) {
-    static_assert(G == 6 || G == 8, "two heads per wave");
     extern __shared__ __align__(16) uint16_t pf_smem[];
-    prefill_body<G, 16, 1, false, 2, PF_VPAIR_TIGHT>(p, pf_smem);
+    prefill_body<G, pf_fine_bq(G), 1, false, 2, PF_VPAIR_TIGHT>(p, pf_smem);
 }
 
 // The same over an E4M3 cache (p.kscale / p.vscale set).
