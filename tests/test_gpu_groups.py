@@ -323,21 +323,23 @@ def test_groups_more_rows_than_a_block(dev, G, Hkv):
     assert ok, f"verify e4m3 max |diff| {err}"
 
 
-@pytest.mark.parametrize("G", [6, 8])
-def test_prefill_many_tiles_sampled_rows(dev, G):
-    """G = 6 / 8 prompts with enough query tiles for the library's
-    32-query kernel (9 prompts of 1,000 tokens: 291 tiles x 4 kv heads, at
-    least 4 x CUs; smaller grids take the 16-query kernel, which the cases
-    above cover), all rows computed, 2-row groups at 24 places checked
+@pytest.mark.parametrize("G,nseq", [(1, 16), (2, 16), (4, 9), (6, 9), (8, 9)])
+def test_prefill_many_tiles_sampled_rows(dev, G, nseq):
+    """Prompts with enough query tiles for the library's full-size kernel
+    (nseq prompts of 1,000 tokens: at least CUs workgroups for G <= 4, 4 x
+    CUs for G = 6 / 8; smaller grids take the fine-tile kernel, which the
+    cases above cover), all rows computed, 2-row groups at 24 places checked
     against the oracle."""
-    print(f"case prefill many tiles G={G}", flush=True)
+    print(f"case prefill many tiles G={G} seqs={nseq}", flush=True)
     from test_gpu_prefill import prefill_case
-    c = prefill_case([0] * 9, [1000] * 9, 4, 170 + G, G=G)
-    assert (c["T"] // 32 + c["seqs"]) * 4 >= 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    c = prefill_case([0] * nseq, [1000] * nseq, 4, 170 + G, G=G)
+    bq = 32 if G >= 6 else 256 // G
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert ((c["T"] + bq - 1) // bq + c["seqs"]) * 4 >= (4 if G >= 6 else 1) * cus
     got, _ = _prefill(c, dev, "lib")
     rng = np.random.default_rng(171 + G)
     for _ in range(24):
-        s = int(rng.integers(0, 9))
+        s = int(rng.integers(0, nseq))
         j = int(rng.integers(0, 999))
         rows = np.array([c["cu"][s] + j, c["cu"][s] + j + 1])
         want = oracle.attn_prefill(np.ascontiguousarray(c["q"][rows]), c["kc"], c["vc"],
