@@ -167,6 +167,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=4096, help="attn: prompt tokens per sequence")
     ap.add_argument("--context", type=int, default=0, help="attn: cached keys before the prompt")
     ap.add_argument("--seqs", type=int, default=1, help="attn: sequences")
+    ap.add_argument("--prefill-split", action="store_true",
+                    help="attn: the library through pkv_attn_prefill_split (keys split over workgroups when the "
+                         "grid has fewer workgroups than CUs, then a merge launch)")
     ap.add_argument("--prefix", type=int, default=16384,
                     help="c4: shared prefix tokens (a multiple of 64 reaches the sequences through the prefix cache; "
                          "otherwise shared pages with the partial last page copied on write)")
@@ -860,9 +863,12 @@ def bench_attn(args):
     scale = 1.0 / 16.0
     flops = 4.0 * D * hq * seqs * float(sum(context + i + 1 for i in range(tokens)))
 
+    ws_bytes = pkv.attn_prefill_workspace(t, hq, hkv, seqs) if args.prefill_split else 0
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev) if args.prefill_split else None
+
     def lib():
         pkv.attn_prefill(q, kc, vc, proj, qstride, hq, hkv, pos_d, cu_d, seqs, bt_d, mb, BS, out, scale, None, 1, t,
-                         seqs * mb)
+                         seqs * mb, workspace=ws)
 
     rk = refabi.RefKernels()
     fname, fgrid, fthreads, fsmem = refabi.flash_launch(t, seqs, hkv, g=G)
@@ -960,7 +966,9 @@ def bench_attn(args):
                         "vs_baseline": None if base is None else round(ref_us / base, 4)},
         "dtype": "bf16",
         "data": "synthetic (bench-attn's hash inputs, reversed block table)",
-        "config": {"workload": "bench-attn: prompt attention alone", "q_heads": hq, "kv_heads": hkv,
+        "config": {"workload": "bench-attn: prompt attention alone", "entry": ("pkv_attn_prefill_split ("
+                   f"{ws_bytes} workspace bytes)" if args.prefill_split else "pkv_attn_prefill"), "q_heads": hq,
+                   "kv_heads": hkv,
                    "head_dim": D, "page": BS, "seqs": seqs, "tokens": tokens, "context": context,
                    "flop_per_launch": flops, "parallelism": "single GPU"},
         "check": {"rows": len(rows), "against": "pkv_attn_decode of the same rows", **check},

@@ -288,6 +288,24 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
                      int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec, int T,
                      int64_t num_blocks, void* stream);
 
+/* The same with a workspace, for grids with fewer workgroups than CUs (one
+ * sequence's prompt chunk of a few thousand tokens, above all after a long
+ * context): each query tile's keys are split over up to 16 workgroups, which
+ * leave (max, sum, weighted values) records in the workspace, and a second
+ * launch folds them into the gated rows (the split-K decode's merge,
+ * reference attn_merge qwen35.cu:2242-2279). No counterpart in the
+ * reference's prompt kernels (attn_mfma / attn_flash_group have no split).
+ * pkv_attn_prefill_workspace gives the bytes for these shapes (0 when the
+ * grid covers the CUs: the call then runs as pkv_attn_prefill and reads no
+ * workspace). bf16 cache, pages of 16 keys or more (otherwise as
+ * pkv_attn_prefill); results within the attention tolerance of it (only the
+ * points where P is rounded differ). */
+int pkv_attn_prefill_workspace(int T, int Hq, int Hkv, int seqs, size_t* bytes);
+int pkv_attn_prefill_split(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
+                           int Hkv, const int32_t* pos, const int32_t* cu, int seqs, const int32_t* block_table,
+                           int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec,
+                           int T, int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Chunked-prefill attention over an E4M3 cache: the reference's
  * attn_group8_g<G> (src/kernels/qwen35.cu:1364-1585 with F8, selected for
  * st.kv_fp8 at src/model.rs:2441-2446): the arguments of pkv_attn_prefill

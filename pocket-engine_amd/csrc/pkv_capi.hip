@@ -219,10 +219,37 @@ int pkv_attn_prep(const void* qkv, int qstride, int Hq, int Hkv, const float* q_
 
 namespace {
 
+// Key ranges per query tile for pkv_attn_prefill_split: 1 when the library
+// kernel's grid (w <= T / BQ + seqs tiles per kv head) covers the CUs, else
+// as many as fit the CUs in one round (floor(CUs / w): a chunk's tiles are
+// near equal after a long context, so a second round would cost a whole
+// range), at least 2 and at most 16.
+int prefill_nsplit(int T, int G, int Hkv, int seqs) {
+    const int bq = pkv::pf_lib_bq(G);
+    const int64_t w = ((int64_t)(T + bq - 1) / bq + seqs) * Hkv, cus = device_cus();
+    if (w <= 0 || w >= cus) return 1;
+    return (int)std::max<int64_t>(2, std::min<int64_t>(16, cus / w));
+}
+
+// Workspace of pkv_attn_prefill_split: records [(row * Hq + head) * nsplit
+// + range] of (max, sum) then 256 weighted values, f32.
+struct PrefillSplitLayout {
+    size_t ms, acc, total;
+};
+PrefillSplitLayout prefill_split_layout(int T, int Hq, int nsplit) {
+    const size_t recs = (size_t)T * Hq * nsplit;
+    PrefillSplitLayout l;
+    l.ms = 0;
+    l.acc = round_up(recs * 2 * 4, 256);
+    l.total = nsplit > 1 ? l.acc + recs * pkv::HEAD_DIM * 4 : 0;
+    return l;
+}
+
 int attn_prefill(const void* q, const void* kcache, const void* vcache, const float* kscale, const float* vscale,
                  const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos, const int32_t* cu, int seqs,
                  const int32_t* block_table, int max_blocks, int block_size, void* out, float scale,
-                 const int32_t* outs, int spec, int T, int64_t num_blocks, void* stream) {
+                 const int32_t* outs, int spec, int T, int64_t num_blocks, void* stream, void* workspace = nullptr,
+                 size_t workspace_bytes = 0) {
     if (T < 0 || seqs < 0 || Hq <= 0 || Hkv <= 0 || max_blocks <= 0 || block_size <= 0 || num_blocks <= 0 ||
         spec < 1)
         return PKV_ERR_INVALID;
@@ -235,6 +262,7 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
         return PKV_ERR_INVALID;
     const bool f8 = kscale != nullptr;
     if (f8 && (!vscale || !aligned(kscale, 4) || !aligned(vscale, 4))) return PKV_ERR_INVALID;
+    if (workspace && !aligned(workspace, 256)) return PKV_ERR_INVALID;
     using PrefillKernel = void (*)(pkv::PrefillParams);
     const PrefillKernel kern =
         f8 ? by_group<PrefillKernel>(G, pkv::prefill_e4m3_kernel<1>, pkv::prefill_e4m3_kernel<2>,
@@ -254,7 +282,15 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     // G = 6 / 8, whose workgroups hold 6 / 8 waves of fewer queries: below
     // four rounds.)
     PrefillKernel kern_run = kern;
-    if (!f8 && block_size >= 16 && (int64_t)tiles * Hkv < (G >= 6 ? 4 : 1) * (int64_t)device_cus()) {
+    // With a workspace and fewer workgroups than CUs: split every query
+    // tile's keys over nsplit workgroups, then merge (bf16, 16-key pages).
+    const int nsplit = workspace && !f8 && block_size >= 16 ? prefill_nsplit(T, G, Hkv, seqs) : 1;
+    if (nsplit > 1) {
+        if (workspace_bytes < prefill_split_layout(T, Hq, nsplit).total) return PKV_ERR_INVALID;
+        kern_run = by_group<PrefillKernel>(G, pkv::prefill_split_kernel<1>, pkv::prefill_split_kernel<2>,
+                                           pkv::prefill_split_kernel<4>, pkv::prefill_split_kernel<6>,
+                                           pkv::prefill_split_kernel<8>);
+    } else if (!f8 && block_size >= 16 && (int64_t)tiles * Hkv < (G >= 6 ? 4 : 1) * (int64_t)device_cus()) {
         kern_run = by_group<PrefillKernel>(G, pkv::prefill_fine_kernel<1>, pkv::prefill_fine_kernel<2>,
                                            pkv::prefill_fine_kernel<4>, pkv::prefill_fine_kernel<6>,
                                            pkv::prefill_fine_kernel<8>);
@@ -297,9 +333,27 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     p.num_blocks = (long)num_blocks;
     p.kscale = kscale;
     p.vscale = vscale;
+    p.nsplit = nsplit;
+    if (nsplit > 1) {
+        const PrefillSplitLayout lay = prefill_split_layout(T, Hq, nsplit);
+        p.part_ms = (float*)((char*)workspace + lay.ms);
+        p.part_acc = (float*)((char*)workspace + lay.acc);
+    } else {
+        p.part_ms = p.part_acc = nullptr;
+    }
     hipEvent_t e0 = t_pf_start, e1 = t_pf_stop;
     t_pf_start = t_pf_stop = nullptr;
-    hipExtLaunchKernelGGL(kern_run, dim3(tiles, Hkv), dim3(threads), smem, (hipStream_t)stream, e0, e1, 0, p);
+    hipExtLaunchKernelGGL(kern_run, dim3(tiles, Hkv, nsplit), dim3(threads), smem, (hipStream_t)stream, e0, e1, 0,
+                          p);
+    if (nsplit > 1) {
+        int st = launch_status();
+        if (st != PKV_OK) return st;
+        using MergeKernel = void (*)(pkv::PrefillParams);
+        const MergeKernel mk = by_group<MergeKernel>(G, pkv::prefill_merge_kernel<1>, pkv::prefill_merge_kernel<2>,
+                                                     pkv::prefill_merge_kernel<4>, pkv::prefill_merge_kernel<6>,
+                                                     pkv::prefill_merge_kernel<8>);
+        hipLaunchKernelGGL(mk, dim3(T, Hkv), dim3(64 * G), 0, (hipStream_t)stream, p);
+    }
     return launch_status();
 }
 
@@ -313,6 +367,21 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
                      int64_t num_blocks, void* stream) {
     return attn_prefill(q, kcache, vcache, nullptr, nullptr, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
                         max_blocks, block_size, out, scale, outs, spec, T, num_blocks, stream);
+}
+
+int pkv_attn_prefill_workspace(int T, int Hq, int Hkv, int seqs, size_t* bytes) {
+    if (T < 0 || Hq <= 0 || Hkv <= 0 || seqs < 0 || Hq % Hkv != 0 || !bytes) return PKV_ERR_INVALID;
+    *bytes = prefill_split_layout(T, Hq, prefill_nsplit(T, Hq / Hkv, Hkv, seqs)).total;
+    return PKV_OK;
+}
+
+int pkv_attn_prefill_split(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
+                           int Hkv, const int32_t* pos, const int32_t* cu, int seqs, const int32_t* block_table,
+                           int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec,
+                           int T, int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream) {
+    return attn_prefill(q, kcache, vcache, nullptr, nullptr, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
+                        max_blocks, block_size, out, scale, outs, spec, T, num_blocks, stream, workspace,
+                        workspace_bytes);
 }
 
 int pkv_attn_prefill_e4m3(const void* q, const void* kcache, const void* vcache, const float* kscale,

@@ -145,7 +145,9 @@ __device__ __forceinline__ void merge_rows(int n, float mscale, MsAt ms_at, AccA
                                            int K = 0) {
     constexpr int U = NW >= 16 ? 10 : 16;
     __shared__ __align__(16) float sh_a[NW][HEAD_DIM + 4];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, d = 4 * lane;
+    // NW = 1: the calling wave alone (other waves of the block may merge
+    // other rows)
+    const int tid = threadIdx.x, lane = tid & 63, w = NW == 1 ? 0 : tid >> 6, d = 4 * lane;
     float M = -INFINITY, S = 0.f, A0 = 0.f, A1 = 0.f, A2 = 0.f, A3 = 0.f;
     for (int i0 = w; i0 < n; i0 += NW * U) {
         float2 mu[U];

@@ -27,6 +27,7 @@
 // while the current one is multiplied (double-buffered LDS).
 #pragma once
 #include "pkv_common.h"
+#include "pkv_decode.hip"
 
 namespace pkv {
 
@@ -50,6 +51,13 @@ struct PrefillParams {
     // per (slot, kv head)
     const float* kscale;
     const float* vscale;
+    // Split keys (prefill_split_kernel): nsplit ranges per query tile, and
+    // their records: (max in log2 units, sum) at part_ms[r * 2] and the
+    // unnormalised weighted values at part_acc[r * 256], r = (row * Hq +
+    // head) * nsplit + range
+    int nsplit;
+    float* part_ms;
+    float* part_acc;
 };
 
 // 16 bytes at byte offset `off` of `base` (a uniform address) by a raw
@@ -213,8 +221,14 @@ __device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s
 // THREADS / 32 keys. F8: an E4M3 cache, dequantised while
 // the tiles load as the reference's attn_group8 does (qwen35.cu:1424-1436):
 // K' = bf16(k * kscale), V' = bf16(v * vscale); the rest is unchanged.
-template <int G, int BQ, int NQB, bool F8, bool UPAGE, int NST, bool DMA, int VP = PF_VPAIR>
+//
+// SPL: this workgroup takes key range blockIdx.z of p.nsplit (ceil(n /
+// nsplit) of the tile's n key tiles each; an empty range returns at once)
+// and leaves a record per (row, query head) for prefill_merge_kernel
+// instead of the gated rows.
+template <int G, int BQ, int NQB, bool F8, bool UPAGE, int NST, bool DMA, int VP = PF_VPAIR, bool SPL = false>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb) {
+    static_assert(!SPL || DMA, "split ranges: the DMA path");
     constexpr int THREADS = pf_threads(BQ, NQB, G);
     // BQ = 16: a wave's 32 columns are 2 heads x 16 queries
     constexpr bool PAIRED = BQ < 32;
@@ -405,7 +419,14 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     // 4 (s % 4) (row 16 kk + x sits at pf_vrow(x) + 256 kk).
     const int tr_at = (4 * lh + ((lane & 15) >> 2)) * VP + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-    const int ntiles = (L + PF_BK - 1) / PF_BK;
+    // The key tiles this workgroup streams: [kbase, kbase + ntiles * 32).
+    int ntiles = (L + PF_BK - 1) / PF_BK, kbase = 0;
+    if constexpr (SPL) {
+        const int per = (ntiles + p.nsplit - 1) / p.nsplit, t0 = (int)blockIdx.z * per;
+        ntiles = min(ntiles, t0 + per) - t0;
+        kbase = t0 * PF_BK;
+        if (ntiles <= 0) return;  // whole workgroup: nothing to merge from this range
+    }
     // Tile k0 from stage buf: S^T, online softmax, O^T update.
     auto compute = [&](int buf, int k0) __attribute__((always_inline)) {
         if (k0 <= last) {
@@ -546,20 +567,20 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         };
 #pragma unroll
         for (int t = 0; t < 4; t++)
-            if (t < ntiles) dma_ids(t * PF_BK, t);
+            if (t < ntiles) dma_ids(kbase + t * PF_BK, t);
         wait_vm<0>();
-        dma_tile(0, 0, 0);
+        dma_tile(kbase, 0, 0);
         if constexpr (NST == 2) {
             // Two stages: iteration i requests tile i + 1 into the stage the
             // barrier that ended iteration i - 1 freed (and the page ids of
             // tile i + 4), computes tile i, waits for its own DMA of tile
             // i + 1, then one barrier publishes it: one tile of lead.
             wait_vm<0>();
-            zero_tail(0, 0);
+            zero_tail(kbase, 0);
             __syncthreads();
             int buf = 0;
             for (int it = 0; it < ntiles; it++) {
-                const int k0 = it * PF_BK;
+                const int k0 = kbase + it * PF_BK;
                 const bool more1 = it + 1 < ntiles, more4 = it + 4 < ntiles;
                 if (more1) dma_tile(k0 + PF_BK, buf ^ 1, (it + 1) & 3);
                 if (more4) dma_ids(k0 + 4 * PF_BK, it & 3);
@@ -574,16 +595,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             }
         } else {
         if (ntiles > 1) {
-            dma_tile(PF_BK, 1, 1);
+            dma_tile(kbase + PF_BK, 1, 1);
             wait_vm<2 * NPW>();
         } else {
             wait_vm<0>();
         }
-        zero_tail(0, 0);
+        zero_tail(kbase, 0);
         __syncthreads();
         int buf = 0;
         for (int it = 0; it < ntiles; it++) {
-            const int k0 = it * PF_BK;
+            const int k0 = kbase + it * PF_BK;
             const bool more2 = it + 2 < ntiles, more4 = it + 4 < ntiles;
             if (more2) dma_tile(k0 + 2 * PF_BK, buf == 0 ? 2 : buf - 1, (it + 2) & 3);
             if (more4) dma_ids(k0 + 4 * PF_BK, it & 3);
@@ -636,6 +657,25 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             buf ^= 1;
         }
     }
+    }
+    if constexpr (SPL) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; qb++) {
+            const int myq = qcol(qb);
+            if (myq >= nb) continue;
+            const size_t r = (((size_t)tb + myq) * p.Hq + h) * p.nsplit + blockIdx.z;
+            float* acc = p.part_acc + r * HEAD_DIM;
+#pragma unroll
+            for (int db = 0; db < 8; db++)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const f32x16& oo = o[qb][db];
+                    *reinterpret_cast<float4*>(acc + 32 * db + 8 * g4 + 4 * lh) =
+                        make_float4(oo[4 * g4], oo[4 * g4 + 1], oo[4 * g4 + 2], oo[4 * g4 + 3]);
+                }
+            if (lh == 0) *reinterpret_cast<float2*>(p.part_ms + r * 2) = make_float2(m[qb], l[qb]);
+        }
+        return;
     }
 #pragma unroll
     for (int qb = 0; qb < NQB; qb++) {
@@ -694,6 +734,45 @@ template <int G>
 __global__ void __launch_bounds__(pf_fine_threads(G), 2) prefill_fine_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
     prefill_body<G, pf_fine_bq(G), 1, false, 2, PF_VPAIR_TIGHT>(p, pf_smem);
+}
+
+// Split keys (pkv_attn_prefill_split, grids with fewer workgroups than CUs,
+// e.g. one sequence's chunk after a long context): grid (query tiles, kv
+// heads, p.nsplit), each workgroup the library kernel's tile over one range
+// of its keys, leaving records; prefill_merge_kernel combines them.
+template <int G>
+__global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_split_kernel(PrefillParams p) {
+    extern __shared__ __align__(16) uint16_t pf_smem[];
+    constexpr int BQ = pf_lib_bq(G);
+    int s, tb, nb;
+    if (!find_prefill_tile<BQ>(p, s, tb, nb) || p.bs_log2 < 4) return;  // 16-key pages or more (host-checked)
+    prefill_tile<G, BQ, pf_lib_nqb(G), false, true, PF_NST, true, PF_VPAIR, true>(p, pf_smem, s, tb, nb);
+}
+
+// Combines the key ranges of prefill_split_kernel: grid (rows, kv heads),
+// a wave per query head of the group; row t of a prompt sequence folds its
+// query tile's non-empty ranges (the decode merge's arithmetic, gated
+// output); other rows are left untouched.
+template <int G>
+__global__ void __launch_bounds__(64 * G) prefill_merge_kernel(PrefillParams p) {
+    constexpr int BQ = pf_lib_bq(G);
+    const int t = blockIdx.x, h = blockIdx.y * G + (threadIdx.x >> 6);
+    // the sequence holding row t: the last s with cu[s] <= t
+    int lo = 0, hi = p.seqs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (p.cu[mid] <= t) lo = mid;
+        else hi = mid - 1;
+    }
+    const int c0 = p.cu[lo], n = p.cu[lo + 1] - c0;
+    if (t < c0 || t >= c0 + n || n <= 1 || is_spec(p.outs, p.spec, lo)) return;
+    const int tb = c0 + (t - c0) / BQ * BQ, nb = min(BQ, c0 + n - tb);
+    const int nt = (p.pos[tb] + nb + PF_BK - 1) / PF_BK, per = (nt + p.nsplit - 1) / p.nsplit;
+    const size_t r0 = ((size_t)t * p.Hq + h) * p.nsplit;
+    merge_rows<1>(
+        (nt + per - 1) / per, 1.f, [&](int z) { return p.part_ms + (r0 + z) * 2; },
+        [&](int z) { return p.part_acc + (r0 + z) * HEAD_DIM; },
+        p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM, p.out + ((size_t)t * p.Hq + h) * HEAD_DIM);
 }
 
 // The same over an E4M3 cache (p.kscale / p.vscale set).

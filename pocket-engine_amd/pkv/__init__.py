@@ -50,6 +50,9 @@ _SIGS = {
     "pkv_time_next_prefill_kernel": (_c_int, [_c_p, _c_p]),
     "pkv_attn_prefill": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_int, _c_p, _c_int,
                                   _c_int, _c_p, _c_f, _c_p, _c_int, _c_int, _c_i64, _c_p]),
+    "pkv_attn_prefill_workspace": (_c_int, [_c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
+    "pkv_attn_prefill_split": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_int, _c_p,
+                                        _c_int, _c_int, _c_p, _c_f, _c_p, _c_int, _c_int, _c_i64, _c_p, _c_sz, _c_p]),
     "pkv_attn_decode_step": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p,
                                       _c_p, _c_p, _c_int, _c_int, _c_p, _c_f, _c_p, _c_int, _c_p, _c_int, _c_int,
                                       _c_i64, _c_p, _c_sz, _c_p]),
@@ -301,11 +304,26 @@ def attn_prefill_e4m3(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, 
 
 
 def attn_prefill(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks, block_size, out,
-                 scale, outs, spec, T, num_blocks, stream=None):
-    """Causal chunked-prefill attention over paged context (MFMA bf16)."""
+                 scale, outs, spec, T, num_blocks, stream=None, workspace=None):
+    """Causal chunked-prefill attention over paged context (MFMA bf16);
+    with a workspace (attn_prefill_workspace bytes), pkv_attn_prefill_split."""
+    if workspace is not None:
+        _check(_lib.pkv_attn_prefill_split(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(qkv), qstride, Hq, Hkv,
+                                           _ptr(pos), _ptr(cu), seqs, _ptr(block_table), max_blocks, block_size,
+                                           _ptr(out), scale, _ptr(outs), spec, T, num_blocks, _ptr(workspace),
+                                           workspace.numel() * workspace.element_size(), _stream(stream)),
+               "pkv_attn_prefill_split")
+        return
     _check(_lib.pkv_attn_prefill(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(qkv), qstride, Hq, Hkv, _ptr(pos),
                                  _ptr(cu), seqs, _ptr(block_table), max_blocks, block_size, _ptr(out), scale,
                                  _ptr(outs), spec, T, num_blocks, _stream(stream)), "pkv_attn_prefill")
+
+
+def attn_prefill_workspace(T, Hq, Hkv, seqs):
+    """Workspace bytes of pkv_attn_prefill_split (0: no split for these shapes)."""
+    n = _c_sz(0)
+    _check(_lib.pkv_attn_prefill_workspace(T, Hq, Hkv, seqs, ctypes.byref(n)), "pkv_attn_prefill_workspace")
+    return n.value
 
 
 class Pool:

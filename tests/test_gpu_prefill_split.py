@@ -1,0 +1,100 @@
+"""pkv_attn_prefill_split: prompt attention with each query tile's keys split
+over several workgroups when the grid has fewer workgroups than CUs, then a
+merge launch. Against the oracle within the attention tolerance (|got -
+want| <= 2e-3 + 1e-2 |want|); rows outside the prompts stay untouched; a
+grid that covers the CUs (no split) gives pkv_attn_prefill's bytes."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import pkv
+from _util import BS, close
+from test_gpu_prefill import i16, i32, prefill_case
+
+pytestmark = pytest.mark.gpu
+SCALE = 1.0 / 16.0
+
+
+def run_split(c, dev, workspace=True, init=0x3333):
+    T, Hq, Hkv = c["T"], c["Hq"], c["Hkv"]
+    out = torch.from_numpy(np.full((T, Hq, 256), init, np.uint16).view(np.int16)).to(dev)
+    nbytes = pkv.attn_prefill_workspace(T, Hq, Hkv, c["seqs"])
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev) if workspace else None
+    pkv.attn_prefill(i16(c["q"], dev), i16(c["kc"], dev), i16(c["vc"], dev), i16(c["qkv"], dev), c["qstride"], Hq,
+                     Hkv, i32(c["pos"], dev), i32(c["cu"], dev), c["seqs"], i32(c["bt"], dev), c["max_blocks"], BS,
+                     out, SCALE, None, 1, T, c["pages"], workspace=ws)
+    torch.cuda.synchronize()
+    return out.cpu().numpy().view(np.uint16), nbytes
+
+
+def want_of(c, init=0x3333):
+    return oracle.attn_prefill(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], c["Hq"], c["Hkv"], c["pos"], c["cu"],
+                               c["seqs"], c["bt"], c["max_blocks"], BS, SCALE,
+                               out=np.full((c["T"], c["Hq"], 256), init, np.uint16))
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 6, 8])
+@pytest.mark.parametrize("ctxs,chunks,seed", [
+    ([2000], [300], 0),             # one chunk after a long context: 8 ranges per tile
+    ([0], [700], 1),                # one prompt, causal tiles of every length
+    ([100, 3000, 0], [70, 130, 33], 2),  # three chunks, ranges ending mid-tile
+])
+def test_split_prefill_matches_oracle(dev, G, ctxs, chunks, seed):
+    print(f"case prefill split G={G} ctx={ctxs} chunk={chunks}", flush=True)
+    c = prefill_case(ctxs, chunks, 4, 200 + seed, decode_rows=1, G=G)
+    got, nbytes = run_split(c, dev)
+    assert nbytes > 0, "these shapes must split"
+    assert (got[0] == 0x3333).all()  # the decode row is left to decode attention
+    ok, err = close(got, want_of(c))
+    assert ok, f"max |diff| {err}"
+
+
+def test_split_prefill_skips_spec_sequences(dev):
+    """A verifying sequence (outs >= 0) is left to decode attention, as in
+    pkv_attn_prefill (qwen35.cu:94-100)."""
+    print("case prefill split spec rows", flush=True)
+    c = prefill_case([500, 40], [90, 4], 4, 230, G=4)
+    T, Hq = c["T"], c["Hq"]
+    out = torch.from_numpy(np.full((T, Hq, 256), 0x3333, np.uint16).view(np.int16)).to(dev)
+    ws = torch.empty(pkv.attn_prefill_workspace(T, Hq, 4, c["seqs"]), dtype=torch.uint8, device=dev)
+    outs = np.full(2 * 4, -1, np.int32)  # [seqs][spec]: sequence 1 verifies drafts
+    outs[4] = 0
+    pkv.attn_prefill(i16(c["q"], dev), i16(c["kc"], dev), i16(c["vc"], dev), i16(c["qkv"], dev), c["qstride"], Hq, 4,
+                     i32(c["pos"], dev), i32(c["cu"], dev), c["seqs"], i32(c["bt"], dev), c["max_blocks"], BS, out,
+                     SCALE, i32(outs, dev), 4, T, c["pages"], workspace=ws)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    assert (got[90:] == 0x3333).all()
+    want = oracle.attn_prefill(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], Hq, 4, c["pos"], c["cu"],
+                               c["seqs"], c["bt"], c["max_blocks"], BS, SCALE, outs=outs, spec=4,
+                               out=np.full((T, Hq, 256), 0x3333, np.uint16))
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
+
+
+def test_split_prefill_rejects_a_short_workspace(dev):
+    print("case prefill split short workspace", flush=True)
+    c = prefill_case([2000], [300], 4, 240, G=4)
+    T, Hq = c["T"], c["Hq"]
+    need = pkv.attn_prefill_workspace(T, Hq, 4, c["seqs"])
+    ws = torch.empty(need - 256, dtype=torch.uint8, device=dev)
+    out = torch.zeros(T, Hq, 256, dtype=torch.int16, device=dev)
+    with pytest.raises(pkv.PkvError) as e:
+        pkv.attn_prefill(i16(c["q"], dev), i16(c["kc"], dev), i16(c["vc"], dev), i16(c["qkv"], dev), c["qstride"],
+                         Hq, 4, i32(c["pos"], dev), i32(c["cu"], dev), c["seqs"], i32(c["bt"], dev), c["max_blocks"],
+                         BS, out, SCALE, None, 1, T, c["pages"], workspace=ws)
+    assert e.value.status == pkv.ERR_INVALID
+
+
+def test_split_prefill_without_a_split_is_prefill(dev):
+    """A grid that covers the CUs needs no workspace (0 bytes) and gives the
+    bytes of pkv_attn_prefill."""
+    print("case prefill split none", flush=True)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    n = (cus // 4 + 8) * 64  # query tiles x 4 kv heads >= CUs
+    c = prefill_case([0], [n], 4, 250, G=4)
+    assert pkv.attn_prefill_workspace(c["T"], c["Hq"], 4, c["seqs"]) == 0
+    got, _ = run_split(c, dev)
+    plain, _ = run_split(c, dev, workspace=False)
+    assert np.array_equal(got, plain)
