@@ -1,6 +1,7 @@
 """Seeded random sweep over the attention entry points: each case draws an
 entry point (decode, verify, their E4M3 forms, the fused step, prompts
-through the library and through the code object, bf16 and E4M3), a query-
+through the library (also with split keys) and through the code object,
+bf16 and E4M3), a query-
 head group G in {1, 2, 4, 6, 8}, a kv-head count, ragged lengths and a key-
 range size, and compares the GPU result with the oracle within the north
 star's tolerance (|got - want| <= 2e-3 + 1e-2 |want|; appended cache rows
@@ -22,7 +23,8 @@ from test_gpu_verify import run_oracle as run_oracle_v, run_verify, verify_case
 
 pytestmark = pytest.mark.gpu
 SCALE = 1.0 / 16.0
-KINDS = ["decode", "verify", "decode8", "verify8", "step", "prefill", "prefill8", "prefill_ref", "prefill8_ref"]
+KINDS = ["decode", "verify", "decode8", "verify8", "step", "prefill", "prefill8", "prefill_ref", "prefill8_ref",
+         "prefill_split"]
 
 
 @pytest.fixture(autouse=True)
@@ -54,7 +56,7 @@ def e4m3_of(c, rng, amp):
     return k8, v8, ks, vs
 
 
-@pytest.mark.parametrize("seed", range(40))
+@pytest.mark.parametrize("seed", range(50))
 def test_random_case_matches_oracle(dev, seed):
     rng, kind, G, Hkv, min_range, lens = draw(seed)
     print(f"case sweep seed={seed} kind={kind} G={G} Hkv={Hkv} min_range={min_range} lens={lens[:8]}"
@@ -91,7 +93,11 @@ def test_random_case_matches_oracle(dev, seed):
         chunks = [int(x) for x in rng.integers(1, 160, n)]
         c = prefill_case(ctxs, chunks, Hkv, seed, decode_rows=1, G=G)
         entry = "ref" if kind.endswith("_ref") else "lib"
-        if kind.startswith("prefill8"):
+        if kind == "prefill_split":
+            from test_gpu_prefill_split import run_split, want_of
+            got, _ = run_split(c, dev)
+            want = want_of(c)
+        elif kind.startswith("prefill8"):
             f8 = e4m3_of(c, rng, 0.004)
             got, init = _prefill(c, dev, entry, f8=f8)
             want = oracle.attn_prefill8(c["q"], f8[0], f8[1], f8[2], f8[3], c["qkv"], c["qstride"], c["Hq"], Hkv,
