@@ -98,3 +98,39 @@ def test_split_prefill_without_a_split_is_prefill(dev):
     got, _ = run_split(c, dev)
     plain, _ = run_split(c, dev, workspace=False)
     assert np.array_equal(got, plain)
+
+
+def test_split_prefill_graph_replay_matches_eager(dev):
+    """The split kernel and its merge captured into a HIP graph and replayed
+    3 times (eager launches and synchronizations between) give the eager
+    bytes each time."""
+    print("case prefill split graph replay", flush=True)
+    c = prefill_case([1500], [200], 4, 260, G=4)
+    T, Hq = c["T"], c["Hq"]
+    args = [i16(c[k], dev) for k in ("q", "kc", "vc", "qkv")]
+    pos, cu, bt = i32(c["pos"], dev), i32(c["cu"], dev), i32(c["bt"], dev)
+    ws = torch.empty(pkv.attn_prefill_workspace(T, Hq, 4, c["seqs"]), dtype=torch.uint8, device=dev)
+    out = torch.zeros(T, Hq, 256, dtype=torch.int16, device=dev)
+
+    def launch():
+        pkv.attn_prefill(*args, c["qstride"], Hq, 4, pos, cu, c["seqs"], bt, c["max_blocks"], BS, out, SCALE, None,
+                         1, T, c["pages"], workspace=ws)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        launch()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = out.cpu().numpy().copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch()
+    for r in range(3):
+        if r % 2:
+            launch()
+            torch.cuda.synchronize()
+        out.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager), f"replay {r}"
