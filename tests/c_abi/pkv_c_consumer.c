@@ -16,7 +16,9 @@
  *     4. the decode output equals the last row of pkv_attn_prefill over the
  *        prompt plus that token (same keys) within the attention tolerance
  *        |got - want| <= 2e-3 + 1e-2 |want| — the reference's decode-vs-
- *        prefill check (bench-attn --check, src/main.rs:843-938).
+ *        prefill check (bench-attn --check, src/main.rs:843-938);
+ *     5. pkv_attn_prefill_split over the same prompts matches it within the
+ *        same tolerance.
  * Prints one line per check and "ok" at the end; exits non-zero on failure.
  */
 #include <hip/hip_runtime_api.h>
@@ -294,6 +296,27 @@ static int run_gpu(void) {
     }
     printf("decode vs prefill last rows: max |diff| %.3g\n", worst);
     check(within, "decode row == prefill's last row within 2e-3 + 1e-2 |want|");
+
+    /* 5. the same prompts with split keys (this grid is smaller than the CUs) */
+    size_t pws = 0;
+    PKV_OK_(pkv_attn_prefill_workspace(T2, HQ, HKV, NSEQ, &pws));
+    check(pws > 0, "pkv_attn_prefill_workspace: these prompts split");
+    void* pws_d = dmalloc(pws);
+    void* out_s = dmalloc((size_t)T2 * HQ * D * 2);
+    PKV_OK_(pkv_attn_prefill_split(q2_d, kc, vc, qkv2_d, qstride, HQ, HKV, pos2_d, cu2_d, NSEQ, dbt_d, max_blocks, BS,
+                                   out_s, scale, NULL, 1, T2, NBLOCKS, pws_d, pws, NULL));
+    HIP_OK(hipDeviceSynchronize());
+    uint16_t* hs = malloc((size_t)T2 * HQ * D * 2);
+    HIP_OK(hipMemcpy(hs, out_s, (size_t)T2 * HQ * D * 2, hipMemcpyDeviceToHost));
+    int split_ok = 1;
+    for (size_t i = 0; i < (size_t)T2 * HQ * D; i++) {
+        const double want = bf2f(hp[i]), got = bf2f(hs[i]);
+        if (!(fabs(got - want) <= 2e-3 + 1e-2 * fabs(want))) split_ok = 0;
+    }
+    check(split_ok, "pkv_attn_prefill_split == pkv_attn_prefill within 2e-3 + 1e-2 |want|, every row");
+    free(hs);
+    HIP_OK(hipFree(pws_d));
+    HIP_OK(hipFree(out_s));
 
     free(pos); free(slot); free(tseq); free(bt); free(qkv); free(q); free(dbt); free(dqkv); free(dq);
     free(hf); free(hu); free(hn); free(pos2); free(q2); free(qkv2); free(hp);

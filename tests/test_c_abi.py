@@ -4,9 +4,10 @@ the HIP runtime's C API, as an engine's FFI binding would (the reference's
 Rust binds HIP through a C ABI, src/hip.rs:134-181). Host mode covers status
 codes, the block allocator, the KV manager and argument checks; GPU mode
 runs prompts admitted by the KV manager through append, gather (byte-exact),
-the fused / unfused / no-allocation decode step (identical bytes) and a
+the fused / unfused / no-allocation decode step (identical bytes), a
 prefill over the same keys (decode row within 2e-3 + 1e-2 |want| of the
-prefill's last row)."""
+prefill's last row) and the same prefill with split keys (every row within
+that tolerance of it)."""
 import os
 import subprocess
 
