@@ -297,9 +297,8 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
  * reference's prompt kernels (attn_mfma / attn_flash_group have no split).
  * pkv_attn_prefill_workspace gives the bytes for these shapes (0 when the
  * grid covers the CUs: the call then runs as pkv_attn_prefill and reads no
- * workspace). bf16 cache, pages of 16 keys or more (otherwise as
- * pkv_attn_prefill); results within the attention tolerance of it (only the
- * points where P is rounded differ). */
+ * workspace). Results within the attention tolerance of pkv_attn_prefill
+ * (only the points where P is rounded differ). */
 int pkv_attn_prefill_workspace(int T, int Hq, int Hkv, int seqs, size_t* bytes);
 int pkv_attn_prefill_split(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
                            int Hkv, const int32_t* pos, const int32_t* cu, int seqs, const int32_t* block_table,
@@ -316,6 +315,13 @@ int pkv_attn_prefill_e4m3(const void* q, const void* kcache, const void* vcache,
                           const int32_t* cu, int seqs, const int32_t* block_table, int max_blocks, int block_size,
                           void* out, float scale, const int32_t* outs, int spec, int T, int64_t num_blocks,
                           void* stream);
+/* pkv_attn_prefill_e4m3 with split keys for small grids, as
+ * pkv_attn_prefill_split (workspace: pkv_attn_prefill_workspace bytes). */
+int pkv_attn_prefill_e4m3_split(const void* q, const void* kcache, const void* vcache, const float* kscale,
+                                const float* vscale, const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos,
+                                const int32_t* cu, int seqs, const int32_t* block_table, int max_blocks,
+                                int block_size, void* out, float scale, const int32_t* outs, int spec, int T,
+                                int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Device: attention input preparation (the reference's append site)

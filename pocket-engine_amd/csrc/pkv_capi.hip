@@ -284,12 +284,15 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     PrefillKernel kern_run = kern;
     // With a workspace and fewer workgroups than CUs: split every query
     // tile's keys over nsplit workgroups, then merge (bf16, 16-key pages).
-    const int nsplit = workspace && !f8 && block_size >= 16 ? prefill_nsplit(T, G, Hkv, seqs) : 1;
+    const int nsplit = workspace ? prefill_nsplit(T, G, Hkv, seqs) : 1;
     if (nsplit > 1) {
         if (workspace_bytes < prefill_split_layout(T, Hq, nsplit).total) return PKV_ERR_INVALID;
-        kern_run = by_group<PrefillKernel>(G, pkv::prefill_split_kernel<1>, pkv::prefill_split_kernel<2>,
-                                           pkv::prefill_split_kernel<4>, pkv::prefill_split_kernel<6>,
-                                           pkv::prefill_split_kernel<8>);
+        kern_run = f8 ? by_group<PrefillKernel>(G, pkv::prefill_split_kernel<1, true>,
+                                                pkv::prefill_split_kernel<2, true>, pkv::prefill_split_kernel<4, true>,
+                                                pkv::prefill_split_kernel<6, true>, pkv::prefill_split_kernel<8, true>)
+                      : by_group<PrefillKernel>(G, pkv::prefill_split_kernel<1>, pkv::prefill_split_kernel<2>,
+                                                pkv::prefill_split_kernel<4>, pkv::prefill_split_kernel<6>,
+                                                pkv::prefill_split_kernel<8>);
     } else if (!f8 && block_size >= 16 && (int64_t)tiles * Hkv < (G >= 6 ? 4 : 1) * (int64_t)device_cus()) {
         kern_run = by_group<PrefillKernel>(G, pkv::prefill_fine_kernel<1>, pkv::prefill_fine_kernel<2>,
                                            pkv::prefill_fine_kernel<4>, pkv::prefill_fine_kernel<6>,
@@ -380,6 +383,17 @@ int pkv_attn_prefill_split(const void* q, const void* kcache, const void* vcache
                            int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec,
                            int T, int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream) {
     return attn_prefill(q, kcache, vcache, nullptr, nullptr, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
+                        max_blocks, block_size, out, scale, outs, spec, T, num_blocks, stream, workspace,
+                        workspace_bytes);
+}
+
+int pkv_attn_prefill_e4m3_split(const void* q, const void* kcache, const void* vcache, const float* kscale,
+                                const float* vscale, const void* qkv, int qstride, int Hq, int Hkv, const int32_t* pos,
+                                const int32_t* cu, int seqs, const int32_t* block_table, int max_blocks,
+                                int block_size, void* out, float scale, const int32_t* outs, int spec, int T,
+                                int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!kscale || !vscale) return PKV_ERR_INVALID;
+    return attn_prefill(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table,
                         max_blocks, block_size, out, scale, outs, spec, T, num_blocks, stream, workspace,
                         workspace_bytes);
 }

@@ -228,7 +228,6 @@ __device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s
 // instead of the gated rows.
 template <int G, int BQ, int NQB, bool F8, bool UPAGE, int NST, bool DMA, int VP = PF_VPAIR, bool SPL = false>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb) {
-    static_assert(!SPL || DMA, "split ranges: the DMA path");
     constexpr int THREADS = pf_threads(BQ, NQB, G);
     // BQ = 16: a wave's 32 columns are 2 heads x 16 queries
     constexpr bool PAIRED = BQ < 32;
@@ -622,20 +621,20 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         }
     } else {
     // Only the first LDT threads load and store tiles.
-    if (UPAGE && loader) fetch_ids(0);
+    if (UPAGE && loader) fetch_ids(kbase);
     // NST 3: iteration i stores tile i + 1 (loaded during iteration i - 1)
     // into the stage tile i - 2 used, requests tile i + 2, computes tile i,
     // then one barrier. NST 2: iteration i requests tile i + 1, computes
     // tile i, and stores between two barriers.
     if (loader) {
-        load_tile(0);
-        store_tile(0, 0);
-        if (NST == 3 && ntiles > 1) load_tile(PF_BK);
+        load_tile(kbase);
+        store_tile(0, kbase);
+        if (NST == 3 && ntiles > 1) load_tile(kbase + PF_BK);
     }
     __syncthreads();
     int buf = 0;
     for (int it = 0; it < ntiles; it++) {
-        const int k0 = it * PF_BK;
+        const int k0 = kbase + it * PF_BK;
         if (loader) {
             if constexpr (NST == 3) {
                 if (it + 1 < ntiles) {
@@ -736,17 +735,25 @@ __global__ void __launch_bounds__(pf_fine_threads(G), 2) prefill_fine_kernel(Pre
     prefill_body<G, pf_fine_bq(G), 1, false, 2, PF_VPAIR_TIGHT>(p, pf_smem);
 }
 
-// Split keys (pkv_attn_prefill_split, grids with fewer workgroups than CUs,
-// e.g. one sequence's chunk after a long context): grid (query tiles, kv
-// heads, p.nsplit), each workgroup the library kernel's tile over one range
-// of its keys, leaving records; prefill_merge_kernel combines them.
-template <int G>
+// Split keys (pkv_attn_prefill_split / _e4m3_split, grids with fewer
+// workgroups than CUs, e.g. one sequence's chunk after a long context): grid
+// (query tiles, kv heads, p.nsplit), each workgroup the library kernel's
+// tile over one range of its keys, leaving records; prefill_merge_kernel
+// combines them.
+template <int G, bool F8 = false>
 __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_split_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
-    constexpr int BQ = pf_lib_bq(G);
+    constexpr int BQ = pf_lib_bq(G), NQB = pf_lib_nqb(G);
     int s, tb, nb;
-    if (!find_prefill_tile<BQ>(p, s, tb, nb) || p.bs_log2 < 4) return;  // 16-key pages or more (host-checked)
-    prefill_tile<G, BQ, pf_lib_nqb(G), false, true, PF_NST, true, PF_VPAIR, true>(p, pf_smem, s, tb, nb);
+    if (!find_prefill_tile<BQ>(p, s, tb, nb)) return;
+    // the tile paths of prefill_body
+    constexpr bool DMA = !F8;
+    if (DMA && p.bs_log2 >= 4)
+        prefill_tile<G, BQ, NQB, F8, true, PF_NST, DMA, PF_VPAIR, true>(p, pf_smem, s, tb, nb);
+    else if (p.bs_log2 >= __builtin_ctz(pf_load_threads(pf_threads(BQ, NQB, G)) / 32))
+        prefill_tile<G, BQ, NQB, F8, true, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb);
+    else
+        prefill_tile<G, BQ, NQB, F8, false, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb);
 }
 
 // Combines the key ranges of prefill_split_kernel: grid (rows, kv heads),

@@ -51,6 +51,9 @@ _SIGS = {
     "pkv_attn_prefill": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_int, _c_p, _c_int,
                                   _c_int, _c_p, _c_f, _c_p, _c_int, _c_int, _c_i64, _c_p]),
     "pkv_attn_prefill_workspace": (_c_int, [_c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
+    "pkv_attn_prefill_e4m3_split": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p,
+                                             _c_int, _c_p, _c_int, _c_int, _c_p, _c_f, _c_p, _c_int, _c_int, _c_i64,
+                                             _c_p, _c_sz, _c_p]),
     "pkv_attn_prefill_split": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p, _c_p, _c_int, _c_p,
                                         _c_int, _c_int, _c_p, _c_f, _c_p, _c_int, _c_int, _c_i64, _c_p, _c_sz, _c_p]),
     "pkv_attn_decode_step": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_p,
@@ -295,8 +298,16 @@ def attn_verify_e4m3(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, p
 
 
 def attn_prefill_e4m3(q, kcache, vcache, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,
-                      block_size, out, scale, outs, spec, T, num_blocks, stream=None):
-    """Causal chunked-prefill attention over an E4M3 cache (reference attn_group8)."""
+                      block_size, out, scale, outs, spec, T, num_blocks, stream=None, workspace=None):
+    """Causal chunked-prefill attention over an E4M3 cache (reference attn_group8);
+    with a workspace (attn_prefill_workspace bytes), pkv_attn_prefill_e4m3_split."""
+    if workspace is not None:
+        _check(_lib.pkv_attn_prefill_e4m3_split(
+            _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(kscale), _ptr(vscale), _ptr(qkv), qstride, Hq, Hkv, _ptr(pos),
+            _ptr(cu), seqs, _ptr(block_table), max_blocks, block_size, _ptr(out), scale, _ptr(outs), spec, T,
+            num_blocks, _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(stream)),
+            "pkv_attn_prefill_e4m3_split")
+        return
     _check(_lib.pkv_attn_prefill_e4m3(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(kscale), _ptr(vscale), _ptr(qkv),
                                       qstride, Hq, Hkv, _ptr(pos), _ptr(cu), seqs, _ptr(block_table), max_blocks,
                                       block_size, _ptr(out), scale, _ptr(outs), spec, T, num_blocks, _stream(stream)),

@@ -205,17 +205,24 @@ def paged_prompt_case(ctxs, chunks, Hkv, G, bs, seed):
                 pos=np.array(pos, np.int32), cu=np.array(cu, np.int32), seqs=len(lens), T=T, Hq=Hq, Hkv=Hkv)
 
 
+@pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("e4m3", [False, True])
 @pytest.mark.parametrize("G,Hkv", [(4, 4), (6, 4), (1, 4), (8, 2)])
 @pytest.mark.parametrize("bs", [4, 8, 32, 64])
-def test_prefill_block_sizes_match_oracle(dev, e4m3, G, Hkv, bs):
+def test_prefill_block_sizes_match_oracle(dev, e4m3, G, Hkv, bs, split):
     """Pages of 4 / 8 / 32 / 64 keys (any power of two; the reference engine
     uses 16): below 16 keys the tiles load through registers with a page id
     per key (pages smaller than the loading threads' key groups) or per key
-    group, at 32 and 64 by LDS DMA (bf16) — for every group shape."""
-    print(f"case prefill bs={bs} G={G} Hkv={Hkv} e4m3={e4m3}", flush=True)
+    group, at 32 and 64 by LDS DMA (bf16) — for every group shape; and the
+    same through the split-key entry points (these small grids split)."""
+    print(f"case prefill bs={bs} G={G} Hkv={Hkv} e4m3={e4m3} split={split}", flush=True)
     c = paged_prompt_case([100, 0, 37], [70, 33, 130], Hkv, G, bs, 200 + bs + G)
     T, Hq = c["T"], c["Hq"]
+    ws = None
+    if split:
+        nbytes = pkv.attn_prefill_workspace(T, Hq, Hkv, c["seqs"])
+        assert nbytes > 0
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     init = np.full((T, Hq, D), 0x3333, np.uint16)
     out = torch.from_numpy(init.view(np.int16).copy()).to(dev)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16) if a.dtype == np.uint16
@@ -227,12 +234,12 @@ def test_prefill_block_sizes_match_oracle(dev, e4m3, G, Hkv, bs):
         ks = (rng.random(c["kc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
         vs = (rng.random(c["vc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
         pkv.attn_prefill_e4m3(t(c["q"]), t(k8), t(v8), t(ks), t(vs), t(c["qkv"]), c["qstride"], Hq, Hkv, pos, cu,
-                              c["seqs"], bt, c["max_blocks"], bs, out, SCALE, None, 1, T, c["pages"])
+                              c["seqs"], bt, c["max_blocks"], bs, out, SCALE, None, 1, T, c["pages"], workspace=ws)
         want = oracle.attn_prefill8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["cu"],
                                     c["seqs"], c["bt"], c["max_blocks"], bs, SCALE, out=init.copy())
     else:
         pkv.attn_prefill(t(c["q"]), t(c["kc"]), t(c["vc"]), t(c["qkv"]), c["qstride"], Hq, Hkv, pos, cu, c["seqs"],
-                         bt, c["max_blocks"], bs, out, SCALE, None, 1, T, c["pages"])
+                         bt, c["max_blocks"], bs, out, SCALE, None, 1, T, c["pages"], workspace=ws)
         want = oracle.attn_prefill(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["cu"],
                                    c["seqs"], c["bt"], c["max_blocks"], bs, SCALE, out=init.copy())
     torch.cuda.synchronize()

@@ -134,3 +134,34 @@ def test_split_prefill_graph_replay_matches_eager(dev):
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy(), eager), f"replay {r}"
+
+
+@pytest.mark.parametrize("G", [4, 6])
+def test_split_prefill_e4m3_matches_oracle(dev, G):
+    """pkv_attn_prefill_e4m3_split: a chunk after a long context over an
+    E4M3 cache against the oracle."""
+    print(f"case prefill e4m3 split G={G}", flush=True)
+    from test_gpu_e4m3 import e4m3_cache
+    c = prefill_case([3000, 0], [150, 90], 4, 270 + G, decode_rows=1, G=G)
+    T, Hq = c["T"], c["Hq"]
+    rng = np.random.default_rng(271 + G)
+    k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
+    ks = (rng.random(c["kc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+    vs = (rng.random(c["vc"].shape[:2]) * 0.004 + 0.001).astype(np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16) if a.dtype == np.uint16
+                                   else np.ascontiguousarray(a)).to(dev)
+    init = np.full((T, Hq, 256), 0x3333, np.uint16)
+    out = t(init.copy())
+    nbytes = pkv.attn_prefill_workspace(T, Hq, 4, c["seqs"])
+    assert nbytes > 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    pkv.attn_prefill_e4m3(t(c["q"]), t(k8), t(v8), t(ks), t(vs), t(c["qkv"]), c["qstride"], Hq, 4, t(c["pos"]),
+                          t(c["cu"]), c["seqs"], t(c["bt"]), c["max_blocks"], BS, out, SCALE, None, 1, T, c["pages"],
+                          workspace=ws)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    want = oracle.attn_prefill8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], Hq, 4, c["pos"], c["cu"], c["seqs"],
+                                c["bt"], c["max_blocks"], BS, SCALE, out=init.copy())
+    assert (got[0] == 0x3333).all()
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
