@@ -102,7 +102,7 @@ def measure_traffic(args, seed, algorithmic_bytes, want=None):
              "--kv", args.kv, "--q-heads", str(args.q_heads), "--batch", str(args.batch), "--pages", str(args.pages),
              "--prefix", str(args.prefix), "--tokens", str(args.tokens), "--context", str(args.context),
              "--seqs", str(args.seqs)]
-    for flag in ("unfused", "with_prep", "refabi", "verify_kernel"):
+    for flag in ("unfused", "with_prep", "refabi", "verify_kernel", "prefill_split"):
         if getattr(args, flag):
             child.append("--" + flag.replace("_", "-"))
     if args.wg_per_cu or args.min_range:
@@ -943,7 +943,7 @@ def bench_attn(args):
                "single_thread_us": round(flops / rate1 * 1e6, 1), "cpu": _cpu_model()}
 
     alg = seqs * (context + tokens) * hkv * D * 2 * 2 + 3 * t * hq * D * 2
-    traffic, traffic_detail = measure_traffic(args, 0, alg, want="prefill")
+    traffic, traffic_detail = measure_traffic(args, 0, alg, want="prefill_split" if ws_bytes else "prefill")
     published = {(4, 4096, 0, 1): 1160.0}  # bench-attn prefill g4 4096 tokens, RTX 5090
     base = published.get((G, tokens, context, seqs))
     tf = flops / (kern_us * 1e-6) / 1e12
@@ -972,7 +972,9 @@ def bench_attn(args):
                    "head_dim": D, "page": BS, "seqs": seqs, "tokens": tokens, "context": context,
                    "flop_per_launch": flops, "parallelism": "single GPU"},
         "check": {"rows": len(rows), "against": "pkv_attn_decode of the same rows", **check},
-        "roofline": {"bound": "mfma", "kernel": f"prefill_kernel<{G}> (events at its start and end)",
+        "roofline": {"bound": "mfma", "kernel": (f"prefill_split_kernel<{G}> (events at its start and end; the merge launch after it "
+                                "is outside)" if ws_bytes else
+                                f"the prompt kernel pkv_attn_prefill picks for G={G} (events at its start and end)"),
                      "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4), "median_us": round(kern_us, 1),
                      "traffic": None if traffic is None else round(traffic), "traffic_detail": traffic_detail},

@@ -288,17 +288,24 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
                      int max_blocks, int block_size, void* out, float scale, const int32_t* outs, int spec, int T,
                      int64_t num_blocks, void* stream);
 
-/* The same with a workspace, for grids with fewer workgroups than CUs (one
- * sequence's prompt chunk of a few thousand tokens, above all after a long
- * context): each query tile's keys are split over up to 16 workgroups, which
- * leave (max, sum, weighted values) records in the workspace, and a second
- * launch folds them into the gated rows (the split-K decode's merge,
- * reference attn_merge qwen35.cu:2242-2279). No counterpart in the
+/* The same with a workspace, for prompts whose query tiles would leave CUs
+ * idle (one sequence's prompt chunk of a few thousand tokens, above all
+ * after a long context, also beside many one-token decode rows): the kernel
+ * counts the prompt's query tiles from cu and, when their workgroups do not
+ * fill the CUs, splits each tile's keys over max(2, CUs / workgroups)
+ * workgroups (ranges of at least 128 keys), which leave (max, sum, weighted
+ * values) records in the workspace; a second launch folds them into the
+ * gated rows (the split-K decode's merge, reference attn_merge
+ * qwen35.cu:2242-2279). Otherwise the rows are written directly, as
+ * pkv_attn_prefill (G = 6 / 8 grids whose tile bound fills the CUs but not
+ * four rounds run pkv_attn_prefill's kernel). No counterpart in the
  * reference's prompt kernels (attn_mfma / attn_flash_group have no split).
- * pkv_attn_prefill_workspace gives the bytes for these shapes (0 when the
- * grid covers the CUs: the call then runs as pkv_attn_prefill and reads no
- * workspace). Results within the attention tolerance of pkv_attn_prefill
- * (only the points where P is rounded differ). */
+ * pkv_attn_prefill_workspace gives the bytes for these shapes: records for
+ * at most max(2 min((ceil(T / BQ) + seqs) Hkv, CUs - 1), CUs) workgroups
+ * of BQ x G rows of 1,032 bytes (BQ = 256 / G queries, 32 for G = 6 / 8),
+ * 68 MB at G = 4 on 256 CUs while that bound is 128 workgroups or fewer. Results
+ * within the attention tolerance of pkv_attn_prefill (only the points where
+ * P is rounded differ); with no split, its bytes. */
 int pkv_attn_prefill_workspace(int T, int Hq, int Hkv, int seqs, size_t* bytes);
 int pkv_attn_prefill_split(const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,
                            int Hkv, const int32_t* pos, const int32_t* cu, int seqs, const int32_t* block_table,

@@ -219,29 +219,25 @@ int pkv_attn_prep(const void* qkv, int qstride, int Hq, int Hkv, const float* q_
 
 namespace {
 
-// Key ranges per query tile for pkv_attn_prefill_split: 1 when the library
-// kernel's grid (w <= T / BQ + seqs tiles per kv head) covers the CUs, else
-// as many as fit the CUs in one round (floor(CUs / w): a chunk's tiles are
-// near equal after a long context, so a second round would cost a whole
-// range), at least 2 and at most 16.
-int prefill_nsplit(int T, int G, int Hkv, int seqs) {
-    const int bq = pkv::pf_lib_bq(G);
-    const int64_t w = ((int64_t)(T + bq - 1) / bq + seqs) * Hkv, cus = device_cus();
-    if (w <= 0 || w >= cus) return 1;
-    return (int)std::max<int64_t>(2, std::min<int64_t>(16, cus / w));
-}
-
-// Workspace of pkv_attn_prefill_split: records [(row * Hq + head) * nsplit
-// + range] of (max, sum) then 256 weighted values, f32.
+// Workspace of pkv_attn_prefill_split: BQ x G records, of (max, sum) then
+// 256 weighted values (f32), per split workgroup. The kernel takes the
+// query tile count R from cu; the host bounds it by U = ceil(T / BQ) + seqs
+// (each prompt rounds up once), so a split grid (parts x R x Hkv < 2 cus
+// workgroups, and no more than max(2 R Hkv, cus)) holds at most
+// max(2 min(U Hkv, cus - 1), cus) workgroups: the workspace's bound, cap.
 struct PrefillSplitLayout {
+    int64_t cap;
     size_t ms, acc, total;
 };
-PrefillSplitLayout prefill_split_layout(int T, int Hq, int nsplit) {
-    const size_t recs = (size_t)T * Hq * nsplit;
+PrefillSplitLayout prefill_split_layout(int T, int Hq, int Hkv, int seqs) {
+    const int G = Hq / Hkv, bq = pkv::pf_lib_bq(G);
+    const int64_t cus = device_cus(), w = ((int64_t)(T + bq - 1) / bq + seqs) * Hkv;
     PrefillSplitLayout l;
+    l.cap = std::max<int64_t>(2 * std::min<int64_t>(w, cus - 1), cus);
+    const size_t recs = (size_t)l.cap * bq * G;
     l.ms = 0;
     l.acc = round_up(recs * 2 * 4, 256);
-    l.total = nsplit > 1 ? l.acc + recs * pkv::HEAD_DIM * 4 : 0;
+    l.total = l.acc + recs * pkv::HEAD_DIM * 4;
     return l;
 }
 
@@ -282,18 +278,31 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     // G = 6 / 8, whose workgroups hold 6 / 8 waves of fewer queries: below
     // four rounds.)
     PrefillKernel kern_run = kern;
-    // With a workspace and fewer workgroups than CUs: split every query
-    // tile's keys over nsplit workgroups, then merge (bf16, 16-key pages).
-    const int nsplit = workspace ? prefill_nsplit(T, G, Hkv, seqs) : 1;
-    if (nsplit > 1) {
-        if (workspace_bytes < prefill_split_layout(T, Hq, nsplit).total) return PKV_ERR_INVALID;
+    // With a workspace: the split kernel, which splits every query tile's
+    // keys over several workgroups when the prompt's tiles leave CUs idle
+    // (it counts them from cu), then the merge. G = 6 / 8 without a sure
+    // split (the bound U Hkv already covers the CUs) where the fine kernel
+    // would run keeps the fine kernel (a 4,096-token prompt at G = 6: 383
+    // against the library tile's 405 us).
+    // Without drafts to verify (outs null) every sequence of two or more
+    // rows is a prompt, so at least T - seqs rows are: when their tiles
+    // alone fill the CUs no split can happen, and the call runs as without
+    // a workspace (no merge launch).
+    const int64_t cus = device_cus();
+    const bool fine = !f8 && block_size >= 16 && (int64_t)tiles * Hkv < (G >= 6 ? 4 : 1) * cus;
+    const bool no_split = !outs && (int64_t)(T - seqs + bq - 1) / bq * Hkv >= cus;
+    const bool split = workspace && !no_split && !(fine && G >= 6 && (int64_t)tiles * Hkv >= cus);
+    PrefillSplitLayout lay{};
+    if (split) {
+        lay = prefill_split_layout(T, Hq, Hkv, seqs);
+        if (workspace_bytes < lay.total) return PKV_ERR_INVALID;
         kern_run = f8 ? by_group<PrefillKernel>(G, pkv::prefill_split_kernel<1, true>,
                                                 pkv::prefill_split_kernel<2, true>, pkv::prefill_split_kernel<4, true>,
                                                 pkv::prefill_split_kernel<6, true>, pkv::prefill_split_kernel<8, true>)
                       : by_group<PrefillKernel>(G, pkv::prefill_split_kernel<1>, pkv::prefill_split_kernel<2>,
                                                 pkv::prefill_split_kernel<4>, pkv::prefill_split_kernel<6>,
                                                 pkv::prefill_split_kernel<8>);
-    } else if (!f8 && block_size >= 16 && (int64_t)tiles * Hkv < (G >= 6 ? 4 : 1) * (int64_t)device_cus()) {
+    } else if (fine) {
         kern_run = by_group<PrefillKernel>(G, pkv::prefill_fine_kernel<1>, pkv::prefill_fine_kernel<2>,
                                            pkv::prefill_fine_kernel<4>, pkv::prefill_fine_kernel<6>,
                                            pkv::prefill_fine_kernel<8>);
@@ -336,19 +345,16 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     p.num_blocks = (long)num_blocks;
     p.kscale = kscale;
     p.vscale = vscale;
-    p.nsplit = nsplit;
-    if (nsplit > 1) {
-        const PrefillSplitLayout lay = prefill_split_layout(T, Hq, nsplit);
-        p.part_ms = (float*)((char*)workspace + lay.ms);
-        p.part_acc = (float*)((char*)workspace + lay.acc);
-    } else {
-        p.part_ms = p.part_acc = nullptr;
-    }
+    p.cus = (int)cus;
+    p.split_cap = split ? (int)lay.cap : 0;
+    p.part_ms = split ? (float*)((char*)workspace + lay.ms) : nullptr;
+    p.part_acc = split ? (float*)((char*)workspace + lay.acc) : nullptr;
     hipEvent_t e0 = t_pf_start, e1 = t_pf_stop;
     t_pf_start = t_pf_stop = nullptr;
-    hipExtLaunchKernelGGL(kern_run, dim3(tiles, Hkv, nsplit), dim3(threads), smem, (hipStream_t)stream, e0, e1, 0,
-                          p);
-    if (nsplit > 1) {
+    // the split kernel: a 1-D grid over both of its launches' shapes
+    const dim3 grid = split ? dim3((unsigned)std::max<int64_t>((int64_t)tiles * Hkv, 2 * cus)) : dim3(tiles, Hkv);
+    hipExtLaunchKernelGGL(kern_run, grid, dim3(threads), smem, (hipStream_t)stream, e0, e1, 0, p);
+    if (split) {
         int st = launch_status();
         if (st != PKV_OK) return st;
         using MergeKernel = void (*)(pkv::PrefillParams);
@@ -374,7 +380,7 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
 
 int pkv_attn_prefill_workspace(int T, int Hq, int Hkv, int seqs, size_t* bytes) {
     if (T < 0 || Hq <= 0 || Hkv <= 0 || seqs < 0 || Hq % Hkv != 0 || !bytes) return PKV_ERR_INVALID;
-    *bytes = prefill_split_layout(T, Hq, prefill_nsplit(T, Hq / Hkv, Hkv, seqs)).total;
+    *bytes = prefill_split_layout(T, Hq, Hkv, seqs).total;
     return PKV_OK;
 }
 

@@ -51,11 +51,12 @@ struct PrefillParams {
     // per (slot, kv head)
     const float* kscale;
     const float* vscale;
-    // Split keys (prefill_split_kernel): nsplit ranges per query tile, and
-    // their records: (max in log2 units, sum) at part_ms[r * 2] and the
-    // unnormalised weighted values at part_acc[r * 256], r = (row * Hq +
-    // head) * nsplit + range
-    int nsplit;
+    // Split keys (prefill_split_kernel): the device's CUs (the split fills
+    // them), the workgroups whose records part_ms / part_acc hold, and the
+    // records: (max in log2 units, sum) at part_ms[r * 2] and the
+    // unnormalised weighted values at part_acc[r * 256], r = workgroup *
+    // BQ * G + query * G + head in group (pf_split_rec)
+    int cus, split_cap;
     float* part_ms;
     float* part_acc;
 };
@@ -127,6 +128,27 @@ constexpr int PF_IDS_BYTES = pf_ids_bytes(PF_THREADS);
 constexpr int pf_lib_bq(int G) { return G >= 6 ? 32 : 256 / G; }
 constexpr int pf_lib_nqb(int G) { return G == 4 ? PF_NQB : 1; }
 constexpr int pf_lib_threads(int G) { return pf_threads(pf_lib_bq(G), pf_lib_nqb(G), G); }
+
+// Split keys (prefill_split_kernel). R query tiles x Hkv kv heads = w
+// workgroups leave CUs idle when w < cus: each tile's keys then go to
+// max(2, cus / w) ranges (one round of cus workgroups for a small w; two
+// for w >= cus / 2, where halving the ranges beats leaving them whole),
+// never under PF_SPLIT_MIN key tiles each (a range then still amortises its
+// query load and records). A split grid holds parts * w < 2 cus workgroups.
+constexpr int PF_SPLIT_MIN = 4;
+__host__ __device__ constexpr int pf_split_parts(int w, int cus) {
+    return w <= 0 || w >= cus ? 1 : (cus / w > 2 ? cus / w : 2);
+}
+// Key tiles per range of a query tile of nt key tiles.
+__host__ __device__ constexpr int pf_split_per(int nt, int parts) {
+    return (nt + parts - 1) / parts > PF_SPLIT_MIN ? (nt + parts - 1) / parts : PF_SPLIT_MIN;
+}
+// Record of query q (in its tile) and head hh (in its group) from split
+// workgroup wg.
+template <int BQ, int G>
+__device__ __forceinline__ size_t pf_split_rec(int wg, int q, int hh) {
+    return ((size_t)wg * BQ + q) * G + hh;
+}
 constexpr size_t prefill_smem_bytes(int nst = PF_NST, int threads = PF_THREADS) {
     return (size_t)nst * PF_STAGE * 2 + pf_ids_bytes(threads);
 }
@@ -180,37 +202,65 @@ __device__ __forceinline__ void dma_pairs(const void* base, const uint32_t (&off
     }
 }
 
-// The query tile of this workgroup among the prompt sequences: tile
-// total - 1 - blockIdx.x of the concatenated BQ-query tiles of the prompt
-// sequences (sequences of more than one row that do not verify drafts).
-// Returns false if the grid has more blocks than tiles.
+// The query tiles of sequence i (0 past the last): a prompt sequence
+// (more than one row, not verifying drafts) has ceil(rows / BQ).
 template <int BQ>
-__device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s, int& tb, int& nb) {
+__device__ __forceinline__ int seq_tiles(const PrefillParams& p, int i) {
+    if (i >= p.seqs) return 0;
+    const int n = p.cu[i + 1] - p.cu[i];
+    return n > 1 && !is_spec(p.outs, p.spec, i) ? (n + BQ - 1) / BQ : 0;
+}
+
+// The prompt's query tiles, summed by each wave over its lanes (64
+// sequences a round: a mixed step's one-row decode sequences cost a load
+// round per 64, not one each).
+template <int BQ>
+__device__ __forceinline__ int prompt_tiles(const PrefillParams& p) {
+    const int lane = threadIdx.x & 63;
+    int total = 0;
+    for (int c = 0; c < p.seqs; c += 64) total += seq_tiles<BQ>(p, c + lane);
+#pragma unroll
+    for (int o = 32; o; o >>= 1) total += __shfl_xor(total, o);
+    return __builtin_amdgcn_readfirstlane(total);
+}
+
+// The query tile of this workgroup among the prompt sequences: tile
+// total - 1 - `tile` of the concatenated BQ-query tiles of the prompt
+// sequences, found by each wave with a prefix sum over its lanes. Returns
+// false if the grid has more blocks than tiles. Called by whole waves.
+template <int BQ>
+__device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int tile, int& s, int& tb, int& nb,
+                                                  int total = -1) {
     // Tiles are taken last first: a sequence's later tiles attend more keys,
     // so the longest work is dispatched first and the short tiles fill the
     // tail.
-    int tile = blockIdx.x;
-    {
-        int total = 0;
-        for (int i = 0; i < p.seqs; i++) {
-            const int n = p.cu[i + 1] - p.cu[i];
-            if (n > 1 && !is_spec(p.outs, p.spec, i)) total += (n + BQ - 1) / BQ;
-        }
-        if (tile >= total) return false;
-        tile = total - 1 - tile;
-    }
+    if (total < 0) total = prompt_tiles<BQ>(p);
+    if (tile >= total) return false;
+    tile = total - 1 - tile;
+    const int lane = threadIdx.x & 63;
+    int base = 0;  // tiles of the sequences before this round
     s = -1;
-    for (int i = 0; i < p.seqs; i++) {
-        const int n = p.cu[i + 1] - p.cu[i];
-        if (n <= 1 || is_spec(p.outs, p.spec, i)) continue;
-        const int tiles = (n + BQ - 1) / BQ;
-        if (tile < tiles) {
-            s = i;
+    for (int c = 0; c < p.seqs; c += 64) {
+        const int k = seq_tiles<BQ>(p, c + lane);
+        int incl = k;  // inclusive prefix sum over lanes
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o);
+            if (lane >= o) incl += v;
+        }
+        // the first lane whose tiles reach past `tile`
+        const unsigned long long hit = __ballot(base + incl > tile);
+        if (hit) {
+            const int l = __ffsll((long long)hit) - 1;
+            s = c + l;
+            tile -= base + __shfl(incl - k, l);
             break;
         }
-        tile -= tiles;
+        base += __shfl(incl, 63);
     }
+    s = __builtin_amdgcn_readfirstlane(s);
     if (s < 0) return false;
+    tile = __builtin_amdgcn_readfirstlane(tile);
     tb = p.cu[s] + tile * BQ;
     nb = min(BQ, p.cu[s + 1] - tb);
     return true;
@@ -222,12 +272,14 @@ __device__ __forceinline__ bool find_prefill_tile(const PrefillParams& p, int& s
 // the tiles load as the reference's attn_group8 does (qwen35.cu:1424-1436):
 // K' = bf16(k * kscale), V' = bf16(v * vscale); the rest is unchanged.
 //
-// SPL: this workgroup takes key range blockIdx.z of p.nsplit (ceil(n /
-// nsplit) of the tile's n key tiles each; an empty range returns at once)
-// and leaves a record per (row, query head) for prefill_merge_kernel
-// instead of the gated rows.
+// Workgroup (query tile, kv head kvh, key range part). SPL with parts > 1:
+// this workgroup, number wg of the split grid, takes key range part of
+// parts (pf_split_per key tiles each; an empty range returns at once) and
+// leaves a record per (row, query head) for prefill_merge_kernel instead of
+// the gated rows.
 template <int G, int BQ, int NQB, bool F8, bool UPAGE, int NST, bool DMA, int VP = PF_VPAIR, bool SPL = false>
-__device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb) {
+__device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* pf_smem, int s, int tb, int nb,
+                                             int kvh, int part = 0, int parts = 1, int wg = 0) {
     constexpr int THREADS = pf_threads(BQ, NQB, G);
     // BQ = 16: a wave's 32 columns are 2 heads x 16 queries
     constexpr bool PAIRED = BQ < 32;
@@ -241,7 +293,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31,
               lh = lane >> 5;
     const bool loader = LDT == THREADS || tid < LDT;  // wave-uniform
-    const int kvh = blockIdx.y;
     // This lane's query head, and the wave's first query block (BQ >= 32).
     const int h = kvh * G + (PAIRED ? 2 * wave + (lq >> 4) : wave % G);
     const int qb0 = PAIRED ? 0 : (wave / G) * NQB;
@@ -421,7 +472,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     // The key tiles this workgroup streams: [kbase, kbase + ntiles * 32).
     int ntiles = (L + PF_BK - 1) / PF_BK, kbase = 0;
     if constexpr (SPL) {
-        const int per = (ntiles + p.nsplit - 1) / p.nsplit, t0 = (int)blockIdx.z * per;
+        const int per = pf_split_per(ntiles, parts), t0 = part * per;
         ntiles = min(ntiles, t0 + per) - t0;
         kbase = t0 * PF_BK;
         if (ntiles <= 0) return;  // whole workgroup: nothing to merge from this range
@@ -657,12 +708,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         }
     }
     }
-    if constexpr (SPL) {
+    if (SPL && parts > 1) {
 #pragma unroll
         for (int qb = 0; qb < NQB; qb++) {
             const int myq = qcol(qb);
             if (myq >= nb) continue;
-            const size_t r = (((size_t)tb + myq) * p.Hq + h) * p.nsplit + blockIdx.z;
+            const size_t r = pf_split_rec<BQ, G>(wg, myq, h - kvh * G);
             float* acc = p.part_acc + r * HEAD_DIM;
 #pragma unroll
             for (int db = 0; db < 8; db++)
@@ -703,17 +754,18 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
 template <int G, int BQ, int NQB, bool F8 = false, int NST = PF_NST, int VP = PF_VPAIR>
 __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* pf_smem) {
     int s, tb, nb;
-    if (!find_prefill_tile<BQ>(p, s, tb, nb)) return;
+    if (!find_prefill_tile<BQ>(p, blockIdx.x, s, tb, nb)) return;
+    const int kvh = blockIdx.y;
     // bf16 with pages of 16 keys or more: tiles by LDS DMA; otherwise
     // through registers, with uniform page ids per chunk when pages hold at
     // least (loading threads) / 32 keys.
     constexpr bool DMA = !F8;
     if (DMA && p.bs_log2 >= 4)
-        prefill_tile<G, BQ, NQB, F8, true, NST, DMA, VP>(p, pf_smem, s, tb, nb);
+        prefill_tile<G, BQ, NQB, F8, true, NST, DMA, VP>(p, pf_smem, s, tb, nb, kvh, 0);
     else if (p.bs_log2 >= __builtin_ctz(pf_load_threads(pf_threads(BQ, NQB, G)) / 32))
-        prefill_tile<G, BQ, NQB, F8, true, NST, false, VP>(p, pf_smem, s, tb, nb);
+        prefill_tile<G, BQ, NQB, F8, true, NST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
     else
-        prefill_tile<G, BQ, NQB, F8, false, NST, false, VP>(p, pf_smem, s, tb, nb);
+        prefill_tile<G, BQ, NQB, F8, false, NST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
 }
 
 // The library's prompt kernels for G query heads per kv head (shapes above).
@@ -735,35 +787,65 @@ __global__ void __launch_bounds__(pf_fine_threads(G), 2) prefill_fine_kernel(Pre
     prefill_body<G, pf_fine_bq(G), 1, false, 2, PF_VPAIR_TIGHT>(p, pf_smem);
 }
 
-// Split keys (pkv_attn_prefill_split / _e4m3_split, grids with fewer
-// workgroups than CUs, e.g. one sequence's chunk after a long context): grid
-// (query tiles, kv heads, p.nsplit), each workgroup the library kernel's
-// tile over one range of its keys, leaving records; prefill_merge_kernel
-// combines them.
+// Index b (< n) of a grid of n workgroups in an order where consecutive
+// indices share an XCD: the dispatcher hands workgroup ids to the 8 XCDs in
+// turn, and id b becomes index b / 8 of its XCD's contiguous share of the
+// grid (the first n % 8 XCDs take one more).
+__device__ __forceinline__ int xcd_major(int b, int n) {
+    const int q = n >> 3, r = n & 7, xcd = b & 7, slot = b >> 3;
+    return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+}
+
+// Split keys (pkv_attn_prefill_split / _e4m3_split): a 1-D grid of at least
+// max(host tile bound x kv heads, 2 cus) workgroups. The kernel counts the
+// prompt's R query tiles from cu (the host only bounds them) and takes
+// parts = pf_split_parts(R Hkv, cus) ranges per tile: workgroup l = x + R
+// (kvh + Hkv part) is tile x, kv head kvh, key range part, and the rest of
+// the grid returns. With parts > 1 (one or two rounds over the CUs) the
+// tiles of one (kv head, range) go to one XCD, which then reads those keys
+// through one L2, and each workgroup leaves records for
+// prefill_merge_kernel; with parts = 1 (a grid that fills the CUs) it is
+// the library kernel's launch, longest tiles first, rows written directly.
 template <int G, bool F8 = false>
 __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_split_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
     constexpr int BQ = pf_lib_bq(G), NQB = pf_lib_nqb(G);
+    // (uniform values: readfirstlane keeps them in SGPRs for the DMA bases)
+    const int R = __builtin_amdgcn_readfirstlane(prompt_tiles<BQ>(p));
+    int parts = pf_split_parts(R * p.Hkv, p.cus);
+    if (parts * R * p.Hkv > p.split_cap) parts = 1;
+    parts = __builtin_amdgcn_readfirstlane(parts);
+    const int n = parts * R * p.Hkv, b = blockIdx.x;
+    if (b >= n) return;
+    const int l = parts > 1 ? xcd_major(b, n) : b;
+    const int x = __builtin_amdgcn_readfirstlane(l % R), kvh = __builtin_amdgcn_readfirstlane((l / R) % p.Hkv),
+              part = __builtin_amdgcn_readfirstlane(l / (R * p.Hkv));
     int s, tb, nb;
-    if (!find_prefill_tile<BQ>(p, s, tb, nb)) return;
+    if (!find_prefill_tile<BQ>(p, x, s, tb, nb, R)) return;
     // the tile paths of prefill_body
     constexpr bool DMA = !F8;
     if (DMA && p.bs_log2 >= 4)
-        prefill_tile<G, BQ, NQB, F8, true, PF_NST, DMA, PF_VPAIR, true>(p, pf_smem, s, tb, nb);
+        prefill_tile<G, BQ, NQB, F8, true, PF_NST, DMA, PF_VPAIR, true>(p, pf_smem, s, tb, nb, kvh, part, parts, l);
     else if (p.bs_log2 >= __builtin_ctz(pf_load_threads(pf_threads(BQ, NQB, G)) / 32))
-        prefill_tile<G, BQ, NQB, F8, true, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb);
+        prefill_tile<G, BQ, NQB, F8, true, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb, kvh, part, parts, l);
     else
-        prefill_tile<G, BQ, NQB, F8, false, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb);
+        prefill_tile<G, BQ, NQB, F8, false, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb, kvh, part, parts,
+                                                                           l);
 }
 
 // Combines the key ranges of prefill_split_kernel: grid (rows, kv heads),
 // a wave per query head of the group; row t of a prompt sequence folds its
 // query tile's non-empty ranges (the decode merge's arithmetic, gated
-// output); other rows are left untouched.
+// output); other rows, and every row when the split kernel took one range
+// per tile, are left untouched.
 template <int G>
 __global__ void __launch_bounds__(64 * G) prefill_merge_kernel(PrefillParams p) {
     constexpr int BQ = pf_lib_bq(G);
-    const int t = blockIdx.x, h = blockIdx.y * G + (threadIdx.x >> 6);
+    const int t = blockIdx.x, kvh = blockIdx.y, hh = threadIdx.x >> 6, h = kvh * G + hh, lane = threadIdx.x & 63;
+    // nothing to merge without a split
+    const int total = prompt_tiles<BQ>(p);
+    const int parts = pf_split_parts(total * p.Hkv, p.cus);
+    if (parts == 1 || parts * total * p.Hkv > p.split_cap) return;
     // the sequence holding row t: the last s with cu[s] <= t
     int lo = 0, hi = p.seqs - 1;
     while (lo < hi) {
@@ -773,12 +855,19 @@ __global__ void __launch_bounds__(64 * G) prefill_merge_kernel(PrefillParams p) 
     }
     const int c0 = p.cu[lo], n = p.cu[lo + 1] - c0;
     if (t < c0 || t >= c0 + n || n <= 1 || is_spec(p.outs, p.spec, lo)) return;
+    // the tiles of the prompts before sequence lo
+    int before = 0;
+    for (int i = lane; i < lo; i += 64) before += seq_tiles<BQ>(p, i);
+#pragma unroll
+    for (int o = 32; o; o >>= 1) before += __shfl_xor(before, o);
     const int tb = c0 + (t - c0) / BQ * BQ, nb = min(BQ, c0 + n - tb);
-    const int nt = (p.pos[tb] + nb + PF_BK - 1) / PF_BK, per = (nt + p.nsplit - 1) / p.nsplit;
-    const size_t r0 = ((size_t)t * p.Hq + h) * p.nsplit;
+    // the split kernel's x of this tile (tiles run last first)
+    const int x = total - 1 - (before + (t - c0) / BQ);
+    const int nt = (p.pos[tb] + nb + PF_BK - 1) / PF_BK, per = pf_split_per(nt, parts);
+    auto rec = [&](int z) { return pf_split_rec<BQ, G>((z * p.Hkv + kvh) * total + x, t - tb, hh); };
     merge_rows<1>(
-        (nt + per - 1) / per, 1.f, [&](int z) { return p.part_ms + (r0 + z) * 2; },
-        [&](int z) { return p.part_acc + (r0 + z) * HEAD_DIM; },
+        (nt + per - 1) / per, 1.f, [&](int z) { return p.part_ms + rec(z) * 2; },
+        [&](int z) { return p.part_acc + rec(z) * HEAD_DIM; },
         p.qkv + (size_t)t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM, p.out + ((size_t)t * p.Hq + h) * HEAD_DIM);
 }
 

@@ -331,7 +331,7 @@ def attn_prefill(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_
 
 
 def attn_prefill_workspace(T, Hq, Hkv, seqs):
-    """Workspace bytes of pkv_attn_prefill_split (0: no split for these shapes)."""
+    """Workspace bytes of pkv_attn_prefill_split / _e4m3_split for these shapes."""
     n = _c_sz(0)
     _check(_lib.pkv_attn_prefill_workspace(T, Hq, Hkv, seqs, ctypes.byref(n)), "pkv_attn_prefill_workspace")
     return n.value

@@ -300,7 +300,7 @@ static int run_gpu(void) {
     /* 5. the same prompts with split keys (this grid is smaller than the CUs) */
     size_t pws = 0;
     PKV_OK_(pkv_attn_prefill_workspace(T2, HQ, HKV, NSEQ, &pws));
-    check(pws > 0, "pkv_attn_prefill_workspace: these prompts split");
+    check(pws > 0, "pkv_attn_prefill_workspace: room for the split records");
     void* pws_d = dmalloc(pws);
     void* out_s = dmalloc((size_t)T2 * HQ * D * 2);
     PKV_OK_(pkv_attn_prefill_split(q2_d, kc, vc, qkv2_d, qstride, HQ, HKV, pos2_d, cu2_d, NSEQ, dbt_d, max_blocks, BS,

@@ -1,8 +1,12 @@
 """pkv_attn_prefill_split: prompt attention with each query tile's keys split
-over several workgroups when the grid has fewer workgroups than CUs, then a
-merge launch. Against the oracle within the attention tolerance (|got -
-want| <= 2e-3 + 1e-2 |want|); rows outside the prompts stay untouched; a
-grid that covers the CUs (no split) gives pkv_attn_prefill's bytes."""
+over several workgroups when the prompt's tiles leave CUs idle, then a merge
+launch. Against the oracle within the attention tolerance (|got - want| <=
+2e-3 + 1e-2 |want|); rows outside the prompts stay untouched; a grid that
+covers the CUs (no split) gives pkv_attn_prefill's bytes.
+
+parts() states the kernel's rule (the prompt's R query tiles x Hkv = w
+workgroups split into max(2, CUs / w) ranges when w < CUs) so that each case
+says which regime it covers."""
 import numpy as np
 import pytest
 import torch
@@ -14,6 +18,16 @@ from test_gpu_prefill import i16, i32, prefill_case
 
 pytestmark = pytest.mark.gpu
 SCALE = 1.0 / 16.0
+
+
+def parts(c, G):
+    """Key ranges per query tile the split kernel takes for case c."""
+    bq = 32 if G >= 6 else 256 // G
+    n = np.diff(c["cu"])
+    R = int(sum((k + bq - 1) // bq for k in n if k > 1))
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    w = R * c["Hkv"]
+    return 1 if w >= cus else max(2, cus // w)
 
 
 def run_split(c, dev, workspace=True, init=0x3333):
@@ -36,6 +50,7 @@ def want_of(c, init=0x3333):
 
 @pytest.mark.parametrize("G", [1, 2, 4, 6, 8])
 @pytest.mark.parametrize("ctxs,chunks,seed", [
+    ([3000], [20], 3),              # one short tile: up to 64 ranges of >= 4 key tiles
     ([2000], [300], 0),             # one chunk after a long context: 8 ranges per tile
     ([0], [700], 1),                # one prompt, causal tiles of every length
     ([100, 3000, 0], [70, 130, 33], 2),  # three chunks, ranges ending mid-tile
@@ -43,9 +58,53 @@ def want_of(c, init=0x3333):
 def test_split_prefill_matches_oracle(dev, G, ctxs, chunks, seed):
     print(f"case prefill split G={G} ctx={ctxs} chunk={chunks}", flush=True)
     c = prefill_case(ctxs, chunks, 4, 200 + seed, decode_rows=1, G=G)
-    got, nbytes = run_split(c, dev)
-    assert nbytes > 0, "these shapes must split"
+    assert parts(c, G) > 1, "these shapes must split"
+    got, _ = run_split(c, dev)
     assert (got[0] == 0x3333).all()  # the decode row is left to decode attention
+    ok, err = close(got, want_of(c))
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("G", [2, 4, 8])
+def test_split_prefill_beside_decode_rows(dev, G):
+    """A chunk beside 60 one-token decode rows: the host's tile bound (60
+    sequences) covers the CUs, the prompt's tiles do not, so the kernel
+    splits; the decode rows are left to decode attention."""
+    print(f"case prefill split beside decode rows G={G}", flush=True)
+    c = prefill_case([2500], [200], 4, 280 + G, decode_rows=60, G=G)
+    assert parts(c, G) > 1
+    got, _ = run_split(c, dev)
+    assert (got[:60] == 0x3333).all()
+    ok, err = close(got, want_of(c))
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("G", [1, 4, 6])
+def test_split_prefill_two_rounds_match_prefill(dev, G):
+    """A 2,560-token prompt after 500 keys: R x Hkv between CUs / 2 and CUs
+    at G = 4 (two ranges per tile, two rounds of workgroups). Against
+    pkv_attn_prefill (itself pinned to the oracle) over the whole output,
+    within the attention tolerance."""
+    print(f"case prefill split two rounds G={G}", flush=True)
+    c = prefill_case([500], [2560], 4, 290 + G, G=G)
+    got, _ = run_split(c, dev)
+    plain, _ = run_split(c, dev, workspace=False)
+    ok, err = close(got, plain)
+    assert ok, f"max |diff| {err}"
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_prefill_many_sequences_match_oracle(dev, split):
+    """40 one-token decode sequences, then 30 short prompts (2-5 rows, so
+    one tile each) at sequence indices 40-69: the kernels find their tiles
+    64 sequences a round, and these tiles sit on both sides of the round
+    boundary; through pkv_attn_prefill and pkv_attn_prefill_split."""
+    print(f"case prefill many sequences split={split}", flush=True)
+    ctxs = [50 + 37 * i for i in range(30)]
+    chunks = [2 + i % 4 for i in range(30)]
+    c = prefill_case(ctxs, chunks, 4, 300 + split, decode_rows=40, G=4)
+    got, _ = run_split(c, dev, workspace=split)
+    assert (got[:40] == 0x3333).all()
     ok, err = close(got, want_of(c))
     assert ok, f"max |diff| {err}"
 
@@ -88,13 +147,13 @@ def test_split_prefill_rejects_a_short_workspace(dev):
 
 
 def test_split_prefill_without_a_split_is_prefill(dev):
-    """A grid that covers the CUs needs no workspace (0 bytes) and gives the
-    bytes of pkv_attn_prefill."""
+    """A prompt whose tiles cover the CUs is not split and gives the bytes of
+    pkv_attn_prefill."""
     print("case prefill split none", flush=True)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     n = (cus // 4 + 8) * 64  # query tiles x 4 kv heads >= CUs
     c = prefill_case([0], [n], 4, 250, G=4)
-    assert pkv.attn_prefill_workspace(c["T"], c["Hq"], 4, c["seqs"]) == 0
+    assert parts(c, 4) == 1
     got, _ = run_split(c, dev)
     plain, _ = run_split(c, dev, workspace=False)
     assert np.array_equal(got, plain)
@@ -152,8 +211,8 @@ def test_split_prefill_e4m3_matches_oracle(dev, G):
                                    else np.ascontiguousarray(a)).to(dev)
     init = np.full((T, Hq, 256), 0x3333, np.uint16)
     out = t(init.copy())
+    assert parts(c, G) > 1
     nbytes = pkv.attn_prefill_workspace(T, Hq, 4, c["seqs"])
-    assert nbytes > 0
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     pkv.attn_prefill_e4m3(t(c["q"]), t(k8), t(v8), t(ks), t(vs), t(c["qkv"]), c["qstride"], Hq, 4, t(c["pos"]),
                           t(c["cu"]), c["seqs"], t(c["bt"]), c["max_blocks"], BS, out, SCALE, None, 1, T, c["pages"],
