@@ -58,8 +58,16 @@ template <int NR = 1, int G = 4, class Epi>
 __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __restrict__ bt, WaveLds8& lds, int t,
                                             int kvh, int j0, int j1, Epi epi, const int* Lr = nullptr) {
     static_assert(NR >= 1 && NR <= 4 && NR * G <= 16, "up to 16 columns of up to 4 rows");
+    // Decode (one row, G <= 8 columns of 16): columns NCOL .. 2 NCOL - 1
+    // repeat columns 0 .. NCOL - 1 (same q, so bit-identical scores, max,
+    // sum and rescale) and take the bf16 remainders of the P.V weights while
+    // the first NCOL take the high parts: one MFMA per page and 16-dim block
+    // instead of two; the two halves are added once at the end.
+    constexpr int NCOL = NR * G;
+    constexpr bool DUP = NR == 1 && 2 * NCOL <= 16;
     const int lane = threadIdx.x & 63, sig = lane & 15, rho = lane >> 4;
-    const int col_r = sig / G, col_g = sig % G;
+    const int csig = DUP && sig >= NCOL && sig < 2 * NCOL ? sig - NCOL : sig;  // the column this lane computes
+    const int col_r = csig / G, col_g = csig % G;
     // this lane's column: its row's key bound (decode: the piece's), and
     // whether the column is a row that attends
     const int myL = NR == 1 ? j1 : col_r == 0 ? Lr[0] : col_r == 1 ? Lr[1] : col_r == 2 ? Lr[2] : col_r == 3 ? Lr[3] : 0;
@@ -209,14 +217,21 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
         wave_sync();  // V staged
         typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 #pragma unroll
-        for (int pg = 0; pg < 2; pg++)
+        for (int pg = 0; pg < 2; pg++) {
+            // DUP: the remainder columns' lanes supply their weights' low parts
+            const s16x4 pw = DUP && sig >= NCOL ? pw_lo[pg] : pw_hi[pg];
 #pragma unroll
             for (int db = 0; db < 16; db++) {
                 const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                     (lds_s16x4*)(tr + pg * PAGE * V8_VSTR + 16 * db));
-                acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pw_hi[pg], acc[db], 0, 0, 0);
-                acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pw_lo[pg], acc[db], 0, 0, 0);
+                if constexpr (DUP) {
+                    acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pw, acc[db], 0, 0, 0);
+                } else {
+                    acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pw_hi[pg], acc[db], 0, 0, 0);
+                    acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pw_lo[pg], acc[db], 0, 0, 0);
+                }
             }
+        }
         wave_sync();  // lds.v / lds.sc are rewritten for the next unit
     };
     using NONE = std::integral_constant<int, 0>;
@@ -231,7 +246,14 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     unit(u1, u1, NONE{});
     // Totals: a column's sum over its 4 lane groups.
     l = add_xor32(add_xor16(l));
-    if (active) epi(sig, rho, acc, m, l);
+    if constexpr (DUP) {
+        // column c (high parts) + column c + NCOL (remainders), same dims
+#pragma unroll
+        for (int db = 0; db < 16; db++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[db][i] += __shfl_down(acc[db][i], NCOL, 16);
+    }
+    if (active && sig < NCOL) epi(sig, rho, acc, m, l);
 }
 
 // Writes a piece's result for the lanes of head g of the group (dims
