@@ -227,7 +227,7 @@ namespace {
 // max(2 min(U Hkv, cus - 1), cus) workgroups: the workspace's bound, cap.
 struct PrefillSplitLayout {
     int64_t cap;
-    size_t ms, acc, total;
+    size_t plan, ms, acc, total;
 };
 PrefillSplitLayout prefill_split_layout(int T, int Hq, int Hkv, int seqs) {
     const int G = Hq / Hkv, bq = pkv::pf_lib_bq(G);
@@ -235,8 +235,9 @@ PrefillSplitLayout prefill_split_layout(int T, int Hq, int Hkv, int seqs) {
     PrefillSplitLayout l;
     l.cap = std::max<int64_t>(2 * std::min<int64_t>(w, cus - 1), cus);
     const size_t recs = (size_t)l.cap * bq * G;
-    l.ms = 0;
-    l.acc = round_up(recs * 2 * 4, 256);
+    l.plan = 0;  // the split plan (2 ints) in the first 256 bytes
+    l.ms = 256;
+    l.acc = round_up(l.ms + recs * 2 * 4, 256);
     l.total = l.acc + recs * pkv::HEAD_DIM * 4;
     return l;
 }
@@ -349,6 +350,7 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     p.split_cap = split ? (int)lay.cap : 0;
     p.part_ms = split ? (float*)((char*)workspace + lay.ms) : nullptr;
     p.part_acc = split ? (float*)((char*)workspace + lay.acc) : nullptr;
+    p.split_plan = split ? (int*)((char*)workspace + lay.plan) : nullptr;
     hipEvent_t e0 = t_pf_start, e1 = t_pf_stop;
     t_pf_start = t_pf_stop = nullptr;
     // the split kernel: a 1-D grid over both of its launches' shapes

@@ -39,6 +39,15 @@ __device__ __forceinline__ uint32_t f2b_bits(float f) {
 }
 __device__ __forceinline__ float rbf(float x) { return __uint_as_float(f2b_bits(x) << 16); }
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return f2b_bits(lo) | (f2b_bits(hi) << 16); }
+// x / y for the gated epilogue (y = 1 + exp(-gate) >= 1): the reciprocal
+// and one residual correction (q + (x - y q) / y), which gives IEEE's
+// correctly rounded quotient except in rare last-bit cases, before the
+// bf16 rounding; x / inf is 0 as in IEEE.
+__device__ __forceinline__ float gated_div(float x, float y) {
+    const float r = __builtin_amdgcn_rcpf(y), q = x * r;
+    const float c = __builtin_fmaf(__builtin_fmaf(-y, q, x), r, q);
+    return __builtin_isinf(y) ? 0.f * x : c;
+}
 // Two finite floats to packed bf16 with the hardware's round-to-nearest-even
 // conversion (one v_cvt_pk_bf16_f32); for values that are never NaN.
 typedef float f32x2 __attribute__((ext_vector_type(2)));

@@ -59,6 +59,9 @@ struct PrefillParams {
     int cus, split_cap;
     float* part_ms;
     float* part_acc;
+    // the split kernel's plan for prefill_merge_kernel: parts and the
+    // prompt's query tiles R, written by the split grid's workgroup 0
+    int* split_plan;
 };
 
 // 16 bytes at byte offset `off` of `base` (a uniform address) by a raw
@@ -149,6 +152,9 @@ template <int BQ, int G>
 __device__ __forceinline__ size_t pf_split_rec(int wg, int q, int hh) {
     return ((size_t)wg * BQ + q) * G + hh;
 }
+// Split workgroup index of (query tile x, kv head kvh, range z) among R
+// tiles.
+__device__ __forceinline__ int pf_split_index(int x, int kvh, int z, int R, int Hkv) { return x + R * (kvh + Hkv * z); }
 constexpr size_t prefill_smem_bytes(int nst = PF_NST, int threads = PF_THREADS) {
     return (size_t)nst * PF_STAGE * 2 + pf_ids_bytes(threads);
 }
@@ -471,8 +477,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
 
     // The key tiles this workgroup streams: [kbase, kbase + ntiles * 32).
     int ntiles = (L + PF_BK - 1) / PF_BK, kbase = 0;
+    bool records = false;  // SPL: this tile takes more than one range
     if constexpr (SPL) {
         const int per = pf_split_per(ntiles, parts), t0 = part * per;
+        records = parts > 1 && ntiles > per;
         ntiles = min(ntiles, t0 + per) - t0;
         kbase = t0 * PF_BK;
         if (ntiles <= 0) return;  // whole workgroup: nothing to merge from this range
@@ -708,7 +716,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         }
     }
     }
-    if (SPL && parts > 1) {
+    // a tile with one range writes its gated rows, as the unsplit kernel
+    if (SPL && records) {
 #pragma unroll
         for (int qb = 0; qb < NQB; qb++) {
             const int myq = qcol(qb);
@@ -727,27 +736,67 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         }
         return;
     }
+    // Gated rows: bf16(rbf(O / l) * sigmoid(gate)). The wave's 32 columns
+    // are 32 rows (query, head); lane (lq, lh) holds 4-dim pieces of row lq,
+    // so stores straight from the accumulators would hit 32 rows per
+    // instruction. Instead each wave stages rbf(O / l) as bf16 (hardware
+    // round to nearest even, the same bits as rbf) in its own
+    // LDS region, 64 dims at a time (rows of 64 + 8 elements), and reads it
+    // back as 16-byte pieces: lane i takes row 8 k + i / 8, dims 8 (i % 8)
+    // of the pass, so 8 lanes cover 128 contiguous bytes of a row, for the
+    // gate loads and the output stores alike.
+    constexpr int ER = 72;  // staged row stride (elements)
+    static_assert(32 * ER * 2 * (THREADS / 64) <= 2 * pf_stage(PF_VPAIR_TIGHT) * 2, "epilogue staging fits 2 stages");
+    __syncthreads();  // every wave is past the last tile's stage
+    uint16_t* ew = pf_smem + wave * 32 * ER;
+    const int er = lane >> 3, ec = lane & 7;  // read: rows er + 8 k, dims 8 ec of the pass
 #pragma unroll
     for (int qb = 0; qb < NQB; qb++) {
-        const int myq = qcol(qb);
-        if (myq >= nb) continue;
         const float inv = l[qb] > 0.f ? 1.f / l[qb] : 0.f;
-        const size_t t = (size_t)tb + myq;
-        const uint16_t* gate = p.qkv + t * p.qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM;
-        uint16_t* orow = p.out + (t * p.Hq + h) * HEAD_DIM;
+        // row r of the staged tile is the column of lane lq = r
+        auto row_q = [&](int r) { return PAIRED ? (r & 15) : (qb0 + qb) * 32 + r; };
+        auto row_h = [&](int r) { return kvh * G + (PAIRED ? 2 * wave + (r >> 4) : wave % G); };
+        // gate pieces of every pass, requested up front
+        uint4 graw[4][4];
 #pragma unroll
-        for (int db = 0; db < 8; db++)
+        for (int ps = 0; ps < 4; ps++)
 #pragma unroll
-            for (int g4 = 0; g4 < 4; g4++) {
-                const int d = 32 * db + 8 * g4 + 4 * lh;
-                const uint2 graw = *reinterpret_cast<const uint2*>(gate + d);
-                const f32x16& oo = o[qb][db];
-                *reinterpret_cast<uint2*>(orow + d) =
-                    make_uint2(pack2(rbf(oo[4 * g4] * inv) / (1.f + __expf(-bf_lo(graw.x))),
-                                     rbf(oo[4 * g4 + 1] * inv) / (1.f + __expf(-bf_hi(graw.x)))),
-                               pack2(rbf(oo[4 * g4 + 2] * inv) / (1.f + __expf(-bf_lo(graw.y))),
-                                     rbf(oo[4 * g4 + 3] * inv) / (1.f + __expf(-bf_hi(graw.y)))));
+            for (int k = 0; k < 4; k++) {
+                const int r = er + 8 * k, q = row_q(r);
+                const size_t t = (size_t)tb + (q < nb ? q : 0);
+                graw[ps][k] = *reinterpret_cast<const uint4*>(p.qkv + t * p.qstride + (size_t)row_h(r) * 2 * HEAD_DIM +
+                                                              HEAD_DIM + 64 * ps + 8 * ec);
             }
+#pragma unroll
+        for (int ps = 0; ps < 4; ps++) {
+            // dims 64 ps + 32 (db - 2 ps) + 8 g4 + 4 lh of row lq
+#pragma unroll
+            for (int db = 2 * ps; db < 2 * ps + 2; db++)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const f32x16& oo = o[qb][db];
+                    *reinterpret_cast<uint2*>(ew + lq * ER + 32 * (db - 2 * ps) + 8 * g4 + 4 * lh) =
+                        make_uint2(pack2_hw(oo[4 * g4] * inv, oo[4 * g4 + 1] * inv),
+                                   pack2_hw(oo[4 * g4 + 2] * inv, oo[4 * g4 + 3] * inv));
+                }
+            wave_sync();
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int r = er + 8 * k, q = row_q(r);
+                const uint4 y = *reinterpret_cast<const uint4*>(ew + r * ER + 8 * ec);
+                const uint4 g = graw[ps][k];
+                const uint32_t yw[4] = {y.x, y.y, y.z, y.w}, gw[4] = {g.x, g.y, g.z, g.w};
+                uint32_t ow[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    ow[j] = pack2_hw(gated_div(bf_lo(yw[j]), 1.f + __expf(-bf_lo(gw[j]))),
+                                     gated_div(bf_hi(yw[j]), 1.f + __expf(-bf_hi(gw[j]))));
+                if (q < nb)
+                    *reinterpret_cast<uint4*>(p.out + (((size_t)tb + q) * p.Hq + row_h(r)) * HEAD_DIM + 64 * ps +
+                                              8 * ec) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+            }
+            wave_sync();  // the region is rewritten by the next pass
+        }
     }
 }
 
@@ -787,6 +836,15 @@ __global__ void __launch_bounds__(pf_fine_threads(G), 2) prefill_fine_kernel(Pre
     prefill_body<G, pf_fine_bq(G), 1, false, 2, PF_VPAIR_TIGHT>(p, pf_smem);
 }
 
+// How prefill_split_kernel splits the prompt's R query tiles (called by
+// whole waves, uniform results): parts = pf_split_parts(R Hkv, cus) ranges
+// per tile when R Hkv < cus (each tile's keys cut evenly), else, or when
+// the grid would exceed the workspace (split_cap workgroups), 1.
+__device__ __forceinline__ int pf_split_plan(const PrefillParams& p, int R) {
+    const int w = R * p.Hkv, parts = pf_split_parts(w, p.cus);
+    return (long)parts * w > p.split_cap ? 1 : parts;
+}
+
 // Index b (< n) of a grid of n workgroups in an order where consecutive
 // indices share an XCD: the dispatcher hands workgroup ids to the 8 XCDs in
 // turn, and id b becomes index b / 8 of its XCD's contiguous share of the
@@ -799,23 +857,27 @@ __device__ __forceinline__ int xcd_major(int b, int n) {
 // Split keys (pkv_attn_prefill_split / _e4m3_split): a 1-D grid of at least
 // max(host tile bound x kv heads, 2 cus) workgroups. The kernel counts the
 // prompt's R query tiles from cu (the host only bounds them) and takes
-// parts = pf_split_parts(R Hkv, cus) ranges per tile: workgroup l = x + R
-// (kvh + Hkv part) is tile x, kv head kvh, key range part, and the rest of
-// the grid returns. With parts > 1 (one or two rounds over the CUs) the
-// tiles of one (kv head, range) go to one XCD, which then reads those keys
-// through one L2, and each workgroup leaves records for
-// prefill_merge_kernel; with parts = 1 (a grid that fills the CUs) it is
-// the library kernel's launch, longest tiles first, rows written directly.
+// parts = pf_split_plan ranges per tile: workgroup l = x + R (kvh + Hkv
+// part) is tile x, kv head kvh, key range part, and the rest of the grid
+// returns. With parts > 1 (one or two rounds over the CUs) the tiles of one
+// (kv head, range) go to one XCD, which then reads those keys through one
+// L2; a tile that takes more than one range leaves records for
+// prefill_merge_kernel, a tile with one range writes its gated rows. With
+// parts = 1 (a grid that fills the CUs) it is the library kernel's launch,
+// longest tiles first, rows written directly. The plan goes to
+// p.split_plan for the merge.
 template <int G, bool F8 = false>
 __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_split_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
     constexpr int BQ = pf_lib_bq(G), NQB = pf_lib_nqb(G);
     // (uniform values: readfirstlane keeps them in SGPRs for the DMA bases)
     const int R = __builtin_amdgcn_readfirstlane(prompt_tiles<BQ>(p));
-    int parts = pf_split_parts(R * p.Hkv, p.cus);
-    if (parts * R * p.Hkv > p.split_cap) parts = 1;
-    parts = __builtin_amdgcn_readfirstlane(parts);
+    const int parts = __builtin_amdgcn_readfirstlane(pf_split_plan(p, R));
     const int n = parts * R * p.Hkv, b = blockIdx.x;
+    if (b == 0 && threadIdx.x == 0 && p.split_plan) {
+        p.split_plan[0] = parts;
+        p.split_plan[1] = R;
+    }
     if (b >= n) return;
     const int l = parts > 1 ? xcd_major(b, n) : b;
     const int x = __builtin_amdgcn_readfirstlane(l % R), kvh = __builtin_amdgcn_readfirstlane((l / R) % p.Hkv),
@@ -842,10 +904,9 @@ template <int G>
 __global__ void __launch_bounds__(64 * G) prefill_merge_kernel(PrefillParams p) {
     constexpr int BQ = pf_lib_bq(G);
     const int t = blockIdx.x, kvh = blockIdx.y, hh = threadIdx.x >> 6, h = kvh * G + hh, lane = threadIdx.x & 63;
-    // nothing to merge without a split
-    const int total = prompt_tiles<BQ>(p);
-    const int parts = pf_split_parts(total * p.Hkv, p.cus);
-    if (parts == 1 || parts * total * p.Hkv > p.split_cap) return;
+    // nothing to merge without a split (the split kernel's plan)
+    const int parts = p.split_plan[0], total = p.split_plan[1];
+    if (parts <= 1) return;
     // the sequence holding row t: the last s with cu[s] <= t
     int lo = 0, hi = p.seqs - 1;
     while (lo < hi) {
@@ -864,7 +925,9 @@ __global__ void __launch_bounds__(64 * G) prefill_merge_kernel(PrefillParams p) 
     // the split kernel's x of this tile (tiles run last first)
     const int x = total - 1 - (before + (t - c0) / BQ);
     const int nt = (p.pos[tb] + nb + PF_BK - 1) / PF_BK, per = pf_split_per(nt, parts);
-    auto rec = [&](int z) { return pf_split_rec<BQ, G>((z * p.Hkv + kvh) * total + x, t - tb, hh); };
+    // a tile with one range wrote its rows itself
+    if (nt <= per) return;
+    auto rec = [&](int z) { return pf_split_rec<BQ, G>(pf_split_index(x, kvh, z, total, p.Hkv), t - tb, hh); };
     merge_rows<1>(
         (nt + per - 1) / per, 1.f, [&](int z) { return p.part_ms + rec(z) * 2; },
         [&](int z) { return p.part_acc + rec(z) * HEAD_DIM; },
