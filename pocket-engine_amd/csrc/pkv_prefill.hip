@@ -314,7 +314,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     // This wave's queries: blocks qb0 + qb (queries 32 (qb0 + qb) + lq of the
     // tile), q^T operands scaled into log2 units.
     bf16x8 qf[NQB][16];
-    {
+    // (called once the tile path has requested its first page ids, so the
+    // q loads overlap that request)
+    auto load_q = [&]() __attribute__((always_inline)) {
         const float f = p.scale * LOG2E;
 #pragma unroll
         for (int qb = 0; qb < NQB; qb++) {
@@ -324,13 +326,15 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
 #pragma unroll
             for (int kk = 0; kk < 16; kk++) {
                 uint4 raw = ok ? *reinterpret_cast<const uint4*>(qrow + 16 * kk + 8 * lh) : make_uint4(0, 0, 0, 0);
-                // (outside the key loop: exact software rounding, NaN-preserving)
-                raw = make_uint4(pack2(bf_lo(raw.x) * f, bf_hi(raw.x) * f), pack2(bf_lo(raw.y) * f, bf_hi(raw.y) * f),
-                                 pack2(bf_lo(raw.z) * f, bf_hi(raw.z) * f), pack2(bf_lo(raw.w) * f, bf_hi(raw.w) * f));
+                // round to nearest even (the hardware conversion)
+                raw = make_uint4(pack2_hw(bf_lo(raw.x) * f, bf_hi(raw.x) * f),
+                                 pack2_hw(bf_lo(raw.y) * f, bf_hi(raw.y) * f),
+                                 pack2_hw(bf_lo(raw.z) * f, bf_hi(raw.z) * f),
+                                 pack2_hw(bf_lo(raw.w) * f, bf_hi(raw.w) * f));
                 qf[qb][kk] = as_bf16x8(raw);
             }
         }
-    }
+    };
     f32x16 o[NQB][8];
 #pragma unroll
     for (int qb = 0; qb < NQB; qb++)
@@ -626,6 +630,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
 #pragma unroll
         for (int t = 0; t < 4; t++)
             if (t < ntiles) dma_ids(kbase + t * PF_BK, t);
+        load_q();
         wait_vm<0>();
         dma_tile(kbase, 0, 0);
         if constexpr (NST == 2) {
@@ -681,6 +686,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     } else {
     // Only the first LDT threads load and store tiles.
     if (UPAGE && loader) fetch_ids(kbase);
+    load_q();
     // NST 3: iteration i stores tile i + 1 (loaded during iteration i - 1)
     // into the stage tile i - 2 used, requests tile i + 2, computes tile i,
     // then one barrier. NST 2: iteration i requests tile i + 1, computes
