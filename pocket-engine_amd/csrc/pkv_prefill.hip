@@ -724,21 +724,43 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     }
     // a tile with one range writes its gated rows, as the unsplit kernel
     if (SPL && records) {
+        // Records (f32) go out as the gated rows do: each wave stages its
+        // 32 rows, 64 dims a pass (rows of 64 + 4 floats), and writes 16-byte
+        // pieces with 16 lanes per 256 contiguous bytes of a record.
+        constexpr int RR = 68;  // staged row stride (floats)
+        static_assert(32 * RR * 4 * (THREADS / 64) <= PF_NST * PF_STAGE * 2, "record staging fits the stages");
+        __syncthreads();  // every wave is past the last tile's stage
+        float* rw = reinterpret_cast<float*>(pf_smem) + wave * 32 * RR;
+        const int rr = lane >> 4, rc = lane & 15;  // read: rows rr + 4 k, floats 4 rc of the pass
 #pragma unroll
         for (int qb = 0; qb < NQB; qb++) {
-            const int myq = qcol(qb);
-            if (myq >= nb) continue;
-            const size_t r = pf_split_rec<BQ, G>(wg, myq, h - kvh * G);
-            float* acc = p.part_acc + r * HEAD_DIM;
+            auto row_q = [&](int r) { return PAIRED ? (r & 15) : (qb0 + qb) * 32 + r; };
+            auto row_hh = [&](int r) { return PAIRED ? 2 * wave + (r >> 4) : wave % G; };
+            if (lh == 0 && qcol(qb) < nb) {
+                const size_t r = pf_split_rec<BQ, G>(wg, qcol(qb), h - kvh * G);
+                *reinterpret_cast<float2*>(p.part_ms + r * 2) = make_float2(m[qb], l[qb]);
+            }
 #pragma unroll
-            for (int db = 0; db < 8; db++)
+            for (int ps = 0; ps < 4; ps++) {
 #pragma unroll
-                for (int g4 = 0; g4 < 4; g4++) {
-                    const f32x16& oo = o[qb][db];
-                    *reinterpret_cast<float4*>(acc + 32 * db + 8 * g4 + 4 * lh) =
-                        make_float4(oo[4 * g4], oo[4 * g4 + 1], oo[4 * g4 + 2], oo[4 * g4 + 3]);
+                for (int db = 2 * ps; db < 2 * ps + 2; db++)
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; g4++) {
+                        const f32x16& oo = o[qb][db];
+                        *reinterpret_cast<float4*>(rw + lq * RR + 32 * (db - 2 * ps) + 8 * g4 + 4 * lh) =
+                            make_float4(oo[4 * g4], oo[4 * g4 + 1], oo[4 * g4 + 2], oo[4 * g4 + 3]);
+                    }
+                wave_sync();
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const int r = rr + 4 * k, q = row_q(r);
+                    const float4 v = *reinterpret_cast<const float4*>(rw + r * RR + 4 * rc);
+                    if (q < nb)
+                        *reinterpret_cast<float4*>(p.part_acc + pf_split_rec<BQ, G>(wg, q, row_hh(r)) * HEAD_DIM +
+                                                   64 * ps + 4 * rc) = v;
                 }
-            if (lh == 0) *reinterpret_cast<float2*>(p.part_ms + r * 2) = make_float2(m[qb], l[qb]);
+                wave_sync();  // the region is rewritten by the next pass
+            }
         }
         return;
     }
