@@ -300,8 +300,9 @@ int pkv_attn_prefill(const void* q, const void* kcache, const void* vcache, cons
  * pkv_attn_prefill (G = 6 / 8 grids whose tile bound fills the CUs but not
  * four rounds run pkv_attn_prefill's kernel). No counterpart in the
  * reference's prompt kernels (attn_mfma / attn_flash_group have no split).
- * pkv_attn_prefill_workspace gives the bytes for these shapes: records for
- * at most max(2 min((ceil(T / BQ) + seqs) Hkv, CUs - 1), CUs) workgroups
+ * pkv_attn_prefill_workspace gives the bytes for these shapes: 256 bytes
+ * where the split launch leaves its plan for the merge launch, then records
+ * for at most max(2 min((ceil(T / BQ) + seqs) Hkv, CUs - 1), CUs) workgroups
  * of BQ x G rows of 1,032 bytes (BQ = 256 / G queries, 32 for G = 6 / 8),
  * 68 MB at G = 4 on 256 CUs while that bound is 128 workgroups or fewer. Results
  * within the attention tolerance of pkv_attn_prefill (only the points where
