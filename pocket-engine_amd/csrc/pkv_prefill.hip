@@ -503,12 +503,41 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
 #pragma unroll
                 for (int r = 0; r < 16; r++) st[qb][r] = 0.f;
             const uint16_t* krow = K + pf_krow(lq) + 8 * lh;
+            // The bf16 three-stage LDS-DMA kernels (library and split, G != 6)
+            // read K fragments four MFMAs ahead: the scheduler left two, and
+            // each pair of MFMAs waited on its reads (C4 +2 %, one 4,096-token
+            // prompt -4 %, at 28 more bytes of scratch per lane). Elsewhere
+            // the extra registers cost more than the waits.
+            constexpr bool KDEEP = DMA && !F8 && NST == 3 && G != 6;
+            if constexpr (KDEEP) {
+                constexpr int KD = 4;  // K fragments in flight
+                uint4 kf[KD];
 #pragma unroll
-            for (int kk = 0; kk < 16; kk++) {
-                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 16 * kk));
+                for (int i = 0; i < KD; i++) kf[i] = *reinterpret_cast<const uint4*>(krow + 16 * i);
 #pragma unroll
-                for (int qb = 0; qb < NQB; qb++)
-                    st[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb][kk], st[qb], 0, 0, 0);
+                for (int kk = 0; kk < 16; kk++) {
+                    const bf16x8 a = as_bf16x8(kf[kk % KD]);
+                    if (kk + KD < 16) kf[kk % KD] = *reinterpret_cast<const uint4*>(krow + 16 * (kk + KD));
+#pragma unroll
+                    for (int qb = 0; qb < NQB; qb++)
+                        st[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb][kk], st[qb], 0, 0, 0);
+                }
+                // 4 DS reads, then (MFMA, DS read) x 12, then 4 MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+                for (int i = 0; i < 12; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < 16; kk++) {
+                    const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 16 * kk));
+#pragma unroll
+                    for (int qb = 0; qb < NQB; qb++)
+                        st[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb][kk], st[qb], 0, 0, 0);
+                }
             }
             uint4 pb[NQB][2];
 #pragma unroll
