@@ -503,12 +503,13 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
 #pragma unroll
                 for (int r = 0; r < 16; r++) st[qb][r] = 0.f;
             const uint16_t* krow = K + pf_krow(lq) + 8 * lh;
-            // The bf16 three-stage LDS-DMA kernels (library and split, G != 6)
-            // read K fragments four MFMAs ahead: the scheduler left two, and
-            // each pair of MFMAs waited on its reads (C4 +2 %, one 4,096-token
-            // prompt -4 %, at 28 more bytes of scratch per lane). Elsewhere
-            // the extra registers cost more than the waits.
-            constexpr bool KDEEP = DMA && !F8 && NST == 3 && G != 6;
+            // The bf16 LDS-DMA tile paths (library, split, fine and
+            // code-object kernels, G != 6) read K fragments four MFMAs ahead:
+            // the scheduler left two, and each pair of MFMAs waited on its
+            // reads (C4 +2 %, one 4,096-token prompt -4 %, a 2,048-token chunk
+            // on the fine kernel and the code object -4 / -5 %). The E4M3 and
+            // G = 6 kernels keep the scheduler's order (more scratch).
+            constexpr bool KDEEP = DMA && !F8 && G != 6;
             if constexpr (KDEEP) {
                 constexpr int KD = 4;  // K fragments in flight
                 uint4 kf[KD];
