@@ -180,6 +180,9 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="report the eager step only (default: the K steps are also captured into one HIP graph and "
                          "replayed, as the reference engine replays its decode step, and value is the replayed step)")
+    ap.add_argument("--passes", type=int, default=5,
+                    help="timed passes over the K steps (eager with kernel events, then one graph replay, "
+                         "alternating); the reported step and kernel times are medians over the passes")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run kernels of known traffic (2 GiB copy, read-only sum, fill; x3 each), to scale rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE")
@@ -365,29 +368,16 @@ def main():
             pkv.time_next_range_kernel(ev[0], ev[1])
         step_on(i, stream, ev)
 
-    kev = HipEvents(args.steps)
+    P = max(1, args.passes)
+    kev = HipEvents(args.steps * P)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    # Timed region: K steps; events bracket the dominant kernel of each step
-    # (the fused step kernel, or the key-range kernel with --unfused).
-    evs = kev.pairs
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(stream)
-    for k in range(args.steps):
-        step(args.warmup + k, evs[k])
-    t1.record(stream)
-    torch.cuda.synchronize()
-    total_ms = t0.elapsed_time(t1)
-    kern_ms = kev.elapsed_ms()
-    ms_step = total_ms / args.steps
-
-    graph_us = None
+    g = None
     if not args.no_graph:
-        # The same K steps captured into one HIP graph and replayed: the
-        # device time without per-launch dispatch gaps (the reference engine
-        # replays a captured graph per step, src/engine.rs:704-720).
+        # The same K steps captured into one HIP graph (the reference engine
+        # replays a captured graph per step, src/engine.rs:704-720); one
+        # untimed replay before the timed passes.
         g = torch.cuda.CUDAGraph()
         cs = torch.cuda.Stream()
         cs.wait_stream(torch.cuda.current_stream())
@@ -399,12 +389,40 @@ def main():
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
-        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        g0.record(stream)
-        g.replay()
-        g1.record(stream)
+    # P timed passes, each over the same K steps (the appends rewrite the
+    # same slots with the same rows, so every pass is the same workload):
+    # an eager pass whose events bracket the dominant kernel of every step
+    # (the fused step kernel, or the key-range kernel with --unfused), then
+    # one replay of the graph, each bracketed by synchronize. Eager and graph
+    # passes alternate so the kernel time and the step time are taken under
+    # the same clocks; the reported figures are medians over the passes.
+    eager_ms, graph_ms, kern_pass_ms, kern_ms = [], [], [], []
+    for r in range(P):
+        evs = kev.pairs[r * args.steps:(r + 1) * args.steps]
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        graph_us = 1e3 * g0.elapsed_time(g1) / args.steps
+        t0.record(stream)
+        for k in range(args.steps):
+            step(args.warmup + k, evs[k])
+        t1.record(stream)
+        torch.cuda.synchronize()
+        eager_ms.append(t0.elapsed_time(t1))
+        if g is not None:
+            g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            g0.record(stream)
+            g.replay()
+            g1.record(stream)
+            torch.cuda.synchronize()
+            graph_ms.append(g0.elapsed_time(g1))
+    all_kern = kev.elapsed_ms()
+    for r in range(P):
+        km = all_kern[r * args.steps:(r + 1) * args.steps]
+        kern_ms += km
+        kern_pass_ms.append(sum(km))
+    med = lambda xs: float(np.median(np.asarray(xs)))
+    total_ms = med(eager_ms)
+    ms_step = total_ms / args.steps
+    graph_us = None if g is None else 1e3 * med(graph_ms) / args.steps
 
     keys = [meta.keys(args.warmup + k) for k in range(args.steps)]
     if e4m3:
@@ -428,9 +446,10 @@ def main():
                  "verify_range_kernel<4>" if args.verify_kernel else "decode_range_kernel<4,false>")
     else:
         kern_bytes = step_bytes  # the fused kernel does the whole step
-        kname = "decode_range_kernel<4,true> (fused append + attention + merge)"
-    kern_avg_us = 1e3 * sum(kern_ms) / len(kern_ms)
-    kern_gbs = sum(kern_bytes) / (sum(kern_ms) * 1e-3) / 1e9
+        kname = "decode_range_kernel<4,true> (fused append + key ranges; the merge is a second launch)"
+    kern_med_pass_ms = med(kern_pass_ms)  # the median pass's K kernel durations, summed
+    kern_avg_us = 1e3 * kern_med_pass_ms / args.steps
+    kern_gbs = sum(kern_bytes) / (kern_med_pass_ms * 1e-3) / 1e9
 
     copy_gbs, read_gbs = hbm_copy_probe(dev)
     # algorithmic bytes of the dominant kernel over the child's steps 0 .. 3
@@ -463,7 +482,11 @@ def main():
         "ms_per_step": round(step_ms, 5),
         "us_per_step": round(step_ms * 1e3, 2),
         "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
-        "step_timing": "eager" if graph_us is None else "HIP graph replay of the K steps",
+        "step_timing": (f"eager: median of {P} passes of the K steps" if graph_us is None else
+                        f"HIP graph replay of the K steps: median of {P} replays, each alternating with an eager "
+                        "pass that times the kernel"),
+        "us_per_step_passes": [round(1e3 * x / args.steps, 2) for x in (graph_ms if graph_ms else eager_ms)],
+        "kernel_us_passes": [round(1e3 * x / args.steps, 2) for x in kern_pass_ms],
         "us_per_step_eager": round(ms_step * 1e3, 2),
         "gbs_eager": round(gbs_eager, 1),
         "higher_is_better": True,
@@ -479,7 +502,8 @@ def main():
                    "path": ("attn_prep (E4M3 store), key ranges over the E4M3 cache, merge" if e4m3 else
                             f"reference-ABI code object (append, attn_paged_g{G}, attn_merge)" if args.refabi else
                             "attn_prep (norm + rotary + append), key ranges, merge" if args.with_prep else
-                            "unfused (append, key ranges, merge)" if args.unfused else "fused step (one launch)"),
+                            "unfused (append, key ranges, merge)" if args.unfused else
+                            "fused step (two launches: append + key ranges, then merge)"),
                    "batch": B, "ctx": "4096" if args.config == "c2" else "U[512,8192]", "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page": BS,
                    "pool_pages": pages, "seed": seed, "mean_keys_per_step": round(float(np.mean(keys)), 1),
                    "parallelism": "single GPU"},
@@ -1097,6 +1121,7 @@ def cpu_baseline(kc, vc, q, qkv, meta, st, Hq, Hkv, qstride, dev):
                 break
     us_step_mt = total_mt / reps_mt * 1e6 * full_keys / sample_keys
     return {"value": round(us_step_mt, 1), "unit": "us/step", "cores": nthr, "kind": "port",
+            "arith": "f64 (the oracle: scalar C, scores, softmax and weighted sums in double)",
             "sample": f"oracle append + decode of one full step: all {len(sel)} sequences, {sample_keys} keys, "
                       f"{nthr} threads (tokens split into key-balanced sets), {reps_mt} repetitions in "
                       f"{total_mt:.1f} s; 1 thread: {reps} repetitions in {total:.1f} s, {dt:.2f} s per step "

@@ -172,8 +172,7 @@ int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_str
 
 /* pkv_attn_decode_step without a workspace argument, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). No counterpart in the reference (whose split partials
- * come from a caller buffer, model.rs:1490-1494). The workspace is a
+ * forbid hipMalloc). It has no counterpart in the reference. The workspace is a
  * file-scope device array of PKV_NOALLOC_SCRATCH_BYTES per GPU; the call
  * allocates nothing (no hipMalloc / hipFree, no allocating library routine).
  * Same arguments and results as pkv_attn_decode_step otherwise. Returns
@@ -254,8 +253,9 @@ int pkv_time_next_prefill_kernel(void* start_event, void* stop_event);
  * f32 amax / 448 per 128 columns at fs[(col / 128) * frows + t], mode 2 one
  * E8M0 byte per 32 columns in the 128-row x 4-block tiles of MXFP8. Rows the
  * call skips get none. frows (the engine's row capacity) must be >= T. The
- * request is cleared by the call that runs the merge (a _split call keeps
- * it for its _merge); fmode 0 clears it. While it is set, every row is
+ * request is cleared by the next call that runs the merge (a _split call
+ * keeps it for its _merge), also when that call fails its argument checks
+ * and writes nothing; fmode 0 clears it. While it is set, every row is
  * finished by the merge kernel (the key-range kernel leaves a partial record
  * for every piece), which costs a little time. */
 int pkv_attn_fp8_next(void* fq, void* fs, int fmode, int frows);

@@ -480,16 +480,20 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
                        const int32_t* block_table, int max_blocks, int block_size, void* out, float scale,
                        const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T, int64_t num_blocks,
                        void* workspace, size_t workspace_bytes, void* stream) {
+    // A call that merges consumes a pending FP8 output request before any
+    // check, so a call that fails leaves no request behind for the next one.
+    pkv::Fp8Out fo = {nullptr, nullptr, 0, 0};
+    if (phases & 6) {
+        fo = t_fp8;
+        t_fp8 = {nullptr, nullptr, 0, 0};
+    }
     if (T < 0 || Hq <= 0 || Hkv <= 0 || max_blocks <= 0 || num_blocks <= 0 || spec < 1) return PKV_ERR_INVALID;
     const int G = Hkv > 0 && Hq % Hkv == 0 ? Hq / Hkv : 0;
     if (!supported_group(G) || block_size != 16 || (Hkv > 4 && Hkv % 4 != 0)) return PKV_ERR_UNSUPPORTED;
     // The fused step's kernel is the G = 4 decode body.
     if ((phases & 4) && G != 4) return PKV_ERR_UNSUPPORTED;
     if (num_blocks > (int64_t)INT32_MAX / 16) return PKV_ERR_INVALID;
-    if (T == 0) {
-        if (phases & 6) t_fp8 = {nullptr, nullptr, 0, 0};  // a call that merges consumes the request
-        return PKV_OK;
-    }
+    if (T == 0) return PKV_OK;
     if (!q || !kcache || !vcache || !qkv || !pos || !tok_seq || !block_table || !out || !workspace)
         return PKV_ERR_INVALID;
     const bool f8 = kscale != nullptr;
@@ -515,9 +519,7 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
     const int n_wg = decode_n_wg() * (f8 ? F8_WG_PER_CU : 1);
     const DecodeLayout lay = decode_layout(T, Hq, n_wg, verify);
     if (workspace_bytes < lay.total) return PKV_ERR_INVALID;
-    const pkv::Fp8Out fo = t_fp8;
     if (fo.mode && T > fo.rows) return PKV_ERR_INVALID;
-    if (phases & 6) t_fp8 = {nullptr, nullptr, 0, 0};  // consumed by the call that merges
     pkv::DecodeParams p;
     p.fo = fo;
     p.q = (const uint16_t*)q;
@@ -634,7 +636,10 @@ int pkv_attn_decode_e4m3(const void* q, const void* kcache, const void* vcache, 
                          const int32_t* tok_seq, const int32_t* block_table, int max_blocks, int block_size, void* out,
                          float scale, const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T,
                          int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream) {
-    if (!kscale || !vscale) return PKV_ERR_INVALID;
+    if (!kscale || !vscale) {
+        t_fp8 = {nullptr, nullptr, 0, 0};  // the failed call still consumes a pending FP8 request
+        return PKV_ERR_INVALID;
+    }
     return attn_decode_phases(3, nullptr, kscale, vscale, PKV_DECODE_PASS);
 }
 
@@ -643,7 +648,10 @@ int pkv_attn_verify_e4m3(const void* q, const void* kcache, const void* vcache, 
                          const int32_t* tok_seq, const int32_t* block_table, int max_blocks, int block_size, void* out,
                          float scale, const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T,
                          int64_t num_blocks, void* workspace, size_t workspace_bytes, void* stream) {
-    if (!kscale || !vscale) return PKV_ERR_INVALID;
+    if (!kscale || !vscale) {
+        t_fp8 = {nullptr, nullptr, 0, 0};
+        return PKV_ERR_INVALID;
+    }
     return attn_decode_phases(8 | 3, nullptr, kscale, vscale, PKV_DECODE_PASS);
 }
 
@@ -698,14 +706,19 @@ int pkv_attn_decode_step_noalloc(const void* k_rows, const void* v_rows, int64_t
                                  const int32_t* block_table, int max_blocks, int block_size, void* out, float scale,
                                  const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T,
                                  int64_t num_blocks, void* stream) {
-    if (T < 0 || Hq <= 0) return PKV_ERR_INVALID;
+    if (T < 0 || Hq <= 0 || decode_layout(T, Hq, decode_n_wg()).total > PKV_NOALLOC_SCRATCH_BYTES) {
+        t_fp8 = {nullptr, nullptr, 0, 0};  // the failed call still consumes a pending FP8 request
+        return T < 0 || Hq <= 0 ? PKV_ERR_INVALID : PKV_ERR_UNSUPPORTED;
+    }
     // The fused step runs the bf16 key-range kernel (decode_n_wg() ranges);
     // its layout must fit the array. Nothing in it needs clearing: the range
     // kernel writes every offset and partial the merge reads.
-    if (decode_layout(T, Hq, decode_n_wg()).total > PKV_NOALLOC_SCRATCH_BYTES) return PKV_ERR_UNSUPPORTED;
     void* workspace = nullptr;
     const int st = scratch_ptr(&workspace);
-    if (st != PKV_OK) return st;
+    if (st != PKV_OK) {
+        t_fp8 = {nullptr, nullptr, 0, 0};
+        return st;
+    }
     const size_t workspace_bytes = PKV_NOALLOC_SCRATCH_BYTES;
     const AppendArgs app{k_rows, v_rows, row_stride, slot_map};
     return attn_decode_phases(4 | 2, &app, nullptr, nullptr, PKV_DECODE_PASS);

@@ -157,3 +157,36 @@ def test_fp8_next_is_cleared_by_the_merging_call(dev):
     assert (fq.cpu().numpy() != 0x7F).any()
     with pytest.raises(pkv.PkvError):
         pkv.attn_fp8_next(fq, None, 1, FROWS)
+
+
+@pytest.mark.parametrize("entry", ["decode", "step", "step_noalloc_bad_group"])
+def test_fp8_request_consumed_by_a_failing_call(dev, entry):
+    """A merging call that fails its argument checks still consumes the
+    pending request: the next valid call writes no copies through the stale
+    fq / fs (they may have been freed after the error)."""
+    print(f"case fp8 request consumed by failing {entry}", flush=True)
+    c = decode_case([300, 40, 17], 16, 4, 6)
+    T = len(c["pos"])
+    fq, fs = fp8_buffers(T, 16 * D, 1, FROWS, dev)
+    pkv.attn_fp8_next(fq, fs, 1, 2)  # frows 2 < T: the merging call must refuse it
+    with pytest.raises(pkv.PkvError):
+        run(c, dev, "step" if entry.startswith("step") else "decode")
+    if entry == "step_noalloc_bad_group":
+        # a second request, refused by the no-allocation step's group check
+        pkv.attn_fp8_next(fq, fs, 1, FROWS)
+        cc = decode_case([50], 24, 4, 7)
+        q, qkv = t_(cc["q"], dev), t_(cc["qkv"], dev)
+        pos, ts, bt, cu = (t_(np.asarray(cc[k], np.int32), dev) for k in ("pos", "tok_seq", "bt", "cu"))
+        kc, vc = t_(cc["kc"], dev), t_(cc["vc"], dev)
+        out = torch.zeros(1, 24, D, dtype=torch.int16, device=dev)
+        slot = t_(np.zeros(1, np.int32), dev)
+        with pytest.raises(pkv.PkvError):
+            pkv.attn_decode_step_noalloc(qkv.data_ptr(), qkv.data_ptr(), 2 * 4 * D * 2, slot, q, kc, vc, qkv,
+                                         cc["qstride"], 24, 4, pos, ts, bt, cc["max_blocks"], BS, out, SCALE, cu, 0,
+                                         None, 1, 1, cc["pages"])
+    got = run(c, dev, "decode")
+    torch.cuda.synchronize()
+    assert (fq.cpu().numpy() == 0x7F).all() and torch.isnan(fs).all()
+    ok, err = close(got, oracle.attn_decode(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], 16, 4, c["pos"],
+                                            c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])[0])
+    assert ok, err
