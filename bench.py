@@ -198,7 +198,7 @@ def main():
                          "reference's attn_prep) on the raw qkv rows, followed by the key ranges and the merge")
     ap.add_argument("--q-heads", type=int, default=16,
                     help="query heads over the 4 kv heads (16: the configs' G = 4; 24: the reference's 27B shape, "
-                         "G = 6; c2/c3 then run unfused: append, then decode attention)")
+                         "G = 6, whose fused step is the verify kernel with the append fused in)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the HBM traffic measurement (two short child runs of the same workload under "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by 2 GiB device copies in the same runs)")
@@ -257,8 +257,6 @@ def main():
     dev = torch.device("cuda:0")
     Hq, Hkv, D, BS = args.q_heads, 4, 256, 16
     G = Hq // Hkv
-    if G != 4:
-        args.unfused = True  # the fused step serves G = 4
     B, pages = args.batch, args.pages
     S = args.warmup + args.steps
     if args.config == "c2":
@@ -446,7 +444,8 @@ def main():
                  "verify_range_kernel<4>" if args.verify_kernel else "decode_range_kernel<4,false>")
     else:
         kern_bytes = step_bytes  # the fused kernel does the whole step
-        kname = "decode_range_kernel<4,true> (fused append + key ranges; the merge is a second launch)"
+        kname = (f"decode_range_kernel<4,true>" if G == 4 else f"verify_range_kernel<{G},true>") + \
+            " (fused append + key ranges; the merge is a second launch)"
     kern_med_pass_ms = med(kern_pass_ms)  # the median pass's K kernel durations, summed
     kern_avg_us = 1e3 * kern_med_pass_ms / args.steps
     kern_gbs = sum(kern_bytes) / (kern_med_pass_ms * 1e-3) / 1e9

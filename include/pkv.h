@@ -155,9 +155,10 @@ int pkv_attn_decode_merge(const void* q, const void* kcache, const void* vcache,
  * are consecutive rows cu[s] .. cu[s+1]-1 at consecutive positions and
  * slot_map[t] is the slot of pos[t]. Keys at positions the step itself feeds
  * are read from k_rows/v_rows; the step's rows are written to the pools.
- * `cu` is required; G = Hq / Hkv = 4 only (PKV_ERR_UNSUPPORTED otherwise;
- * other groups run pkv_append then pkv_attn_decode). row_stride is in bytes
- * (a multiple of 16). No
+ * `cu` is required; G = Hq / Hkv in {1, 2, 4, 6, 8} (G = 4: the decode
+ * key-range kernel; other groups: the verify kernel, rows of a sequence in
+ * segments as pkv_attn_verify, with the append fused in). row_stride is in
+ * bytes (a multiple of 16). No
  * reference counterpart as one call: it saves the append launch. */
 int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map,
                          const void* q, const void* kcache, const void* vcache, const void* qkv, int qstride, int Hq,

@@ -490,8 +490,6 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
     if (T < 0 || Hq <= 0 || Hkv <= 0 || max_blocks <= 0 || num_blocks <= 0 || spec < 1) return PKV_ERR_INVALID;
     const int G = Hkv > 0 && Hq % Hkv == 0 ? Hq / Hkv : 0;
     if (!supported_group(G) || block_size != 16 || (Hkv > 4 && Hkv % 4 != 0)) return PKV_ERR_UNSUPPORTED;
-    // The fused step's kernel is the G = 4 decode body.
-    if ((phases & 4) && G != 4) return PKV_ERR_UNSUPPORTED;
     if (num_blocks > (int64_t)INT32_MAX / 16) return PKV_ERR_INVALID;
     if (T == 0) return PKV_OK;
     if (!q || !kcache || !vcache || !qkv || !pos || !tok_seq || !block_table || !out || !workspace)
@@ -500,10 +498,12 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
     // bf16 decode for G != 4 runs the verify kernels (each row of a
     // sequence's consecutive rows attends its own keys, the same results as
     // one token at a time), which read cu.
-    if (G != 4 && !f8 && (phases & 3)) phases |= 8;
+    // The fused step (bit 4) for G != 4 is the verify kernel with the
+    // append fused in, then the verify merge.
+    if (G != 4 && !f8 && (phases & 7)) phases |= 8;
     if ((skip_prompts || (phases & 8)) && !cu) return PKV_ERR_INVALID;
     const bool verify = phases & 8;
-    if (verify && (phases & 4)) return PKV_ERR_INVALID;
+    if (verify && (phases & 4) && G == 4) return PKV_ERR_INVALID;
     if (f8 && ((phases & 4) || !vscale || !aligned(kscale, 4) || !aligned(vscale, 4))) return PKV_ERR_INVALID;
     if (qstride < 2 * Hq * pkv::HEAD_DIM || qstride % 8 != 0) return PKV_ERR_INVALID;
     if (!aligned(q, 16) || !aligned(kcache, 16) || !aligned(vcache, 16) || !aligned(qkv, 16) || !aligned(out, 16) ||
@@ -552,25 +552,36 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
         hipEvent_t e0 = t_ev_start, e1 = t_ev_stop;
         t_ev_start = t_ev_stop = nullptr;
         using RangeKernel = void (*)(pkv::DecodeParams, const int*, const int*, const int*, const int*, const int*);
+        using RangeKernelS =
+            void (*)(pkv::DecodeParams, const int*, const int*, const int*, const int*, const int*, const int*);
         const RangeKernel rk = verify && f8 ? by_group<RangeKernel>(G, pkv::verify_range8_kernel<1>,
                                                                     pkv::verify_range8_kernel<2>,
                                                                     pkv::verify_range8_kernel<4>,
                                                                     pkv::verify_range8_kernel<6>,
                                                                     pkv::verify_range8_kernel<8>)
-                               : verify ? by_group<RangeKernel>(G, pkv::verify_range_kernel<1>,
-                                                                pkv::verify_range_kernel<2>,
-                                                                pkv::verify_range_kernel<4>,
-                                                                pkv::verify_range_kernel<6>,
-                                                                pkv::verify_range_kernel<8>)
                                : f8 ? by_group<RangeKernel>(G, pkv::decode_range8_kernel<1>,
                                                             pkv::decode_range8_kernel<2>,
                                                             pkv::decode_range8_kernel<4>,
                                                             pkv::decode_range8_kernel<6>,
                                                             pkv::decode_range8_kernel<8>)
                                     : nullptr;
+        const RangeKernelS vk = !verify || f8 ? nullptr
+                                : (phases & 4) ? by_group<RangeKernelS>(G, pkv::verify_range_kernel<1, true>,
+                                                                        pkv::verify_range_kernel<2, true>,
+                                                                        pkv::verify_range_kernel<4, true>,
+                                                                        pkv::verify_range_kernel<6, true>,
+                                                                        pkv::verify_range_kernel<8, true>)
+                                               : by_group<RangeKernelS>(G, pkv::verify_range_kernel<1>,
+                                                                        pkv::verify_range_kernel<2>,
+                                                                        pkv::verify_range_kernel<4>,
+                                                                        pkv::verify_range_kernel<6>,
+                                                                        pkv::verify_range_kernel<8>);
         if (rk)
             hipExtLaunchKernelGGL(rk, dim3(n_wg, groups), dim3(threads), 0, (hipStream_t)stream, e0, e1, 0, p, pos,
                                   tok_seq, block_table, cu, outs);
+        else if (vk)
+            hipExtLaunchKernelGGL(vk, dim3(n_wg, groups), dim3(threads), 0, (hipStream_t)stream, e0, e1, 0, p, pos,
+                                  tok_seq, block_table, cu, outs, slot_map);
         else if (phases & 4)
             hipExtLaunchKernelGGL((pkv::decode_range_kernel<4, true>), dim3(n_wg, groups), dim3(threads), 0,
                                   (hipStream_t)stream, e0, e1, 0, p, pos, tok_seq, block_table, cu, outs, slot_map);
@@ -706,7 +717,9 @@ int pkv_attn_decode_step_noalloc(const void* k_rows, const void* v_rows, int64_t
                                  const int32_t* block_table, int max_blocks, int block_size, void* out, float scale,
                                  const int32_t* cu, int skip_prompts, const int32_t* outs, int spec, int T,
                                  int64_t num_blocks, void* stream) {
-    if (T < 0 || Hq <= 0 || decode_layout(T, Hq, decode_n_wg()).total > PKV_NOALLOC_SCRATCH_BYTES) {
+    // G = 4 runs the decode records, other groups the verify records
+    const bool vrec = Hkv > 0 && Hq != 4 * Hkv;
+    if (T < 0 || Hq <= 0 || decode_layout(T, Hq, decode_n_wg(), vrec).total > PKV_NOALLOC_SCRATCH_BYTES) {
         t_fp8 = {nullptr, nullptr, 0, 0};  // the failed call still consumes a pending FP8 request
         return T < 0 || Hq <= 0 ? PKV_ERR_INVALID : PKV_ERR_UNSUPPORTED;
     }

@@ -480,6 +480,48 @@ __device__ __forceinline__ void decode_piece(const DecodeParams& p, const int* _
         piece_body<G, false>(p, bt, lds, t, kvh, j0, j1, L, INT_MAX, 0, epi);
 }
 
+// The fused step's append, shared by the fused key-range kernels: block
+// (b, y) writes the step's K and V rows of kv heads 4y .. 4y + 3 for tokens
+// b, b + n_wg, .. into their slots (slot_map; -1 or past the pool: skipped).
+// No range of the launch reads these slots from the cache: keys the step
+// feeds come from the source rows. begin() issues the first token's loads
+// before the range search; finish() stores them after it (the latency
+// overlaps the search) and appends the block's other tokens. Block: 64
+// threads per kv head, one uint4 of K or V per thread and token.
+struct StepAppend {
+    long slot = -1;
+    uint4 val;
+    __device__ __forceinline__ const uint4* src(const DecodeParams& p, int t, int i) const {
+        const int per_row = (blockDim.x >> 6) * HEAD_DIM / 8;  // uint4 per K (or V) row slice
+        const bool is_v = i >= per_row;
+        return reinterpret_cast<const uint4*>((is_v ? p.v_rows : p.k_rows) + (size_t)t * p.row_stride +
+                                              (size_t)blockIdx.y * 4 * HEAD_DIM) +
+               (is_v ? i - per_row : i);
+    }
+    __device__ __forceinline__ void store(const DecodeParams& p, long s, int i, uint4 v) const {
+        const int per_row = (blockDim.x >> 6) * HEAD_DIM / 8;
+        const bool is_v = i >= per_row;
+        reinterpret_cast<uint4*>((is_v ? p.vc : p.kc) + ((size_t)s * p.Hkv + blockIdx.y * 4) * HEAD_DIM)
+            [is_v ? i - per_row : i] = v;
+    }
+    __device__ __forceinline__ void begin(const DecodeParams& p, const int* __restrict__ slot_map) {
+        const int b = blockIdx.x;
+        if (b < p.T) {
+            slot = slot_map[b];
+            val = *src(p, b, threadIdx.x);
+        }
+    }
+    __device__ __forceinline__ void finish(const DecodeParams& p, const int* __restrict__ slot_map) const {
+        const int b = blockIdx.x, tid = threadIdx.x;
+        const long cap = p.num_blocks * PAGE;
+        if (slot >= 0 && slot < cap) store(p, slot, tid, val);
+        for (int t = b + p.n_wg; t < p.T; t += p.n_wg) {
+            const long s = slot_map[t];
+            if (s >= 0 && s < cap) store(p, s, tid, *src(p, t, tid));
+        }
+    }
+};
+
 // The workgroup's key range [start, end) of the flattened key space (keys
 // of token t: lenf(t)), cut into equal ranges of R = max(min_range,
 // ceil(W / n_wg)) keys, and the token t0 holding key `start` at offset off0.
@@ -565,31 +607,9 @@ __global__ void __launch_bounds__(256, 1)
     // loads at every piece start.
     __shared__ int sh_pos[256], sh_seq[256];
     const int T = p.T, nthr = blockDim.x, tid = threadIdx.x, b = blockIdx.x;
-    const int nkv = nthr >> 6, kv0 = blockIdx.y * 4;
     const bool tab = T <= nthr;
-    // FUSED: this block appends the step's rows of its kv heads for tokens
-    // b, b + n_wg, .. (no range reads these slots from the cache in this
-    // launch). The first token's loads are issued now and stored after the
-    // range search, so their latency overlaps it.
-    const int per_row = nkv * HEAD_DIM / 8;  // uint4 per K (or V) row slice; 2 per_row == nthr
-    long app_slot = -1;
-    uint4 app_val;
-    auto app_src = [&](int t, int i) {
-        const bool is_v = i >= per_row;
-        return reinterpret_cast<const uint4*>((is_v ? p.v_rows : p.k_rows) + (size_t)t * p.row_stride +
-                                              (size_t)kv0 * HEAD_DIM)[is_v ? i - per_row : i];
-    };
-    auto app_store = [&](int t, long slot, int i, uint4 v) {
-        const bool is_v = i >= per_row;
-        reinterpret_cast<uint4*>((is_v ? p.vc : p.kc) + ((size_t)slot * p.Hkv + kv0) * HEAD_DIM)[is_v ? i - per_row : i] =
-            v;
-    };
-    if constexpr (FUSED) {
-        if (b < T) {
-            app_slot = slot_map[b];
-            app_val = app_src(b, tid);
-        }
-    }
+    StepAppend app;
+    if constexpr (FUSED) app.begin(p, slot_map);
     int start, end, t0, off0;
     const bool any = find_range(
         p,
@@ -602,15 +622,9 @@ __global__ void __launch_bounds__(256, 1)
             return L;
         },
         sh_scan, sh_t0, start, end, t0, off0);
-    if constexpr (FUSED) {
-        if (app_slot >= 0 && app_slot < p.num_blocks * PAGE) app_store(b, app_slot, tid, app_val);
-        for (int t = b + p.n_wg; t < T; t += p.n_wg) {
-            const long slot = slot_map[t];
-            if (slot >= 0 && slot < p.num_blocks * PAGE) app_store(t, slot, tid, app_src(t, tid));
-        }
-    }
+    if constexpr (FUSED) app.finish(p, slot_map);
     if (!any) return;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = kv0 + wave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = blockIdx.y * 4 + wave;
     int t = t0, off = off0;
     while (off < end && t < T) {
         const int L = !tab || p.skip_prompts ? decode_len(t, pos, tok_seq, cu, p.skip_prompts, outs, p.spec)

@@ -70,9 +70,15 @@ __device__ __forceinline__ int seg_len(int t, int T, const int* __restrict__ pos
 // row r, query head kvh * G + g, dims 16 db + 4 gq + i in acc[db][i]; m in
 // log2 units, l the sum of weights (m = -inf, l = 0 when the piece has no
 // key for the row).
-template <int G, class Epi>
+// FUSED (the fused decode step): keys at positions [P0, Ls) of the segment,
+// the ones the step itself feeds, come from the step's source rows (row
+// row0 + position - P0 of k_rows / v_rows) instead of the cache, chosen per
+// lane on the pages that hold such keys (from the page of P0 on); earlier
+// pages take the plain cache addresses.
+template <int G, bool FUSED = false, class Epi>
 __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* __restrict__ bt, uint16_t* vl, int t,
-                                             int kvh, int j0, int j1, const int (&Lr)[VF_ROWS], Epi epi) {
+                                             int kvh, int j0, int j1, const int (&Lr)[VF_ROWS], Epi epi,
+                                             int P0 = INT_MAX, int row0 = 0) {
     constexpr int NR = vf_rows(G);
     const int lane = threadIdx.x & 63, c16 = lane & 15, gq = lane >> 4;
     const int r_me = c16 / G, g_me = c16 % G;
@@ -102,15 +108,27 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
     struct Buf {
         uint4 kb[NK], vb[NV];
     };
-    auto load_k = [&](Buf& B, size_t base, int pi) {
-        const uint16_t* r = p.kc + base + (size_t)c16 * row_elems + 8 * gq;
+    // Address of key `key` of page pi (cache slot row, or with FRESH the
+    // source row of a key the step feeds) plus `off` elements.
+    auto src = [&](const uint16_t* pool, const uint16_t* rows, int pi, size_t base, int key, int off, auto fresh) {
+        const uint16_t* c = pool + base + (size_t)key * row_elems + off;
+        if constexpr (!decltype(fresh)::value) {
+            return c;
+        } else {
+            const int kp = pi * PAGE + key;
+            const uint16_t* f = rows + (ptrdiff_t)(row0 + kp - P0) * p.row_stride + (size_t)kvh * HEAD_DIM + off;
+            return kp >= P0 && kp < j1 ? f : c;
+        }
+    };
+    auto load_k = [&](Buf& B, size_t base, int pi, auto fresh) {
+        const uint16_t* r = src(p.kc, p.k_rows, pi, base, c16, 8 * gq, fresh);
 #pragma unroll
         for (int c = 0; c < NK; c++) B.kb[c] = load_nt(r + 32 * c);
     };
-    auto load_v = [&](Buf& B, size_t base) {
-        const uint16_t* r = p.vc + base + (size_t)(lane >> 5) * row_elems + 8 * (lane & 31);
+    auto load_v = [&](Buf& B, size_t base, int pi, auto fresh) {
 #pragma unroll
-        for (int k = 0; k < NV; k++) B.vb[k] = load_nt(r + (size_t)(2 * k) * row_elems);
+        for (int k = 0; k < NV; k++)
+            B.vb[k] = load_nt(src(p.vc, p.v_rows, pi, base, 2 * k + (lane >> 5), 8 * (lane & 31), fresh));
     };
     // A operand of step c: K dims dim0(c) .. + 7 of key c16
     auto k_frag = [&](const Buf& B, int c) -> bf16x8 {
@@ -128,8 +146,12 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
 
     // One page from buffer B; with PREFETCH, B is refilled with page nxt as
     // soon as its K and V have been consumed.
+    using PLAIN = std::integral_constant<bool, false>;
+    using FRESHM = std::integral_constant<bool, true>;
+    // prefetch: NONE (last page), PLAIN or FRESHM (the next page's mode)
+    struct NONE {};
     auto page = [&](Buf& B, int pi, int nxt, auto prefetch) {
-        constexpr bool PREFETCH = decltype(prefetch)::value;
+        constexpr bool PREFETCH = !std::is_same_v<decltype(prefetch), NONE>;
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < 8; c++) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_frag(B, c), qf[c], s, 0, 0, 0);
@@ -143,8 +165,8 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
         }
         if constexpr (PREFETCH) {
             const size_t next = page_base(nxt);
-            load_k(B, next, nxt);
-            load_v(B, next);
+            load_k(B, next, nxt, prefetch);
+            load_v(B, next, nxt, prefetch);
         }
         const int k0 = pi * PAGE + 4 * gq;
         float sc[4], mx = -INFINITY;
@@ -186,14 +208,27 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
         }
         wave_sync();  // reads done before the next page is staged
     };
-    using NOPF = std::integral_constant<bool, false>;
-    using PF = std::integral_constant<bool, true>;
     const int pg0 = j0 / PAGE, pg1 = (j1 - 1) / PAGE;
+    // first page holding keys the step feeds (none: pg1 + 1)
+    const int pf = FUSED ? max(pg0, min(pg1 + 1, P0 / PAGE)) : pg1 + 1;
     Buf A;
-    load_k(A, page_base(pg0), pg0);
-    load_v(A, page_base(pg0));
-    for (int pi = pg0; pi < pg1; pi++) page(A, pi, pi + 1, PF{});
-    page(A, pg1, 0, NOPF{});
+    if (pf > pg1) {
+        load_k(A, page_base(pg0), pg0, PLAIN{});
+        load_v(A, page_base(pg0), pg0, PLAIN{});
+        for (int pi = pg0; pi < pg1; pi++) page(A, pi, pi + 1, PLAIN{});
+    } else if constexpr (FUSED) {
+        if (pf == pg0) {
+            load_k(A, page_base(pg0), pg0, FRESHM{});
+            load_v(A, page_base(pg0), pg0, FRESHM{});
+        } else {
+            load_k(A, page_base(pg0), pg0, PLAIN{});
+            load_v(A, page_base(pg0), pg0, PLAIN{});
+            for (int pi = pg0; pi < pf - 1; pi++) page(A, pi, pi + 1, PLAIN{});
+            page(A, pf - 1, pf, FRESHM{});
+        }
+        for (int pi = pf; pi < pg1; pi++) page(A, pi, pi + 1, FRESHM{});
+    }
+    page(A, pg1, 0, NONE{});
 
     l = add_xor32(add_xor16(l));
     if (myL == 0) return;
@@ -238,21 +273,27 @@ struct VerifyEpi {
 // tokens), offs[T] = W, offs[T + 1] = R. The bound caps it at 256 VGPRs (no
 // spills); it runs one workgroup per CU (two ranges per CU measured slower:
 // 856 against 817 us at C5).
-template <int G>
+// FUSED (the fused decode step for groups other than 4): the kernel also
+// appends the step's K/V rows (StepAppend) and reads the keys the step feeds
+// from those source rows (verify_piece), so no range waits for a write.
+template <int G, bool FUSED = false>
 __global__ void __launch_bounds__(256, 2)
     verify_range_kernel(DecodeParams p, const int* __restrict__ pos, const int* __restrict__ tok_seq,
                         const int* __restrict__ block_table, const int* __restrict__ cu,
-                        const int* __restrict__ outs) {
+                        const int* __restrict__ outs, const int* __restrict__ slot_map) {
     constexpr int NR = vf_rows(G);
     __shared__ int sh_scan[16];
     __shared__ int sh_t0[2];
     __shared__ __align__(16) uint16_t sh_v[4][VF_LDS];
     const int T = p.T, nthr = blockDim.x, tid = threadIdx.x, b = blockIdx.x;
+    StepAppend app;
+    if constexpr (FUSED) app.begin(p, slot_map);
     int nr, start, end, t0, off0;
-    if (!find_range(
-            p, [&](int t) { return seg_len<NR>(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr); }, sh_scan,
-            sh_t0, start, end, t0, off0))
-        return;
+    const bool any = find_range(
+        p, [&](int t) { return seg_len<NR>(t, T, pos, tok_seq, cu, p.skip_prompts, outs, p.spec, nr); }, sh_scan,
+        sh_t0, start, end, t0, off0);
+    if constexpr (FUSED) app.finish(p, slot_map);
+    if (!any) return;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kvh = blockIdx.y * 4 + wave;
     int t = t0, off = off0;
     while (off < end && t < T) {
@@ -269,7 +310,15 @@ __global__ void __launch_bounds__(256, 2)
             const int seq = __builtin_amdgcn_readfirstlane(tok_seq[t]);
             const int j0 = max(start, off) - off, j1 = min(end, off + Ls) - off;
             const VerifyEpi<G> epi{p, t, kvh, t + b, j0 == 0 && j1 == Ls && !p.fo.mode};
-            verify_piece<G>(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Lr, epi);
+            if constexpr (FUSED) {
+                // the sequence's first row this step and its position
+                const int row0 = __builtin_amdgcn_readfirstlane(cu[seq]);
+                const int P0 = __builtin_amdgcn_readfirstlane(pos[row0]);
+                verify_piece<G, true>(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Lr,
+                                      epi, P0, row0);
+            } else {
+                verify_piece<G>(p, block_table + (size_t)seq * p.max_blocks, sh_v[wave], t, kvh, j0, j1, Lr, epi);
+            }
             off += Ls;
         }
         t++;

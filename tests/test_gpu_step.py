@@ -33,11 +33,12 @@ def default_config():
     pkv.attn_decode_config(1, 32)
 
 
-def step_case(lens, Hkv, seed, per_seq=1):
+def step_case(lens, Hkv, seed, per_seq=1, G=4):
     """A step in which every sequence feeds `per_seq` new tokens (decode,
     or verification of per_seq - 1 drafts) at consecutive positions ending at
-    len - 1; their K/V rows come from qkv rows like the reference's layout."""
-    Hq = 4 * Hkv
+    len - 1; their K/V rows come from qkv rows like the reference's layout.
+    G query heads per kv head."""
+    Hq = G * Hkv
     c = decode_case(lens, Hq, Hkv, seed)
     rng = np.random.default_rng(seed + 100)
     B = len(lens)
@@ -103,6 +104,79 @@ def test_fused_step_matches_unfused_and_oracle(dev, lens, Hkv, per_seq, seed):
     assert np.array_equal(u_kc, o_kc) and np.array_equal(u_vc, o_vc)
     assert np.array_equal(f_out, u_out), "fused and unfused outputs differ"
     ok, err = close(f_out, o_out)
+    assert ok, err
+
+
+@pytest.mark.parametrize("lens,Hkv,per_seq,G,seed", [
+    ([1, 2, 17, 33, 700, 4097], 4, 1, 6, 20),  # the reference's 27B shape (24 q / 4 kv heads)
+    ([900, 1200, 64, 3], 4, 2, 6, 21),         # 2 fresh tokens per sequence: a whole 2-row segment
+    ([3000, 77, 8193], 4, 3, 6, 22),           # 3 fresh: a 2-row segment and a 1-row one
+    ([2000, 3000, 15], 8, 1, 6, 23),           # two kv-head groups
+    ([500, 16, 4100], 4, 2, 8, 24),
+    ([500, 16, 4100], 4, 4, 2, 25),
+    ([500, 16, 4100], 4, 1, 1, 26),
+])
+def test_fused_step_other_groups(dev, lens, Hkv, per_seq, G, seed):
+    """The fused step for G != 4 (the verify kernel with the append fused in,
+    then the verify merge): caches bit-exact against the oracle's append,
+    outputs bit-identical to pkv_append + pkv_attn_decode (the same kernel
+    body reading the cache), within tolerance of the oracle."""
+    print(f"case step G={G} lens={lens} Hkv={Hkv} per_seq={per_seq}", flush=True)
+    c = step_case(lens, Hkv, seed, per_seq, G=G)
+    f_out, f_kc, f_vc = run(c, dev, fused=True)
+    u_out, u_kc, u_vc = run(c, dev, fused=False)
+    o_out, o_kc, o_vc = oracle_step(c)
+    assert np.array_equal(f_kc, o_kc) and np.array_equal(f_vc, o_vc), "fused append differs from the oracle"
+    assert np.array_equal(u_kc, o_kc) and np.array_equal(u_vc, o_vc)
+    assert np.array_equal(f_out, u_out), "fused and unfused outputs differ"
+    ok, err = close(f_out, o_out, what=f"fused step G={G}")
+    assert ok, err
+
+
+def test_fused_step_g6_c3_full_size(dev):
+    """C3 at the 27B shape (batch 64, contexts U[512, 8192], 24 q / 4 kv
+    heads, a 65,536-page pool): the fused step equals append + decode bit for
+    bit on every row and writes the same caches; 8 sequences against the
+    oracle."""
+    from pkv import synth
+    from _util import bits, host_pages, oracle_decode_rows
+    print("case step G=6 c3 full", flush=True)
+    Hq, Hkv, pages = 24, 4, 65536
+    lens = synth.c3_lengths(seed=31)
+    meta = synth.decode_meta(lens, pages, steps=1, seed=31)
+    st = meta.step(0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(31)
+    kc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    vc = (torch.randn(pages * BS, Hkv, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    B = meta.B
+    q = (torch.randn(B, Hq, D, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    qstride = synth.qkv_stride(Hq, Hkv)
+    qkv = (torch.randn(B, qstride, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    pos, ts, cu = i32(st["pos"], dev), i32(st["tok_seq"], dev), i32(st["cu"], dev)
+    slot, bt = i32(st["slot_map"], dev), i32(meta.block_table, dev)
+    ws = torch.empty(pkv.attn_decode_workspace(B, Hq), dtype=torch.uint8, device=dev)
+    k_rows = qkv.data_ptr() + 2 * (2 * Hq * D)
+    v_rows = k_rows + 2 * Hkv * D
+    kc0, vc0 = kc.clone(), vc.clone()
+    out_f = torch.zeros(B, Hq, D, dtype=torch.bfloat16, device=dev)
+    pkv.attn_decode_step(k_rows, v_rows, qstride * 2, slot, q, kc, vc, qkv, qstride, Hq, Hkv, pos, ts, bt,
+                         meta.max_blocks, BS, out_f, SCALE, cu, 0, None, 1, B, pages, ws)
+    out_u = torch.zeros_like(out_f)
+    pkv.append(k_rows, v_rows, qstride * 2, slot, B, Hkv, D * 2, kc0, vc0, pages * BS)
+    pkv.attn_decode(q, kc0, vc0, qkv, qstride, Hq, Hkv, pos, ts, bt, meta.max_blocks, BS, out_u, SCALE, cu, 0, None,
+                    1, B, pages, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(kc.view(torch.int16), kc0.view(torch.int16)) and torch.equal(vc.view(torch.int16),
+                                                                                  vc0.view(torch.int16))
+    assert torch.equal(out_f.view(torch.int16), out_u.view(torch.int16)), "fused and unfused outputs differ"
+    del kc0, vc0
+    sel = np.arange(0, B, 8)
+    need = (st["pos"][sel] + BS) // BS
+    kc_h, vc_h, bt_h, _ = host_pages(kc, vc, meta.block_table[sel], need)
+    want = oracle_decode_rows(bits(q)[sel], kc_h, vc_h, bits(qkv)[sel], qstride, Hq, Hkv, st["pos"][sel],
+                              np.arange(len(sel), dtype=np.int32), bt_h, meta.max_blocks, SCALE)
+    ok, err = close(bits(out_f)[sel], want, what="c3 G=6 fused step, 8 of 64 sequences")
     assert ok, err
 
 
