@@ -956,7 +956,7 @@ def bench_attn(args):
             s, r = it
             oracle.attn_prefill(np.ascontiguousarray(q_h[r]), kc_h, vc_h, np.ascontiguousarray(proj_h[r]), qstride,
                                 hq, hkv, pos[r], np.array([0, 2], np.int32), 1, np.ascontiguousarray(bt_h[s:s + 1]),
-                                mb, BS, scale)
+                                mb, BS, scale, threads=1)
 
         rate1, rate_mt, nthr, detail = _cpu_rates(items, run, lambda it: 4.0 * D * hq * float(
             (pos[it[1]].astype(np.int64) + 1).sum()))
@@ -1077,7 +1077,7 @@ def cpu_baseline(kc, vc, q, qkv, meta, st, Hq, Hkv, qstride, dev):
     while True:
         oracle.append(k_new, v_new, slots, kc_h, vc_h)
         oracle.attn_decode(q_h, kc_h, vc_h, qkv_h, qstride, Hq, Hkv, pos, np.arange(len(sel), dtype=np.int32), bts,
-                           meta.max_blocks, BS, 1 / 16)
+                           meta.max_blocks, BS, 1 / 16, threads=1)
         reps += 1
         total = time.perf_counter() - t
         if total >= 10.0 or reps >= 8:
@@ -1108,7 +1108,7 @@ def cpu_baseline(kc, vc, q, qkv, meta, st, Hq, Hkv, qstride, dev):
         if len(ps) == 0:
             return
         oracle.append(kn, vn, sl, kc_h, vc_h)  # disjoint slots per set
-        oracle.attn_decode(qq, kc_h, vc_h, qk, qstride, Hq, Hkv, ps, ts, bt_, meta.max_blocks, BS, 1 / 16)
+        oracle.attn_decode(qq, kc_h, vc_h, qk, qstride, Hq, Hkv, ps, ts, bt_, meta.max_blocks, BS, 1 / 16, threads=1)
 
     reps_mt, t = 0, time.perf_counter()
     with concurrent.futures.ThreadPoolExecutor(nthr) as ex:
@@ -1217,7 +1217,7 @@ def cpu_baseline_prefill(kc, vc, q, qkv, bt, pos, cu, B, Hq, Hkv, qstride, mb, f
         s, rows = it
         oracle.attn_prefill(np.ascontiguousarray(q_h[rows]), kc_h, vc_h, np.ascontiguousarray(qkv_h[rows]), qstride,
                             Hq, Hkv, pos[rows], np.array([0, len(rows)], np.int32), 1,
-                            np.ascontiguousarray(bt_h[s:s + 1]), mb, BS, 1 / 16)
+                            np.ascontiguousarray(bt_h[s:s + 1]), mb, BS, 1 / 16, threads=1)
 
     def weight(it):
         return 4.0 * D * Hq * float((pos[it[1]].astype(np.int64) + 1).sum())
@@ -1271,7 +1271,7 @@ def cpu_baseline_rows(kc, vc, q, qkv, bt, pos, tok_seq, Hq, Hkv, qstride, mb, sa
         fn = oracle.attn_decode8 if kscale is not None else oracle.attn_decode
         fn(np.ascontiguousarray(q_h[i:i + 1]), hosts[0], hosts[1], *args8, np.ascontiguousarray(qkv_h[i:i + 1]),
            qstride, Hq, Hkv, np.array([pos[r]], np.int32), np.array([remap[int(tok_seq[r])]], np.int32), bt_h, mb,
-           BS, 1 / 16)
+           BS, 1 / 16, threads=1)
 
     def weight(i):
         return float(pos[sample_rows[i]] + 1)

@@ -52,6 +52,11 @@ _lib.orc_attn_prefill.restype = _I
 _lib.orc_attn_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I]
 _lib.orc_attn_prefill_t.restype = _I
 _lib.orc_attn_prefill_t.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I, _I]
+_lib.orc_attn_prefill_part.restype = _I
+_lib.orc_attn_prefill_part.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I, _I, _I, _I,
+                                       _I, _I]
+_lib.orc_dequant_e4m3.restype = None
+_lib.orc_dequant_e4m3.argtypes = [_P, _P, _L, _P]
 _lib.orc_mtp_slots.argtypes = [_P, _P, _P, _I, _I, _P, _I, _P, _P, _I]
 _lib.orc_mtp_next.argtypes = [_P, _P, _P, _I, _P, _I, _I, _P, _I, _P, _P, _P, _I]
 _lib.orc_attn_prep.argtypes = [_P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _F, _I, _L, _P, _P, _P]
@@ -122,17 +127,45 @@ def page_copy(kcache, vcache, src, dst, page_bytes):
 
 
 def attn_decode(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size, scale,
-                cu=None, skip_prompts=0, outs=None, spec=1, out=None):
-    """bf16 (uint16) arrays in; returns (out uint16 [T][Hq][256], o_raw f32)."""
+                cu=None, skip_prompts=0, outs=None, spec=1, out=None, threads=None):
+    """bf16 (uint16) arrays in; returns (out uint16 [T][Hq][256], o_raw f32).
+    threads: host threads over row ranges (None: up to 16)."""
     T = len(pos)
     if out is None:
         out = np.zeros((T, Hq, 256), np.uint16)
     raw = np.zeros((T, Hq, 256), np.float32)
     cu, outs, pos, tok_seq, block_table = _i32(cu), _i32(outs), _i32(pos), _i32(tok_seq), _i32(block_table)
-    _lib.orc_attn_decode(_p(q), _p(kcache), _p(vcache), _p(qkv), qstride, Hq, Hkv, _p(pos),
-                         _p(tok_seq), _p(block_table), max_blocks, block_size, _p(out), scale,
-                         _p(cu), skip_prompts, _p(outs), spec, T, _p(raw))
+    q, kcache, vcache, qkv = (np.ascontiguousarray(a) for a in (q, kcache, vcache, qkv))
+    q, qkv = q.reshape(T, -1), qkv.reshape(T, -1)
+
+    def run(t0, t1):
+        qs, qk, ps, ts, os_, rs = q[t0:t1], qkv[t0:t1], pos[t0:t1], tok_seq[t0:t1], out[t0:t1], raw[t0:t1]
+        _lib.orc_attn_decode(_p(qs), _p(kcache), _p(vcache), _p(qk), qstride, Hq, Hkv, _p(ps), _p(ts),
+                             _p(block_table), max_blocks, block_size, _p(os_), scale, _p(cu), skip_prompts, _p(outs),
+                             spec, t1 - t0, _p(rs))
+
+    _row_parts(pos, threads, run)
     return out, raw
+
+
+def _row_parts(pos, threads, run):
+    """Runs run(t0, t1) over contiguous row ranges balanced by attended keys
+    (pos + 1), on up to `threads` host threads (None: up to 16; ctypes
+    releases the GIL). The decode oracles' rows are independent: a row reads
+    only its own q, qkv, pos, tok_seq and writes only its own outputs."""
+    T = len(pos)
+    if T == 0:
+        return
+    nthr = max(1, min(threads or 16, os.cpu_count() or 1, T))
+    cum = np.concatenate([[0], np.cumsum(np.asarray(pos, np.int64) + 1)])
+    tb = sorted(set([0] + [int(np.searchsorted(cum, cum[-1] * i / nthr)) for i in range(1, nthr)] + [T]))
+    parts = [(tb[i], tb[i + 1]) for i in range(len(tb) - 1) if tb[i] < tb[i + 1]]
+    if len(parts) == 1:
+        run(*parts[0])
+        return
+    import concurrent.futures
+    with concurrent.futures.ThreadPoolExecutor(len(parts)) as ex:
+        list(ex.map(lambda tt: run(*tt), parts))
 
 
 def attn_single(q, kcache, vcache, D, Hq, Hkv, bt_row, L, block_size, scale):
@@ -171,15 +204,36 @@ P_TILE = 32  # the reference's prefill key tile (AM_BN, amd/attention.cuh:10)
 
 
 def attn_prefill(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks, block_size, scale,
-                 outs=None, spec=1, out=None, p_tile=P_TILE):
+                 outs=None, spec=1, out=None, p_tile=P_TILE, threads=None):
     """Chunked prefill. p_tile = 32 (default): the reference's tiled softmax
     with P rounded to bf16 for P.V; p_tile = 0: P in double (textbook)."""
     T = len(pos)
     if out is None:
         out = np.zeros((T, Hq, 256), np.uint16)
     pos, cu, block_table, outs = _i32(pos), _i32(cu), _i32(block_table), _i32(outs)
-    _lib.orc_attn_prefill_t(_p(q), _p(kcache), _p(vcache), _p(qkv), qstride, Hq, Hkv, _p(pos), _p(cu), seqs,
-                            _p(block_table), max_blocks, block_size, _p(out), scale, _p(outs), spec, p_tile)
+    q, kcache, vcache, qkv = (np.ascontiguousarray(a) for a in (q, kcache, vcache, qkv))
+    # (row range, head range) parts, balanced by attended keys, run on
+    # threads (ctypes releases the GIL; every part writes its own outputs)
+    nthr = max(1, min(threads or 16, os.cpu_count() or 1))
+    hparts = min(Hq, nthr)
+    hb = [Hq * i // hparts for i in range(hparts + 1)]
+    tparts = max(1, min(T, (2 * nthr + hparts - 1) // hparts))
+    cum = np.concatenate([[0], np.cumsum(pos.astype(np.int64) + 1)])
+    tb = [0] + [int(np.searchsorted(cum, cum[-1] * i / tparts)) for i in range(1, tparts)] + [T]
+    jobs = [(tb[i], tb[i + 1], hb[j], hb[j + 1]) for i in range(tparts) for j in range(hparts) if tb[i] < tb[i + 1]]
+
+    def run(job):
+        t0, t1, h0, h1 = job
+        _lib.orc_attn_prefill_part(_p(q), _p(kcache), _p(vcache), _p(qkv), qstride, Hq, Hkv, _p(pos), _p(cu), seqs,
+                                   _p(block_table), max_blocks, block_size, _p(out), scale, _p(outs), spec, p_tile, t0,
+                                   t1, h0, h1)
+
+    if len(jobs) == 1:
+        run(jobs[0])
+    else:
+        import concurrent.futures
+        with concurrent.futures.ThreadPoolExecutor(min(nthr, len(jobs))) as ex:
+            list(ex.map(run, jobs))
     return out
 
 
@@ -260,9 +314,11 @@ def attn_prep8(qkv, qstride, Hq, Hkv, q_norm, k_norm, rope, rope_stride, sec_h, 
 
 
 def attn_decode8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks,
-                 block_size, scale, cu=None, skip_prompts=0, outs=None, spec=1, out=None, return_raw=False):
+                 block_size, scale, cu=None, skip_prompts=0, outs=None, spec=1, out=None, return_raw=False,
+                 threads=None):
     """Decode attention over an E4M3 cache (reference attn_paged8 semantics).
-    Returns out, or (out, o_raw f32 ungated) with return_raw."""
+    Returns out, or (out, o_raw f32 ungated) with return_raw. threads: host
+    threads over row ranges (None: up to 16)."""
     T = len(pos)
     if out is None:
         out = np.zeros((T, Hq, 256), np.uint16)
@@ -270,25 +326,35 @@ def attn_decode8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, pos
     cu, outs, pos, tok_seq, block_table = _i32(cu), _i32(outs), _i32(pos), _i32(tok_seq), _i32(block_table)
     kscale = np.ascontiguousarray(kscale, np.float32)
     vscale = np.ascontiguousarray(vscale, np.float32)
-    _lib.orc_attn_decode8(_p(q), _p(kcache8), _p(vcache8), _p(kscale), _p(vscale), _p(qkv), qstride, Hq, Hkv,
-                          _p(pos), _p(tok_seq), _p(block_table), max_blocks, block_size, _p(out), scale, _p(cu),
-                          skip_prompts, _p(outs), spec, T, _p(raw))
+    q, kcache8, vcache8, qkv = (np.ascontiguousarray(a) for a in (q, kcache8, vcache8, qkv))
+    q, qkv = q.reshape(T, -1), qkv.reshape(T, -1)
+
+    def run(t0, t1):
+        qs, qk, ps, ts, os_, rs = q[t0:t1], qkv[t0:t1], pos[t0:t1], tok_seq[t0:t1], out[t0:t1], raw[t0:t1]
+        _lib.orc_attn_decode8(_p(qs), _p(kcache8), _p(vcache8), _p(kscale), _p(vscale), _p(qk), qstride, Hq, Hkv,
+                              _p(ps), _p(ts), _p(block_table), max_blocks, block_size, _p(os_), scale, _p(cu),
+                              skip_prompts, _p(outs), spec, t1 - t0, _p(rs))
+
+    _row_parts(pos, threads, run)
     return (out, raw) if return_raw else out
 
 
 def attn_prefill8(q, kcache8, vcache8, kscale, vscale, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,
-                  block_size, scale, out=None, p_tile=P_TILE):
+                  block_size, scale, out=None, p_tile=P_TILE, threads=None):
     """Chunked prefill over an E4M3 cache (reference attn_group8)."""
     T = len(pos)
     if out is None:
         out = np.zeros((T, Hq, 256), np.uint16)
-    pos, cu, block_table = _i32(pos), _i32(cu), _i32(block_table)
     kscale = np.ascontiguousarray(kscale, np.float32)
     vscale = np.ascontiguousarray(vscale, np.float32)
-    num_slots = kcache8.size // (Hkv * 256)
-    _lib.orc_attn_prefill8(_p(q), _p(kcache8), _p(vcache8), _p(kscale), _p(vscale), num_slots, _p(qkv), qstride, Hq,
-                           Hkv, _p(pos), _p(cu), seqs, _p(block_table), max_blocks, block_size, _p(out), scale, p_tile)
-    return out
+    kcache8, vcache8 = np.ascontiguousarray(kcache8), np.ascontiguousarray(vcache8)
+    n = kcache8.size // 256
+    kb, vb = np.empty((n, 256), np.uint16), np.empty((n, 256), np.uint16)
+    # orc_attn_prefill8's dequantisation, then the bf16 prefill (in parts)
+    _lib.orc_dequant_e4m3(_p(kcache8), _p(kscale), n, _p(kb))
+    _lib.orc_dequant_e4m3(_p(vcache8), _p(vscale), n, _p(vb))
+    return attn_prefill(q, kb, vb, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks, block_size, scale,
+                        out=out, p_tile=p_tile, threads=threads)
 
 
 def mx_index(r, kb, KB):

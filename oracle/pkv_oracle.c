@@ -270,10 +270,13 @@ void orc_merge(const double* M, const double* S, const double* A, int n, double*
  * (pack4, attention.cuh:115), and earlier sums are rescaled by
  * exp2(b_old - b) (attention.cuh:108-110). Returns the number of token rows
  * written. ---- */
-int orc_attn_prefill_t(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, const uint16_t* qkv,
-                       int qstride, int Hq, int Hkv, const int* pos, const int* cu, int seqs, const int* block_table,
-                       int max_blocks, int block_size, uint16_t* out, float scale, const int* outs, int spec,
-                       int p_tile) {
+/* orc_attn_prefill_part: the same over token rows [t0, t1) and query heads
+ * [h0, h1) only (each (row, head) output is independent of the others; the
+ * tests split one prefill over threads this way). */
+int orc_attn_prefill_part(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, const uint16_t* qkv,
+                          int qstride, int Hq, int Hkv, const int* pos, const int* cu, int seqs,
+                          const int* block_table, int max_blocks, int block_size, uint16_t* out, float scale,
+                          const int* outs, int spec, int p_tile, int t0, int t1, int h0, int h1) {
     const double LOG2E = 1.4426950408889634;
     const int G = Hq / Hkv;
     int rows = 0;
@@ -282,10 +285,11 @@ int orc_attn_prefill_t(const uint16_t* q, const uint16_t* kcache, const uint16_t
         const int n = cu[s + 1] - cu[s];
         if (n <= 1 || is_spec(outs, spec, s)) continue;
         const int* bt = block_table + (size_t)s * max_blocks;
-        for (int t = cu[s]; t < cu[s + 1]; t++) {
+        const int ta = cu[s] > t0 ? cu[s] : t0, tb = cu[s + 1] < t1 ? cu[s + 1] : t1;
+        for (int t = ta; t < tb; t++) {
             const int L = pos[t] + 1;
             double* sc = (double*)malloc(sizeof(double) * (size_t)L);
-            for (int h = 0; h < Hq; h++) {
+            for (int h = h0; h < h1; h++) {
                 const int kvh = h / G;
                 for (int d = 0; d < HEAD_DIM; d++)
                     qd[d] = rbf(orc_b2f(q[((size_t)t * Hq + h) * HEAD_DIM + d]) * (scale * (float)LOG2E));
@@ -337,6 +341,14 @@ int orc_attn_prefill_t(const uint16_t* q, const uint16_t* kcache, const uint16_t
         }
     }
     return rows;
+}
+
+int orc_attn_prefill_t(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, const uint16_t* qkv,
+                       int qstride, int Hq, int Hkv, const int* pos, const int* cu, int seqs, const int* block_table,
+                       int max_blocks, int block_size, uint16_t* out, float scale, const int* outs, int spec,
+                       int p_tile) {
+    return orc_attn_prefill_part(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, cu, seqs, block_table, max_blocks,
+                                 block_size, out, scale, outs, spec, p_tile, 0, cu[seqs], 0, Hq);
 }
 
 int orc_attn_prefill(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, const uint16_t* qkv,
@@ -606,6 +618,14 @@ int orc_attn_decode8(const uint16_t* q, const uint8_t* kcache8, const uint8_t* v
  * qwen35.cu:1364-1585 with F8): every K / V row is dequantised to
  * bf16(e4m3 * scale) as the reference loads its tiles (qwen35.cu:1424-1436),
  * then orc_attn_prefill. num_slots rows of Hkv heads. */
+/* E4M3 rows to bf16(e4m3 * scale), the dequantisation orc_attn_prefill8
+ * applies (n rows of 256, one scale per row). */
+void orc_dequant_e4m3(const uint8_t* c8, const float* scale, long n, uint16_t* out) {
+    for (long r = 0; r < n; r++)
+        for (int d = 0; d < HEAD_DIM; d++)
+            out[r * HEAD_DIM + d] = orc_f2b(orc_e4m3_to_f(c8[r * HEAD_DIM + d]) * scale[r]);
+}
+
 int orc_attn_prefill8(const uint16_t* q, const uint8_t* kcache8, const uint8_t* vcache8, const float* kscale,
                       const float* vscale, long num_slots, const uint16_t* qkv, int qstride, int Hq, int Hkv,
                       const int* pos, const int* cu, int seqs, const int* block_table, int max_blocks,

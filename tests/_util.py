@@ -166,8 +166,8 @@ def oracle_decode_rows(q, kc, vc, qkv, qstride, Hq, Hkv, pos, tok_seq, bt, max_b
             np.ascontiguousarray(qkv[ids]), qstride, Hq, Hkv, np.ascontiguousarray(pos[ids], np.int32),
             np.ascontiguousarray(tok_seq[ids], np.int32), bt, max_blocks, BS, scale)
         if decode8:
-            return ids, oracle.attn_decode8(*args)
-        return ids, oracle.attn_decode(*args)[0]
+            return ids, oracle.attn_decode8(*args, threads=1)
+        return ids, oracle.attn_decode(*args, threads=1)[0]  # the sets already run on threads
 
     for ids, o in run_threads(one, balanced_sets(np.asarray(pos) + 1, 4 * oracle_threads())):
         out[ids] = o

@@ -32,11 +32,11 @@ def test_status_strings():
 def test_invalid_and_unsupported_arguments_return_before_launch():
     L = pkv._lib
     # decode: G = Hq / Hkv outside 1, 2, 4, 6, 8 (or Hq not a multiple of
-    # Hkv) is unsupported, block size must be 16; the fused step is G = 4 only
+    # Hkv) is unsupported, block size must be 16, for the fused step too
     for Hq, Hkv in ((10, 2), (12, 8), (3, 2), (24, 2)):
         assert L.pkv_attn_decode(1, 1, 1, 1, 8192, Hq, Hkv, 1, 1, 1, 4, 16, 1, 0.1, 1, 0, None, 1, 3, 10, 1,
                                  1 << 30, None) == pkv.ERR_UNSUPPORTED
-    assert L.pkv_attn_decode_step(16, 16, 4096, 16, 16, 16, 16, 16, 12288, 12, 2, 16, 16, 16, 4, 16, 16, 0.1, 16, 0,
+    assert L.pkv_attn_decode_step(16, 16, 4096, 16, 16, 16, 16, 16, 12288, 10, 2, 16, 16, 16, 4, 16, 16, 0.1, 16, 0,
                                   None, 1, 3, 10, 256, 1 << 30, None) == pkv.ERR_UNSUPPORTED
     assert L.pkv_attn_decode(1, 1, 1, 1, 8192, 16, 4, 1, 1, 1, 4, 32, 1, 0.1, 1, 0, None, 1, 3, 10, 1, 1 << 30,
                              None) == pkv.ERR_UNSUPPORTED

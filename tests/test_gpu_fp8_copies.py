@@ -172,17 +172,17 @@ def test_fp8_request_consumed_by_a_failing_call(dev, entry):
     with pytest.raises(pkv.PkvError):
         run(c, dev, "step" if entry.startswith("step") else "decode")
     if entry == "step_noalloc_bad_group":
-        # a second request, refused by the no-allocation step's group check
+        # a second request, refused by the no-allocation step's group check (G = 5)
         pkv.attn_fp8_next(fq, fs, 1, FROWS)
-        cc = decode_case([50], 24, 4, 7)
+        cc = decode_case([50], 20, 4, 7)
         q, qkv = t_(cc["q"], dev), t_(cc["qkv"], dev)
         pos, ts, bt, cu = (t_(np.asarray(cc[k], np.int32), dev) for k in ("pos", "tok_seq", "bt", "cu"))
         kc, vc = t_(cc["kc"], dev), t_(cc["vc"], dev)
-        out = torch.zeros(1, 24, D, dtype=torch.int16, device=dev)
+        out = torch.zeros(1, 20, D, dtype=torch.int16, device=dev)
         slot = t_(np.zeros(1, np.int32), dev)
         with pytest.raises(pkv.PkvError):
             pkv.attn_decode_step_noalloc(qkv.data_ptr(), qkv.data_ptr(), 2 * 4 * D * 2, slot, q, kc, vc, qkv,
-                                         cc["qstride"], 24, 4, pos, ts, bt, cc["max_blocks"], BS, out, SCALE, cu, 0,
+                                         cc["qstride"], 20, 4, pos, ts, bt, cc["max_blocks"], BS, out, SCALE, cu, 0,
                                          None, 1, 1, cc["pages"])
     got = run(c, dev, "decode")
     torch.cuda.synchronize()

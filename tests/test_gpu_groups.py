@@ -88,19 +88,19 @@ def test_e4m3_groups_match_oracle(dev, entry, G, Hkv):
     assert ok, f"max |diff| {err}"
 
 
-def test_fused_step_rejects_other_groups(dev):
-    """The fused append + decode step serves G = 4 only; other groups get
-    PKV_ERR_UNSUPPORTED before any launch."""
-    c = decode_case([40, 50], 24, 4, 3)
+def test_fused_step_rejects_unsupported_groups(dev):
+    """The fused append + decode step serves G in {1, 2, 4, 6, 8}; another
+    group (G = 5) gets PKV_ERR_UNSUPPORTED before any launch."""
+    c = decode_case([40, 50], 20, 4, 3)
     T = 2
-    q = torch.zeros(T, 24, D, dtype=torch.int16, device=dev)
+    q = torch.zeros(T, 20, D, dtype=torch.int16, device=dev)
     kc = torch.zeros(c["pages"] * BS, 4, D, dtype=torch.int16, device=dev)
     rows = torch.zeros(T, 4 * D, dtype=torch.int16, device=dev)
     qkv = torch.zeros(T, c["qstride"], dtype=torch.int16, device=dev)
     i = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
-    ws = torch.empty(pkv.attn_decode_workspace(T, 24), dtype=torch.uint8, device=dev)
+    ws = torch.empty(pkv.attn_decode_workspace(T, 20), dtype=torch.uint8, device=dev)
     with pytest.raises(pkv.PkvError, match="unsupported"):
-        pkv.attn_decode_step(rows, rows, 4 * D * 2, i([0, 16]), q, kc, kc, qkv, c["qstride"], 24, 4, i(c["pos"]),
+        pkv.attn_decode_step(rows, rows, 4 * D * 2, i([0, 16]), q, kc, kc, qkv, c["qstride"], 20, 4, i(c["pos"]),
                              i(c["tok_seq"]), i(c["bt"]), c["max_blocks"], BS, q, SCALE, i(c["cu"]), 0, None, 1, T,
                              c["pages"], ws)
 

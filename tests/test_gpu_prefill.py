@@ -223,7 +223,7 @@ def test_prefill_c4_through_kv_manager(dev):
         return rows, oracle.attn_prefill(np.ascontiguousarray(q_h[rows]), kc_h, vc_h,
                                          np.ascontiguousarray(qkv_h[rows]), qstride, Hq, Hkv, pos[rows],
                                          np.array([0, len(rows)], np.int32), 1, np.ascontiguousarray(bt_h[s:s + 1]),
-                                         mb, BS, SCALE)
+                                         mb, BS, SCALE, threads=1)
 
     rows_all = np.concatenate([g[1] for g in groups])
     want = np.zeros((len(rows_all), Hq, D), np.uint16)
