@@ -53,6 +53,7 @@ ATOL, RTOL = 2e-3, 1e-2
 # max-rel over |want| > ATOL, elements above ATOL); conftest prints them at
 # the end of the run.
 PARITY_LOG = []
+EXPLAIN_LOG = []  # (test, line) of explain_beyond
 
 
 class Closeness(tuple):
@@ -76,7 +77,38 @@ def bf16_ulp(w):
     return np.exp2(np.floor(np.log2(a)) - 7)
 
 
-def close(got_bits, want_bits, atol=ATOL, rtol=RTOL, what=""):
+def explain_beyond(got_bits, want_bits, raw, qkv, qstride, Hq, atol=ATOL, rtol=RTOL):
+    """For every element beyond both bounds alone (|d| > max(atol, rtol
+    |want|)): its (row, head, dim), want, got, the oracle's unrounded output
+    o (raw, f32 of the f64 value), its bf16 rounding rbf(o), how far o lies
+    from that rounding's nearest tie point (in bf16 ulps of o), and which of
+    rbf(o) - 1 ulp, rbf(o), rbf(o) + 1 ulp gives `got` once gated as the
+    epilogue does: bf16(rbf * sigmoid(gate)). Returns the lines."""
+    import oracle
+    g = oracle.b2f(got_bits).astype(np.float64)
+    w = oracle.b2f(want_bits).astype(np.float64)
+    err = np.abs(g - w)
+    idx = np.argwhere(err > np.maximum(atol, rtol * np.abs(w)))
+    lines = []
+    for t, h, d in idx:
+        o = np.float32(raw[t, h, d])
+        gate = float(oracle.b2f(np.array([qkv[t, h * 512 + 256 + d]], np.uint16))[0])
+        r = float(oracle.b2f(oracle.f2b(np.array([o], np.float32)))[0])
+        ulp = float(bf16_ulp(r))
+        tie = r + ulp / 2 if o >= r else r - ulp / 2
+        which = []
+        for k, cand in ((-1, r - ulp), (0, r), (1, r + ulp)):
+            y = np.float32(cand) / (np.float32(1) + np.exp(np.float32(-gate), dtype=np.float32))
+            if float(oracle.b2f(oracle.f2b(np.array([y], np.float32)))[0]) == g[t, h, d]:
+                which.append(k)
+        lines.append(f"beyond both: (row {t}, head {h}, dim {d}) want {w[t, h, d]:.6g} got {g[t, h, d]:.6g} "
+                     f"|diff| {err[t, h, d]:.3e} rel {err[t, h, d] / abs(w[t, h, d]):.3e}; oracle o {float(o):.8g}, "
+                     f"rbf(o) {r:.6g}, |o - tie| {abs(float(o) - tie) / ulp:.4f} ulp, gate {gate:.4g}; got = gated "
+                     f"rbf(o) {'/'.join(f'{k:+d}' for k in which) if which else '(none of +-1)'} ulp")
+    return lines
+
+
+def close(got_bits, want_bits, atol=ATOL, rtol=RTOL, what="", explain=None):
     """The north-star attention tolerance on bf16 outputs (max-abs 2e-3,
     relative 1e-2) in the numpy / torch allclose form: every element with
     |got - want| <= atol + rtol * |want|. The additive form is needed by the
@@ -102,6 +134,10 @@ def close(got_bits, want_bits, atol=ATOL, rtol=RTOL, what=""):
     PARITY_LOG.append((test, what, r.n, r.max_abs, r.max_rel, r.max_ulp, r.n_either))
     print(f"parity {what}: {r.n} elements, max-abs {r.max_abs:.3e}, max-rel {r.max_rel:.3e} (|want| > {atol}), "
           f"max {r.max_ulp:.0f} ulp, {r.n_either} beyond both bounds alone", flush=True)
+    if explain is not None and r.n_either:
+        for line in explain_beyond(got_bits, want_bits, atol=atol, rtol=rtol, **explain):
+            print(line, flush=True)
+            EXPLAIN_LOG.append((test, line))
     return r
 
 

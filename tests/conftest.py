@@ -25,7 +25,7 @@ def pytest_terminal_summary(terminalreporter):
     """Prints the figures of every oracle comparison of the run
     (tests/_util.close), so the parity evidence is in the log."""
     try:
-        from _util import ATOL, PARITY_LOG, RTOL
+        from _util import ATOL, EXPLAIN_LOG, PARITY_LOG, RTOL
     except ImportError:
         return
     if not PARITY_LOG:
@@ -39,3 +39,5 @@ def pytest_terminal_summary(terminalreporter):
                   f"{max(r[3] for r in PARITY_LOG):.3e}, worst max_rel {max(r[4] for r in PARITY_LOG):.3e}, worst "
                   f"{max(r[5] for r in PARITY_LOG):.0f} ulp, {sum(r[6] for r in PARITY_LOG)} elements beyond both "
                   f"bounds alone")
+    for test, line in EXPLAIN_LOG:
+        tr.write_line(f"{test} {line}")

@@ -113,7 +113,10 @@ def test_ref_decode_groups_match_oracle(dev, rk, G, Hkv, lens, seed, Z):
     (model.rs:1053-1054)."""
     print(f"case refabi decode G={G} Hkv={Hkv} lens={lens[:6]} Z={Z}", flush=True)
     c = decode_case(lens, G * Hkv, Hkv, seed)
-    ok, err = close(ref_decode(rk, c, dev, Z=Z), oracle_decode(c))
+    want, raw = oracle.attn_decode(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], c["Hq"], c["Hkv"], c["pos"],
+                                   c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
+    ok, err = close(ref_decode(rk, c, dev, Z=Z), want,
+                    explain=dict(raw=raw, qkv=c["qkv"], qstride=c["qstride"], Hq=c["Hq"]))
     assert ok, f"max |diff| {err}"
 
 
