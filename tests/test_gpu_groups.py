@@ -332,9 +332,10 @@ def test_groups_more_rows_than_a_block(dev, G, Hkv):
     k8, v8 = e4m3_cache(c["kc"].shape, rng), e4m3_cache(c["vc"].shape, rng)
     ks = (rng.random(c["kc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
     vs = (rng.random(c["vc"].shape[:2]) * 0.02 + 0.001).astype(np.float32)
-    want = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], c["Hq"], Hkv, c["pos"], c["tok_seq"],
-                               c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"])
-    ok, err = close(run_decode8(c, k8, v8, ks, vs, dev, entry="verify"), want)
+    want, raw = oracle.attn_decode8(c["q"], k8, v8, ks, vs, c["qkv"], c["qstride"], c["Hq"], Hkv, c["pos"],
+                                    c["tok_seq"], c["bt"], c["max_blocks"], BS, SCALE, cu=c["cu"], return_raw=True)
+    ok, err = close(run_decode8(c, k8, v8, ks, vs, dev, entry="verify"), want,
+                    explain=dict(raw=raw, qkv=c["qkv"], qstride=c["qstride"], Hq=c["Hq"]))
     assert ok, f"verify e4m3 max |diff| {err}"
 
 
