@@ -1042,11 +1042,14 @@ def hbm_copy_probe(dev):
 
 
 def cpu_baseline(kc, vc, q, qkv, meta, st, Hq, Hkv, qstride, dev):
-    """The oracle (scalar C) on the first timed step's workload — append +
-    decode of all 64 sequences — timed on the host with 1 thread and with
-    up to 16 threads (the box's CPU share), tokens split into key-balanced
-    sets (ctypes releases the GIL, so the C calls run in parallel). The
-    line's value is the threaded figure; the 1-thread one rides along."""
+    """Scalar host code on the first timed step's workload — append + decode
+    of all 64 sequences — timed on the host with 1 thread and with up to 16
+    threads (the box's CPU share), tokens split into key-balanced sets (ctypes
+    releases the GIL, so the C calls run in parallel). Two implementations:
+    the one-pass f32 port (orc_attn_decode_f32: online softmax, K / V rows
+    read once per kv-head group, f32 throughout), whose threaded figure is
+    the line's value, and the f64 oracle (the checker: two passes, double
+    sums), reported beside it."""
     import numpy as np
     import torch
 
@@ -1071,23 +1074,11 @@ def cpu_baseline(kc, vc, q, qkv, meta, st, Hq, Hkv, qstride, dev):
     k_new = np.ascontiguousarray(qkv_h[:, 2 * Hq * D:2 * Hq * D + Hkv * D])
     v_new = np.ascontiguousarray(qkv_h[:, 2 * Hq * D + Hkv * D:2 * Hq * D + 2 * Hkv * D])
     slots = (bts[np.arange(len(sel)), pos // BS] * BS + pos % BS).astype(np.int32)
-    # The same step repeated (the append rewrites the same slots) until about
-    # 10 s of CPU work: a bounded sample, mean per step.
-    reps, t = 0, time.perf_counter()
-    while True:
-        oracle.append(k_new, v_new, slots, kc_h, vc_h)
-        oracle.attn_decode(q_h, kc_h, vc_h, qkv_h, qstride, Hq, Hkv, pos, np.arange(len(sel), dtype=np.int32), bts,
-                           meta.max_blocks, BS, 1 / 16, threads=1)
-        reps += 1
-        total = time.perf_counter() - t
-        if total >= 10.0 or reps >= 8:
-            break
-    dt = total / reps
     sample_keys = int((pos + 1).sum())
     full_keys = int((st["pos"] + 1).sum())
-    us_step = dt * 1e6 * full_keys / sample_keys
+    scale_f = full_keys / sample_keys
 
-    # Threaded: longest-first assignment of tokens to the lightest set.
+    # Threaded runs: longest-first assignment of tokens to the lightest set.
     import concurrent.futures
     nthr = max(1, min(16, os.cpu_count() or 1, len(sel)))
     sets = [[] for _ in range(nthr)]
@@ -1103,29 +1094,57 @@ def cpu_baseline(kc, vc, q, qkv, meta, st, Hq, Hkv, qstride, dev):
                       np.ascontiguousarray(q_h[ids]), np.ascontiguousarray(qkv_h[ids]), pos[ids].copy(),
                       np.arange(len(ids), dtype=np.int32), np.ascontiguousarray(bts[ids])))
 
-    def run(part):
-        kn, vn, sl, qq, qk, ps, ts, bt_ = part
-        if len(ps) == 0:
-            return
-        oracle.append(kn, vn, sl, kc_h, vc_h)  # disjoint slots per set
-        oracle.attn_decode(qq, kc_h, vc_h, qk, qstride, Hq, Hkv, ps, ts, bt_, meta.max_blocks, BS, 1 / 16, threads=1)
+    def decode(f32, qq, qk, ps, ts, bt_):
+        if f32:
+            oracle.attn_decode_f32(qq, kc_h, vc_h, qk, qstride, Hq, Hkv, ps, ts, bt_, meta.max_blocks, BS, 1 / 16)
+        else:
+            oracle.attn_decode(qq, kc_h, vc_h, qk, qstride, Hq, Hkv, ps, ts, bt_, meta.max_blocks, BS, 1 / 16,
+                               threads=1)
 
-    reps_mt, t = 0, time.perf_counter()
-    with concurrent.futures.ThreadPoolExecutor(nthr) as ex:
+    def timed(f32, budget1, budget_mt):
+        # The same step repeated (the append rewrites the same slots) to a
+        # bounded sample, mean per step: 1 thread, then the threaded sets.
+        reps, t = 0, time.perf_counter()
         while True:
-            list(ex.map(run, parts))
-            reps_mt += 1
-            total_mt = time.perf_counter() - t
-            if total_mt >= 5.0 or reps_mt >= 16:
+            oracle.append(k_new, v_new, slots, kc_h, vc_h)
+            decode(f32, q_h, qkv_h, pos, np.arange(len(sel), dtype=np.int32), bts)
+            reps += 1
+            total = time.perf_counter() - t
+            if total >= budget1 or reps >= 8:
                 break
-    us_step_mt = total_mt / reps_mt * 1e6 * full_keys / sample_keys
-    return {"value": round(us_step_mt, 1), "unit": "us/step", "cores": nthr, "kind": "port",
-            "arith": "f64 (the oracle: scalar C, scores, softmax and weighted sums in double)",
-            "sample": f"oracle append + decode of one full step: all {len(sel)} sequences, {sample_keys} keys, "
-                      f"{nthr} threads (tokens split into key-balanced sets), {reps_mt} repetitions in "
-                      f"{total_mt:.1f} s; 1 thread: {reps} repetitions in {total:.1f} s, {dt:.2f} s per step "
-                      f"(scale factor {full_keys / sample_keys:.3f})",
-            "single_thread_us_per_step": round(us_step, 1),
+
+        def run(part):
+            kn, vn, sl, qq, qk, ps, ts, bt_ = part
+            if len(ps) == 0:
+                return
+            oracle.append(kn, vn, sl, kc_h, vc_h)  # disjoint slots per set
+            decode(f32, qq, qk, ps, ts, bt_)
+
+        reps_mt, t = 0, time.perf_counter()
+        with concurrent.futures.ThreadPoolExecutor(nthr) as ex:
+            while True:
+                list(ex.map(run, parts))
+                reps_mt += 1
+                total_mt = time.perf_counter() - t
+                if total_mt >= budget_mt or reps_mt >= 16:
+                    break
+        return reps, total, reps_mt, total_mt
+
+    r1, t1, rm, tm = timed(True, 5.0, 3.0)
+    us1, usm = t1 / r1 * 1e6 * scale_f, tm / rm * 1e6 * scale_f
+    r1d, t1d, rmd, tmd = timed(False, 5.0, 3.0)
+    us1d, usmd = t1d / r1d * 1e6 * scale_f, tmd / rmd * 1e6 * scale_f
+    return {"value": round(usm, 1), "unit": "us/step", "cores": nthr, "kind": "port",
+            "arith": "f32 (one-pass scalar C port: online softmax, f32 scores, weights and sums)",
+            "sample": f"append + decode of one full step: all {len(sel)} sequences, {sample_keys} keys; "
+                      f"{nthr} threads (tokens split into key-balanced sets): {rm} repetitions in {tm:.1f} s; "
+                      f"1 thread: {r1} repetitions in {t1:.1f} s, {us1 / 1e6:.2f} s per step (scale factor "
+                      f"{scale_f:.3f})",
+            "single_thread_us_per_step": round(us1, 1),
+            "f64_oracle": {"value": round(usmd, 1), "cores": nthr, "single_thread_us_per_step": round(us1d, 1),
+                           "arith": "f64 (the checker: scores, softmax and weighted sums in double)",
+                           "sample": f"the same step: {rmd} repetitions in {tmd:.1f} s on {nthr} threads, {r1d} in "
+                                     f"{t1d:.1f} s on 1"},
             "cpu": _cpu_model()}
 
 

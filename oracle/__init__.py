@@ -52,6 +52,8 @@ _lib.orc_attn_prefill.restype = _I
 _lib.orc_attn_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I]
 _lib.orc_attn_prefill_t.restype = _I
 _lib.orc_attn_prefill_t.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I, _I]
+_lib.orc_attn_decode_f32.restype = _I
+_lib.orc_attn_decode_f32.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _F, _P, _I, _P, _I, _I]
 _lib.orc_attn_prefill_part.restype = _I
 _lib.orc_attn_prefill_part.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _I, _P, _F, _P, _I, _I, _I, _I,
                                        _I, _I]
@@ -146,6 +148,21 @@ def attn_decode(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_ta
 
     _row_parts(pos, threads, run)
     return out, raw
+
+
+def attn_decode_f32(q, kcache, vcache, qkv, qstride, Hq, Hkv, pos, tok_seq, block_table, max_blocks, block_size,
+                    scale, cu=None, skip_prompts=0, outs=None, spec=1, out=None):
+    """orc_attn_decode_f32: the one-pass f32 scalar decode (the CPU
+    baseline's f32 leg; the f64 attn_decode is the checker). One thread."""
+    T = len(pos)
+    if out is None:
+        out = np.zeros((T, Hq, 256), np.uint16)
+    cu, outs, pos, tok_seq, block_table = _i32(cu), _i32(outs), _i32(pos), _i32(tok_seq), _i32(block_table)
+    q, kcache, vcache, qkv = (np.ascontiguousarray(a) for a in (q, kcache, vcache, qkv))
+    _lib.orc_attn_decode_f32(_p(q), _p(kcache), _p(vcache), _p(qkv), qstride, Hq, Hkv, _p(pos), _p(tok_seq),
+                             _p(block_table), max_blocks, block_size, _p(out), scale, _p(cu), skip_prompts, _p(outs),
+                             spec, T)
+    return out
 
 
 def _row_parts(pos, threads, run):

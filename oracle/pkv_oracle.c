@@ -206,6 +206,69 @@ int orc_attn_decode(const uint16_t* q, const uint16_t* kcache, const uint16_t* v
     return rows;
 }
 
+/* ---- the same decode attention as a one-pass scalar f32 implementation
+ * (the CPU baseline's second leg, not a checker): per (token, kv head) each
+ * key's K and V rows are read once for the G query heads of the group, the
+ * scores and the online softmax (running max, rescale on a new max) and the
+ * weighted sums are f32, as a plain CPU port of attn_paged_g<G>
+ * (qwen35.cu:1146-1309) would keep them. Same rows, skipping and gated
+ * epilogue as orc_attn_decode. Returns the number of rows written. ---- */
+int orc_attn_decode_f32(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, const uint16_t* qkv,
+                        int qstride, int Hq, int Hkv, const int* pos, const int* tok_seq, const int* block_table,
+                        int max_blocks, int block_size, uint16_t* out, float scale, const int* cu, int skip_prompts,
+                        const int* outs, int spec, int T) {
+    const int G = Hq / Hkv;
+    if (G > 16) return -1;
+    int rows = 0;
+    float qf[16][HEAD_DIM], A[16][HEAD_DIM], kr[HEAD_DIM], vr[HEAD_DIM], m[16], l[16];
+    for (int t = 0; t < T; t++) {
+        const int sq = tok_seq[t];
+        if (skip_prompts && cu[sq + 1] - cu[sq] > 1 && !is_spec(outs, spec, sq)) continue;
+        const int L = pos[t] + 1;
+        const int* bt = block_table + (size_t)sq * max_blocks;
+        for (int kvh = 0; kvh < Hkv; kvh++) {
+            for (int g = 0; g < G; g++) {
+                const int h = kvh * G + g;
+                for (int d = 0; d < HEAD_DIM; d++) {
+                    qf[g][d] = orc_b2f(q[((size_t)t * Hq + h) * HEAD_DIM + d]) * scale;
+                    A[g][d] = 0.f;
+                }
+                m[g] = -INFINITY;
+                l[g] = 0.f;
+            }
+            for (int j = 0; j < L; j++) {
+                const size_t at = ((size_t)orc_slot(bt, j, block_size) * Hkv + kvh) * HEAD_DIM;
+                for (int d = 0; d < HEAD_DIM; d++) {
+                    kr[d] = orc_b2f(kcache[at + d]);
+                    vr[d] = orc_b2f(vcache[at + d]);
+                }
+                for (int g = 0; g < G; g++) {
+                    float sc = 0.f;
+                    for (int d = 0; d < HEAD_DIM; d++) sc += qf[g][d] * kr[d];
+                    if (sc > m[g]) {
+                        const float c = expf(m[g] - sc); /* 0 on the first key */
+                        l[g] *= c;
+                        for (int d = 0; d < HEAD_DIM; d++) A[g][d] *= c;
+                        m[g] = sc;
+                    }
+                    const float p = expf(sc - m[g]);
+                    l[g] += p;
+                    for (int d = 0; d < HEAD_DIM; d++) A[g][d] += p * vr[d];
+                }
+            }
+            for (int g = 0; g < G; g++) {
+                const int h = kvh * G + g;
+                for (int d = 0; d < HEAD_DIM; d++) {
+                    const float gate = orc_b2f(qkv[(size_t)t * qstride + (size_t)h * 2 * HEAD_DIM + HEAD_DIM + d]);
+                    out[((size_t)t * Hq + h) * HEAD_DIM + d] = gated((double)(A[g][d] / l[g]), gate);
+                }
+            }
+        }
+        rows++;
+    }
+    return rows;
+}
+
 /* ---- generic single-query attention (f32 or bf16 cache, any head dim) for
  * the CPU plumbing config: o[h][d] = softmax(q . k * scale) v over keys
  * 0..L-1 of one sequence, ungated, f32 output. ---- */

@@ -133,6 +133,31 @@ def test_decode_gate_and_closed_forms():
     assert np.array_equal(out, want)
 
 
+@pytest.mark.parametrize("lens,Hq,Hkv,seed", [([1, 17, 300], 16, 4, 11), ([900, 40], 24, 4, 12), ([64], 8, 8, 13)])
+def test_decode_f32_scalar_port_within_tolerance_of_the_oracle(lens, Hq, Hkv, seed):
+    """The one-pass f32 scalar decode (the CPU baseline's f32 leg) against the
+    f64 oracle: within the attention tolerance; the golden fixtures' cases
+    within it too (gates 0); a skipped prompt row is left untouched."""
+    from _util import close
+    c = decode_case(lens, Hq, Hkv, seed=seed)
+    want, _ = oracle.attn_decode(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["tok_seq"],
+                                 c["bt"], c["max_blocks"], BS, 1.0 / 16.0)
+    got = oracle.attn_decode_f32(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], Hq, Hkv, c["pos"], c["tok_seq"],
+                                 c["bt"], c["max_blocks"], BS, 1.0 / 16.0)
+    ok, err = close(got, want, what="f32 scalar port vs f64 oracle")
+    assert ok, err
+    g = np.load(GOLD)
+    cg = {k[2:]: g[k] for k in g.files if k.startswith("a_")}
+    Hq2, Hkv2 = int(cg["Hq"]), int(cg["Hkv"])
+    B = len(cg["pos"])
+    qstride = (2 * Hq2 + 2 * Hkv2) * D
+    gate = np.zeros((B, qstride), np.uint16)
+    got = oracle.attn_decode_f32(cg["q"], cg["kc"], cg["vc"], gate, qstride, Hq2, Hkv2, cg["pos"],
+                                 np.arange(B, dtype=np.int32), cg["bt"], cg["bt"].shape[1], BS, 1.0 / 16.0)
+    ok, err = close(got, bf16_bits(oracle.b2f(bf16_bits(cg["expect"])) * 0.5), what="f32 port vs SDPA golden")
+    assert ok, err
+
+
 def test_decode_wrong_head_mapping_would_fail():
     """GQA: q head h reads kv head h // G. Pools whose kv heads differ give
     different outputs per group, and equal outputs within a group only when q
