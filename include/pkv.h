@@ -178,9 +178,11 @@ int pkv_attn_decode_step(const void* k_rows, const void* v_rows, int64_t row_str
  * allocates nothing (no hipMalloc / hipFree, no allocating library routine).
  * Same arguments and results as pkv_attn_decode_step otherwise. Returns
  * PKV_ERR_UNSUPPORTED when the step's workspace exceeds the array:
- * 256-aligned (T + 2) int32 offsets, then (T + R) * Hq partial rows of 2 + 256
- * f32 (R = key ranges = CUs x pkv_attn_decode_config's wg_per_cu); at Hq = 16
- * on a 256-CU device, T <= 759. Every call on one GPU shares that GPU's array, so calls that
+ * 256-aligned (T + 2) int32 offsets, then (T + R) * Hq * n partial rows of
+ * 2 + 256 f32 (R = key ranges = CUs x pkv_attn_decode_config's wg_per_cu;
+ * n = 1 for G = 4, else the verify kernel's rows per segment: 4 for G <= 4,
+ * 2 for G = 6 or 8); on a 256-CU device T <= 759 at Hq = 16 (G = 4) and
+ * T <= 82 at Hq = 24 (G = 6). Every call on one GPU shares that GPU's array, so calls that
  * overlap on one GPU (different streams, or host threads) race; calls in
  * order on one stream are safe. */
 int pkv_attn_decode_step_noalloc(const void* k_rows, const void* v_rows, int64_t row_stride, const int32_t* slot_map,

@@ -82,9 +82,11 @@ struct DecodeLayout {
 
 // Partial rows: (T + n_wg) indices x Hq heads, times 4 query rows per index
 // for the verify kernel.
-DecodeLayout decode_layout(int T, int Hq, int n_wg, bool verify = false) {
+// verify: the verify kernels' records, one per segment row (vf_rows(G); the
+// workspace queries, which do not know G, size for the most, VF_ROWS).
+DecodeLayout decode_layout(int T, int Hq, int n_wg, bool verify = false, int G = 0) {
     DecodeLayout d;
-    const size_t rows = (size_t)(T + n_wg) * Hq * (verify ? pkv::VF_ROWS : 1);
+    const size_t rows = (size_t)(T + n_wg) * Hq * (verify ? (G > 0 ? pkv::vf_rows(G) : pkv::VF_ROWS) : 1);
     d.offs = 0;
     d.ms = round_up((size_t)(T + 2) * 4, 256);
     d.acc = d.ms + round_up(rows * 2 * 4, 256);
@@ -517,7 +519,7 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
             return PKV_ERR_INVALID;
     }
     const int n_wg = decode_n_wg() * (f8 ? F8_WG_PER_CU : 1);
-    const DecodeLayout lay = decode_layout(T, Hq, n_wg, verify);
+    const DecodeLayout lay = decode_layout(T, Hq, n_wg, verify, G);
     if (workspace_bytes < lay.total) return PKV_ERR_INVALID;
     if (fo.mode && T > fo.rows) return PKV_ERR_INVALID;
     pkv::DecodeParams p;
@@ -719,7 +721,9 @@ int pkv_attn_decode_step_noalloc(const void* k_rows, const void* v_rows, int64_t
                                  int64_t num_blocks, void* stream) {
     // G = 4 runs the decode records, other groups the verify records
     const bool vrec = Hkv > 0 && Hq != 4 * Hkv;
-    if (T < 0 || Hq <= 0 || decode_layout(T, Hq, decode_n_wg(), vrec).total > PKV_NOALLOC_SCRATCH_BYTES) {
+    if (T < 0 || Hq <= 0 ||
+        decode_layout(T, Hq, decode_n_wg(), vrec, Hkv > 0 && Hq % Hkv == 0 ? Hq / Hkv : 0).total >
+            PKV_NOALLOC_SCRATCH_BYTES) {
         t_fp8 = {nullptr, nullptr, 0, 0};  // the failed call still consumes a pending FP8 request
         return T < 0 || Hq <= 0 ? PKV_ERR_INVALID : PKV_ERR_UNSUPPORTED;
     }

@@ -237,7 +237,7 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
 
 // Writes a verify piece's result for the lanes of (row r, head g): the gated
 // output when the piece holds all of the segment's keys, else the partial
-// record at index idx (VF_ROWS records per index).
+// record at index idx (vf_rows(G) records per index, one per segment row).
 template <int G>
 struct VerifyEpi {
     const DecodeParams& p;
@@ -256,7 +256,7 @@ struct VerifyEpi {
                     gate4(acc[db][0], acc[db][1], acc[db][2], acc[db][3], inv, graw);
             }
         } else {
-            const size_t row = ((size_t)idx * VF_ROWS + r) * p.Hq + h;
+            const size_t row = ((size_t)idx * vf_rows(G) + r) * p.Hq + h;
             float* pa = p.part_acc + row * HEAD_DIM + 4 * gq;
 #pragma unroll
             for (int db = 0; db < 16; db++)
@@ -386,7 +386,7 @@ __global__ void __launch_bounds__(64 * NW)
     const int R = p.offs[T + 1];
     const int b0 = o0 / R, b1 = (o1 - 1) / R;
     if (b0 == b1 && !p.fo.mode) return;
-    merge_head<NW>(p, t, (th + b0) * VF_ROWS + r, VF_ROWS, b1 - b0 + 1, blockIdx.y);
+    merge_head<NW>(p, t, (th + b0) * NR + r, NR, b1 - b0 + 1, blockIdx.y);
 }
 
 }  // namespace pkv

@@ -53,6 +53,28 @@ def test_noalloc_step_matches_workspace_step_twice(dev):
         assert ok, f"call {i}: max |diff| {err}"
 
 
+def test_noalloc_step_g6_matches_workspace_step_twice(dev):
+    """The reference's 27B shape (24 query heads over 4 kv heads: the verify
+    kernel's records, 2 per index) at C3's batch: the no-allocation step
+    equals the workspace step bit for bit on two calls in a row, the second
+    smaller, and is within tolerance of the oracle."""
+    pkv.attn_decode_config(1, 32)
+    rng = np.random.default_rng(17)
+    big = [int(x) for x in rng.integers(512, 8193, 64)]
+    small = [int(x) for x in rng.integers(1, 900, 7)]
+    for i, (lens, per_seq) in enumerate([(big, 1), (small, 2)]):
+        print(f"case noalloc G=6 call {i} B={len(lens)} per_seq={per_seq}", flush=True)
+        c = step_case(lens, 4, 60 + i, per_seq, G=6)
+        n_out, n_kc, n_vc = run_step(c, dev, noalloc=True)
+        w_out, w_kc, w_vc = run_step(c, dev, noalloc=False)
+        assert np.array_equal(n_out, w_out), f"call {i}: outputs differ from pkv_attn_decode_step"
+        assert np.array_equal(n_kc, w_kc) and np.array_equal(n_vc, w_vc), f"call {i}: caches differ"
+        o_out, o_kc, o_vc = oracle_step(c)
+        assert np.array_equal(n_kc, o_kc) and np.array_equal(n_vc, o_vc), f"call {i}: append differs from oracle"
+        ok, err = close(n_out, o_out, what=f"noalloc G=6 call {i}")
+        assert ok, f"call {i}: max |diff| {err}"
+
+
 def test_noalloc_step_rejects_a_step_beyond_the_array(dev):
     L = pkv._lib
     # T = 4096 tokens at Hq = 16 needs ~70 MiB of partials: refused before any launch
