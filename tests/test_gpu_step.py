@@ -211,12 +211,14 @@ def test_fused_step_many_one_key_sequences(dev):
     assert ok, err
 
 
-def test_step_graph_replay_matches_eager(dev):
+@pytest.mark.parametrize("G", [4, 6])
+def test_step_graph_replay_matches_eager(dev, G):
     """The step captured into a HIP graph (torch.cuda.CUDAGraph) and replayed
     5 times, with eager launches and synchronizations in between, reproduces
-    the eager outputs and caches bit for bit each time."""
-    print("case step graph replay", flush=True)
-    c = step_case([4000, 900, 6000, 33], 4, 7)
+    the eager outputs and caches bit for bit each time (G = 6: the verify
+    kernel's fused step)."""
+    print(f"case step graph replay G={G}", flush=True)
+    c = step_case([4000, 900, 6000, 33], 4, 7, G=G)
     Hq, Hkv, T = c["Hq"], c["Hkv"], c["T"]
     eager_out, eager_kc, _ = run(c, dev, fused=True)
     kc, vc = i16(c["kc"], dev), i16(c["vc"], dev)
