@@ -114,6 +114,16 @@ constexpr int pow2_floor(int x) { return x >= 1024 ? 1024 : x >= 512 ? 512 : x >
 // Threads that load and store tiles through registers: a power of two
 // (whole 16-byte chunks each); any others only compute.
 constexpr int pf_load_threads(int threads) { return pow2_floor(threads); }
+constexpr bool pf_pow2(int x) { return (x & (x - 1)) == 0; }
+constexpr int pf_log2(int x) { return x <= 1 ? 0 : 1 + pf_log2(x / 2); }
+// Register tile paths of a workgroup whose thread count is not a power of
+// two (G = 6: 6 or 3 waves) load through every thread, each wave taking
+// key pairs (2 w, 2 w + 1) + KPU u of the tile (KPU = threads / 32), so a
+// wave's chunk u lies in one page whenever pages hold 2 keys or more.
+// Otherwise the first pf_load_threads() threads load KPU-key groups, one
+// page each, when pages hold KPU keys or more. Smallest page (log2) that
+// takes the uniform-page path:
+constexpr int pf_upage_log2(int threads) { return pf_pow2(threads) ? pf_log2(pf_load_threads(threads) / 32) : 1; }
 // Waves that issue the DMA path's tile loads (pairs per wave 16 / that: 2,
 // 4 or 8).
 constexpr int pf_dma_waves(int threads) { return pow2_floor(threads) / 64 > 8 ? 8 : pow2_floor(threads) / 64; }
@@ -291,9 +301,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     constexpr bool PAIRED = BQ < 32;
     static_assert(!PAIRED || (BQ == 16 && NQB == 1 && G % 2 == 0), "16-query tiles pair heads");
     static_assert(PAIRED || BQ % (32 * NQB) == 0, "whole 32-query blocks");
-    // Tiles load through the first LDT threads (a power of two).
-    constexpr int LDT = pf_load_threads(THREADS);
-    static_assert(PF_BK * HEAD_DIM / 8 % LDT == 0, "whole 16-byte chunks per thread");
+    // Register paths: tiles load through the first LDT threads (a power of
+    // two), or (WP) through every thread, in wave-sized key pairs.
+    constexpr bool WP = !DMA && !pf_pow2(THREADS);
+    constexpr int LDT = WP ? THREADS : pf_load_threads(THREADS);
+    static_assert(WP || PF_BK * HEAD_DIM / 8 % LDT == 0, "whole 16-byte chunks per thread");
+    static_assert(!WP || THREADS % 64 == 0, "whole waves");
     // Buffer b: K tile at pf_smem + b * STAGE, V tile right after it.
     constexpr int STAGE = pf_stage(VP);
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31,
@@ -361,7 +374,15 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     // past L are zeroed when the tile is stored to LDS, so no load result is
     // overwritten while in flight.
     constexpr int KPU = LDT / 32;
-    constexpr int NCH = PF_BK / KPU;
+    constexpr int NCH = (PF_BK + KPU - 1) / KPU;
+    // chunk u of this thread holds a key of the tile (wave-uniform: WP
+    // leaves the last chunk to the waves whose pairs fit)
+    auto chunk_ok = [&](int u) {
+        if constexpr (WP)
+            return u * KPU + (tid >> 5) < PF_BK;
+        else
+            return true;
+    };
     const int kl0 = tid >> 5, c8 = (tid & 31) * 8;
     uint4 kr[NCH], vr[NCH];
     // E4M3: the raw bytes and scales stay in registers until the tile is
@@ -404,8 +425,22 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             return *reinterpret_cast<const uint4*>(base + 2 * at);
         }
     };
-    const uint32_t lane_at = (uint32_t)(kl0 * row + kvh * HEAD_DIM + c8);  // lane part of an element offset
-    const uint32_t lane_sc = (uint32_t)(kl0 * p.Hkv + kvh);               // and of a scale index
+    // the lane's key within its group (WP: within its wave's pair)
+    uint32_t lane_at, lane_sc;  // lane parts of an element offset and of a scale index
+    if constexpr (WP) {
+        lane_at = (uint32_t)((lane >> 5) * row + kvh * HEAD_DIM + c8);
+        lane_sc = (uint32_t)((lane >> 5) * p.Hkv + kvh);
+    } else {
+        lane_at = (uint32_t)(kl0 * row + kvh * HEAD_DIM + c8);
+        lane_sc = (uint32_t)(kl0 * p.Hkv + kvh);
+    }
+    // first key of the uniform-page group of chunk u, relative to the tile
+    auto group_key = [&](int u) {
+        if constexpr (WP)
+            return u * KPU + 2 * wave;
+        else
+            return u * KPU;
+    };
     // UPAGE: the page ids of the tile loaded next (uniform), fetched one
     // tile ahead so their latency hides behind a whole tile of work (the
     // block-table reads are vector loads: the barriers keep the compiler
@@ -413,13 +448,14 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     int ids[NCH];
     auto fetch_ids = [&](int k0) {
 #pragma unroll
-        for (int u = 0; u < NCH; u++) ids[u] = bt[min((k0 + u * KPU) >> bs_log2, last_pi)];
+        for (int u = 0; u < NCH; u++) ids[u] = bt[min((k0 + group_key(u)) >> bs_log2, last_pi)];
     };
     auto load_tile = [&](int k0) {
         if constexpr (UPAGE) {
 #pragma unroll
             for (int u = 0; u < NCH; u++) {
-                const int kg = k0 + u * KPU;
+                if constexpr (WP) if (!chunk_ok(u)) continue;
+                const int kg = k0 + group_key(u);
                 long pg = __builtin_amdgcn_readfirstlane(ids[u]);
                 pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
                 const size_t slot = ((size_t)pg << bs_log2) + (kg & bs_mask);  // uniform
@@ -437,6 +473,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         } else {
 #pragma unroll
             for (int u = 0; u < NCH; u++) {
+                if constexpr (WP) if (!chunk_ok(u)) continue;
                 const int kp = k0 + u * KPU + kl0;
                 const size_t slot = (page_id(kp >> bs_log2) << bs_log2) + (kp & bs_mask);
                 if constexpr (F8) {
@@ -457,6 +494,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
         // only one chunk's bf16 values are live)
 #pragma unroll
         for (int u = 0; u < NCH; u++) {
+            if constexpr (WP) if (!chunk_ok(u)) continue;
             uint4 kx, vx;
             if constexpr (F8) {
                 kx = cvt8(kw[u], ksv[u]);
@@ -869,7 +907,7 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* p
     constexpr bool DMA = !F8;
     if (DMA && p.bs_log2 >= 4)
         prefill_tile<G, BQ, NQB, F8, true, NST, DMA, VP>(p, pf_smem, s, tb, nb, kvh, 0);
-    else if (p.bs_log2 >= __builtin_ctz(pf_load_threads(pf_threads(BQ, NQB, G)) / 32))
+    else if (p.bs_log2 >= pf_upage_log2(pf_threads(BQ, NQB, G)))
         prefill_tile<G, BQ, NQB, F8, true, NST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
     else
         prefill_tile<G, BQ, NQB, F8, false, NST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
@@ -946,7 +984,7 @@ __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_split_kernel(Pre
     constexpr bool DMA = !F8;
     if (DMA && p.bs_log2 >= 4)
         prefill_tile<G, BQ, NQB, F8, true, PF_NST, DMA, PF_VPAIR, true>(p, pf_smem, s, tb, nb, kvh, part, parts, l);
-    else if (p.bs_log2 >= __builtin_ctz(pf_load_threads(pf_threads(BQ, NQB, G)) / 32))
+    else if (p.bs_log2 >= pf_upage_log2(pf_threads(BQ, NQB, G)))
         prefill_tile<G, BQ, NQB, F8, true, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb, kvh, part, parts, l);
     else
         prefill_tile<G, BQ, NQB, F8, false, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb, kvh, part, parts,
