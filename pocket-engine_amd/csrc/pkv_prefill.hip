@@ -73,6 +73,21 @@ __device__ __forceinline__ uint4 buf_load16(const void* base, uint32_t off) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 8 bytes / 4 bytes the same way (the E4M3 register path's raw bytes and
+// scales).
+__device__ __forceinline__ uint2 buf_load8(const void* base, uint32_t off) {
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                                                       0x00020000);
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ float buf_load4f(const void* base, uint32_t off) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                                                       0x00020000);
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
 constexpr int PF_BK = 32;  // keys per tile
 // Tile layout in LDS (K and V alike, row-major [key][d]): keys r and r + 16
 // are one 1,024-byte pair (one 64-lane global_load_lds_dwordx4 fills it) and
@@ -460,8 +475,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                 pg = pg < 0 ? 0 : pg >= p.num_blocks ? p.num_blocks - 1 : pg;
                 const size_t slot = ((size_t)pg << bs_log2) + (kg & bs_mask);  // uniform
                 if constexpr (F8) {
-                    raw8(p.kc, p.kscale, slot, lane_at, lane_sc, kw[u], ksv[u]);
-                    raw8(p.vc, p.vscale, slot, lane_at, lane_sc, vw[u], vsv[u]);
+                    // buffer loads: the slot row in the descriptor, the
+                    // lane's byte and scale offsets one VGPR each
+                    kw[u] = buf_load8(reinterpret_cast<const uint8_t*>(p.kc) + slot * row, lane_at);
+                    vw[u] = buf_load8(reinterpret_cast<const uint8_t*>(p.vc) + slot * row, lane_at);
+                    ksv[u] = buf_load4f(p.kscale + slot * p.Hkv, 4 * lane_sc);
+                    vsv[u] = buf_load4f(p.vscale + slot * p.Hkv, 4 * lane_sc);
                 } else {
                     // buffer loads: uniform base in the descriptor, the lane's
                     // 32-bit byte offset in one VGPR shared by K and V
@@ -504,7 +523,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                 vx = vr[u];
             }
             if (tail && k0 + u * KPU + kl0 >= L) kx = vx = make_uint4(0, 0, 0, 0);
-            const int r = pf_row_of_key(u * KPU + kl0);
+            // WP: the lane's LDS rows are recomputed per tile (an opaque
+            // copy of kl0) instead of held across the loop, which costs a
+            // few VALU where keeping them spilled the raw chunks
+            int kl = kl0;
+            if constexpr (WP) asm volatile("" : "+v"(kl));
+            const int r = pf_row_of_key(u * KPU + kl);
             *reinterpret_cast<uint4*>(sk + pf_krow(r) + c8) = kx;
             *reinterpret_cast<uint4*>(sv + pf_vrow<VP>(r) + c8) = vx;
         }
