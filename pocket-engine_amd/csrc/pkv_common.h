@@ -26,6 +26,15 @@ __device__ __forceinline__ uint4 load_nt(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16 bytes at byte offset `off` of `base` (a uniform address: it goes in the
+// buffer descriptor, the offset stays one VGPR), nontemporal.
+__device__ __forceinline__ uint4 buf_load16_nt(const void* base, uint32_t off) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                                                       0x00020000);
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 __device__ __forceinline__ float b2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }

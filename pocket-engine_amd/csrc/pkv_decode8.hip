@@ -58,6 +58,9 @@ template <int NR = 1, int G = 4, class Epi>
 __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __restrict__ bt, WaveLds8& lds, int t,
                                             int kvh, int j0, int j1, Epi epi, const int* Lr = nullptr) {
     static_assert(NR >= 1 && NR <= 4 && NR * G <= 16, "up to 16 columns of up to 4 rows");
+    // wave-uniform bounds (page ids and bases then stay scalar)
+    j0 = __builtin_amdgcn_readfirstlane(j0);
+    j1 = __builtin_amdgcn_readfirstlane(j1);
     // Decode (one row, G <= 8 columns of 16): columns NCOL .. 2 NCOL - 1
     // repeat columns 0 .. NCOL - 1 (same q, so bit-identical scores, max,
     // sum and rescale) and take the bf16 remainders of the P.V weights while
@@ -105,25 +108,29 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     };
     uint4 kb[2][4], vb[8];
     float sc_ld;  // kscale (lanes 0..31) or vscale (lanes 32..63) of unit key lane % 32
+    // Loads take a uniform page base plus a 32-bit lane offset fixed for the
+    // piece (the saddr form: no per-load 64-bit address arithmetic).
+    const uint32_t k_lane = (uint32_t)(sig * row_bytes + kvh * HEAD_DIM + 16 * rho);
     auto load_k = [&](long pg_a, long pg_b) {
 #pragma unroll
         for (int pg = 0; pg < 2; pg++) {
-            const uint8_t* r = kc + ((size_t)(pg ? pg_b : pg_a) * PAGE + sig) * row_bytes + (size_t)kvh * HEAD_DIM +
-                               16 * rho;
+            const uint8_t* r = kc + (size_t)(pg ? pg_b : pg_a) * PAGE * row_bytes;
 #pragma unroll
-            for (int c = 0; c < 4; c++) kb[pg][c] = load_nt(r + 64 * c);
+            for (int c = 0; c < 4; c++) kb[pg][c] = buf_load16_nt(r, k_lane + 64 * c);
         }
         const int key = lane & 31;
         const size_t at = ((size_t)(key < PAGE ? pg_a : pg_b) * PAGE + (key & (PAGE - 1))) * Hkv + kvh;
         sc_ld = (lane < 32 ? p.kscale : p.vscale)[at];
     };
+    // V: load k < 4 reads key 4 rho + k of the first page, k >= 4 key
+    // 4 rho + k - 4 of the second (unit key vkey(k)), dims 16 sig .. + 15.
+    auto vkey = [&](int k) { return 16 * (k >> 2) + 4 * rho + (k & 3); };
+    const uint32_t v_lane = (uint32_t)(4 * rho * row_bytes + kvh * HEAD_DIM + 16 * sig);
     auto load_v = [&](long pg_a, long pg_b) {
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const int key = 8 * rho + k;  // rho is the quarter u here
-            const long pg = key < PAGE ? pg_a : pg_b;
-            vb[k] = load_nt(vc + ((size_t)pg * PAGE + (key & (PAGE - 1))) * row_bytes + (size_t)kvh * HEAD_DIM +
-                            16 * sig);
+            const uint8_t* r = vc + (size_t)(k < 4 ? pg_a : pg_b) * PAGE * row_bytes;
+            vb[k] = buf_load16_nt(r, v_lane + (uint32_t)((k & 3) * row_bytes));
         }
     };
 
@@ -174,11 +181,11 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
         // a column with no key yet subtracts 0 (its weights are all 0)
         const float mref = mn == -INFINITY ? 0.f : mn;
         const float cr_me = __builtin_amdgcn_exp2f(m - mref);  // 0 while m = -inf
-        // V rows to LDS as bf16 (exact): row 8 rho + k, dims 16 sig .. + 15;
+        // V rows to LDS as bf16 (exact): row vkey(k), dims 16 sig .. + 15;
         // rows of keys outside [j0, j1) as zeros (a stale slot may hold NaN)
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const int row = 8 * rho + k, kp = UNIT8 * u + row;
+            const int row = vkey(k), kp = UNIT8 * u + row;
             const bool in = kp >= j0 && kp < j1;
             uint16_t* d = lds.v + row * V8_VSTR + 16 * sig;
             *reinterpret_cast<uint4*>(d) = in ? e4m3x8_to_bf16x8(vb[k].x, vb[k].y) : make_uint4(0, 0, 0, 0);
