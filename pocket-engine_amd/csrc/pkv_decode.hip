@@ -286,22 +286,33 @@ __device__ __forceinline__ void piece_body(const DecodeParams& p, const int* __r
     };
     uint4 kb[4][2], vb[8];
     // MODE 1: plain cache addresses; MODE 2: per-lane cache / source rows.
+    // PLAIN pages load by buffer loads: the page's (uniform) base in the
+    // descriptor, the lane's byte offsets fixed for the piece.
+    const uint32_t k_lane = (uint32_t)(2 * (8 * sig + rho * row_elems)), v_lane = (uint32_t)(2 * (8 * ch + 8 * hv * row_elems));
+    const uint32_t row_b = (uint32_t)(2 * row_elems);
     auto load_k = [&](int pi, size_t base, auto mode) {
         constexpr bool FRESH = decltype(mode)::value == 2;
 #pragma unroll
         for (int pp = 0; pp < 4; pp++) {
-            const uint16_t* r = FRESH ? src(p.kc, p.k_rows, pi, base, 4 * pp + rho, 8 * sig)
-                                      : p.kc + base + 8 * sig + (size_t)(4 * pp + rho) * row_elems;
-            kb[pp][0] = load_nt(r);
-            kb[pp][1] = load_nt(r + 128);
+            if constexpr (FRESH) {
+                const uint16_t* r = src(p.kc, p.k_rows, pi, base, 4 * pp + rho, 8 * sig);
+                kb[pp][0] = load_nt(r);
+                kb[pp][1] = load_nt(r + 128);
+            } else {
+                kb[pp][0] = buf_load16_nt(p.kc + base, k_lane + 4 * pp * row_b);
+                kb[pp][1] = buf_load16_nt(p.kc + base, k_lane + 4 * pp * row_b + 256);
+            }
         }
     };
     auto load_v = [&](int pi, size_t base, auto mode) {
         constexpr bool FRESH = decltype(mode)::value == 2;
 #pragma unroll
-        for (int k = 0; k < 8; k++)
-            vb[k] = load_nt(FRESH ? src(p.vc, p.v_rows, pi, base, 8 * hv + k, 8 * ch)
-                                  : p.vc + base + 8 * ch + (size_t)(8 * hv + k) * row_elems);
+        for (int k = 0; k < 8; k++) {
+            if constexpr (FRESH)
+                vb[k] = load_nt(src(p.vc, p.v_rows, pi, base, 8 * hv + k, 8 * ch));
+            else
+                vb[k] = buf_load16_nt(p.vc + base, v_lane + k * row_b);
+        }
     };
     using NONE = std::integral_constant<int, 0>;
     using PLAIN = std::integral_constant<int, 1>;
