@@ -120,15 +120,29 @@ __device__ __forceinline__ void verify_piece(const DecodeParams& p, const int* _
             return kp >= P0 && kp < j1 ? f : c;
         }
     };
+    // Plain pages load by buffer loads: the page's (uniform) base in the
+    // descriptor, the lane's byte offsets fixed for the piece.
+    const uint32_t k_lane = (uint32_t)(2 * ((size_t)c16 * row_elems + 8 * gq));
+    const uint32_t v_lane = (uint32_t)(2 * ((size_t)(lane >> 5) * row_elems + 8 * (lane & 31)));
+    const uint32_t row_b = (uint32_t)(2 * row_elems);
     auto load_k = [&](Buf& B, size_t base, int pi, auto fresh) {
-        const uint16_t* r = src(p.kc, p.k_rows, pi, base, c16, 8 * gq, fresh);
+        if constexpr (decltype(fresh)::value) {
+            const uint16_t* r = src(p.kc, p.k_rows, pi, base, c16, 8 * gq, fresh);
 #pragma unroll
-        for (int c = 0; c < NK; c++) B.kb[c] = load_nt(r + 32 * c);
+            for (int c = 0; c < NK; c++) B.kb[c] = load_nt(r + 32 * c);
+        } else {
+#pragma unroll
+            for (int c = 0; c < NK; c++) B.kb[c] = buf_load16_nt(p.kc + base, k_lane + 64 * c);
+        }
     };
     auto load_v = [&](Buf& B, size_t base, int pi, auto fresh) {
 #pragma unroll
-        for (int k = 0; k < NV; k++)
-            B.vb[k] = load_nt(src(p.vc, p.v_rows, pi, base, 2 * k + (lane >> 5), 8 * (lane & 31), fresh));
+        for (int k = 0; k < NV; k++) {
+            if constexpr (decltype(fresh)::value)
+                B.vb[k] = load_nt(src(p.vc, p.v_rows, pi, base, 2 * k + (lane >> 5), 8 * (lane & 31), fresh));
+            else
+                B.vb[k] = buf_load16_nt(p.vc + base, v_lane + 2 * k * row_b);
+        }
     };
     // A operand of step c: K dims dim0(c) .. + 7 of key c16
     auto k_frag = [&](const Buf& B, int c) -> bf16x8 {
