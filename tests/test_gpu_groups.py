@@ -208,13 +208,15 @@ def paged_prompt_case(ctxs, chunks, Hkv, G, bs, seed):
 @pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("e4m3", [False, True])
 @pytest.mark.parametrize("G,Hkv", [(4, 4), (6, 4), (1, 4), (8, 2)])
-@pytest.mark.parametrize("bs", [4, 8, 32, 64])
+@pytest.mark.parametrize("bs", [1, 2, 4, 8, 32, 64])
 def test_prefill_block_sizes_match_oracle(dev, e4m3, G, Hkv, bs, split):
-    """Pages of 4 / 8 / 32 / 64 keys (any power of two; the reference engine
-    uses 16): below 16 keys the tiles load through registers with a page id
-    per key (pages smaller than the loading threads' key groups) or per key
-    group, at 32 and 64 by LDS DMA (bf16) — for every group shape; and the
-    same through the split-key entry points (these small grids split)."""
+    """Pages of 1 / 2 / 4 / 8 / 32 / 64 keys (any power of two; the reference
+    engine uses 16): below 16 keys the tiles load through registers with a
+    page id per key (pages smaller than the loading threads' key groups; at
+    G = 6, whose 6 waves load in key pairs, pages of 1 key) or per key group
+    (G = 6: per wave key pair from 2 keys up), at 32 and 64 by LDS DMA (bf16)
+    — for every group shape; and the same through the split-key entry points
+    (these small grids split)."""
     print(f"case prefill bs={bs} G={G} Hkv={Hkv} e4m3={e4m3} split={split}", flush=True)
     c = paged_prompt_case([100, 0, 37], [70, 33, 130], Hkv, G, bs, 200 + bs + G)
     T, Hq = c["T"], c["Hq"]
