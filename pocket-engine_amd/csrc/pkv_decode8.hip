@@ -149,6 +149,20 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
         constexpr bool PREFETCH = decltype(prefetch)::value != 0;
         long na = 0, nb = 0;
         if constexpr (PREFETCH) unit_pages(next_u, na, nb);
+        // V first: the unit's V bytes (requested at the start of the
+        // previous unit) go to LDS, and the next unit's V is requested at
+        // once, so it has a whole unit to arrive.
+        // V rows to LDS as bf16 (exact): row vkey(k), dims 16 sig .. + 15;
+        // rows of keys outside [j0, j1) as zeros (a stale slot may hold NaN)
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int row = vkey(k), kp = UNIT8 * u + row;
+            const bool in = kp >= j0 && kp < j1;
+            uint16_t* d = lds.v + row * V8_VSTR + 16 * sig;
+            *reinterpret_cast<uint4*>(d) = in ? e4m3x8_to_bf16x8(vb[k].x, vb[k].y) : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4*>(d + 8) = in ? e4m3x8_to_bf16x8(vb[k].z, vb[k].w) : make_uint4(0, 0, 0, 0);
+        }
+        if constexpr (PREFETCH) load_v(na, nb);
         f32x4 sacc[2];
 #pragma unroll
         for (int pg = 0; pg < 2; pg++) {
@@ -181,17 +195,6 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
         // a column with no key yet subtracts 0 (its weights are all 0)
         const float mref = mn == -INFINITY ? 0.f : mn;
         const float cr_me = __builtin_amdgcn_exp2f(m - mref);  // 0 while m = -inf
-        // V rows to LDS as bf16 (exact): row vkey(k), dims 16 sig .. + 15;
-        // rows of keys outside [j0, j1) as zeros (a stale slot may hold NaN)
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int row = vkey(k), kp = UNIT8 * u + row;
-            const bool in = kp >= j0 && kp < j1;
-            uint16_t* d = lds.v + row * V8_VSTR + 16 * sig;
-            *reinterpret_cast<uint4*>(d) = in ? e4m3x8_to_bf16x8(vb[k].x, vb[k].y) : make_uint4(0, 0, 0, 0);
-            *reinterpret_cast<uint4*>(d + 8) = in ? e4m3x8_to_bf16x8(vb[k].z, vb[k].w) : make_uint4(0, 0, 0, 0);
-        }
-        if constexpr (PREFETCH) load_v(na, nb);
         // P^T operands: the lane's own weights times vscale, as a bf16 high
         // part plus a bf16 remainder (two MFMAs: ~16 mantissa bits, where one
         // bf16 would add 2^-9 relative error per weight to products the
