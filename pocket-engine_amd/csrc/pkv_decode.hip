@@ -29,7 +29,9 @@
 //   V: lane (half h = lane / 32, chunk c = lane % 32) loads keys 8h .. 8h + 7,
 //      dims 8c .. 8c + 7 (16 bytes each: a full 512-byte row per half-wave);
 //      probabilities reach it through 272 bytes of LDS; 256 FMAs per lane.
-// K/V loads are nontemporal (read once). The next page's K is requested
+// K/V loads are nontemporal (read once): buffer loads with the page's base in
+// the descriptor for cache pages, global loads for the step's own rows. The
+// next page's K is requested
 // right after q.k and its V right after P.V, so one page (16 KiB) is always
 // in flight per wave; page ids come through the scalar cache. No MFMA.
 //
@@ -288,7 +290,8 @@ __device__ __forceinline__ void piece_body(const DecodeParams& p, const int* __r
     // MODE 1: plain cache addresses; MODE 2: per-lane cache / source rows.
     // PLAIN pages load by buffer loads: the page's (uniform) base in the
     // descriptor, the lane's byte offsets fixed for the piece.
-    const uint32_t k_lane = (uint32_t)(2 * (8 * sig + rho * row_elems)), v_lane = (uint32_t)(2 * (8 * ch + 8 * hv * row_elems));
+    const uint32_t k_lane = (uint32_t)(2 * (8 * sig + rho * row_elems));
+    const uint32_t v_lane = (uint32_t)(2 * (8 * ch + 8 * hv * row_elems));
     const uint32_t row_b = (uint32_t)(2 * row_elems);
     auto load_k = [&](int pi, size_t base, auto mode) {
         constexpr bool FRESH = decltype(mode)::value == 2;

@@ -108,8 +108,8 @@ __device__ __forceinline__ void piece_body8(const DecodeParams& p, const int* __
     };
     uint4 kb[2][4], vb[8];
     float sc_ld;  // kscale (lanes 0..31) or vscale (lanes 32..63) of unit key lane % 32
-    // Loads take a uniform page base plus a 32-bit lane offset fixed for the
-    // piece (the saddr form: no per-load 64-bit address arithmetic).
+    // Buffer loads: the page's (uniform) base in the descriptor and a 32-bit
+    // lane offset fixed for the piece (no per-load 64-bit address math).
     const uint32_t k_lane = (uint32_t)(sig * row_bytes + kvh * HEAD_DIM + 16 * rho);
     auto load_k = [&](long pg_a, long pg_b) {
 #pragma unroll
