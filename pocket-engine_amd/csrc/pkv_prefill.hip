@@ -146,6 +146,12 @@ constexpr int PF_STAGE = PF_K_ELEMS + PF_V_ELEMS;
 // LDS stages of K / V tiles: 3 (one barrier per tile) unless the launch's
 // shared memory only holds 2 (two barriers per tile).
 constexpr int PF_NST = 3;
+// Stages of the library's bf16 prompt kernel (LDS-DMA tiles): 4 with two
+// tiles per barrier for G = 6, whose 6 waves sit 2, 2, 1, 1 on the SIMDs
+// (the waves drift within a step and the lone ones fill in: C4 at 24 query
+// heads 7.16 -> 6.68 ms), else 3 with a barrier per tile (4 stages measured
+// 1.3 % slower at G = 4).
+constexpr int pf_lib_nst(int G) { return G == 6 ? 4 : 3; }
 // The DMA path's page-id ring after the stages: per DMA wave 4 slots x 4 ids.
 constexpr int pf_ids_bytes(int threads) { return pf_dma_waves(threads) * 4 * 4 * 4; }
 constexpr int PF_IDS_BYTES = pf_ids_bytes(PF_THREADS);
@@ -663,7 +669,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                 }
         }
     };
-    static_assert(NST == 2 || NST == 3, "2 or 3 stages");
+    static_assert(NST == 2 || NST == 3 || (NST == 4 && DMA), "2 or 3 stages (4 with LDS DMA)");
     if constexpr (DMA) {
         // Iteration i requests tile i + 2 (stage (i + 2) % 3, freed by the
         // barrier that ended iteration i - 1) and the page ids of tile i + 4,
@@ -745,6 +751,36 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                     else wait_vm<0>();
                     buf ^= 1;
                     zero_tail(k0 + PF_BK, buf);
+                    __syncthreads();
+                }
+            }
+        } else if constexpr (NST == 4) {
+            // Four stages, two tiles per barrier: step s (tiles i = 2 s and
+            // i + 1) requests tiles i + 2 and i + 3 into the stages of tiles
+            // i - 2 and i - 1 (freed by the barrier that ended step s - 1)
+            // and the page ids of tiles i + 6 and i + 7 into the ring slots
+            // tiles i + 2 and i + 3 were read from, computes tiles i and
+            // i + 1 with no barrier between them, waits for its own
+            // requests, then one barrier publishes tiles i + 2 and i + 3.
+            if (ntiles > 1) dma_tile(kbase + PF_BK, 1, 1);
+            if (ntiles > 4) dma_ids(kbase + 4 * PF_BK, 0);
+            if (ntiles > 5) dma_ids(kbase + 5 * PF_BK, 1);
+            wait_vm<0>();
+            zero_tail(kbase, 0);
+            if (ntiles > 1) zero_tail(kbase + PF_BK, 1);
+            __syncthreads();
+            for (int it = 0; it < ntiles; it += 2) {
+                const int k0 = kbase + it * PF_BK;
+                if (it + 2 < ntiles) dma_tile(k0 + 2 * PF_BK, (it + 2) & 3, (it + 2) & 3);
+                if (it + 3 < ntiles) dma_tile(k0 + 3 * PF_BK, (it + 3) & 3, (it + 3) & 3);
+                if (it + 6 < ntiles) dma_ids(k0 + 6 * PF_BK, (it + 2) & 3);
+                if (it + 7 < ntiles) dma_ids(k0 + 7 * PF_BK, (it + 3) & 3);
+                compute(it & 3, k0);
+                if (it + 1 < ntiles) compute((it + 1) & 3, k0 + PF_BK);
+                if (it + 2 < ntiles) {
+                    wait_vm<0>();
+                    zero_tail(k0 + 2 * PF_BK, (it + 2) & 3);
+                    if (it + 3 < ntiles) zero_tail(k0 + 3 * PF_BK, (it + 3) & 3);
                     __syncthreads();
                 }
             }
@@ -929,19 +965,20 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* p
     // through registers, with uniform page ids per chunk when pages hold at
     // least (loading threads) / 32 keys.
     constexpr bool DMA = !F8;
+    constexpr int RNST = NST > 3 ? 3 : NST;  // stages of the register paths
     if (DMA && p.bs_log2 >= 4)
         prefill_tile<G, BQ, NQB, F8, true, NST, DMA, VP>(p, pf_smem, s, tb, nb, kvh, 0);
     else if (p.bs_log2 >= pf_upage_log2(pf_threads(BQ, NQB, G)))
-        prefill_tile<G, BQ, NQB, F8, true, NST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
+        prefill_tile<G, BQ, NQB, F8, true, RNST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
     else
-        prefill_tile<G, BQ, NQB, F8, false, NST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
+        prefill_tile<G, BQ, NQB, F8, false, RNST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
 }
 
 // The library's prompt kernels for G query heads per kv head (shapes above).
 template <int G>
 __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
-    prefill_body<G, pf_lib_bq(G), pf_lib_nqb(G)>(p, pf_smem);
+    prefill_body<G, pf_lib_bq(G), pf_lib_nqb(G), false, pf_lib_nst(G)>(p, pf_smem);
 }
 
 // Few query tiles (the library kernel's grid would not fill four rounds of
@@ -1007,7 +1044,8 @@ __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_split_kernel(Pre
     // the tile paths of prefill_body
     constexpr bool DMA = !F8;
     if (DMA && p.bs_log2 >= 4)
-        prefill_tile<G, BQ, NQB, F8, true, PF_NST, DMA, PF_VPAIR, true>(p, pf_smem, s, tb, nb, kvh, part, parts, l);
+        prefill_tile<G, BQ, NQB, F8, true, DMA ? pf_lib_nst(G) : PF_NST, DMA, PF_VPAIR, true>(p, pf_smem, s, tb, nb,
+                                                                                           kvh, part, parts, l);
     else if (p.bs_log2 >= pf_upage_log2(pf_threads(BQ, NQB, G)))
         prefill_tile<G, BQ, NQB, F8, true, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb, kvh, part, parts, l);
     else
