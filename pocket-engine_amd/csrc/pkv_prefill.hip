@@ -150,7 +150,7 @@ constexpr int PF_NST = 3;
 // tiles per barrier for G = 6, whose 6 waves sit 2, 2, 1, 1 on the SIMDs
 // (the waves drift within a step and the lone ones fill in: C4 at 24 query
 // heads 7.16 -> 6.68 ms), else 3 with a barrier per tile (4 stages measured
-// 1.3 % slower at G = 4).
+// 0.6-1.5 % slower at G = 2, 4 and 8, whose 8 waves sit two per SIMD).
 constexpr int pf_lib_nst(int G) { return G == 6 ? 4 : 3; }
 // The DMA path's page-id ring after the stages: per DMA wave 4 slots x 4 ids.
 constexpr int pf_ids_bytes(int threads) { return pf_dma_waves(threads) * 4 * 4 * 4; }
