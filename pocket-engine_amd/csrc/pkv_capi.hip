@@ -277,22 +277,23 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
     // Few query tiles (one prompt, or one sequence's chunk, of a few
     // thousand tokens): the fine-tile kernel, half the queries per
     // workgroup and two workgroups per CU, fills and balances the CUs.
-    // (G <= 4: when the 8-wave workgroups would not cover the CUs once;
-    // G = 6 / 8, whose workgroups hold 6 / 8 waves of fewer queries: below
-    // four rounds.)
+    // (G != 8: when the library's workgroups would not cover the CUs once;
+    // G = 8, whose 8 waves hold fewer queries: below four rounds. At G = 6
+    // the library kernel's two-tile steps beat the fine kernel once its
+    // workgroups cover the CUs: 2,048 / 3,072 / 6,000-token prompts 121 /
+    // 226 / 546 us against 136 / 236 / 571.)
     PrefillKernel kern_run = kern;
     // With a workspace: the split kernel, which splits every query tile's
     // keys over several workgroups when the prompt's tiles leave CUs idle
     // (it counts them from cu), then the merge. G = 6 / 8 without a sure
     // split (the bound U Hkv already covers the CUs) where the fine kernel
-    // would run keeps the fine kernel (a 4,096-token prompt at G = 6: 383
-    // against the library tile's 405 us).
+    // would run keeps the fine kernel.
     // Without drafts to verify (outs null) every sequence of two or more
     // rows is a prompt, so at least T - seqs rows are: when their tiles
     // alone fill the CUs no split can happen, and the call runs as without
     // a workspace (no merge launch).
     const int64_t cus = device_cus();
-    const bool fine = !f8 && block_size >= 16 && (int64_t)tiles * Hkv < (G >= 6 ? 4 : 1) * cus;
+    const bool fine = !f8 && block_size >= 16 && (int64_t)tiles * Hkv < (G == 8 ? 4 : 1) * cus;
     const bool no_split = !outs && (int64_t)(T - seqs + bq - 1) / bq * Hkv >= cus;
     const bool split = workspace && !no_split && !(fine && G >= 6 && (int64_t)tiles * Hkv >= cus);
     PrefillSplitLayout lay{};
