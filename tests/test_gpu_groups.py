@@ -341,6 +341,23 @@ def test_groups_more_rows_than_a_block(dev, G, Hkv):
     assert ok, f"verify e4m3 max |diff| {err}"
 
 
+def test_prefill_g6_library_kernel_all_rows(dev):
+    """The G = 6 library prompt kernel (four LDS stages, a barrier every
+    second key tile) on a grid that covers the CUs, every row against the
+    oracle: a 1,070-token chunk after 1,000 cached keys and a 1,025-token
+    prompt (odd and even tile counts, partial last tiles)."""
+    print("case prefill G=6 library kernel all rows", flush=True)
+    from test_gpu_prefill import prefill_case
+    c = prefill_case([1000, 0], [1070, 1025], 4, 181, G=6)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert ((c["T"] + 31) // 32 + c["seqs"]) * 4 >= cus
+    got, init = _prefill(c, dev, "lib")
+    want = oracle.attn_prefill(c["q"], c["kc"], c["vc"], c["qkv"], c["qstride"], c["Hq"], 4, c["pos"], c["cu"],
+                               c["seqs"], c["bt"], c["max_blocks"], BS, SCALE, out=init.copy())
+    ok, err = close(got, want)
+    assert ok, f"max |diff| {err}"
+
+
 @pytest.mark.parametrize("G,nseq", [(1, 16), (2, 16), (4, 9), (6, 9), (8, 9)])
 def test_prefill_many_tiles_sampled_rows(dev, G, nseq):
     """Prompts with enough query tiles for the library's full-size kernel
