@@ -669,7 +669,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
                 }
         }
     };
-    static_assert(NST == 2 || NST == 3 || (NST == 4 && DMA), "2 or 3 stages (4 with LDS DMA)");
+    static_assert(NST >= 2 && NST <= 4, "2, 3 or 4 stages");
     if constexpr (DMA) {
         // Iteration i requests tile i + 2 (stage (i + 2) % 3, freed by the
         // barrier that ended iteration i - 1) and the page ids of tile i + 4,
@@ -815,6 +815,38 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
     // Only the first LDT threads load and store tiles.
     if (UPAGE && loader) fetch_ids(kbase);
     load_q();
+    if constexpr (NST == 4) {
+        // Four stages, two tiles per barrier, one tile of registers: step s
+        // (tiles i = 2 s and i + 1) stores tile i + 2 (requested during the
+        // previous step) into the stage of tile i - 2, requests tile i + 3,
+        // computes tile i, stores tile i + 3 into the stage of tile i - 1,
+        // requests tile i + 4, computes tile i + 1, then one barrier
+        // publishes tiles i + 2 and i + 3.
+        if (loader) {
+            load_tile(kbase);
+            store_tile(0, kbase);
+            if (ntiles > 1) {
+                load_tile(kbase + PF_BK);
+                store_tile(1, kbase + PF_BK);
+            }
+            if (ntiles > 2) load_tile(kbase + 2 * PF_BK);
+        }
+        __syncthreads();
+        for (int it = 0; it < ntiles; it += 2) {
+            const int k0 = kbase + it * PF_BK;
+            if (loader && it + 2 < ntiles) {
+                store_tile((it + 2) & 3, k0 + 2 * PF_BK);
+                if (it + 3 < ntiles) load_tile(k0 + 3 * PF_BK);
+            }
+            compute(it & 3, k0);
+            if (loader && it + 3 < ntiles) {
+                store_tile((it + 3) & 3, k0 + 3 * PF_BK);
+                if (it + 4 < ntiles) load_tile(k0 + 4 * PF_BK);
+            }
+            if (it + 1 < ntiles) compute((it + 1) & 3, k0 + PF_BK);
+            if (it + 2 < ntiles) __syncthreads();
+        }
+    } else {
     // NST 3: iteration i stores tile i + 1 (loaded during iteration i - 1)
     // into the stage tile i - 2 used, requests tile i + 2, computes tile i,
     // then one barrier. NST 2: iteration i requests tile i + 1, computes
@@ -848,6 +880,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, uint16_t* p
             __syncthreads();
             buf ^= 1;
         }
+    }
     }
     }
     // a tile with one range writes its gated rows, as the unsplit kernel
@@ -965,13 +998,12 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, uint16_t* p
     // through registers, with uniform page ids per chunk when pages hold at
     // least (loading threads) / 32 keys.
     constexpr bool DMA = !F8;
-    constexpr int RNST = NST > 3 ? 3 : NST;  // stages of the register paths
     if (DMA && p.bs_log2 >= 4)
         prefill_tile<G, BQ, NQB, F8, true, NST, DMA, VP>(p, pf_smem, s, tb, nb, kvh, 0);
     else if (p.bs_log2 >= pf_upage_log2(pf_threads(BQ, NQB, G)))
-        prefill_tile<G, BQ, NQB, F8, true, RNST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
+        prefill_tile<G, BQ, NQB, F8, true, NST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
     else
-        prefill_tile<G, BQ, NQB, F8, false, RNST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
+        prefill_tile<G, BQ, NQB, F8, false, NST, false, VP>(p, pf_smem, s, tb, nb, kvh, 0);
 }
 
 // The library's prompt kernels for G query heads per kv head (shapes above).
@@ -1096,7 +1128,7 @@ __global__ void __launch_bounds__(64 * G) prefill_merge_kernel(PrefillParams p) 
 template <int G>
 __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_e4m3_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
-    prefill_body<G, pf_lib_bq(G), pf_lib_nqb(G), true>(p, pf_smem);
+    prefill_body<G, pf_lib_bq(G), pf_lib_nqb(G), true, pf_lib_nst(G)>(p, pf_smem);
 }
 
 }  // namespace pkv
