@@ -271,7 +271,7 @@ int attn_prefill(const void* q, const void* kcache, const void* vcache, const fl
                                      pkv::prefill_kernel<6>, pkv::prefill_kernel<8>);
     int bq = pkv::pf_lib_bq(G);
     int threads = pkv::pf_lib_threads(G);
-    size_t smem = pkv::prefill_smem_bytes(pkv::pf_lib_nst(G), threads);
+    size_t smem = pkv::prefill_smem_bytes(f8 ? pkv::pf_lib_nst_f8(G) : pkv::pf_lib_nst(G), threads);
     // Upper bound on query tiles: each prompt sequence rounds up once.
     int tiles = (T + bq - 1) / bq + seqs;
     // Few query tiles (one prompt, or one sequence's chunk, of a few

@@ -152,6 +152,10 @@ constexpr int PF_NST = 3;
 // heads 7.16 -> 6.68 ms), else 3 with a barrier per tile (4 stages measured
 // 0.6-1.5 % slower at G = 2, 4 and 8, whose 8 waves sit two per SIMD).
 constexpr int pf_lib_nst(int G) { return G == 6 ? 4 : 3; }
+// The E4M3 prompt kernels (tiles through registers) take four stages and two
+// tiles per barrier for every group: C4 over E4M3 at G = 4 / 6 / 8 4.84 /
+// 10.39 / 9.55 -> 4.70 / 9.64 / 9.21 ms.
+constexpr int pf_lib_nst_f8(int G) { return 4; }
 // The DMA path's page-id ring after the stages: per DMA wave 4 slots x 4 ids.
 constexpr int pf_ids_bytes(int threads) { return pf_dma_waves(threads) * 4 * 4 * 4; }
 constexpr int PF_IDS_BYTES = pf_ids_bytes(PF_THREADS);
@@ -1079,10 +1083,11 @@ __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_split_kernel(Pre
         prefill_tile<G, BQ, NQB, F8, true, DMA ? pf_lib_nst(G) : PF_NST, DMA, PF_VPAIR, true>(p, pf_smem, s, tb, nb,
                                                                                            kvh, part, parts, l);
     else if (p.bs_log2 >= pf_upage_log2(pf_threads(BQ, NQB, G)))
-        prefill_tile<G, BQ, NQB, F8, true, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb, kvh, part, parts, l);
+        prefill_tile<G, BQ, NQB, F8, true, F8 ? pf_lib_nst_f8(G) : PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb,
+                                                                                             kvh, part, parts, l);
     else
-        prefill_tile<G, BQ, NQB, F8, false, PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb, kvh, part, parts,
-                                                                           l);
+        prefill_tile<G, BQ, NQB, F8, false, F8 ? pf_lib_nst_f8(G) : PF_NST, false, PF_VPAIR, true>(p, pf_smem, s, tb, nb,
+                                                                                              kvh, part, parts, l);
 }
 
 // Combines the key ranges of prefill_split_kernel: grid (rows, kv heads),
@@ -1128,7 +1133,7 @@ __global__ void __launch_bounds__(64 * G) prefill_merge_kernel(PrefillParams p) 
 template <int G>
 __global__ void __launch_bounds__(pf_lib_threads(G), 1) prefill_e4m3_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint16_t pf_smem[];
-    prefill_body<G, pf_lib_bq(G), pf_lib_nqb(G), true, pf_lib_nst(G)>(p, pf_smem);
+    prefill_body<G, pf_lib_bq(G), pf_lib_nqb(G), true, pf_lib_nst_f8(G)>(p, pf_smem);
 }
 
 }  // namespace pkv
