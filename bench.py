@@ -203,6 +203,9 @@ def main():
                     help="skip the HBM traffic measurement (two short child runs of the same workload under "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by 2 GiB device copies in the same runs)")
     ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--no-others", action="store_true",
+                    help="default run only: skip the short child runs of the other workloads (c2, c4, c5, bench-attn, "
+                         "c3 at 24 query heads, c3 over an E4M3 cache) whose figures go into other_configs")
     ap.add_argument("--unfused", action="store_true",
                     help="append, key ranges and merge as three launches instead of the fused step")
     args = ap.parse_args()
@@ -472,7 +475,9 @@ def main():
                                 append_rows=0 if e4m3 else B)
 
     line = {
-        "metric": "paged decode step us + achieved HBM GB/s (% of peak) at batch 64, 1 MI355X",
+        "metric": ("paged decode step us + achieved HBM GB/s (% of peak) at batch 64, 1 MI355X" if args.config == "c3"
+                   else "paged decode step us + achieved HBM GB/s (% of peak), one sequence at 4096 context, "
+                        "1 MI355X"),
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -496,7 +501,9 @@ def main():
                  "synthetic (seeded N(0,1)*0.5 K/V/q, U[512,8192] contexts)"),
         "config": {"workload": ("c3: batch-64 paged decode step (append 1 token/seq + paged decode attention)"
                                 if args.config == "c3" else
-                                "c2: single-sequence paged decode step at 4096 context (append + attention)"),
+                                "c2: single-sequence paged decode step at 4096 context (append + attention)") +
+                               (f", {Hq} query heads over {Hkv} kv heads (G = {G})" if G != 4 else "") +
+                               (", E4M3 cache" if e4m3 else ""),
                    "kv": args.kv,
                    "path": ("attn_prep (E4M3 store), key ranges over the E4M3 cache, merge" if e4m3 else
                             f"reference-ABI code object (append, attn_paged_g{G}, attn_merge)" if args.refabi else
@@ -515,7 +522,63 @@ def main():
                      "traffic_detail": traffic_detail},
         "cpu_baseline": cpu,
     }
+    if default_workload(args):
+        line["other_configs"] = other_configs()
     print(json.dumps(line), flush=True)
+
+
+# The other workloads' short runs (child processes, after the metric's own
+# run), as flags of this script. c3 at 24 query heads is the reference's 27B
+# shape (G = 6); the E4M3 line is the step over an E4M3 cache.
+OTHER_CONFIGS = [
+    ("c2", ["--config", "c2", "--seed", "1"]),
+    ("c4", ["--config", "c4", "--seed", "1", "--steps", "10", "--warmup", "2"]),
+    ("c5", ["--config", "c5", "--seed", "1"]),
+    ("attn", ["--config", "attn"]),
+    ("c3_g6", ["--q-heads", "24", "--seed", "1"]),
+    ("c3_e4m3", ["--kv", "e4m3", "--seed", "1"]),
+]
+
+
+def default_workload(args):
+    """True for the metric's own workload with no flag that changes it (the
+    run the driver makes)."""
+    return (args.config == "c3" and args.kv == "bf16" and args.q_heads == 16 and args.batch == 64
+            and args.pages == 65536 and not args.no_others and not args.traffic_child
+            and not (args.refabi or args.unfused or args.with_prep or args.verify_kernel)
+            and args.wg_per_cu is None and args.min_range is None)
+
+
+def other_configs():
+    """Runs each OTHER_CONFIGS workload in a child process (no CPU leg, no
+    counter runs; 200 s limit each) and keeps the headline fields of its JSON
+    line, or the error."""
+    import signal
+    import subprocess
+
+    out = {}
+    for name, flags in OTHER_CONFIGS:
+        cmd = [sys.executable, "-u", os.path.abspath(__file__), "--no-cpu", "--no-traffic", "--no-others"] + flags
+        proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, start_new_session=True,
+                                text=True)
+        try:
+            text, _ = proc.communicate(timeout=200)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)  # the process group this call started
+            proc.communicate()
+            out[name] = {"flags": " ".join(flags), "error": "timed out after 200 s"}
+            continue
+        lines = [ln for ln in text.splitlines() if ln.startswith("{")]
+        if proc.returncode != 0 or not lines:
+            out[name] = {"flags": " ".join(flags), "error": f"exit {proc.returncode}"}
+            continue
+        d = json.loads(lines[-1])
+        r = d.get("roofline") or {}
+        out[name] = {"flags": " ".join(flags), "workload": (d.get("config") or {}).get("workload"),
+                     "metric": d.get("metric"), "value": d.get("value"), "unit": d.get("unit"),
+                     "ms_per_step": d.get("ms_per_step"), "vs_baseline": d.get("vs_baseline"),
+                     "roofline": {k: r.get(k) for k in ("bound", "kernel", "achieved", "peak", "unit", "frac")}}
+    return out
 
 
 def bench_prefill(args):
