@@ -34,6 +34,15 @@ __device__ __forceinline__ uint4 buf_load16_nt(const void* base, uint32_t off) {
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// The same without the nontemporal hint: for lines read again soon (prompt
+// tiles shared by query tiles; E4M3 K pieces, where each instruction reads
+// half of every 128-byte line and the next one the other half).
+__device__ __forceinline__ uint4 buf_load16(const void* base, uint32_t off) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                                                       0x00020000);
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 __device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }

@@ -64,15 +64,6 @@ struct PrefillParams {
     int* split_plan;
 };
 
-// 16 bytes at byte offset `off` of `base` (a uniform address) by a raw
-// buffer load: the descriptor holds the base, the offset stays one VGPR.
-__device__ __forceinline__ uint4 buf_load16(const void* base, uint32_t off) {
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
-                                                                       0x00020000);
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
 // 8 bytes / 4 bytes the same way (the E4M3 register path's raw bytes and
 // scales).
 __device__ __forceinline__ uint2 buf_load8(const void* base, uint32_t off) {
