@@ -597,7 +597,7 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
     if ((phases & 2) && verify) {
         // waves per (row, head) block chosen as for decode_merge_kernel below
         using MergeKernel = void (*)(pkv::DecodeParams, const int*, const int*, const int*, const int*);
-        const int nw = (int64_t)T * Hq < device_cus() ? 16 : (int64_t)T + n_wg <= 8 * (int64_t)T ? 1 : 4;
+        const int nw = (int64_t)T * Hq < device_cus() ? 16 : (int64_t)T + n_wg <= 12 * (int64_t)T ? 1 : 4;
         const bool r4 = pkv::vf_rows(G) == 4;
         const MergeKernel mk = nw == 16 ? (r4 ? pkv::verify_merge_kernel<4, 16> : pkv::verify_merge_kernel<2, 16>)
                                : nw == 1 ? (r4 ? pkv::verify_merge_kernel<4, 1> : pkv::verify_merge_kernel<2, 1>)
@@ -608,12 +608,14 @@ int attn_decode_phases(int phases, const AppendArgs* app, const float* kscale, c
     if (phases & 2) {
         // Waves per (token, head) block: 16 when there are fewer blocks than
         // CUs (a head's records, up to one per range, load in one round);
-        // one when a token has at most 8 records on average ((T + n_wg) / T:
-        // one wave folds 16 per round and skips the cross-wave combine);
-        // else 4. Any count is correct; this only picks the faster launch.
+        // one when a token has at most 12 records on average ((T + n_wg) / T:
+        // one wave folds 16 per round and skips the cross-wave combine;
+        // measured faster at 9, the E4M3 C3 step's two ranges per CU, and
+        // slower at 17); else 4. Any count is correct; this only picks the
+        // faster launch.
         if ((int64_t)T * Hq < device_cus())
             hipLaunchKernelGGL(pkv::decode_merge_kernel<16>, dim3(T, Hq), dim3(1024), 0, (hipStream_t)stream, p);
-        else if ((int64_t)T + n_wg <= 8 * (int64_t)T)
+        else if ((int64_t)T + n_wg <= 12 * (int64_t)T)
             hipLaunchKernelGGL(pkv::decode_merge_kernel<1>, dim3(T, Hq), dim3(64), 0, (hipStream_t)stream, p);
         else
             hipLaunchKernelGGL(pkv::decode_merge_kernel<4>, dim3(T, Hq), dim3(256), 0, (hipStream_t)stream, p);
