@@ -61,7 +61,8 @@ def default_config():
     ([513, 8193, 1000, 4000, 777, 64], 4, 3),
     ([33] * 40, 4, 4),                   # many short sequences per range
     ([300, 5000], 8, 5),                 # two kv-head groups (Hkv 8)
-    ([700] * 24, 4, 9),                  # merge blocks of 4 waves (24 x 16 heads, ~12 records each)
+    ([700] * 24, 4, 9),                  # one-wave merge blocks at its bound (24 x 16 heads, ~12 records each)
+    ([700] * 16, 4, 10),                 # merge blocks of 4 waves (16 x 16 heads, ~17 records each)
 ])
 def test_decode_matches_oracle(dev, lens, Hkv, seed):
     print(f"case decode lens={lens[:6]} Hkv={Hkv} seed={seed}", flush=True)

@@ -93,6 +93,7 @@ def run_decode8(c, k8, v8, ks, vs, dev, skip=0, outs=None, spec=1, out_init=None
     ([31, 32, 33, 47, 48, 49, 95], 4, 5, 16),
     ([5, 40, 17, 33] * 75, 4, 6, 32),     # 300 rows: more than a block's token tables
     ([100, 3, 47] * 30, 1, 7, 32),        # Hkv 1 (64-thread blocks), 90 rows
+    ([600] * 56, 4, 8, 32),               # two ranges per CU: ~10 records per row, one-wave merge blocks
 ])
 def test_decode_e4m3_matches_oracle(dev, entry, lens, Hkv, seed, min_range):
     print(f"case {entry} e4m3 lens={lens} Hkv={Hkv} min_range={min_range}", flush=True)
