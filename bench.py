@@ -205,7 +205,8 @@ def main():
     ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-others", action="store_true",
                     help="default run only: skip the short child runs of the other workloads (c2, c4, c5, bench-attn, "
-                         "c3 at 24 query heads, c3 over an E4M3 cache) whose figures go into other_configs")
+                         "c3 at 24 query heads, c3 over an E4M3 cache) whose figures go into other_configs (also "
+                         "skipped under rocprofv3)")
     ap.add_argument("--unfused", action="store_true",
                     help="append, key ranges and merge as three launches instead of the fused step")
     args = ap.parse_args()
@@ -542,8 +543,11 @@ OTHER_CONFIGS = [
 
 def default_workload(args):
     """True for the metric's own workload with no flag that changes it (the
-    run the driver makes)."""
+    run the driver makes), outside rocprofv3: under the profiler (whose
+    launcher sets ROCPROF_OUTPUT_PATH for the program) the child runs would
+    add their launches, some of the same kernels, to the command's trace."""
     return (args.config == "c3" and args.kv == "bf16" and args.q_heads == 16 and args.batch == 64
+            and "ROCPROF_OUTPUT_PATH" not in os.environ
             and args.pages == 65536 and not args.no_others and not args.traffic_child
             and not (args.refabi or args.unfused or args.with_prep or args.verify_kernel)
             and args.wg_per_cu is None and args.min_range is None)
