@@ -64,8 +64,9 @@ struct PrefillParams {
     int* split_plan;
 };
 
-// 8 bytes / 4 bytes the same way (the E4M3 register path's raw bytes and
-// scales).
+// 8 bytes / 4 bytes by raw buffer loads, as buf_load16 (the base in the
+// descriptor, the offset one VGPR): the E4M3 register path's raw bytes and
+// scales.
 __device__ __forceinline__ uint2 buf_load8(const void* base, uint32_t off) {
     typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
