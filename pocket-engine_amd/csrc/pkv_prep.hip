@@ -82,13 +82,29 @@ __device__ __forceinline__ void prep_head(const PrepArgs& a, int t, int hh) {
     if (!is_q && !has_slot) return;
     const uint16_t* src = is_q ? row + (size_t)hh * 2 * HEAD_DIM : row + (size_t)a.Hq * 2 * HEAD_DIM +
                                                                      (size_t)(hh - a.Hq) * HEAD_DIM;
+    // The row, the norm weights, then the rotary positions and frequencies
+    // of the lane's 4 dims, all requested before anything waits (loads
+    // return in order: the squared sum waits for the row alone), so the 4
+    // cos / sin evaluations below wait on one round trip, not one each.
     const uint2 raw = *reinterpret_cast<const uint2*>(src + 4 * lane);
+    const float4 w = *reinterpret_cast<const float4*>((is_q ? a.q_norm : a.k_norm) + 4 * lane);
+    // (Every lane loads them, from valid indices: under a lane condition the
+    // compiler could not count the loads, and the squared sum would wait
+    // for all of them.)
+    int rpos[4];
+    float rinv[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int d = (4 * lane + e) & (ROPE_DIM / 2 - 1);
+        const int axis = (d % 3 == 1 && d < 3 * a.sec_h) ? 1 : (d % 3 == 2 && d < 3 * a.sec_w) ? 2 : 0;
+        rpos[e] = a.rope[(size_t)axis * a.rope_stride + t];
+        rinv[e] = a.inv_freq[d];
+    }
     const float x[4] = {bf_lo(raw.x), bf_hi(raw.x), bf_lo(raw.y), bf_hi(raw.y)};
     float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
     const float scale = 1.f / sqrtf(ss / HEAD_DIM + a.eps);
-    const float4 w = *reinterpret_cast<const float4*>((is_q ? a.q_norm : a.k_norm) + 4 * lane);
     float y[4] = {rbf(x[0] * scale * w.x), rbf(x[1] * scale * w.y), rbf(x[2] * scale * w.z), rbf(x[3] * scale * w.w)};
     // Rotary: lanes 0..7 hold dims d = 0..31 ("lo"), lanes 8..15 dims d + 32.
     float yp[4];
@@ -98,9 +114,7 @@ __device__ __forceinline__ void prep_head(const PrepArgs& a, int t, int hh) {
         const bool lo_half = lane < ROPE_DIM / 8;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int d = (4 * lane + e) & (ROPE_DIM / 2 - 1);
-            const int axis = (d % 3 == 1 && d < 3 * a.sec_h) ? 1 : (d % 3 == 2 && d < 3 * a.sec_w) ? 2 : 0;
-            const float f = (float)a.rope[(size_t)axis * a.rope_stride + t] * a.inv_freq[d];
+            const float f = (float)rpos[e] * rinv[e];
             const float c = rbf(cosf(f)), s = rbf(sinf(f));
             const float lo = lo_half ? y[e] : yp[e], hi = lo_half ? yp[e] : y[e];
             y[e] = lo_half ? rbf(rbf(lo * c) - rbf(hi * s)) : rbf(rbf(hi * c) + rbf(lo * s));
