@@ -153,7 +153,9 @@ def measure_traffic(args, seed, algorithmic_bytes, want=None):
                   "in the same runs"}
 
 
-def main():
+def build_parser():
+    """The command line of this script (the driver's contract: --gpus,
+    --steps, --warmup; the rest selects and shapes the workload)."""
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
@@ -209,7 +211,11 @@ def main():
                          "skipped under rocprofv3)")
     ap.add_argument("--unfused", action="store_true",
                     help="append, key ranges and merge as three launches instead of the fused step")
-    args = ap.parse_args()
+    return ap
+
+
+def main():
+    args = build_parser().parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the paged KV path shards by "
               "sequence with no exchange, so N-GPU throughput is N x the one-GPU figure. Run with --gpus 1.",
